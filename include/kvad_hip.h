@@ -1,0 +1,182 @@
+/*
+ * kvad_hip.h -- C ABI of libkvad_hip, the MI355X (gfx950) implementation of
+ * kvad's quantised matmul and decode attention.
+ *
+ * Every entry point replaces one operator of the reference crate
+ * (bisand/kvad, crates/llm) and is written so that the Rust side can bind it
+ * with a plain `extern "C"` block: plain C types, pointers and sizes, no
+ * ownership crossing the boundary except through the opaque handles below.
+ *
+ * Conventions (mirroring the reference):
+ *   - Every function returns an int status: KH_OK (0), KH_DECLINED (1: the
+ *     caller should run its CPU kernel, as `matvec_many` returning None does,
+ *     quant.rs:626-633), or a negative error.  kh_last_error() gives the
+ *     message for the calling thread.  Nothing aborts.
+ *   - Functions taking host pointers are synchronous: they copy inputs in,
+ *     run, copy results out and return.  `_dev` variants take device
+ *     pointers and are asynchronous on the context's stream.
+ *   - Weights are uploaded from borrowed host arrays in kvad's own layout
+ *     (quant.rs:121-127, qcache.rs:30-40): the handle owns the device copy.
+ *   - Calls on one context are serialised by an internal mutex; separate
+ *     contexts may be used from separate threads.
+ */
+#ifndef KVAD_HIP_H
+#define KVAD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KH_OK 0
+#define KH_DECLINED 1
+#define KH_EINVAL (-1)
+#define KH_EHIP (-2)
+#define KH_ENOMEM (-3)
+
+/* Precision of a weight: quant.rs:59-64 (F32, Q8, Q4) plus GGML's Q4_K,
+ * whose block layout is gpu/src/mpp.rs:241-251. */
+#define KH_F32 0
+#define KH_Q8 1
+#define KH_Q4 2
+#define KH_Q4K 3
+
+typedef struct kh_ctx kh_ctx;
+typedef struct kh_weight kh_weight;
+typedef struct kh_kv kh_kv;
+
+/* The calling thread's last error message; library-owned, valid until the
+ * thread's next call.  House style of apps/phone/core/kvad_core.h:27. */
+const char *kh_last_error(void);
+
+/* Library version string.  Static; never freed (kvad_core.h:26-27). */
+const char *kh_version(void);
+
+/* ---- context ---------------------------------------------------------- */
+
+/* A device and a stream: the per-session state CpuSession keeps as its rayon
+ * pool (model/mod.rs:979-1072). */
+int kh_init(int device, kh_ctx **out);
+int kh_free(kh_ctx *ctx);
+/* Launch on `hip_stream` (a hipStream_t) instead of the context's own; NULL
+ * restores the own stream.  The caller keeps ownership of the stream. */
+int kh_set_stream(kh_ctx *ctx, void *hip_stream);
+int kh_synchronize(kh_ctx *ctx);
+/* Grow the context's device scratch to `bytes` up front, so that later calls
+ * do not allocate. */
+int kh_reserve(kh_ctx *ctx, size_t bytes);
+
+/* ---- weights ---------------------------------------------------------- */
+
+/* Weight::from_q8 (quant.rs:287-290): scales f32[rows*cols/32], qs
+ * i8[rows*cols], row-major; cols % 32 == 0 (quant.rs:131-142). */
+int kh_weight_q8(kh_ctx *ctx, size_t rows, size_t cols, const float *scales, const int8_t *qs,
+                 kh_weight **out);
+/* Weight::from_q4 (quant.rs:292-295): scales f32[rows*cols/32], qs
+ * u8[rows*cols/2]; byte k of a block holds weight k (low nibble) and k+16
+ * (high nibble), bias 8 (quant.rs:258-274). */
+int kh_weight_q4(kh_ctx *ctx, size_t rows, size_t cols, const float *scales, const uint8_t *qs,
+                 kh_weight **out);
+/* GGML Q4_K blocks, 144 bytes per 256 weights, rows of cols/256 blocks
+ * (gpu/src/mpp.rs:241-251); cols % 256 == 0. */
+int kh_weight_q4k(kh_ctx *ctx, size_t rows, size_t cols, const uint8_t *blocks, kh_weight **out);
+/* Weight::from_f32 (quant.rs:331-333): data f32[rows*cols]. */
+int kh_weight_f32(kh_ctx *ctx, size_t rows, size_t cols, const float *data, kh_weight **out);
+/* Weight::quantize (quant.rs:209-281) on the device, from f32 data
+ * [rows, cols]: precision KH_Q8 or KH_Q4 as the reference quantises, KH_Q4K
+ * with this library's packing of GGML's block (any valid packing; the GEMV
+ * reads whatever bytes it is given).  Bit-identical to the CPU quantiser.
+ * `data` is a host pointer; the _dev form takes a device pointer. */
+int kh_weight_quantize(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision, kh_weight **out);
+int kh_weight_quantize_dev(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision,
+                           kh_weight **out);
+/* Weight::parts (quant.rs:336-342): copy the stored arrays back to the host.
+ * qs receives rows*cols (q8), rows*cols/2 (q4), rows*cols/256*144 (Q4_K) or
+ * 4*rows*cols (f32) bytes; scales rows*cols/32 floats (q8/q4; else unused). */
+int kh_weight_parts(const kh_weight *w, void *qs, float *scales);
+int kh_weight_free(kh_weight *w);
+/* rows, cols, precision and device bytes (Weight::bytes, quant.rs:365-371). */
+int kh_weight_info(const kh_weight *w, size_t *rows, size_t *cols, int *precision, size_t *bytes);
+/* Weight::row (quant.rs:374-402): row r dequantised to f32 (the embedding
+ * lookup).  Q4_K rows decode as mpp.rs:304-315. */
+int kh_weight_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out);
+
+/* ---- GEMV / GEMM ------------------------------------------------------ */
+
+/* Weight::matvec_bt (quant.rs:481-512): y[rows] = x[cols] W^T (+ bias).
+ * Quantised weights quantise x per 32-block first (QActivation::new,
+ * quant.rs:1044-1066).  bias may be NULL. */
+int kh_matvec(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y);
+int kh_matvec_dev(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y);
+
+/* quant::matvec_many (quant.rs:628-671): n GEMVs in one launch, each result
+ * bit-identical to kh_matvec on the same job.  Returns KH_DECLINED when a
+ * weight is f32 or x's length does not match, as the reference returns None. */
+int kh_matvec_many(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x,
+                   float *const *y);
+int kh_matvec_many_dev(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x,
+                       float *const *y);
+
+/* Weight::matmul_bt (quant.rs:751-858): y[m, rows] = xs[m, cols] W^T (+ bias);
+ * m == 1 is kh_matvec. */
+int kh_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
+int kh_matmul_dev(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
+
+/* QActBatch::new (quant.rs:693-714) on the device: m rows of n floats (n %
+ * 32 == 0) -> qs i8[m*n], scales f32[m*n/32], sums i32[m*n/32].  The
+ * activation form the GEMV and GEMM kernels read; a producer kernel that
+ * already holds it can skip kh_matvec's own quantisation step. */
+int kh_qact_dev(kh_ctx *ctx, const float *x, size_t m, size_t n, int8_t *qs, float *scales, int32_t *sums);
+/* Weight::qrow over every row (quant.rs:410-452) for an activation already
+ * quantised by kh_qact_dev: the GEMV kernel alone.  Not for f32 weights. */
+int kh_matvec_q_dev(kh_ctx *ctx, const kh_weight *w, const int8_t *qs, const float *scales, const int32_t *sums,
+                    const float *bias, float *y);
+
+/* Parity hooks.  Pass-1 integers of the GEMV kernel that kh_matvec runs
+ * (quant.rs:426-440): dots[rows * cols/32].  For Q4_K, dots are
+ * sum(q * xq) over each 32-wide sub-block with q the unsigned 4-bit code. */
+int kh_debug_block_dots(kh_ctx *ctx, const kh_weight *w, const float *x, int32_t *dots);
+/* QActivation::new on the device: qs[n], scales[n/32], sums[n/32]. */
+int kh_debug_qact(kh_ctx *ctx, const float *x, size_t n, int8_t *qs, float *scales, int32_t *sums);
+
+/* ---- KV cache and attention ------------------------------------------- */
+
+/* KvCache (model/mod.rs:612-749), device-resident: per layer an append-only
+ * [capacity, k_dim] key and [capacity, v_dim] value array; grows by doubling
+ * (the design of gpu/src/common.rs:547-700). */
+int kh_kv_new(kh_ctx *ctx, size_t n_layer, size_t k_dim, size_t v_dim, size_t capacity, kh_kv **out);
+int kh_kv_free(kh_kv *kv);
+/* KvCache::push (mod.rs:666-669): m rows appended to `layer`. */
+int kh_kv_push(kh_kv *kv, size_t layer, const float *k, const float *v, size_t m);
+int kh_kv_push_dev(kh_kv *kv, size_t layer, const float *k, const float *v, size_t m);
+/* KvCache::len (mod.rs:623), read and set as the model advances it. */
+int kh_kv_len(const kh_kv *kv, size_t *len);
+int kh_kv_set_len(kh_kv *kv, size_t len);
+/* KvCache::truncate (mod.rs:709-725): keep the first `len` positions of
+ * every layer; *kept receives the length actually kept. */
+int kh_kv_truncate(kh_kv *kv, size_t len, size_t *kept);
+/* KvCache::clear (mod.rs:727-738). */
+int kh_kv_clear(kh_kv *kv);
+/* KvCache::keys / values (mod.rs:671-677): copy the pushed rows of a layer
+ * to the host (rows * dim floats); *rows receives the row count. */
+int kh_kv_keys(const kh_kv *kv, size_t layer, float *out, size_t *rows);
+int kh_kv_values(const kh_kv *kv, size_t layer, float *out, size_t *rows);
+/* Device pointers of a layer's arrays (valid until the next push that grows). */
+int kh_kv_layer_ptrs(const kh_kv *kv, size_t layer, float **k, float **v);
+
+/* model::attend (model/mod.rs:769-819): GQA decode attention of one query
+ * (n_head * head_dim floats) over the first n_positions rows of `layer`;
+ * out is n_head * head_dim floats.  Same weights as the reference,
+ * including its skip of weights below 1e-8 (mod.rs:807). */
+int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t n_kv_head,
+              size_t head_dim, const float *q, size_t n_positions, float *out);
+/* The same over raw device arrays: k and v rows are n_kv_head*head_dim wide. */
+int kh_attend_dev(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
+                  const float *k, const float *v, size_t n_positions, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,409 @@
+"""kvad_amd -- MI355X (gfx950) implementation of kvad's quantised matmul and
+decode attention, behind the C ABI in include/kvad_hip.h.
+
+This module is a thin ctypes mirror of that ABI, shaped like the reference's
+Rust operator API so that tests and benchmarks read like the reference's own:
+
+    Weight.matvec_bt(x, bias)        quant.rs:481    Weight::matvec_bt
+    Weight.matmul_bt(xs, m, bias)    quant.rs:751    Weight::matmul_bt
+    Weight.row(r)                    quant.rs:374    Weight::row
+    matvec_many(ctx, jobs)           quant.rs:628    quant::matvec_many
+    KvCache.push/keys/truncate/...   model/mod.rs:612-749
+    attend(ctx, spec, q, cache, layer, n)   model/mod.rs:769
+
+There is no CPU fallback: if libkvad_hip.so is missing this import fails.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+__all__ = [
+    "F32", "Q8", "Q4", "Q4K", "KvadError", "Declined", "lib", "Context", "Weight", "matvec_many",
+    "KvCache", "Spec", "attend", "LIB_PATH",
+]
+
+F32, Q8, Q4, Q4K = 0, 1, 2, 3
+OK, DECLINED = 0, 1
+
+LIB_PATH = Path(os.environ.get("KVAD_HIP_LIB", Path(__file__).resolve().parent / "libkvad_hip.so"))
+
+
+class KvadError(RuntimeError):
+    """A negative status from the library, with kh_last_error()'s message."""
+
+
+class Declined(KvadError):
+    """Status 1: the library declines; the reference would run its CPU kernel."""
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python kvad_amd/build.py` "
+            "(there is no CPU fallback for this path)")
+    return C.CDLL(str(LIB_PATH))
+
+
+lib = _load()
+
+_p = C.c_void_p
+_sz = C.c_size_t
+_fp = C.POINTER(C.c_float)
+_SIGS = {
+    "kh_last_error": (C.c_char_p, []),
+    "kh_version": (C.c_char_p, []),
+    "kh_init": (C.c_int, [C.c_int, C.POINTER(_p)]),
+    "kh_free": (C.c_int, [_p]),
+    "kh_set_stream": (C.c_int, [_p, _p]),
+    "kh_synchronize": (C.c_int, [_p]),
+    "kh_reserve": (C.c_int, [_p, _sz]),
+    "kh_weight_q8": (C.c_int, [_p, _sz, _sz, _p, _p, C.POINTER(_p)]),
+    "kh_weight_q4": (C.c_int, [_p, _sz, _sz, _p, _p, C.POINTER(_p)]),
+    "kh_weight_q4k": (C.c_int, [_p, _sz, _sz, _p, C.POINTER(_p)]),
+    "kh_weight_f32": (C.c_int, [_p, _sz, _sz, _p, C.POINTER(_p)]),
+    "kh_weight_quantize": (C.c_int, [_p, _sz, _sz, _p, C.c_int, C.POINTER(_p)]),
+    "kh_weight_quantize_dev": (C.c_int, [_p, _sz, _sz, _p, C.c_int, C.POINTER(_p)]),
+    "kh_weight_parts": (C.c_int, [_p, _p, _p]),
+    "kh_weight_free": (C.c_int, [_p]),
+    "kh_weight_info": (C.c_int, [_p, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(C.c_int), C.POINTER(_sz)]),
+    "kh_weight_row": (C.c_int, [_p, _p, _sz, _p]),
+    "kh_matvec": (C.c_int, [_p, _p, _p, _p, _p]),
+    "kh_matvec_dev": (C.c_int, [_p, _p, _p, _p, _p]),
+    "kh_matvec_many": (C.c_int, [_p, _sz, _p, _p, _p]),
+    "kh_matvec_many_dev": (C.c_int, [_p, _sz, _p, _p, _p]),
+    "kh_matmul": (C.c_int, [_p, _p, _p, _sz, _p, _p]),
+    "kh_matmul_dev": (C.c_int, [_p, _p, _p, _sz, _p, _p]),
+    "kh_qact_dev": (C.c_int, [_p, _p, _sz, _sz, _p, _p, _p]),
+    "kh_matvec_q_dev": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
+    "kh_debug_block_dots": (C.c_int, [_p, _p, _p, _p]),
+    "kh_debug_qact": (C.c_int, [_p, _p, _sz, _p, _p, _p]),
+    "kh_kv_new": (C.c_int, [_p, _sz, _sz, _sz, _sz, C.POINTER(_p)]),
+    "kh_kv_free": (C.c_int, [_p]),
+    "kh_kv_push": (C.c_int, [_p, _sz, _p, _p, _sz]),
+    "kh_kv_push_dev": (C.c_int, [_p, _sz, _p, _p, _sz]),
+    "kh_kv_len": (C.c_int, [_p, C.POINTER(_sz)]),
+    "kh_kv_set_len": (C.c_int, [_p, _sz]),
+    "kh_kv_truncate": (C.c_int, [_p, _sz, C.POINTER(_sz)]),
+    "kh_kv_clear": (C.c_int, [_p]),
+    "kh_kv_keys": (C.c_int, [_p, _sz, _p, C.POINTER(_sz)]),
+    "kh_kv_values": (C.c_int, [_p, _sz, _p, C.POINTER(_sz)]),
+    "kh_kv_layer_ptrs": (C.c_int, [_p, _sz, C.POINTER(_p), C.POINTER(_p)]),
+    "kh_attend": (C.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
+    "kh_attend_dev": (C.c_int, [_p, _sz, _sz, _sz, _p, _p, _p, _sz, _p]),
+}
+
+
+def declared_symbols() -> list[str]:
+    return list(_SIGS)
+
+
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+def _check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = (lib.kh_last_error() or b"").decode(errors="replace")
+    if rc == DECLINED:
+        raise Declined(msg)
+    raise KvadError(f"status {rc}: {msg}")
+
+
+def _ptr(a) -> int | None:
+    """Host pointer of a contiguous numpy array (None passes NULL)."""
+    if a is None:
+        return None
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("arrays crossing the ABI must be C-contiguous")
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Context:
+    """kh_ctx: one device, one stream."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        _check(lib.kh_init(device, C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            lib.kh_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream: int | None) -> None:
+        _check(lib.kh_set_stream(self.h, stream))
+
+    def synchronize(self) -> None:
+        _check(lib.kh_synchronize(self.h))
+
+    def reserve(self, nbytes: int) -> None:
+        _check(lib.kh_reserve(self.h, nbytes))
+
+
+class Weight:
+    """kvad's Weight (quant.rs:195-199), held on the device."""
+
+    def __init__(self, ctx: Context, handle: C.c_void_p, keep=None):
+        self.ctx = ctx
+        self.h = handle
+        rows, cols, prec, nbytes = _sz(), _sz(), C.c_int(), _sz()
+        _check(lib.kh_weight_info(handle, C.byref(rows), C.byref(cols), C.byref(prec), C.byref(nbytes)))
+        self.rows, self.cols, self.precision, self.bytes = rows.value, cols.value, prec.value, nbytes.value
+
+    @classmethod
+    def from_q8(cls, ctx: Context, rows: int, cols: int, scales, qs) -> "Weight":
+        scales = _f32(scales)
+        qs = np.ascontiguousarray(qs, dtype=np.int8)
+        h = C.c_void_p()
+        _check(lib.kh_weight_q8(ctx.h, rows, cols, _ptr(scales), _ptr(qs), C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def from_q4(cls, ctx: Context, rows: int, cols: int, scales, qs) -> "Weight":
+        scales = _f32(scales)
+        qs = np.ascontiguousarray(qs, dtype=np.uint8)
+        h = C.c_void_p()
+        _check(lib.kh_weight_q4(ctx.h, rows, cols, _ptr(scales), _ptr(qs), C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def from_q4k(cls, ctx: Context, rows: int, cols: int, blocks) -> "Weight":
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        h = C.c_void_p()
+        _check(lib.kh_weight_q4k(ctx.h, rows, cols, _ptr(blocks), C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def from_f32(cls, ctx: Context, w) -> "Weight":
+        w = _f32(w)
+        h = C.c_void_p()
+        _check(lib.kh_weight_f32(ctx.h, w.shape[0], w.shape[1], _ptr(w), C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def quantize(cls, ctx: Context, w, precision: int) -> "Weight":
+        """Weight::quantize on the device from host f32 [rows, cols]."""
+        w = _f32(w)
+        h = C.c_void_p()
+        _check(lib.kh_weight_quantize(ctx.h, w.shape[0], w.shape[1], _ptr(w), precision, C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def quantize_dev(cls, ctx: Context, rows: int, cols: int, data_ptr: int, precision: int) -> "Weight":
+        h = C.c_void_p()
+        _check(lib.kh_weight_quantize_dev(ctx.h, rows, cols, data_ptr, precision, C.byref(h)))
+        return cls(ctx, h)
+
+    def parts(self):
+        """Weight::parts: (scales or None, qs bytes) copied to the host."""
+        n = self.rows * self.cols
+        if self.precision == Q8:
+            qs, sc = np.empty(n, np.int8), np.empty(n // 32, np.float32)
+        elif self.precision == Q4:
+            qs, sc = np.empty(n // 2, np.uint8), np.empty(n // 32, np.float32)
+        elif self.precision == Q4K:
+            qs, sc = np.empty(n // 256 * 144, np.uint8), None
+        else:
+            qs, sc = np.empty(n, np.float32), None
+        _check(lib.kh_weight_parts(self.h, _ptr(qs), _ptr(sc)))
+        return sc, qs
+
+    def free(self) -> None:
+        if self.h:
+            lib.kh_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def matvec_bt(self, x, bias=None) -> np.ndarray:
+        x = _f32(x)
+        assert x.size == self.cols, "matvec_bt shape mismatch"
+        b = None if bias is None else _f32(bias)
+        y = np.empty(self.rows, np.float32)
+        _check(lib.kh_matvec(self.ctx.h, self.h, _ptr(x), _ptr(b), _ptr(y)))
+        return y
+
+    def matvec_bt_dev(self, x_ptr: int, y_ptr: int, bias_ptr: int | None = None) -> None:
+        _check(lib.kh_matvec_dev(self.ctx.h, self.h, x_ptr, bias_ptr, y_ptr))
+
+    def matvec_q_dev(self, qs_ptr: int, scales_ptr: int, sums_ptr: int, y_ptr: int,
+                     bias_ptr: int | None = None) -> None:
+        _check(lib.kh_matvec_q_dev(self.ctx.h, self.h, qs_ptr, scales_ptr, sums_ptr, bias_ptr, y_ptr))
+
+    def matmul_bt(self, xs, m: int, bias=None) -> np.ndarray:
+        xs = _f32(xs)
+        assert xs.size == m * self.cols, "matmul_bt shape mismatch"
+        b = None if bias is None else _f32(bias)
+        y = np.empty(m * self.rows, np.float32)
+        _check(lib.kh_matmul(self.ctx.h, self.h, _ptr(xs), m, _ptr(b), _ptr(y)))
+        return y
+
+    def matmul_bt_dev(self, xs_ptr: int, m: int, y_ptr: int, bias_ptr: int | None = None) -> None:
+        _check(lib.kh_matmul_dev(self.ctx.h, self.h, xs_ptr, m, bias_ptr, y_ptr))
+
+    def row(self, r: int) -> np.ndarray:
+        out = np.empty(self.cols, np.float32)
+        _check(lib.kh_weight_row(self.ctx.h, self.h, r, _ptr(out)))
+        return out
+
+    def block_dots(self, x) -> np.ndarray:
+        x = _f32(x)
+        d = np.empty(self.rows * (self.cols // 32), np.int32)
+        _check(lib.kh_debug_block_dots(self.ctx.h, self.h, _ptr(x), _ptr(d)))
+        return d.reshape(self.rows, self.cols // 32)
+
+
+def matvec_many(ctx: Context, jobs) -> list[np.ndarray] | None:
+    """quant::matvec_many: None when a weight is f32, as the reference does."""
+    n = len(jobs)
+    xs = [_f32(x) for _, x in jobs]
+    # the same array object twice in a row is the same input, as in Rust
+    for i in range(1, n):
+        if jobs[i][1] is jobs[i - 1][1]:
+            xs[i] = xs[i - 1]
+    ys = [np.empty(w.rows, np.float32) for w, _ in jobs]
+    W = (C.c_void_p * n)(*[w.h.value for w, _ in jobs])
+    X = (C.c_void_p * n)(*[_ptr(x) for x in xs])
+    Y = (C.c_void_p * n)(*[_ptr(y) for y in ys])
+    rc = lib.kh_matvec_many(ctx.h, n, W, X, Y)
+    if rc == DECLINED:
+        return None
+    _check(rc)
+    return ys
+
+
+def qact_dev(ctx: Context, x_ptr: int, m: int, n: int, qs_ptr: int, scales_ptr: int, sums_ptr: int) -> None:
+    """QActBatch::new on device pointers."""
+    _check(lib.kh_qact_dev(ctx.h, x_ptr, m, n, qs_ptr, scales_ptr, sums_ptr))
+
+
+def qact(ctx: Context, x):
+    """QActivation::new on the device: (qs, scales, sums)."""
+    x = _f32(x)
+    n = x.size
+    qs = np.empty(n, np.int8)
+    sc = np.empty(n // 32, np.float32)
+    su = np.empty(n // 32, np.int32)
+    _check(lib.kh_debug_qact(ctx.h, _ptr(x), n, _ptr(qs), _ptr(sc), _ptr(su)))
+    return qs, sc, su
+
+
+@dataclass(frozen=True)
+class Spec:
+    """The attention geometry of model::Spec (model/mod.rs:298-312)."""
+
+    n_head: int
+    n_kv_head: int
+    head_dim: int
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_kv_head * self.head_dim
+
+    @property
+    def group_size(self) -> int:
+        return self.n_head // self.n_kv_head
+
+
+class KvCache:
+    """KvCache (model/mod.rs:612-749) with device-resident layers."""
+
+    def __init__(self, ctx: Context, n_layer: int, k_dim: int, v_dim: int, capacity: int = 0):
+        h = C.c_void_p()
+        _check(lib.kh_kv_new(ctx.h, n_layer, k_dim, v_dim, capacity, C.byref(h)))
+        self.ctx, self.h = ctx, h
+        self.n_layer, self.k_dim, self.v_dim = n_layer, k_dim, v_dim
+
+    def free(self) -> None:
+        if self.h:
+            lib.kh_kv_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def push(self, layer: int, k, v) -> None:
+        k, v = _f32(k), _f32(v)
+        m = k.size // self.k_dim
+        assert k.size == m * self.k_dim and v.size == m * self.v_dim
+        _check(lib.kh_kv_push(self.h, layer, _ptr(k), _ptr(v), m))
+
+    def push_dev(self, layer: int, k_ptr: int, v_ptr: int, m: int) -> None:
+        _check(lib.kh_kv_push_dev(self.h, layer, k_ptr, v_ptr, m))
+
+    @property
+    def len(self) -> int:
+        n = _sz()
+        _check(lib.kh_kv_len(self.h, C.byref(n)))
+        return n.value
+
+    @len.setter
+    def len(self, value: int) -> None:
+        _check(lib.kh_kv_set_len(self.h, value))
+
+    def truncate(self, n: int) -> int:
+        kept = _sz()
+        _check(lib.kh_kv_truncate(self.h, n, C.byref(kept)))
+        return kept.value
+
+    def clear(self) -> None:
+        _check(lib.kh_kv_clear(self.h))
+
+    def _read(self, fn, layer: int, dim: int) -> np.ndarray:
+        rows = _sz()
+        _check(fn(self.h, layer, None, C.byref(rows)))
+        out = np.empty(rows.value * dim, np.float32)
+        _check(fn(self.h, layer, _ptr(out) if out.size else None, C.byref(rows)))
+        return out
+
+    def keys(self, layer: int) -> np.ndarray:
+        return self._read(lib.kh_kv_keys, layer, self.k_dim)
+
+    def values(self, layer: int) -> np.ndarray:
+        return self._read(lib.kh_kv_values, layer, self.v_dim)
+
+    def layer_ptrs(self, layer: int) -> tuple[int, int]:
+        k, v = C.c_void_p(), C.c_void_p()
+        _check(lib.kh_kv_layer_ptrs(self.h, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+
+def attend(ctx: Context, spec: Spec, q, cache: KvCache, layer: int, n_positions: int) -> np.ndarray:
+    """model::attend over a device cache layer."""
+    q = _f32(q)
+    out = np.empty(spec.n_head * spec.head_dim, np.float32)
+    _check(lib.kh_attend(ctx.h, cache.h, layer, spec.n_head, spec.n_kv_head, spec.head_dim, _ptr(q),
+                         n_positions, _ptr(out)))
+    return out
+
+
+def attend_dev(ctx: Context, spec: Spec, q_ptr: int, k_ptr: int, v_ptr: int, n_positions: int,
+               out_ptr: int) -> None:
+    _check(lib.kh_attend_dev(ctx.h, spec.n_head, spec.n_kv_head, spec.head_dim, q_ptr, k_ptr, v_ptr,
+                             n_positions, out_ptr))

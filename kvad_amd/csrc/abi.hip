@@ -1,0 +1,691 @@
+// The C ABI of libkvad_hip (include/kvad_hip.h): contexts, weight upload,
+// the KV cache, and the entry points that stage host buffers around the
+// kernel launchers.
+#include <cstring>
+#include <memory>
+
+#include "common.hpp"
+
+namespace kh {
+
+static thread_local std::string g_error;
+
+void set_error(const std::string &msg) { g_error = msg; }
+
+int fail(int code, const std::string &msg) {
+    set_error(msg);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    set_error(std::string(what) + ": " + hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? KH_ENOMEM : KH_EHIP;
+}
+
+int ensure(kh_ctx *ctx, Workspace &w, size_t bytes) {
+    if (bytes <= w.bytes) return KH_OK;
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    want = (want + 4095) / 4096 * 4096;
+    if (w.ptr) {
+        KH_HIP(hipStreamSynchronize(ctx->stream));
+        KH_HIP(hipFree(w.ptr));
+        w.ptr = nullptr;
+        w.bytes = 0;
+    }
+    KH_HIP(hipMalloc(&w.ptr, want));
+    w.bytes = want;
+    return KH_OK;
+}
+
+namespace {
+
+constexpr size_t ALIGN = 256;
+inline size_t up(size_t n) { return (n + ALIGN - 1) / ALIGN * ALIGN; }
+
+struct Guard {
+    std::lock_guard<std::recursive_mutex> lock;
+    explicit Guard(kh_ctx *c) : lock(c->mu) { (void)hipSetDevice(c->device); }
+};
+
+int check_weight(const kh_weight *w) {
+    if (!w || !w->ctx) return fail(KH_EINVAL, "null weight");
+    return KH_OK;
+}
+
+// Carves the quantised activation for m rows of k values out of `base`.
+QAct carve_qact(char *base, size_t m, size_t k, size_t *used) {
+    QAct a;
+    size_t off = 0;
+    a.qs = reinterpret_cast<int8_t *>(base + off);
+    off += up(m * k);
+    a.scales = reinterpret_cast<float *>(base + off);
+    off += up(4 * m * k / BLOCK);
+    a.sums = reinterpret_cast<int32_t *>(base + off);
+    off += up(4 * m * k / BLOCK);
+    *used = off;
+    return a;
+}
+
+size_t qact_bytes(size_t m, size_t k) { return up(m * k) + 2 * up(4 * m * k / BLOCK); }
+
+GemvJob job_for(const kh_weight *w, const QAct *a, const float *xf, const float *bias, float *y, int32_t *dots) {
+    GemvJob j{};
+    j.w = w->qs;
+    j.ws = w->scales;
+    if (a) {
+        j.xq = a->qs;
+        j.xs = a->scales;
+        j.xsum = a->sums;
+    }
+    j.xf = xf;
+    j.bias = bias;
+    j.y = y;
+    j.dots = dots;
+    j.rows = (int)w->rows;
+    j.cols = (int)w->cols;
+    return j;
+}
+
+// matvec on device pointers: quantise x (unless f32), then one GEMV launch.
+int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots) {
+    if (w->precision == KH_F32) {
+        GemvJob j = job_for(w, nullptr, x, bias, y, nullptr);
+        return launch_gemv(ctx, KH_F32, &j, 1);
+    }
+    int rc = ensure(ctx, ctx->ws, qact_bytes(1, w->cols));
+    if (rc) return rc;
+    size_t used;
+    QAct a = carve_qact(static_cast<char *>(ctx->ws.ptr), 1, w->cols, &used);
+    if ((rc = launch_qact(ctx, x, 1, w->cols, a))) return rc;
+    GemvJob j = job_for(w, &a, nullptr, bias, y, dots);
+    return launch_gemv(ctx, w->precision, &j, 1);
+}
+
+int matvec_many_device(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x,
+                       float *const *y) {
+    if (n == 0) return KH_OK;
+    for (size_t i = 0; i < n; i++) {
+        if (check_weight(w[i])) return KH_EINVAL;
+        if (w[i]->precision == KH_F32) return fail(KH_DECLINED, "matvec_many: an f32 weight is not this call's to run");
+    }
+    // Adjacent jobs on the same input quantise it once (quant.rs:634-644).
+    std::vector<size_t> which(n);
+    std::vector<size_t> first;  // job index owning each distinct activation
+    size_t total = 0;
+    for (size_t i = 0; i < n; i++) {
+        if (i == 0 || x[i] != x[i - 1] || w[i]->cols != w[i - 1]->cols) {
+            first.push_back(i);
+            total += qact_bytes(1, w[i]->cols);
+        }
+        which[i] = first.size() - 1;
+    }
+    int rc = ensure(ctx, ctx->ws, total);
+    if (rc) return rc;
+    std::vector<QAct> acts(first.size());
+    char *p = static_cast<char *>(ctx->ws.ptr);
+    for (size_t a = 0; a < first.size(); a++) {
+        size_t used;
+        acts[a] = carve_qact(p, 1, w[first[a]]->cols, &used);
+        p += used;
+        if ((rc = launch_qact(ctx, x[first[a]], 1, w[first[a]]->cols, acts[a]))) return rc;
+    }
+    // One launch per precision present; a single precision is one launch.
+    for (int prec : {KH_Q8, KH_Q4, KH_Q4K}) {
+        std::vector<GemvJob> jobs;
+        for (size_t i = 0; i < n; i++)
+            if (w[i]->precision == prec) jobs.push_back(job_for(w[i], &acts[which[i]], nullptr, nullptr, y[i], nullptr));
+        if (!jobs.empty() && (rc = launch_gemv(ctx, prec, jobs.data(), (int)jobs.size()))) return rc;
+    }
+    return KH_OK;
+}
+
+int matmul_device(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
+    if (m == 1) return matvec_device(ctx, w, xs, bias, y, nullptr);
+    return launch_matmul(ctx, w, xs, m, bias, y);
+}
+
+}  // namespace
+}  // namespace kh
+
+using namespace kh;
+
+extern "C" {
+
+const char *kh_last_error(void) { return g_error.c_str(); }
+
+const char *kh_version(void) { return "kvad_hip 0.1.0 (gfx950)"; }
+
+int kh_init(int device, kh_ctx **out) {
+    if (!out) return fail(KH_EINVAL, "kh_init: out is null");
+    *out = nullptr;
+    int n = 0;
+    KH_HIP(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(KH_EINVAL, "kh_init: no such device");
+    KH_HIP(hipSetDevice(device));
+    std::unique_ptr<kh_ctx> ctx(new kh_ctx());
+    ctx->device = device;
+    KH_HIP(hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device));
+    KH_HIP(hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking));
+    ctx->stream = ctx->own;
+    KH_HIP(hipMalloc(&ctx->counters.ptr, 4096));
+    ctx->counters.bytes = 4096;
+    KH_HIP(hipMemset(ctx->counters.ptr, 0, 4096));
+    KH_HIP(hipDeviceSynchronize());
+    *out = ctx.release();
+    return KH_OK;
+}
+
+int kh_free(kh_ctx *ctx) {
+    if (!ctx) return KH_OK;
+    {
+        Guard g(ctx);
+        (void)hipStreamSynchronize(ctx->stream);
+        if (ctx->ws.ptr) (void)hipFree(ctx->ws.ptr);
+        if (ctx->io.ptr) (void)hipFree(ctx->io.ptr);
+        if (ctx->counters.ptr) (void)hipFree(ctx->counters.ptr);
+        if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    }
+    delete ctx;
+    return KH_OK;
+}
+
+int kh_set_stream(kh_ctx *ctx, void *stream) {
+    if (!ctx) return fail(KH_EINVAL, "null context");
+    Guard g(ctx);
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own;
+    return KH_OK;
+}
+
+int kh_synchronize(kh_ctx *ctx) {
+    if (!ctx) return fail(KH_EINVAL, "null context");
+    Guard g(ctx);
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+int kh_reserve(kh_ctx *ctx, size_t bytes) {
+    if (!ctx) return fail(KH_EINVAL, "null context");
+    Guard g(ctx);
+    return ensure(ctx, ctx->ws, bytes);
+}
+
+// ---- weights -------------------------------------------------------------
+
+static int upload(kh_ctx *ctx, int precision, size_t rows, size_t cols, const void *qs, size_t qs_bytes,
+                  const float *scales, size_t n_scales, kh_weight **out) {
+    std::unique_ptr<kh_weight> w(new kh_weight());
+    w->ctx = ctx;
+    w->precision = precision;
+    w->rows = rows;
+    w->cols = cols;
+    KH_HIP(hipMalloc(&w->qs, qs_bytes ? qs_bytes : 16));
+    KH_HIP(hipMemcpy(w->qs, qs, qs_bytes, hipMemcpyHostToDevice));
+    w->bytes = qs_bytes;
+    if (n_scales) {
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&w->scales), 4 * n_scales));
+        KH_HIP(hipMemcpy(w->scales, scales, 4 * n_scales, hipMemcpyHostToDevice));
+        w->bytes += 4 * n_scales;
+    }
+    *out = w.release();
+    return KH_OK;
+}
+
+static int shape_check(size_t rows, size_t cols, size_t multiple, const char *what) {
+    if (rows == 0 || cols == 0 || cols % multiple != 0 || rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX)
+        return fail(KH_EINVAL, std::string(what) + ": needs rows > 0 and cols a positive multiple of " +
+                                   std::to_string(multiple));
+    return KH_OK;
+}
+
+int kh_weight_q8(kh_ctx *ctx, size_t rows, size_t cols, const float *scales, const int8_t *qs, kh_weight **out) {
+    if (!ctx || !out || !scales || !qs) return fail(KH_EINVAL, "kh_weight_q8: null argument");
+    if (shape_check(rows, cols, BLOCK, "kh_weight_q8")) return KH_EINVAL;
+    Guard g(ctx);
+    return upload(ctx, KH_Q8, rows, cols, qs, rows * cols, scales, rows * cols / BLOCK, out);
+}
+
+int kh_weight_q4(kh_ctx *ctx, size_t rows, size_t cols, const float *scales, const uint8_t *qs, kh_weight **out) {
+    if (!ctx || !out || !scales || !qs) return fail(KH_EINVAL, "kh_weight_q4: null argument");
+    if (shape_check(rows, cols, BLOCK, "kh_weight_q4")) return KH_EINVAL;
+    Guard g(ctx);
+    return upload(ctx, KH_Q4, rows, cols, qs, rows * cols / 2, scales, rows * cols / BLOCK, out);
+}
+
+int kh_weight_q4k(kh_ctx *ctx, size_t rows, size_t cols, const uint8_t *blocks, kh_weight **out) {
+    if (!ctx || !out || !blocks) return fail(KH_EINVAL, "kh_weight_q4k: null argument");
+    if (shape_check(rows, cols, QK_K, "kh_weight_q4k")) return KH_EINVAL;
+    Guard g(ctx);
+    return upload(ctx, KH_Q4K, rows, cols, blocks, rows * (cols / QK_K) * Q4K_BYTES, nullptr, 0, out);
+}
+
+int kh_weight_f32(kh_ctx *ctx, size_t rows, size_t cols, const float *data, kh_weight **out) {
+    if (!ctx || !out || !data) return fail(KH_EINVAL, "kh_weight_f32: null argument");
+    if (shape_check(rows, cols, 1, "kh_weight_f32")) return KH_EINVAL;
+    Guard g(ctx);
+    return upload(ctx, KH_F32, rows, cols, data, 4 * rows * cols, nullptr, 0, out);
+}
+
+static size_t qs_bytes_of(int precision, size_t rows, size_t cols) {
+    switch (precision) {
+        case KH_Q8: return rows * cols;
+        case KH_Q4: return rows * cols / 2;
+        case KH_Q4K: return rows * (cols / QK_K) * Q4K_BYTES;
+        default: return 4 * rows * cols;
+    }
+}
+
+static int quantize(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision, bool host,
+                    kh_weight **out) {
+    if (!ctx || !out || !data) return fail(KH_EINVAL, "kh_weight_quantize: null argument");
+    if (precision != KH_Q8 && precision != KH_Q4 && precision != KH_Q4K)
+        return fail(KH_EINVAL, "kh_weight_quantize: precision must be KH_Q8, KH_Q4 or KH_Q4K");
+    if (shape_check(rows, cols, precision == KH_Q4K ? QK_K : BLOCK, "kh_weight_quantize")) return KH_EINVAL;
+    Guard g(ctx);
+    std::unique_ptr<kh_weight> w(new kh_weight());
+    w->ctx = ctx;
+    w->precision = precision;
+    w->rows = rows;
+    w->cols = cols;
+    size_t qb = qs_bytes_of(precision, rows, cols);
+    KH_HIP(hipMalloc(&w->qs, qb));
+    w->bytes = qb;
+    if (precision != KH_Q4K) {
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&w->scales), 4 * rows * cols / BLOCK));
+        w->bytes += 4 * rows * cols / BLOCK;
+    }
+    const float *src = data;
+    float *tmp = nullptr;
+    if (host) {
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&tmp), 4 * rows * cols));
+        KH_HIP(hipMemcpyAsync(tmp, data, 4 * rows * cols, hipMemcpyHostToDevice, ctx->stream));
+        src = tmp;
+    }
+    int rc = launch_quantize(ctx, src, rows, cols, precision, w->qs, w->scales);
+    if (host) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        (void)hipFree(tmp);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    }
+    if (rc) {
+        (void)hipFree(w->qs);
+        if (w->scales) (void)hipFree(w->scales);
+        return rc;
+    }
+    *out = w.release();
+    return KH_OK;
+}
+
+int kh_weight_quantize(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision, kh_weight **out) {
+    return quantize(ctx, rows, cols, data, precision, true, out);
+}
+
+int kh_weight_quantize_dev(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision,
+                           kh_weight **out) {
+    return quantize(ctx, rows, cols, data, precision, false, out);
+}
+
+int kh_weight_parts(const kh_weight *w, void *qs, float *scales) {
+    if (check_weight(w) || !qs) return fail(KH_EINVAL, "kh_weight_parts: null argument");
+    Guard g(w->ctx);
+    KH_HIP(hipMemcpyAsync(qs, w->qs, qs_bytes_of(w->precision, w->rows, w->cols), hipMemcpyDeviceToHost,
+                          w->ctx->stream));
+    if (w->scales && scales)
+        KH_HIP(hipMemcpyAsync(scales, w->scales, 4 * w->rows * w->cols / BLOCK, hipMemcpyDeviceToHost, w->ctx->stream));
+    KH_HIP(hipStreamSynchronize(w->ctx->stream));
+    return KH_OK;
+}
+
+int kh_weight_free(kh_weight *w) {
+    if (!w) return KH_OK;
+    if (w->ctx) {
+        Guard g(w->ctx);
+        (void)hipStreamSynchronize(w->ctx->stream);
+        if (w->qs) (void)hipFree(w->qs);
+        if (w->scales) (void)hipFree(w->scales);
+    }
+    delete w;
+    return KH_OK;
+}
+
+int kh_weight_info(const kh_weight *w, size_t *rows, size_t *cols, int *precision, size_t *bytes) {
+    if (check_weight(w)) return KH_EINVAL;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (precision) *precision = w->precision;
+    if (bytes) *bytes = w->bytes;
+    return KH_OK;
+}
+
+int kh_weight_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out) {
+    if (!ctx || check_weight(w) || !out) return fail(KH_EINVAL, "kh_weight_row: null argument");
+    if (r >= w->rows) return fail(KH_EINVAL, "kh_weight_row: row out of range");
+    Guard g(ctx);
+    int rc = ensure(ctx, ctx->io, 4 * w->cols);
+    if (rc) return rc;
+    float *d = static_cast<float *>(ctx->io.ptr);
+    if ((rc = launch_dequant_row(ctx, w, r, d))) return rc;
+    KH_HIP(hipMemcpyAsync(out, d, 4 * w->cols, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+// ---- GEMV / GEMM -----------------------------------------------------------
+
+int kh_matvec_dev(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y) {
+    if (!ctx || check_weight(w) || !x || !y) return fail(KH_EINVAL, "kh_matvec_dev: null argument");
+    Guard g(ctx);
+    return matvec_device(ctx, w, x, bias, y, nullptr);
+}
+
+static int matvec_host(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y,
+                       int32_t *dots) {
+    Guard g(ctx);
+    const size_t rows = w->rows, cols = w->cols, nb = cols / BLOCK;
+    size_t bytes = up(4 * cols) + 2 * up(4 * rows) + (dots ? up(4 * rows * nb) : 0);
+    int rc = ensure(ctx, ctx->io, bytes);
+    if (rc) return rc;
+    char *p = static_cast<char *>(ctx->io.ptr);
+    float *dx = reinterpret_cast<float *>(p);
+    float *dy = reinterpret_cast<float *>(p + up(4 * cols));
+    float *db = reinterpret_cast<float *>(p + up(4 * cols) + up(4 * rows));
+    int32_t *dd = dots ? reinterpret_cast<int32_t *>(p + up(4 * cols) + 2 * up(4 * rows)) : nullptr;
+    KH_HIP(hipMemcpyAsync(dx, x, 4 * cols, hipMemcpyHostToDevice, ctx->stream));
+    if (bias) KH_HIP(hipMemcpyAsync(db, bias, 4 * rows, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = matvec_device(ctx, w, dx, bias ? db : nullptr, dy, dd))) return rc;
+    KH_HIP(hipMemcpyAsync(y, dy, 4 * rows, hipMemcpyDeviceToHost, ctx->stream));
+    if (dots) KH_HIP(hipMemcpyAsync(dots, dd, 4 * rows * nb, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+int kh_matvec(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y) {
+    if (!ctx || check_weight(w) || !x || !y) return fail(KH_EINVAL, "kh_matvec: null argument");
+    return matvec_host(ctx, w, x, bias, y, nullptr);
+}
+
+int kh_debug_block_dots(kh_ctx *ctx, const kh_weight *w, const float *x, int32_t *dots) {
+    if (!ctx || check_weight(w) || !x || !dots) return fail(KH_EINVAL, "kh_debug_block_dots: null argument");
+    if (w->precision == KH_F32) return fail(KH_EINVAL, "kh_debug_block_dots: f32 weights have no block dots");
+    std::vector<float> y(w->rows);
+    return matvec_host(ctx, w, x, nullptr, y.data(), dots);
+}
+
+int kh_debug_qact(kh_ctx *ctx, const float *x, size_t n, int8_t *qs, float *scales, int32_t *sums) {
+    if (!ctx || !x || !qs || !scales || !sums) return fail(KH_EINVAL, "kh_debug_qact: null argument");
+    if (n % BLOCK) return fail(KH_EINVAL, "kh_debug_qact: n must be a multiple of 32");
+    Guard g(ctx);
+    int rc = ensure(ctx, ctx->io, up(4 * n) + qact_bytes(1, n));
+    if (rc) return rc;
+    char *p = static_cast<char *>(ctx->io.ptr);
+    float *dx = reinterpret_cast<float *>(p);
+    size_t used;
+    QAct a = carve_qact(p + up(4 * n), 1, n, &used);
+    KH_HIP(hipMemcpyAsync(dx, x, 4 * n, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = launch_qact(ctx, dx, 1, n, a))) return rc;
+    KH_HIP(hipMemcpyAsync(qs, a.qs, n, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipMemcpyAsync(scales, a.scales, 4 * (n / BLOCK), hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipMemcpyAsync(sums, a.sums, 4 * (n / BLOCK), hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+int kh_qact_dev(kh_ctx *ctx, const float *x, size_t m, size_t n, int8_t *qs, float *scales, int32_t *sums) {
+    if (!ctx || !x || !qs || !scales || !sums) return fail(KH_EINVAL, "kh_qact_dev: null argument");
+    if (n % BLOCK) return fail(KH_EINVAL, "kh_qact_dev: n must be a multiple of 32");
+    Guard g(ctx);
+    QAct a{qs, scales, sums};
+    return launch_qact(ctx, x, m, n, a);
+}
+
+int kh_matvec_q_dev(kh_ctx *ctx, const kh_weight *w, const int8_t *qs, const float *scales, const int32_t *sums,
+                    const float *bias, float *y) {
+    if (!ctx || check_weight(w) || !qs || !scales || !sums || !y) return fail(KH_EINVAL, "kh_matvec_q_dev: null argument");
+    if (w->precision == KH_F32) return fail(KH_EINVAL, "kh_matvec_q_dev: f32 weights take kh_matvec_dev");
+    Guard g(ctx);
+    QAct a{const_cast<int8_t *>(qs), const_cast<float *>(scales), const_cast<int32_t *>(sums)};
+    GemvJob j = job_for(w, &a, nullptr, bias, y, nullptr);
+    return launch_gemv(ctx, w->precision, &j, 1);
+}
+
+int kh_matvec_many_dev(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x, float *const *y) {
+    if (!ctx || (n && (!w || !x || !y))) return fail(KH_EINVAL, "kh_matvec_many_dev: null argument");
+    Guard g(ctx);
+    return matvec_many_device(ctx, n, w, x, y);
+}
+
+int kh_matvec_many(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x, float *const *y) {
+    if (!ctx || (n && (!w || !x || !y))) return fail(KH_EINVAL, "kh_matvec_many: null argument");
+    Guard g(ctx);
+    for (size_t i = 0; i < n; i++) {
+        if (check_weight(w[i])) return KH_EINVAL;
+        if (w[i]->precision == KH_F32) return fail(KH_DECLINED, "matvec_many: an f32 weight is not this call's to run");
+    }
+    size_t bytes = 0;
+    for (size_t i = 0; i < n; i++) bytes += up(4 * w[i]->cols) + up(4 * w[i]->rows);
+    int rc = ensure(ctx, ctx->io, bytes);
+    if (rc) return rc;
+    char *p = static_cast<char *>(ctx->io.ptr);
+    std::vector<const float *> dx(n);
+    std::vector<float *> dy(n);
+    for (size_t i = 0; i < n; i++) {
+        // the same host input twice in a row stays one device input, so that
+        // the adjacent-job dedupe sees it too
+        if (i > 0 && x[i] == x[i - 1] && w[i]->cols == w[i - 1]->cols) {
+            dx[i] = dx[i - 1];
+        } else {
+            float *d = reinterpret_cast<float *>(p);
+            p += up(4 * w[i]->cols);
+            KH_HIP(hipMemcpyAsync(d, x[i], 4 * w[i]->cols, hipMemcpyHostToDevice, ctx->stream));
+            dx[i] = d;
+        }
+        dy[i] = reinterpret_cast<float *>(p);
+        p += up(4 * w[i]->rows);
+    }
+    if ((rc = matvec_many_device(ctx, n, w, dx.data(), dy.data()))) return rc;
+    for (size_t i = 0; i < n; i++)
+        KH_HIP(hipMemcpyAsync(y[i], dy[i], 4 * w[i]->rows, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+int kh_matmul_dev(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
+    if (!ctx || check_weight(w) || !xs || !y) return fail(KH_EINVAL, "kh_matmul_dev: null argument");
+    if (m == 0) return KH_OK;
+    Guard g(ctx);
+    return matmul_device(ctx, w, xs, m, bias, y);
+}
+
+int kh_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
+    if (!ctx || check_weight(w) || !xs || !y) return fail(KH_EINVAL, "kh_matmul: null argument");
+    if (m == 0) return KH_OK;
+    Guard g(ctx);
+    const size_t rows = w->rows, cols = w->cols;
+    size_t bytes = up(4 * m * cols) + up(4 * m * rows) + up(4 * rows);
+    int rc = ensure(ctx, ctx->io, bytes);
+    if (rc) return rc;
+    char *p = static_cast<char *>(ctx->io.ptr);
+    float *dx = reinterpret_cast<float *>(p);
+    float *dy = reinterpret_cast<float *>(p + up(4 * m * cols));
+    float *db = reinterpret_cast<float *>(p + up(4 * m * cols) + up(4 * m * rows));
+    KH_HIP(hipMemcpyAsync(dx, xs, 4 * m * cols, hipMemcpyHostToDevice, ctx->stream));
+    if (bias) KH_HIP(hipMemcpyAsync(db, bias, 4 * rows, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = matmul_device(ctx, w, dx, m, bias ? db : nullptr, dy))) return rc;
+    KH_HIP(hipMemcpyAsync(y, dy, 4 * m * rows, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+// ---- KV cache --------------------------------------------------------------
+
+int kh_kv_new(kh_ctx *ctx, size_t n_layer, size_t k_dim, size_t v_dim, size_t capacity, kh_kv **out) {
+    if (!ctx || !out) return fail(KH_EINVAL, "kh_kv_new: null argument");
+    if (n_layer == 0 || k_dim == 0 || v_dim == 0 || k_dim % 4 || v_dim % 4)
+        return fail(KH_EINVAL, "kh_kv_new: needs layers and widths that are positive multiples of 4");
+    Guard g(ctx);
+    std::unique_ptr<kh_kv> kv(new kh_kv());
+    kv->ctx = ctx;
+    kv->n_layer = n_layer;
+    kv->k_dim = k_dim;
+    kv->v_dim = v_dim;
+    kv->capacity = capacity ? capacity : 256;  // FIRST, gpu/src/common.rs:547-700
+    kv->k.assign(n_layer, nullptr);
+    kv->v.assign(n_layer, nullptr);
+    kv->rows.assign(n_layer, 0);
+    for (size_t l = 0; l < n_layer; l++) {
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&kv->k[l]), 4 * kv->capacity * k_dim));
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&kv->v[l]), 4 * kv->capacity * v_dim));
+    }
+    *out = kv.release();
+    return KH_OK;
+}
+
+int kh_kv_free(kh_kv *kv) {
+    if (!kv) return KH_OK;
+    {
+        Guard g(kv->ctx);
+        (void)hipStreamSynchronize(kv->ctx->stream);
+        for (size_t l = 0; l < kv->n_layer; l++) {
+            if (kv->k[l]) (void)hipFree(kv->k[l]);
+            if (kv->v[l]) (void)hipFree(kv->v[l]);
+        }
+    }
+    delete kv;
+    return KH_OK;
+}
+
+// Doubles every layer's arrays until `need` positions fit.
+static int kv_grow(kh_kv *kv, size_t need) {
+    if (need <= kv->capacity) return KH_OK;
+    size_t cap = kv->capacity;
+    while (cap < need) cap *= 2;
+    kh_ctx *ctx = kv->ctx;
+    for (size_t l = 0; l < kv->n_layer; l++) {
+        float *nk = nullptr, *nv = nullptr;
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&nk), 4 * cap * kv->k_dim));
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&nv), 4 * cap * kv->v_dim));
+        KH_HIP(hipMemcpyAsync(nk, kv->k[l], 4 * kv->rows[l] * kv->k_dim, hipMemcpyDeviceToDevice, ctx->stream));
+        KH_HIP(hipMemcpyAsync(nv, kv->v[l], 4 * kv->rows[l] * kv->v_dim, hipMemcpyDeviceToDevice, ctx->stream));
+        KH_HIP(hipStreamSynchronize(ctx->stream));
+        KH_HIP(hipFree(kv->k[l]));
+        KH_HIP(hipFree(kv->v[l]));
+        kv->k[l] = nk;
+        kv->v[l] = nv;
+    }
+    kv->capacity = cap;
+    return KH_OK;
+}
+
+static int kv_push(kh_kv *kv, size_t layer, const float *k, const float *v, size_t m, hipMemcpyKind kind) {
+    if (!kv || !k || !v) return fail(KH_EINVAL, "kh_kv_push: null argument");
+    if (layer >= kv->n_layer) return fail(KH_EINVAL, "kh_kv_push: no such layer");
+    if (m == 0) return KH_OK;
+    Guard g(kv->ctx);
+    int rc = kv_grow(kv, kv->rows[layer] + m);
+    if (rc) return rc;
+    size_t r = kv->rows[layer];
+    KH_HIP(hipMemcpyAsync(kv->k[layer] + r * kv->k_dim, k, 4 * m * kv->k_dim, kind, kv->ctx->stream));
+    KH_HIP(hipMemcpyAsync(kv->v[layer] + r * kv->v_dim, v, 4 * m * kv->v_dim, kind, kv->ctx->stream));
+    if (kind == hipMemcpyHostToDevice) KH_HIP(hipStreamSynchronize(kv->ctx->stream));
+    kv->rows[layer] = r + m;
+    return KH_OK;
+}
+
+int kh_kv_push(kh_kv *kv, size_t layer, const float *k, const float *v, size_t m) {
+    return kv_push(kv, layer, k, v, m, hipMemcpyHostToDevice);
+}
+
+int kh_kv_push_dev(kh_kv *kv, size_t layer, const float *k, const float *v, size_t m) {
+    return kv_push(kv, layer, k, v, m, hipMemcpyDeviceToDevice);
+}
+
+int kh_kv_len(const kh_kv *kv, size_t *len) {
+    if (!kv || !len) return fail(KH_EINVAL, "kh_kv_len: null argument");
+    *len = kv->len;
+    return KH_OK;
+}
+
+int kh_kv_set_len(kh_kv *kv, size_t len) {
+    if (!kv) return fail(KH_EINVAL, "kh_kv_set_len: null argument");
+    kv->len = len;
+    return KH_OK;
+}
+
+int kh_kv_truncate(kh_kv *kv, size_t len, size_t *kept) {
+    if (!kv) return fail(KH_EINVAL, "kh_kv_truncate: null argument");
+    if (len < kv->len) {
+        for (size_t l = 0; l < kv->n_layer; l++)
+            if (kv->rows[l] > len) kv->rows[l] = len;
+        kv->len = len;
+    }
+    if (kept) *kept = kv->len;
+    return KH_OK;
+}
+
+int kh_kv_clear(kh_kv *kv) {
+    if (!kv) return fail(KH_EINVAL, "kh_kv_clear: null argument");
+    for (size_t l = 0; l < kv->n_layer; l++) kv->rows[l] = 0;
+    kv->len = 0;
+    return KH_OK;
+}
+
+static int kv_read(const kh_kv *kv, size_t layer, bool keys, float *out, size_t *rows) {
+    if (!kv) return fail(KH_EINVAL, "kh_kv_keys: null argument");
+    if (layer >= kv->n_layer) return fail(KH_EINVAL, "kh_kv_keys: no such layer");
+    Guard g(kv->ctx);
+    size_t r = kv->rows[layer], dim = keys ? kv->k_dim : kv->v_dim;
+    if (rows) *rows = r;
+    if (out && r) {
+        KH_HIP(hipMemcpyAsync(out, keys ? kv->k[layer] : kv->v[layer], 4 * r * dim, hipMemcpyDeviceToHost,
+                              kv->ctx->stream));
+        KH_HIP(hipStreamSynchronize(kv->ctx->stream));
+    }
+    return KH_OK;
+}
+
+int kh_kv_keys(const kh_kv *kv, size_t layer, float *out, size_t *rows) { return kv_read(kv, layer, true, out, rows); }
+
+int kh_kv_values(const kh_kv *kv, size_t layer, float *out, size_t *rows) {
+    return kv_read(kv, layer, false, out, rows);
+}
+
+int kh_kv_layer_ptrs(const kh_kv *kv, size_t layer, float **k, float **v) {
+    if (!kv || layer >= kv->n_layer) return fail(KH_EINVAL, "kh_kv_layer_ptrs: bad argument");
+    if (k) *k = kv->k[layer];
+    if (v) *v = kv->v[layer];
+    return KH_OK;
+}
+
+// ---- attention ---------------------------------------------------------------
+
+int kh_attend_dev(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q, const float *k,
+                  const float *v, size_t n_positions, float *out) {
+    if (!ctx || !q || !out || (n_positions && (!k || !v))) return fail(KH_EINVAL, "kh_attend_dev: null argument");
+    Guard g(ctx);
+    size_t kv_dim = n_kv_head * head_dim;
+    return launch_attend(ctx, (int)n_head, (int)n_kv_head, (int)head_dim, q, k, v, kv_dim, kv_dim, n_positions, out);
+}
+
+int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t n_kv_head, size_t head_dim,
+              const float *q, size_t n_positions, float *out) {
+    if (!ctx || !kv || !q || !out) return fail(KH_EINVAL, "kh_attend: null argument");
+    if (layer >= kv->n_layer) return fail(KH_EINVAL, "kh_attend: no such layer");
+    if (kv->k_dim != n_kv_head * head_dim || kv->v_dim != n_kv_head * head_dim)
+        return fail(KH_EINVAL, "kh_attend: cache width is not n_kv_head * head_dim");
+    if (n_positions > kv->rows[layer]) return fail(KH_EINVAL, "kh_attend: more positions than the cache holds");
+    Guard g(ctx);
+    const size_t nq = n_head * head_dim;
+    int rc = ensure(ctx, ctx->io, 2 * up(4 * nq));
+    if (rc) return rc;
+    float *dq = static_cast<float *>(ctx->io.ptr);
+    float *dout = reinterpret_cast<float *>(static_cast<char *>(ctx->io.ptr) + up(4 * nq));
+    KH_HIP(hipMemcpyAsync(dq, q, 4 * nq, hipMemcpyHostToDevice, ctx->stream));
+    rc = launch_attend(ctx, (int)n_head, (int)n_kv_head, (int)head_dim, dq, kv->k[layer], kv->v[layer], kv->k_dim,
+                       kv->v_dim, n_positions, dout);
+    if (rc) return rc;
+    KH_HIP(hipMemcpyAsync(out, dout, 4 * nq, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+}  // extern "C"

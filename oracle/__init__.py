@@ -1,0 +1,340 @@
+"""Python wrapper of the CPU oracle (oracle/kvad_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, and only as the checker or the CPU baseline --
+never as the path being measured or shipped.
+
+Each function restates the reference line for line; the C source cites the
+lines.  Arrays are numpy, shapes as in the reference.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libkvad_oracle.so"
+LIB_NATIVE = HERE / "libkvad_oracle_native.so"
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "-B"], check=True)
+
+
+def _load(path: Path) -> C.CDLL:
+    if not path.exists():
+        build()
+    return C.CDLL(str(path))
+
+
+_p = C.c_void_p
+_sz = C.c_size_t
+_f = C.c_float
+
+
+def _declare(lib: C.CDLL) -> C.CDLL:
+    sigs = {
+        "kvo_fill_normal": (None, [C.c_uint64, _f, _p, _sz]),
+        "kvo_set_threads": (None, [C.c_int]),
+        "kvo_get_threads": (C.c_int, []),
+        "kvo_quantize_q8": (None, [_p, _sz, _sz, _p, _p]),
+        "kvo_quantize_q4": (None, [_p, _sz, _sz, _p, _p]),
+        "kvo_qact": (None, [_p, _sz, _p, _p, _p]),
+        "kvo_qact_batch": (None, [_p, _sz, _sz, _p, _p, _p]),
+        "kvo_f32_to_f16": (C.c_uint16, [_f]),
+        "kvo_f16_to_f32": (_f, [C.c_uint16]),
+        "kvo_quantize_q4k": (None, [_p, _sz, _sz, _p]),
+        "kvo_row_q8": (None, [_p, _p, _sz, _sz, _p]),
+        "kvo_row_q4": (None, [_p, _p, _sz, _sz, _p]),
+        "kvo_row_q4k": (None, [_p, _sz, _sz, _p]),
+        "kvo_block_dots_q8": (None, [_p, _sz, _sz, _p, _p]),
+        "kvo_block_dots_q4": (None, [_p, _sz, _sz, _p, _p, _p]),
+        "kvo_block_dots_q4k": (None, [_p, _sz, _sz, _p, _p]),
+        "kvo_matvec_q8": (None, [_p, _p, _sz, _sz, _p, _p, _p]),
+        "kvo_matvec_q4": (None, [_p, _p, _sz, _sz, _p, _p, _p]),
+        "kvo_matvec_q4k": (None, [_p, _sz, _sz, _p, _p, _p]),
+        "kvo_matvec_f32": (None, [_p, _sz, _sz, _p, _p, _p]),
+        "kvo_matvec_dequant": (None, [C.c_int, _p, _p, _sz, _sz, _p, _p]),
+        "kvo_matmul_q8": (None, [_p, _p, _sz, _sz, _p, _sz, _p, _p]),
+        "kvo_matmul_q4": (None, [_p, _p, _sz, _sz, _p, _sz, _p, _p]),
+        "kvo_matmul_q4k": (None, [_p, _sz, _sz, _p, _sz, _p, _p]),
+        "kvo_gemm_f32": (None, [_p, _sz, _p, _sz, _sz, _p]),
+        "kvo_matmul_f32": (None, [_p, _sz, _sz, _p, _sz, _p, _p]),
+        "kvo_dot": (_f, [_p, _p, _sz]),
+        "kvo_softmax": (None, [_p, _sz]),
+        "kvo_rms_norm": (None, [_p, _p, _sz, _f, _p]),
+        "kvo_swiglu": (None, [_p, _p, _sz]),
+        "kvo_rope_tables": (None, [_sz, _sz, _f, _p, _p]),
+        "kvo_rope_apply": (None, [_p, _p, _sz, _p, _sz]),
+        "kvo_attend": (None, [_sz, _sz, _sz, _p, _p, _p, _sz, _p]),
+        "kvo_route": (C.c_int, [_p, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, _f, _p, _p, _p]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _declare(_load(LIB))
+_native = None
+
+
+def native_lib() -> C.CDLL:
+    """The -march=native build, for the second CPU-baseline column."""
+    global _native
+    if _native is None:
+        _native = _declare(_load(LIB_NATIVE))
+    return _native
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def P(a):
+    return None if a is None else a.ctypes.data
+
+
+def set_threads(n: int) -> None:
+    lib.kvo_set_threads(n)
+    if _native is not None:
+        _native.kvo_set_threads(n)
+
+
+def threads() -> int:
+    return lib.kvo_get_threads()
+
+
+# ---- seeded inputs --------------------------------------------------------
+
+def normal(seed: int, n: int, scale: float = 1.0) -> np.ndarray:
+    """n values of nervus Rng(seed).normal() * scale (crates/nervus/src/rng.rs:35-39)."""
+    out = np.empty(n, np.float32)
+    lib.kvo_fill_normal(seed, scale, P(out), n)
+    return out
+
+
+# ---- quantisation ---------------------------------------------------------
+
+def quantize_q8(w, rows: int, cols: int):
+    w = _c(w, np.float32)
+    s = np.empty(rows * cols // 32, np.float32)
+    q = np.empty(rows * cols, np.int8)
+    lib.kvo_quantize_q8(P(w), rows, cols, P(s), P(q))
+    return s, q
+
+
+def quantize_q4(w, rows: int, cols: int):
+    w = _c(w, np.float32)
+    s = np.empty(rows * cols // 32, np.float32)
+    q = np.empty(rows * cols // 2, np.uint8)
+    lib.kvo_quantize_q4(P(w), rows, cols, P(s), P(q))
+    return s, q
+
+
+def quantize_q4k(w, rows: int, cols: int) -> np.ndarray:
+    w = _c(w, np.float32)
+    b = np.empty(rows * cols // 256 * 144, np.uint8)
+    lib.kvo_quantize_q4k(P(w), rows, cols, P(b))
+    return b
+
+
+def qact(x):
+    x = _c(x, np.float32)
+    n = x.size
+    q = np.empty(n, np.int8)
+    s = np.empty(n // 32, np.float32)
+    su = np.empty(n // 32, np.int32)
+    lib.kvo_qact(P(x), n, P(q), P(s), P(su))
+    return q, s, su
+
+
+def f32_to_f16(x: float) -> int:
+    return lib.kvo_f32_to_f16(x)
+
+
+def f16_to_f32(h: int) -> float:
+    return lib.kvo_f16_to_f32(h)
+
+
+# ---- rows and dots --------------------------------------------------------
+
+def row_q8(scales, qs, cols: int, r: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    lib.kvo_row_q8(P(_c(scales, np.float32)), P(_c(qs, np.int8)), cols, r, P(out))
+    return out
+
+
+def row_q4(scales, qs, cols: int, r: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    lib.kvo_row_q4(P(_c(scales, np.float32)), P(_c(qs, np.uint8)), cols, r, P(out))
+    return out
+
+
+def row_q4k(blocks, cols: int, r: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    lib.kvo_row_q4k(P(_c(blocks, np.uint8)), cols, r, P(out))
+    return out
+
+
+def block_dots_q8(qs, rows: int, cols: int, xq) -> np.ndarray:
+    d = np.empty(rows * cols // 32, np.int32)
+    lib.kvo_block_dots_q8(P(_c(qs, np.int8)), rows, cols, P(_c(xq, np.int8)), P(d))
+    return d.reshape(rows, cols // 32)
+
+
+def block_dots_q4(qs, rows: int, cols: int, xq, xsums) -> np.ndarray:
+    d = np.empty(rows * cols // 32, np.int32)
+    lib.kvo_block_dots_q4(P(_c(qs, np.uint8)), rows, cols, P(_c(xq, np.int8)), P(_c(xsums, np.int32)), P(d))
+    return d.reshape(rows, cols // 32)
+
+
+def block_dots_q4k(blocks, rows: int, cols: int, xq) -> np.ndarray:
+    d = np.empty(rows * cols // 32, np.int32)
+    lib.kvo_block_dots_q4k(P(_c(blocks, np.uint8)), rows, cols, P(_c(xq, np.int8)), P(d))
+    return d.reshape(rows, cols // 32)
+
+
+# ---- GEMV / GEMM ----------------------------------------------------------
+
+def matvec_q8(scales, qs, rows, cols, x, bias=None, L=None) -> np.ndarray:
+    L = L or lib
+    y = np.empty(rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matvec_q8(P(_c(scales, np.float32)), P(_c(qs, np.int8)), rows, cols, P(_c(x, np.float32)), P(b), P(y))
+    return y
+
+
+def matvec_q4(scales, qs, rows, cols, x, bias=None, L=None) -> np.ndarray:
+    L = L or lib
+    y = np.empty(rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matvec_q4(P(_c(scales, np.float32)), P(_c(qs, np.uint8)), rows, cols, P(_c(x, np.float32)), P(b), P(y))
+    return y
+
+
+def matvec_q4k(blocks, rows, cols, x, bias=None, L=None) -> np.ndarray:
+    L = L or lib
+    y = np.empty(rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matvec_q4k(P(_c(blocks, np.uint8)), rows, cols, P(_c(x, np.float32)), P(b), P(y))
+    return y
+
+
+def matvec_f32(w, rows, cols, x, bias=None) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    lib.kvo_matvec_f32(P(_c(w, np.float32)), rows, cols, P(_c(x, np.float32)), P(b), P(y))
+    return y
+
+
+def matvec_dequant(precision: int, scales, qs, rows, cols, x) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    qs = _c(qs, np.int8 if precision == 1 else np.uint8)
+    lib.kvo_matvec_dequant(precision, P(_c(scales, np.float32)), P(qs), rows, cols, P(_c(x, np.float32)), P(y))
+    return y
+
+
+def matmul_q8(scales, qs, rows, cols, xs, m, bias=None, L=None) -> np.ndarray:
+    L = L or lib
+    y = np.empty(m * rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matmul_q8(P(_c(scales, np.float32)), P(_c(qs, np.int8)), rows, cols, P(_c(xs, np.float32)), m, P(b), P(y))
+    return y
+
+
+def matmul_q4(scales, qs, rows, cols, xs, m, bias=None, L=None) -> np.ndarray:
+    L = L or lib
+    y = np.empty(m * rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matmul_q4(P(_c(scales, np.float32)), P(_c(qs, np.uint8)), rows, cols, P(_c(xs, np.float32)), m, P(b), P(y))
+    return y
+
+
+def matmul_q4k(blocks, rows, cols, xs, m, bias=None, L=None) -> np.ndarray:
+    L = L or lib
+    y = np.empty(m * rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matmul_q4k(P(_c(blocks, np.uint8)), rows, cols, P(_c(xs, np.float32)), m, P(b), P(y))
+    return y
+
+
+def gemm_f32(xs, m, w, rows, cols) -> np.ndarray:
+    out_t = np.empty(rows * m, np.float32)
+    lib.kvo_gemm_f32(P(_c(xs, np.float32)), m, P(_c(w, np.float32)), rows, cols, P(out_t))
+    return out_t
+
+
+def matmul_f32(w, rows, cols, xs, m, bias=None, L=None) -> np.ndarray:
+    L = L or lib
+    y = np.empty(m * rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matmul_f32(P(_c(w, np.float32)), rows, cols, P(_c(xs, np.float32)), m, P(b), P(y))
+    return y
+
+
+# ---- small pieces ---------------------------------------------------------
+
+def dot(a, b) -> float:
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    return lib.kvo_dot(P(a), P(b), a.size)
+
+
+def softmax(x) -> np.ndarray:
+    x = _c(x, np.float32).copy()
+    lib.kvo_softmax(P(x), x.size)
+    return x
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib.kvo_rms_norm(P(x), P(_c(w, np.float32)), x.size, eps, P(out))
+    return out
+
+
+def swiglu(gate, up) -> np.ndarray:
+    g = _c(gate, np.float32).copy()
+    lib.kvo_swiglu(P(g), P(_c(up, np.float32)), g.size)
+    return g
+
+
+def rope_tables(head_dim: int, max_pos: int, theta: float):
+    half = head_dim // 2
+    c = np.empty(max_pos * half, np.float32)
+    s = np.empty(max_pos * half, np.float32)
+    lib.kvo_rope_tables(head_dim, max_pos, theta, P(c), P(s))
+    return c, s
+
+
+def rope_apply(cos_t, sin_t, half: int, x, pos: int) -> np.ndarray:
+    x = _c(x, np.float32).copy()
+    lib.kvo_rope_apply(P(cos_t), P(sin_t), half, P(x), pos)
+    return x
+
+
+def attend(n_head, n_kv_head, head_dim, q, k_cache, v_cache, n_positions, L=None) -> np.ndarray:
+    L = L or lib
+    out = np.empty(n_head * head_dim, np.float32)
+    L.kvo_attend(n_head, n_kv_head, head_dim, P(_c(q, np.float32)), P(_c(k_cache, np.float32)),
+                 P(_c(v_cache, np.float32)), n_positions, P(out))
+    return out
+
+
+def route(logits, top_k: int, scoring: int = 0, select: int = 0, n_group: int = 1, topk_group: int = 1,
+          norm_topk: bool = False, scale: float = 1.0, bias=None):
+    """Router::route: list of (expert, weight) in pick order."""
+    logits = _c(logits, np.float32)
+    n = logits.size
+    e = np.empty(max(top_k, 1), np.int32)
+    w = np.empty(max(top_k, 1), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    got = lib.kvo_route(P(logits), n, top_k, scoring, select, n_group, topk_group, int(norm_topk), scale, P(b),
+                        P(e), P(w))
+    return [(int(e[i]), float(w[i])) for i in range(got)]
