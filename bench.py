@@ -2,18 +2,21 @@
 """Benchmark of the hot path on one MI355X.
 
 Workload: single-token Q4_K GEMV at Llama-3-8B
-shapes -- per layer 4096x4096 (x: 4096), 14336x4096 (x: 4096) and 4096x14336
-(x: 14336) -- over 32 layers of distinct weights (2.42 GB, ten times the
-256 MB Infinity Cache, so every weight byte comes from HBM).  Weights are
-f32 ~ N(0, 0.02) quantised to Q4_K on the device; activations ~ N(0, 1).
-One step = the 96 GEMVs of one decode token, each with its activation
-quantisation, replayed from a HIP graph.  Inputs are resident in HBM.
+shapes, as one decode token issues them: per layer the q/k/v projections
+(4096 + 1024 + 1024 rows x 4096, one matvec_many launch, as they share
+their input), o (4096x4096), gate+up (2 x 14336x4096, one matvec_many
+launch) and down (4096x14336) -- 32 layers of distinct weights (3.9 GB,
+fifteen times the 256 MB Infinity Cache, so every weight byte comes from
+HBM).  Weights are f32 ~ N(0, 0.02) quantised to Q4_K on the device;
+activations ~ N(0, 1) (synthetic, independent per projection).  One step =
+the 128 GEMV launches of one token, each with its activation quantisation,
+replayed from a HIP graph.  Inputs are resident in HBM.
 
 value = algorithmic bytes per step / step time (GB/s), the bytes being
-144*rows*cols/256 + 4*cols + 4*rows per GEMV.  roofline = the GEMV kernel
-alone (graph of the 96 kernel launches on pre-quantised activations), timed
-with HIP events on the stream it runs on.  cpu_baseline = the C oracle's Q4_K
-GEMV on the host's cores over layer 0's three matrices.
+144*rows*cols/256 + 4*cols + 4*rows per GEMV.  roofline = the GEMV kernels
+alone (the same launches on pre-quantised activations), timed with HIP
+events on the stream they run on.  cpu_baseline = the C oracle's Q4_K GEMV
+on the host's cores over layer 0's matrices.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -33,6 +36,8 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
 LLAMA = [(4096, 4096), (14336, 4096), (4096, 14336)]
+LLAMA_LAYER = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+               "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336)}
 QWEN_FFN = [(4864, 896), (4864, 896), (896, 4864)]
 
 
@@ -127,62 +132,73 @@ def main() -> int:
     layers = []
     with torch.cuda.stream(stream):
         for l in range(args.layers):
-            ws = []
-            for rows, cols in LLAMA:
+            L = {}
+            for name, (rows, cols) in LLAMA_LAYER.items():
                 f = torch.randn(rows, cols, device=dev, generator=gen) * 0.02
-                ws.append(K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q4K))
+                L[name] = K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q4K)
+                L["y_" + name] = torch.empty(rows, device=dev)
                 del f
-            x4 = torch.randn(4096, device=dev, generator=gen)
-            x14 = torch.randn(14336, device=dev, generator=gen)
-            ys = [torch.empty(r, device=dev) for r, _ in LLAMA]
-            layers.append((ws, [x4, x4, x14], ys))
+            for name, n in (("x", 4096), ("a", 4096), ("h", 4096), ("m", 14336)):
+                L[name] = torch.randn(n, device=dev, generator=gen)
+            layers.append(L)
     ctx.synchronize()
     torch.cuda.synchronize()
     log(f"quantised {args.layers} layers of Q4_K weights in {time.time() - t0:.1f}s")
-    step_bytes = sum(q4k_bytes(r, c) for r, c in LLAMA) * args.layers
-    weight_bytes = sum(w.bytes for ws, _, _ in layers for w in ws)
+    step_bytes = args.layers * sum(q4k_bytes(r, c) for r, c in LLAMA_LAYER.values())
+    weight_bytes = sum(L[n].bytes for L in layers for n in LLAMA_LAYER)
+    launches = 4 * args.layers
+
+    def many(ws, xs, ys):
+        n = len(ws)
+        arr = lambda vals: (K.C.c_void_p * n)(*vals)
+        rc = K.lib.kh_matvec_many_dev(ctx.h, n, arr([w.h.value for w in ws]), arr(xs), arr(ys))
+        assert rc == 0, K.lib.kh_last_error()
 
     def step():
-        for ws, xs, ys in layers:
-            for w, x, y in zip(ws, xs, ys):
-                w.matvec_bt_dev(x.data_ptr(), y.data_ptr())
+        for L in layers:
+            many([L["q"], L["k"], L["v"]], [L["x"].data_ptr()] * 3,
+                 [L["y_q"].data_ptr(), L["y_k"].data_ptr(), L["y_v"].data_ptr()])
+            L["o"].matvec_bt_dev(L["a"].data_ptr(), L["y_o"].data_ptr())
+            many([L["gate"], L["up"]], [L["h"].data_ptr()] * 2, [L["y_gate"].data_ptr(), L["y_up"].data_ptr()])
+            L["down"].matvec_bt_dev(L["m"].data_ptr(), L["y_down"].data_ptr())
 
     g_step = Graph(torch, ctx, stream, step)
     sec = g_step.time(args.steps, args.warmup)
     log(f"step: {sec * 1e3:.3f} ms, {step_bytes / sec / 1e9:.1f} GB/s")
 
-    # ---- the GEMV kernel alone, on pre-quantised activations --------------
-    acts = {}
+    # ---- the GEMV kernels alone: down's input pre-quantised ---------------
     with torch.cuda.stream(stream):
-        for l, (ws, xs, ys) in enumerate(layers):
-            for i, x in enumerate(xs):
-                n = x.numel()
-                qs = torch.empty(n, dtype=torch.int8, device=dev)
-                sc = torch.empty(n // 32, device=dev)
-                su = torch.empty(n // 32, dtype=torch.int32, device=dev)
-                K.qact_dev(ctx, x.data_ptr(), 1, n, qs.data_ptr(), sc.data_ptr(), su.data_ptr())
-                acts[(l, i)] = (qs, sc, su)
+        for L in layers:
+            n = 14336
+            L["mq"] = (torch.empty(n, dtype=torch.int8, device=dev), torch.empty(n // 32, device=dev),
+                       torch.empty(n // 32, dtype=torch.int32, device=dev))
+            K.qact_dev(ctx, L["m"].data_ptr(), 1, n, *[t.data_ptr() for t in L["mq"]])
     torch.cuda.synchronize()
 
-    def kernels(shape_idx=None):
-        def run():
-            for l, (ws, xs, ys) in enumerate(layers):
-                for i, (w, y) in enumerate(zip(ws, ys)):
-                    if shape_idx is not None and i != shape_idx:
-                        continue
-                    qs, sc, su = acts[(l, i)]
-                    w.matvec_q_dev(qs.data_ptr(), sc.data_ptr(), su.data_ptr(), y.data_ptr())
-        return run
+    def kernels():
+        for L in layers:
+            many([L["q"], L["k"], L["v"]], [L["x"].data_ptr()] * 3,
+                 [L["y_q"].data_ptr(), L["y_k"].data_ptr(), L["y_v"].data_ptr()])
+            L["o"].matvec_bt_dev(L["a"].data_ptr(), L["y_o"].data_ptr())
+            many([L["gate"], L["up"]], [L["h"].data_ptr()] * 2, [L["y_gate"].data_ptr(), L["y_up"].data_ptr()])
+            L["down"].matvec_q_dev(*[t.data_ptr() for t in L["mq"]], L["y_down"].data_ptr())
 
-    g_k = Graph(torch, ctx, stream, kernels())
+    g_k = Graph(torch, ctx, stream, kernels)
     ksec = g_k.time(args.steps, args.warmup)
-    launches = 3 * args.layers
     avg_launch = ksec / launches
     achieved = step_bytes / ksec / 1e9
     log(f"gemv kernels: {avg_launch * 1e6:.2f} us/launch avg, {achieved:.1f} GB/s")
+
+    # ---- each config shape as its own launch ------------------------------
     per_shape = {}
-    for i, (rows, cols) in enumerate(LLAMA):
-        g = Graph(torch, ctx, stream, kernels(i))
+    for name in ("o", "up", "down"):
+        rows, cols = LLAMA_LAYER[name]
+
+        def one():
+            for L in layers:
+                L[name].matvec_bt_dev(L["m" if name == "down" else "x"].data_ptr(), L["y_" + name].data_ptr())
+
+        g = Graph(torch, ctx, stream, one)
         s = g.time(args.steps, args.warmup) / args.layers
         per_shape[f"{rows}x{cols}"] = {"us": round(s * 1e6, 3), "GBps": round(q4k_bytes(rows, cols) / s / 1e9, 1)}
         del g
@@ -210,12 +226,13 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "q4_k weights x int8 activations, i32 block dots, f32 accumulate",
         "data": "synthetic: W ~ N(0,0.02) quantised to Q4_K on device, x ~ N(0,1)",
-        "config": {"workload": "q4k-gemv-llama3-8b", "layers": args.layers,
-                   "shapes": ["4096x4096", "14336x4096", "4096x14336"], "gemvs_per_step": launches,
+        "config": {"workload": "q4k-gemv-llama3-8b-decode", "layers": args.layers,
+                   "per_layer": "qkv 6144x4096 (one launch), o 4096x4096, gate+up 28672x4096 (one launch), "
+                                "down 4096x14336", "launches_per_step": launches,
                    "bytes_per_step": step_bytes, "launch": "hip graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<Q4K>", "avg_launch_us": round(avg_launch * 1e6, 3),
+                     "kernel": "gemv_kernel<Q4K,*>", "avg_launch_us": round(avg_launch * 1e6, 3),
                      "bytes_per_launch": step_bytes // launches},
         "cpu_baseline": cpu,
         "extra": extra,
@@ -229,30 +246,66 @@ def secondary(torch, K, ctx, stream, dev, gen, args):
     """BASELINE configs[0] (Q8 GEMV at Qwen2.5-0.5B FFN shapes, 24 layers) and
     configs[3] (decode attention, Qwen geometry) as extra figures."""
     out = {}
+    qwen = {"q": (896, 896), "k": (128, 896), "v": (128, 896), "o": (896, 896),
+            "gate": (4864, 896), "up": (4864, 896), "down": (896, 4864)}
     qlayers = []
     with torch.cuda.stream(stream):
         for l in range(24):
-            ws = []
-            for rows, cols in QWEN_FFN:
+            L = {}
+            for name, (rows, cols) in qwen.items():
                 f = torch.randn(rows, cols, device=dev, generator=gen) * 0.02
-                ws.append(K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8))
-            x = torch.randn(896, device=dev, generator=gen)
-            h = torch.randn(4864, device=dev, generator=gen)
-            ys = [torch.empty(r, device=dev) for r, _ in QWEN_FFN]
-            qlayers.append((ws, [x, x, h], ys))
+                L[name] = K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8)
+                L["y_" + name] = torch.empty(rows, device=dev)
+            for name, n in (("x", 896), ("a", 896), ("h", 896), ("m", 4864)):
+                L[name] = torch.randn(n, device=dev, generator=gen)
+            qlayers.append(L)
+        f = torch.randn(151936, 896, device=dev, generator=gen) * 0.02
+        head = K.Weight.quantize_dev(ctx, 151936, 896, f.data_ptr(), K.Q8)
+        del f
+        xh = torch.randn(896, device=dev, generator=gen)
+        yh = torch.empty(151936, device=dev)
     torch.cuda.synchronize()
-    qbytes = 24 * sum(q8_bytes(r, c) for r, c in QWEN_FFN)
+    qbytes = 24 * sum(q8_bytes(r, c) for r, c in qwen.values()) + q8_bytes(151936, 896)
+
+    def many(ws, xs, ys):
+        n = len(ws)
+        arr = lambda vals: (K.C.c_void_p * n)(*vals)
+        assert K.lib.kh_matvec_many_dev(ctx.h, n, arr([w.h.value for w in ws]), arr(xs), arr(ys)) == 0
 
     def step():
-        for ws, xs, ys in qlayers:
-            for w, x, y in zip(ws, xs, ys):
-                w.matvec_bt_dev(x.data_ptr(), y.data_ptr())
+        for L in qlayers:
+            many([L["q"], L["k"], L["v"]], [L["x"].data_ptr()] * 3,
+                 [L["y_q"].data_ptr(), L["y_k"].data_ptr(), L["y_v"].data_ptr()])
+            L["o"].matvec_bt_dev(L["a"].data_ptr(), L["y_o"].data_ptr())
+            many([L["gate"], L["up"]], [L["h"].data_ptr()] * 2, [L["y_gate"].data_ptr(), L["y_up"].data_ptr()])
+            L["down"].matvec_bt_dev(L["m"].data_ptr(), L["y_down"].data_ptr())
+        head.matvec_bt_dev(xh.data_ptr(), yh.data_ptr())
 
     g = Graph(torch, ctx, stream, step)
     s = g.time(args.steps, args.warmup)
-    out["q8_gemv_qwen05b_ffn"] = {"GBps": round(qbytes / s / 1e9, 1), "us_per_gemv": round(s / 72 * 1e6, 3),
-                                  "bytes_per_step": qbytes}
-    log(f"q8 qwen ffn: {out['q8_gemv_qwen05b_ffn']}")
+    out["q8_qwen05b_decode_gemvs"] = {"GBps": round(qbytes / s / 1e9, 1), "us_per_token": round(s * 1e6, 2),
+                                      "bytes_per_token": qbytes, "launches": 24 * 4 + 1}
+    del g
+
+    def head_only():
+        for _ in range(8):
+            head.matvec_bt_dev(xh.data_ptr(), yh.data_ptr())
+
+    g = Graph(torch, ctx, stream, head_only)
+    s = g.time(args.steps, args.warmup) / 8
+    out["q8_lm_head_151936x896"] = {"GBps": round(q8_bytes(151936, 896) / s / 1e9, 1), "us": round(s * 1e6, 2)}
+    del g
+
+    def ffn_shapes():
+        for L in qlayers:
+            for name in ("gate", "down"):
+                L[name].matvec_bt_dev(L["m" if name == "down" else "h"].data_ptr(), L["y_" + name].data_ptr())
+
+    g = Graph(torch, ctx, stream, ffn_shapes)
+    s = g.time(args.steps, args.warmup)
+    fb = 24 * (q8_bytes(4864, 896) + q8_bytes(896, 4864))
+    out["q8_qwen05b_ffn_single_launches"] = {"GBps": round(fb / s / 1e9, 1), "us_per_gemv": round(s / 48 * 1e6, 2)}
+    log(f"q8 qwen: {out}")
     del g
 
     spec = K.Spec(14, 2, 64)
@@ -282,14 +335,17 @@ def cpu_baseline(layers, budget_s: float):
 
     import oracle as O
 
-    ws = layers[0][0]
-    xs = [x.cpu().numpy() for x in layers[0][1]]
-    parts = [w.parts()[1] for w in ws]
+    L0 = layers[0]
+    names = ["q", "k", "v", "o", "gate", "up", "down"]
+    inputs = {"q": "x", "k": "x", "v": "x", "o": "a", "gate": "h", "up": "h", "down": "m"}
+    parts = {n: L0[n].parts()[1] for n in names}
+    xs = {n: L0[inputs[n]].cpu().numpy() for n in names}
     threads = O.threads()
 
     def one():
-        for (rows, cols), b, x in zip(LLAMA, parts, xs):
-            O.matvec_q4k(b, rows, cols, x)
+        for n in names:
+            rows, cols = LLAMA_LAYER[n]
+            O.matvec_q4k(parts[n], rows, cols, xs[n])
 
     t = time.perf_counter()
     one()
@@ -301,15 +357,15 @@ def cpu_baseline(layers, budget_s: float):
         one()
         best = min(best, time.perf_counter() - t)
         rounds += 1
-    nbytes = sum(q4k_bytes(r, c) for r, c in LLAMA)
-    # parity spot check of what was timed against the device result
-    ys = [y.cpu().numpy() for y in layers[0][2]]
-    y0 = O.matvec_q4k(parts[0], 4096, 4096, xs[0])
-    agree = float(np.max(np.abs(y0 - ys[0])) / max(np.max(np.abs(y0)), 1e-30))
-    log(f"cpu oracle: {best * 1e3:.1f} ms per 3 GEMVs on {threads} threads ({nbytes / best / 1e9:.1f} GB/s); "
+    nbytes = sum(q4k_bytes(*LLAMA_LAYER[n]) for n in names)
+    # parity spot check: the oracle and the device on the same weights and input
+    y0 = O.matvec_q4k(parts["o"], 4096, 4096, xs["o"])
+    yd = L0["o"].matvec_bt(xs["o"])
+    agree = float(np.max(np.abs(y0 - yd)) / max(np.max(np.abs(y0)), 1e-30))
+    log(f"cpu oracle: {best * 1e3:.1f} ms per layer on {threads} threads ({nbytes / best / 1e9:.1f} GB/s); "
         f"first {first:.2f}s; device-vs-oracle rel err {agree:.2e}")
     return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle matvec_q4k over layer 0's three matrices ({nbytes / 1e6:.1f} MB), best of {rounds}",
+            "sample": f"oracle matvec_q4k over layer 0's seven matrices ({nbytes / 1e6:.1f} MB), best of {rounds}",
             "cpu": cpu_model(), "rel_err_vs_device": agree}
 
 

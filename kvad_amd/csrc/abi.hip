@@ -86,19 +86,51 @@ GemvJob job_for(const kh_weight *w, const QAct *a, const float *xf, const float 
     return j;
 }
 
-// matvec on device pointers: quantise x (unless f32), then one GEMV launch.
-int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots) {
-    if (w->precision == KH_F32) {
-        GemvJob j = job_for(w, nullptr, x, bias, y, nullptr);
-        return launch_gemv(ctx, KH_F32, &j, 1);
-    }
-    int rc = ensure(ctx, ctx->ws, qact_bytes(1, w->cols));
+// Rows wider than this quantise their input in a separate launch: past it,
+// every workgroup re-quantising x in LDS costs more than one small launch.
+size_t fuse_max_cols() {
+    static const size_t v = [] {
+        const char *e = getenv("KVAD_FUSE_MAX_COLS");
+        return e && *e ? (size_t)atol(e) : (size_t)8192;
+    }();
+    return v;
+}
+
+// The GEMV jobs for n matvecs on device pointers, quantising into ws the
+// inputs of wide rows (once per distinct input, quant.rs:634-644).
+int make_jobs(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x, const float *const *bias,
+              float *const *y, int32_t *dots, std::vector<GemvJob> &jobs) {
+    size_t total = 0;
+    for (size_t i = 0; i < n; i++)
+        if (w[i]->precision != KH_F32 && w[i]->cols > fuse_max_cols()) total += qact_bytes(1, w[i]->cols);
+    int rc = total ? ensure(ctx, ctx->ws, total) : KH_OK;
     if (rc) return rc;
-    size_t used;
-    QAct a = carve_qact(static_cast<char *>(ctx->ws.ptr), 1, w->cols, &used);
-    if ((rc = launch_qact(ctx, x, 1, w->cols, a))) return rc;
-    GemvJob j = job_for(w, &a, nullptr, bias, y, dots);
-    return launch_gemv(ctx, w->precision, &j, 1);
+    char *p = static_cast<char *>(ctx->ws.ptr);
+    QAct last{};
+    jobs.clear();
+    for (size_t i = 0; i < n; i++) {
+        const float *b = bias ? bias[i] : nullptr;
+        if (w[i]->precision == KH_F32 || w[i]->cols <= fuse_max_cols()) {
+            jobs.push_back(job_for(w[i], nullptr, x[i], b, y[i], dots));
+            continue;
+        }
+        if (!(i > 0 && x[i] == x[i - 1] && w[i]->cols == w[i - 1]->cols && last.qs)) {
+            size_t used;
+            last = carve_qact(p, 1, w[i]->cols, &used);
+            p += used;
+            if ((rc = launch_qact(ctx, x[i], 1, w[i]->cols, last))) return rc;
+        }
+        jobs.push_back(job_for(w[i], &last, nullptr, b, y[i], dots));
+    }
+    return KH_OK;
+}
+
+// matvec on device pointers.
+int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots) {
+    std::vector<GemvJob> jobs;
+    int rc = make_jobs(ctx, 1, &w, &x, &bias, &y, dots, jobs);
+    if (rc) return rc;
+    return launch_gemv(ctx, w->precision, jobs.data(), 1);
 }
 
 int matvec_many_device(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x,
@@ -108,32 +140,14 @@ int matvec_many_device(kh_ctx *ctx, size_t n, const kh_weight *const *w, const f
         if (check_weight(w[i])) return KH_EINVAL;
         if (w[i]->precision == KH_F32) return fail(KH_DECLINED, "matvec_many: an f32 weight is not this call's to run");
     }
-    // Adjacent jobs on the same input quantise it once (quant.rs:634-644).
-    std::vector<size_t> which(n);
-    std::vector<size_t> first;  // job index owning each distinct activation
-    size_t total = 0;
-    for (size_t i = 0; i < n; i++) {
-        if (i == 0 || x[i] != x[i - 1] || w[i]->cols != w[i - 1]->cols) {
-            first.push_back(i);
-            total += qact_bytes(1, w[i]->cols);
-        }
-        which[i] = first.size() - 1;
-    }
-    int rc = ensure(ctx, ctx->ws, total);
+    std::vector<GemvJob> all;
+    int rc = make_jobs(ctx, n, w, x, nullptr, y, nullptr, all);
     if (rc) return rc;
-    std::vector<QAct> acts(first.size());
-    char *p = static_cast<char *>(ctx->ws.ptr);
-    for (size_t a = 0; a < first.size(); a++) {
-        size_t used;
-        acts[a] = carve_qact(p, 1, w[first[a]]->cols, &used);
-        p += used;
-        if ((rc = launch_qact(ctx, x[first[a]], 1, w[first[a]]->cols, acts[a]))) return rc;
-    }
     // One launch per precision present; a single precision is one launch.
     for (int prec : {KH_Q8, KH_Q4, KH_Q4K}) {
         std::vector<GemvJob> jobs;
         for (size_t i = 0; i < n; i++)
-            if (w[i]->precision == prec) jobs.push_back(job_for(w[i], &acts[which[i]], nullptr, nullptr, y[i], nullptr));
+            if (w[i]->precision == prec) jobs.push_back(all[i]);
         if (!jobs.empty() && (rc = launch_gemv(ctx, prec, jobs.data(), (int)jobs.size()))) return rc;
     }
     return KH_OK;
@@ -167,9 +181,9 @@ int kh_init(int device, kh_ctx **out) {
     KH_HIP(hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device));
     KH_HIP(hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking));
     ctx->stream = ctx->own;
-    KH_HIP(hipMalloc(&ctx->counters.ptr, 4096));
-    ctx->counters.bytes = 4096;
-    KH_HIP(hipMemset(ctx->counters.ptr, 0, 4096));
+    KH_HIP(hipMalloc(&ctx->counters.ptr, 65536));
+    ctx->counters.bytes = 65536;
+    KH_HIP(hipMemset(ctx->counters.ptr, 0, 65536));
     KH_HIP(hipDeviceSynchronize());
     *out = ctx.release();
     return KH_OK;

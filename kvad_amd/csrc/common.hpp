@@ -6,6 +6,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -93,13 +94,15 @@ struct GemvJob {
     const int8_t *xq;       // quantised activation (q8/q4/q4k)
     const float *xs;        // activation scales
     const int32_t *xsum;    // activation block sums
-    const float *xf;        // f32 activation (f32 weights only)
+    const float *xf;        // f32 activation: quantised in the kernel (or read
+                            // as is by f32 weights); null when xq.. are given
     const float *bias;      // or null
     float *y;
     int32_t *dots;          // optional: pass-1 integers, [rows * cols/32]
     int rows;
     int cols;
-    int wave0;              // first wave of this job in the launch
+    int wave0;              // set by the launcher: first workgroup of the job
+    int nwaves;             // set by the launcher: waves working on the job
 };
 
 // Runs every job in one launch (all jobs share `precision`).

@@ -1,28 +1,32 @@
 // Single-token GEMV for kvad's q8 / q4 layouts, GGML Q4_K blocks and f32
-// weights, plus the activation quantiser they consume.
+// weights, plus the activation quantiser.
 //
 // Reference: Weight::matvec_bt / qrow (crates/llm/src/quant.rs:410-512),
 // q4_row_dots (quant.rs:168-189), matvec_many (quant.rs:628-671),
 // QActivation::new (quant.rs:1044-1066), tensor::matvec_bt (tensor.rs:56-79),
 // Q4_K decoding (crates/gpu/src/mpp.rs:241-315).
 //
-// Shape of the kernel.  A wave64 owns R whole weight rows.  Each row is cut
-// into 16-byte chunks (q8: half a 32-block; q4: one block; Q4_K: half of two
-// sub-blocks' nibbles; f32: four weights) and lane l takes chunks l, l+64,
-// l+128, ... of every row it owns, so one load instruction of the wave moves
-// 1 KiB of contiguous weight bytes.  The integer block dots are v_dot4 on
-// int8 lanes; where a 32-block spans two lanes the halves are joined with a
-// lane swap, so the i32 per block is exact.  The scaled f32 terms are
-// summed per lane in chunk order and then across the wave.
+// Shape of the kernel.  A workgroup (4 waves) first stages the activation in
+// LDS as int8 codes, per-32 scales and code sums -- quantising the f32 input
+// itself (QActivation::new, fused into the GEMV so a matvec is one launch),
+// or copying codes a producer already made.  Each wave then owns R weight
+// rows at a time.  A row is cut into 16-byte chunks (q8: half a 32-block;
+// q4: one block; Q4_K: half of two sub-blocks' nibbles) and lane l takes
+// chunks l, l+64, l+128, ... so one load instruction of the wave moves 1 KiB
+// of contiguous weight bytes.  Weight loads are buffer loads: a read past the
+// end of an array returns zeros, so tails need no branches (a chunk past the
+// row end meets zero activations, a row past the last meets zero weights).
+// Block dots are v_dot4 on int8 lanes; a 32-block split over two lanes is
+// joined with a DPP lane swap, so every i32 is exact.  The scaled f32 terms
+// are summed per lane in chunk order, then across the wave with DPP.
 //
-// Bit-exactness.  Block dots (pass 1) equal the reference's integers.  Each
-// f32 term is computed with the reference's operation order (quant.rs:449:
-// (ws * xs) * d), and this file is compiled with -ffp-contract=off so no
-// product is fused.  The sum over blocks is a wave tree, not the reference's
-// two alternating accumulators, so outputs agree to rounding (1e-5
-// relative), not to the bit.  The per-lane order depends only on the chunk
-// index, never on the unroll (CPL) or rows per wave (R), so a row computed
-// in a matvec_many launch equals the same row computed alone, to the bit.
+// Bit-exactness.  Activation codes and block dots equal the reference's
+// integers.  Each f32 term uses the reference's operation order (quant.rs:449:
+// (ws * xs) * d), with contraction off.  The sum over blocks is a wave tree,
+// so outputs agree to rounding (1e-5 relative), not to the bit.  The per-lane
+// order depends only on the chunk index, never on the unroll (CPL) or the
+// rows per wave (R), so a row computed in a matvec_many launch equals the
+// same row computed alone, to the bit.
 #include "common.hpp"
 
 namespace kh {
@@ -31,30 +35,58 @@ namespace {
 constexpr int WAVE = 64;
 constexpr int WAVES_PER_BLOCK = 4;
 constexpr int MAX_JOBS = 24;
+constexpr unsigned RSRC_WORD3 = 0x00020000;  // raw buffer, gfx9 family
 
 struct JobTable {
     GemvJob j[MAX_JOBS];
     int n;
 };
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes > 0xffffffffu ? 0xffffffffu : bytes), RSRC_WORD3);
+}
+__device__ __forceinline__ int4 bld16(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float bldf(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ int bldi(rsrc_t r, unsigned off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// DPP lane movement (gfx9 encodings): quad_perm [1,0,3,2] = xor 1,
+// quad_perm [2,3,0,1] = xor 2, row_half_mirror, row_mirror.
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(int, v)));
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+// Sum over the wave; every lane gets the same value, in a fixed order.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dppf<DPP_XOR1>(v);
+    v += dppf<DPP_XOR2>(v);
+    v += dppf<DPP_HALF_MIRROR>(v);
+    v += dppf<DPP_MIRROR>(v);
+    float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-__device__ __forceinline__ int4 ld16(const void *p) { return *reinterpret_cast<const int4 *>(p); }
-
-__device__ __forceinline__ int byte_of(const int4 &v, int k) {
-    int w = k < 4 ? v.x : k < 8 ? v.y : k < 12 ? v.z : v.w;
-    return (w >> (8 * (k & 3))) & 0xff;
-}
-
-__device__ __forceinline__ float half_bits_to_float(unsigned short h) {
-    _Float16 f = __builtin_bit_cast(_Float16, h);
-    return (float)f;
+__device__ __forceinline__ float half_bits_to_float(unsigned h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffff));
 }
 
 // Chunks of 16 bytes per weight row.
@@ -67,23 +99,19 @@ __host__ __device__ inline int chunks_per_row(int prec, int cols) {
     }
 }
 
+__host__ __device__ inline int align16(int n) { return (n + 15) & ~15; }
+
 // ---------------------------------------------------------------------------
-// activation quantiser: 8 lanes per 32-block, 4 values each
+// activation quantisation: 8 lanes per 32-block, 4 values each
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void qact_kernel(const float *__restrict__ x, size_t nblocks,
-                                                  int8_t *__restrict__ qs, float *__restrict__ scales,
-                                                  int32_t *__restrict__ sums) {
-    size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t b = tid >> 3;
-    int sub = threadIdx.x & 7;
-    bool ok = b < nblocks;
-    float4 v = ok ? reinterpret_cast<const float4 *>(x)[b * 8 + sub] : make_float4(0.f, 0.f, 0.f, 0.f);
-    // amax (quant.rs:1052): max is exact, so the lane order does not matter
+// One lane's share of QActivation::new (quant.rs:1051-1064): returns the four
+// codes packed; *scale and *sum are the block's (same in all 8 lanes).
+__device__ __forceinline__ int quantize4(float4 v, float *scale_out, int *sum_out) {
     float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    a = fmaxf(a, __shfl_xor(a, 1));
-    a = fmaxf(a, __shfl_xor(a, 2));
-    a = fmaxf(a, __shfl_xor(a, 4));
+    a = fmaxf(a, dppf<DPP_XOR1>(a));
+    a = fmaxf(a, dppf<DPP_XOR2>(a));
+    a = fmaxf(a, dppf<DPP_HALF_MIRROR>(a));
     float scale = a / 127.0f;
     float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
     float e[4] = {v.x, v.y, v.z, v.w};
@@ -97,9 +125,25 @@ __global__ __launch_bounds__(256) void qact_kernel(const float *__restrict__ x, 
         s += q;
         packed |= (q & 0xff) << (8 * k);
     }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    s += dpp<DPP_XOR1>(s);
+    s += dpp<DPP_XOR2>(s);
+    s += dpp<DPP_HALF_MIRROR>(s);
+    *scale_out = scale;
+    *sum_out = s;
+    return packed;
+}
+
+__global__ __launch_bounds__(256) void qact_kernel(const float *__restrict__ x, size_t nblocks,
+                                                  int8_t *__restrict__ qs, float *__restrict__ scales,
+                                                  int32_t *__restrict__ sums) {
+    size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t b = tid >> 3;
+    int sub = threadIdx.x & 7;
+    bool ok = b < nblocks;
+    float4 v = ok ? reinterpret_cast<const float4 *>(x)[b * 8 + sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float scale;
+    int s;
+    int packed = quantize4(v, &scale, &s);
     if (ok) {
         reinterpret_cast<int *>(qs)[b * 8 + sub] = packed;
         if (sub == 0) {
@@ -110,239 +154,366 @@ __global__ __launch_bounds__(256) void qact_kernel(const float *__restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------
-// the GEMV kernel family
+// the quantised GEMV kernel family
 // ---------------------------------------------------------------------------
 
-template <int PREC, int CPL, int R>
-__global__ __launch_bounds__(256) void gemv_kernel(JobTable tab) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int wave = blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
-    int ji = 0;
-    while (ji + 1 < tab.n && wave >= tab.j[ji + 1].wave0) ji++;
-    const GemvJob &job = tab.j[ji];
-    const int rows = job.rows, cols = job.cols;
-    const int r0 = (wave - job.wave0) * R;
-    if (wave < job.wave0 || r0 >= rows) return;
+constexpr int WPB = 8;  // waves per workgroup (512 threads)
 
+// Activation blocks the LDS stage holds for a launch whose widest row has
+// `C` chunks at `cpl` chunks per lane per segment: the row's blocks, padded
+// with zero blocks up to what the last segment's lanes index.
+__host__ __device__ inline int padded_blocks(int prec, int C, int cpl) {
+    const int nseg = (C + WAVE * cpl - 1) / (WAVE * cpl);
+    const int cp = nseg * WAVE * cpl;
+    return prec == KH_Q8 ? cp / 2 : cp;
+}
+
+// A row group's weight chunks in registers.
+template <int PREC, int CPL, int R>
+struct Chunks {
+    int4 w[R][CPL];
+    int4 h[R][CPL];      // Q4_K block headers
+    float s[R][CPL];     // q8/q4 block scales
+};
+
+template <int PREC, int CPL, int R>
+__device__ __forceinline__ void load_chunks(Chunks<PREC, CPL, R> &c, const rsrc_t &W, const rsrc_t &WS, int r0,
+                                            int cols, int nb, int seg, int lane) {
+    const int gl = seg * WAVE * CPL + lane;  // chunk of t = 0
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const unsigned r = (unsigned)(r0 + i);
+        if constexpr (PREC == KH_Q8) {
+            const unsigned wo = r * (unsigned)cols + (unsigned)gl * 16;
+            const unsigned so = (r * (unsigned)nb + (unsigned)(gl >> 1)) * 4;
+#pragma unroll
+            for (int t = 0; t < CPL; t++) {
+                c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1024, 0));
+                c.s[i][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(WS, so, t * 128, 0));
+            }
+        } else if constexpr (PREC == KH_Q4) {
+            const unsigned wo = r * (unsigned)(cols / 2) + (unsigned)gl * 16;
+            const unsigned so = (r * (unsigned)nb + (unsigned)gl) * 4;
+#pragma unroll
+            for (int t = 0; t < CPL; t++) {
+                c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1024, 0));
+                c.s[i][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(WS, so, t * 256, 0));
+            }
+        } else {
+            const unsigned row_bytes = (unsigned)(cols / QK_K) * Q4K_BYTES;
+            const unsigned bo = r * row_bytes + (unsigned)(gl >> 3) * Q4K_BYTES;
+            const unsigned wo = bo + 16 + 16 * (unsigned)(gl & 7);
+#pragma unroll
+            for (int t = 0; t < CPL; t++) {  // 64 chunks = 8 blocks = 1152 bytes per step
+                c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1152, 0));
+                c.h[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, bo, t * 1152, 0));
+            }
+        }
+    }
+}
+
+// The chunks' contribution to each row's accumulator, in chunk order.
+template <int PREC, int CPL, int R, bool DOTS>
+__device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, float (&acc)[R], const int8_t *sq,
+                                               const float *ssc, const int *ssum, int seg, int lane, int r0,
+                                               int rows, int nb, int C, int32_t *dots) {
+    const int gl = seg * WAVE * CPL + lane;
+    if constexpr (PREC == KH_Q8) {
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int4 a = *reinterpret_cast<const int4 *>(sq + g * 16);
+            const float as = ssc[g >> 1];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                int d = dot4(c.w[i][t].x, a.x, 0);
+                d = dot4(c.w[i][t].y, a.y, d);
+                d = dot4(c.w[i][t].z, a.z, d);
+                d = dot4(c.w[i][t].w, a.w, d);
+                d += dpp<DPP_XOR1>(d);  // the other half of the 32-block
+                float s = c.s[i][t] * as;
+                s = s * (float)d;
+                acc[i] += (lane & 1) ? 0.0f : s;
+                if (DOTS && !(lane & 1) && g < C && r0 + i < rows) dots[(size_t)(r0 + i) * nb + (g >> 1)] = d;
+            }
+        }
+    } else if constexpr (PREC == KH_Q4) {
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int4 alo = *reinterpret_cast<const int4 *>(sq + g * 32);
+            const int4 ahi = *reinterpret_cast<const int4 *>(sq + g * 32 + 16);
+            const float as = ssc[g];
+            const int asum = ssum[g];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int4 q = c.w[i][t];
+                int lo = dot4(q.x & 0x0f0f0f0f, alo.x, 0);
+                lo = dot4(q.y & 0x0f0f0f0f, alo.y, lo);
+                lo = dot4(q.z & 0x0f0f0f0f, alo.z, lo);
+                lo = dot4(q.w & 0x0f0f0f0f, alo.w, lo);
+                int hi = dot4((q.x >> 4) & 0x0f0f0f0f, ahi.x, 0);
+                hi = dot4((q.y >> 4) & 0x0f0f0f0f, ahi.y, hi);
+                hi = dot4((q.z >> 4) & 0x0f0f0f0f, ahi.z, hi);
+                hi = dot4((q.w >> 4) & 0x0f0f0f0f, ahi.w, hi);
+                const int d = lo + hi - 8 * asum;  // quant.rs:187
+                float s = c.s[i][t] * as;
+                s = s * (float)d;
+                acc[i] += s;
+                if (DOTS && g < C && r0 + i < rows) dots[(size_t)(r0 + i) * nb + g] = d;
+            }
+        }
+    } else {
+        // Q4_K: the sub-block a lane finishes is fixed by the lane (64 % 8 == 0)
+        const int half = lane & 1, cc = (lane & 7) >> 1, j = 2 * cc + half;
+        const int sh = 8 * (j & 3);
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int b0 = (g >> 3) * 8 + 2 * cc;  // sub-blocks b0 (low nibbles), b0 + 1 (high)
+            const int4 alo = *reinterpret_cast<const int4 *>(sq + b0 * 32 + 16 * half);
+            const int4 ahi = *reinterpret_cast<const int4 *>(sq + (b0 + 1) * 32 + 16 * half);
+            const float as = ssc[b0 + half];
+            const int asum = ssum[b0 + half];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int4 q = c.w[i][t];
+                int lo = dot4(q.x & 0x0f0f0f0f, alo.x, 0);
+                lo = dot4(q.y & 0x0f0f0f0f, alo.y, lo);
+                lo = dot4(q.z & 0x0f0f0f0f, alo.z, lo);
+                lo = dot4(q.w & 0x0f0f0f0f, alo.w, lo);
+                int hi = dot4((q.x >> 4) & 0x0f0f0f0f, ahi.x, 0);
+                hi = dot4((q.y >> 4) & 0x0f0f0f0f, ahi.y, hi);
+                hi = dot4((q.z >> 4) & 0x0f0f0f0f, ahi.z, hi);
+                hi = dot4((q.w >> 4) & 0x0f0f0f0f, ahi.w, hi);
+                lo += dpp<DPP_XOR1>(lo);
+                hi += dpp<DPP_XOR1>(hi);
+                const int d = half ? hi : lo;
+                // 6-bit scale and minimum of sub-block j (mpp.rs:276-282);
+                // bytes 4..15 of the block are h.y, h.z, h.w
+                const int4 h = c.h[i][t];
+                const unsigned A = (unsigned)h.y >> sh, B = (unsigned)h.z >> sh, Cw = (unsigned)h.w >> sh;
+                const unsigned sc = j < 4 ? (A & 63) : ((Cw & 0xf) | ((A >> 2) & 0x30));
+                const unsigned mn = j < 4 ? (B & 63) : (((Cw >> 4) & 0xf) | ((B >> 2) & 0x30));
+                const float dl = half_bits_to_float((unsigned)h.x) * (float)sc;
+                const float ml = half_bits_to_float((unsigned)h.x >> 16) * (float)mn;
+                float t1 = dl * (float)d;
+                float t2 = ml * (float)asum;
+                float s = t1 - t2;
+                s = as * s;
+                acc[i] += s;
+                if (DOTS && g < C && r0 + i < rows) dots[(size_t)(r0 + i) * nb + (g >> 3) * 8 + j] = d;
+            }
+        }
+    }
+}
+
+// One launch runs every job of the table.  Workgroups are spread over the
+// jobs in proportion to their rows; each wave walks the row groups
+// lw, lw + nw, ... of its job, loading the next group's weights before it
+// computes the current one.  The first group's loads are issued before the
+// activation is staged, so they fly while the workgroup quantises.
+template <int PREC, int CPL, int R, bool DOTS>
+__global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int blk = blockIdx.x;
+    int ji = 0;
+    for (int i = 1; i < tab.n; i++)
+        if (blk >= tab.j[i].wave0) ji = i;
+    const GemvJob &job = tab.j[ji];
+    const int rows = job.rows, cols = job.cols, nb = cols / BLOCK;
     const int C = chunks_per_row(PREC, cols);
-    const int nb = cols / BLOCK;
     const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
+    const int PB = padded_blocks(PREC, C, CPL);
+    const int ngroups = (rows + R - 1) / R;
+    const int nw = job.nwaves;                              // waves on this job
+    const int lw = (blk - job.wave0) * WPB + wv;            // this wave among them
+
+    size_t wbytes = PREC == KH_Q8 ? (size_t)rows * cols
+                    : PREC == KH_Q4 ? (size_t)rows * cols / 2
+                                    : (size_t)rows * (cols / QK_K) * Q4K_BYTES;
+    const rsrc_t W = rsrc(job.w, wbytes);
+    const rsrc_t WS = rsrc(job.ws, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
+
+    // the wave's work: its row groups, each cut into nseg segments, walked in
+    // order with the next piece's loads in flight while this one computes
+    const int my_groups = lw < ngroups ? (ngroups - lw + nw - 1) / nw : 0;
+    const int steps = my_groups * nseg;
+    Chunks<PREC, CPL, R> cur;
+    if (steps > 0) load_chunks<PREC, CPL, R>(cur, W, WS, lw * R, cols, nb, 0, lane);
+
+    // ---- stage the activation in LDS (zero blocks pad the tail) ---------
+    int8_t *sq = reinterpret_cast<int8_t *>(lds);
+    float *ssc = reinterpret_cast<float *>(lds + (size_t)PB * 32);
+    int *ssum = reinterpret_cast<int *>(ssc + PB);
+    if (job.xf) {  // quantise the f32 input (QActivation::new, quant.rs:1044-1066)
+        for (int base = 0; base < PB * 8; base += WAVE * WPB) {
+            const int i = base + tid, b = i >> 3;
+            float4 v = b < nb ? reinterpret_cast<const float4 *>(job.xf)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            float scale;
+            int s;
+            const int packed = quantize4(v, &scale, &s);
+            if (b < PB) {
+                reinterpret_cast<int *>(sq)[i] = packed;
+                if ((tid & 7) == 0) {
+                    ssc[b] = scale;
+                    ssum[b] = s;
+                }
+            }
+        }
+    } else {  // codes made elsewhere
+        for (int i = tid; i < PB * 2; i += WAVE * WPB)
+            reinterpret_cast<int4 *>(sq)[i] =
+                i < nb * 2 ? reinterpret_cast<const int4 *>(job.xq)[i] : int4{0, 0, 0, 0};
+        for (int i = tid; i < PB; i += WAVE * WPB) {
+            ssc[i] = i < nb ? job.xs[i] : 0.0f;
+            ssum[i] = i < nb ? job.xsum[i] : 0;
+        }
+    }
+    __syncthreads();
 
     float acc[R];
 #pragma unroll
     for (int i = 0; i < R; i++) acc[i] = 0.0f;
-
-    for (int seg = 0; seg < nseg; seg++) {
-        const int gbase = seg * WAVE * CPL + lane;
-        if constexpr (PREC == KH_Q8) {
-            const int8_t *W = static_cast<const int8_t *>(job.w);
-            int4 w[R][CPL];
-#pragma unroll
-            for (int i = 0; i < R; i++)
-#pragma unroll
-                for (int t = 0; t < CPL; t++) {
-                    int g = gbase + t * WAVE, r = r0 + i;
-                    w[i][t] = (g < C && r < rows) ? ld16(W + (size_t)r * cols + (size_t)g * 16) : int4{0, 0, 0, 0};
-                }
-            int4 a[CPL];
-            float as[CPL];
-#pragma unroll
-            for (int t = 0; t < CPL; t++) {
-                int g = gbase + t * WAVE;
-                a[t] = g < C ? ld16(job.xq + (size_t)g * 16) : int4{0, 0, 0, 0};
-                as[t] = g < C ? job.xs[g >> 1] : 0.0f;
-            }
+    for (int step = 0; step < steps; step++) {
+        const int grp = lw + (step / nseg) * nw, seg = step % nseg;
+        const int r0 = grp * R;
+        Chunks<PREC, CPL, R> nxt;
+        const bool more = step + 1 < steps;
+        if (more) {
+            const int ngrp = lw + ((step + 1) / nseg) * nw, nseg_i = (step + 1) % nseg;
+            load_chunks<PREC, CPL, R>(nxt, W, WS, ngrp * R, cols, nb, nseg_i, lane);
+        }
+        compute_chunks<PREC, CPL, R, DOTS>(cur, acc, sq, ssc, ssum, seg, lane, r0, rows, nb, C, job.dots);
+        if (more) cur = nxt;
+        if (seg == nseg - 1) {
 #pragma unroll
             for (int i = 0; i < R; i++) {
+                const float v = wave_sum(acc[i]);
                 const int r = r0 + i;
-#pragma unroll
-                for (int t = 0; t < CPL; t++) {
-                    const int g = gbase + t * WAVE;
-                    int d = dot4(w[i][t].x, a[t].x, 0);
-                    d = dot4(w[i][t].y, a[t].y, d);
-                    d = dot4(w[i][t].z, a[t].z, d);
-                    d = dot4(w[i][t].w, a[t].w, d);
-                    d += __shfl_xor(d, 1);  // the other half of the 32-block
-                    if (!(lane & 1) && g < C && r < rows) {
-                        const int b = g >> 1;
-                        float s = job.ws[(size_t)r * nb + b] * as[t];
-                        s = s * (float)d;
-                        acc[i] += s;
-                        if (job.dots) job.dots[(size_t)r * nb + b] = d;
-                    }
-                }
-            }
-        } else if constexpr (PREC == KH_Q4) {
-            const uint8_t *W = static_cast<const uint8_t *>(job.w);
-            int4 w[R][CPL];
-#pragma unroll
-            for (int i = 0; i < R; i++)
-#pragma unroll
-                for (int t = 0; t < CPL; t++) {
-                    int g = gbase + t * WAVE, r = r0 + i;
-                    w[i][t] = (g < C && r < rows) ? ld16(W + (size_t)r * (cols / 2) + (size_t)g * 16)
-                                                  : int4{0, 0, 0, 0};
-                }
-            int4 alo[CPL], ahi[CPL];
-            float as[CPL];
-            int asum[CPL];
-#pragma unroll
-            for (int t = 0; t < CPL; t++) {
-                int g = gbase + t * WAVE;
-                bool ok = g < C;
-                alo[t] = ok ? ld16(job.xq + (size_t)g * 32) : int4{0, 0, 0, 0};
-                ahi[t] = ok ? ld16(job.xq + (size_t)g * 32 + 16) : int4{0, 0, 0, 0};
-                as[t] = ok ? job.xs[g] : 0.0f;
-                asum[t] = ok ? job.xsum[g] : 0;
-            }
-#pragma unroll
-            for (int i = 0; i < R; i++) {
-                const int r = r0 + i;
-#pragma unroll
-                for (int t = 0; t < CPL; t++) {
-                    const int g = gbase + t * WAVE;
-                    const int4 q = w[i][t];
-                    int lo = dot4(q.x & 0x0f0f0f0f, alo[t].x, 0);
-                    lo = dot4(q.y & 0x0f0f0f0f, alo[t].y, lo);
-                    lo = dot4(q.z & 0x0f0f0f0f, alo[t].z, lo);
-                    lo = dot4(q.w & 0x0f0f0f0f, alo[t].w, lo);
-                    int hi = dot4((q.x >> 4) & 0x0f0f0f0f, ahi[t].x, 0);
-                    hi = dot4((q.y >> 4) & 0x0f0f0f0f, ahi[t].y, hi);
-                    hi = dot4((q.z >> 4) & 0x0f0f0f0f, ahi[t].z, hi);
-                    hi = dot4((q.w >> 4) & 0x0f0f0f0f, ahi[t].w, hi);
-                    const int d = lo + hi - 8 * asum[t];  // quant.rs:187
-                    if (g < C && r < rows) {
-                        float s = job.ws[(size_t)r * nb + g] * as[t];
-                        s = s * (float)d;
-                        acc[i] += s;
-                        if (job.dots) job.dots[(size_t)r * nb + g] = d;
-                    }
-                }
-            }
-        } else if constexpr (PREC == KH_Q4K) {
-            const uint8_t *W = static_cast<const uint8_t *>(job.w);
-            const size_t row_bytes = (size_t)(cols / QK_K) * Q4K_BYTES;
-            int4 w[R][CPL], hdr[R][CPL];
-#pragma unroll
-            for (int i = 0; i < R; i++)
-#pragma unroll
-                for (int t = 0; t < CPL; t++) {
-                    int g = gbase + t * WAVE, r = r0 + i;
-                    bool ok = g < C && r < rows;
-                    const uint8_t *blk = W + (size_t)r * row_bytes + (size_t)(g >> 3) * Q4K_BYTES;
-                    w[i][t] = ok ? ld16(blk + 16 + 16 * (g & 7)) : int4{0, 0, 0, 0};
-                    hdr[i][t] = ok ? ld16(blk) : int4{0, 0, 0, 0};
-                }
-            // lane's chunk g covers, for sub-blocks j0 = 2c (low nibbles) and
-            // j1 = 2c+1 (high nibbles), positions 16*half .. 16*half+15
-            int4 alo[CPL], ahi[CPL];
-            float as[CPL];
-            int asum[CPL];
-#pragma unroll
-            for (int t = 0; t < CPL; t++) {
-                int g = gbase + t * WAVE;
-                bool ok = g < C;
-                int sb = g >> 3, c = (g & 7) >> 1, half = g & 1;
-                int b0 = sb * 8 + 2 * c;          // global 32-block of j0
-                int bown = b0 + half;             // the sub-block this lane finishes
-                alo[t] = ok ? ld16(job.xq + (size_t)b0 * 32 + 16 * half) : int4{0, 0, 0, 0};
-                ahi[t] = ok ? ld16(job.xq + (size_t)(b0 + 1) * 32 + 16 * half) : int4{0, 0, 0, 0};
-                as[t] = ok ? job.xs[bown] : 0.0f;
-                asum[t] = ok ? job.xsum[bown] : 0;
-            }
-#pragma unroll
-            for (int i = 0; i < R; i++) {
-                const int r = r0 + i;
-#pragma unroll
-                for (int t = 0; t < CPL; t++) {
-                    const int g = gbase + t * WAVE;
-                    const int4 q = w[i][t];
-                    int lo = dot4(q.x & 0x0f0f0f0f, alo[t].x, 0);
-                    lo = dot4(q.y & 0x0f0f0f0f, alo[t].y, lo);
-                    lo = dot4(q.z & 0x0f0f0f0f, alo[t].z, lo);
-                    lo = dot4(q.w & 0x0f0f0f0f, alo[t].w, lo);
-                    int hi = dot4((q.x >> 4) & 0x0f0f0f0f, ahi[t].x, 0);
-                    hi = dot4((q.y >> 4) & 0x0f0f0f0f, ahi[t].y, hi);
-                    hi = dot4((q.z >> 4) & 0x0f0f0f0f, ahi[t].z, hi);
-                    hi = dot4((q.w >> 4) & 0x0f0f0f0f, ahi[t].w, hi);
-                    lo += __shfl_xor(lo, 1);
-                    hi += __shfl_xor(hi, 1);
-                    const int half = g & 1;
-                    const int j = 2 * ((g & 7) >> 1) + half;
-                    const int d = half ? hi : lo;
-                    // 6-bit scale and minimum of sub-block j (mpp.rs:276-282)
-                    const int4 h = hdr[i][t];
-                    int sc, mn;
-                    if (j < 4) {
-                        sc = byte_of(h, 4 + j) & 63;
-                        mn = byte_of(h, 8 + j) & 63;
-                    } else {
-                        sc = (byte_of(h, 8 + j) & 0xf) | ((byte_of(h, j) >> 6) << 4);
-                        mn = (byte_of(h, 8 + j) >> 4) | ((byte_of(h, 4 + j) >> 6) << 4);
-                    }
-                    const float dl = half_bits_to_float((unsigned short)(h.x & 0xffff)) * (float)sc;
-                    const float ml = half_bits_to_float((unsigned short)((unsigned)h.x >> 16)) * (float)mn;
-                    if (g < C && r < rows) {
-                        float t1 = dl * (float)d;
-                        float t2 = ml * (float)asum[t];
-                        float s = t1 - t2;
-                        s = as[t] * s;
-                        acc[i] += s;
-                        if (job.dots) job.dots[(size_t)r * nb + (g >> 3) * 8 + j] = d;
-                    }
-                }
-            }
-        } else {  // KH_F32: chunk = 4 consecutive weights
-            const float *W = static_cast<const float *>(job.w);
-#pragma unroll
-            for (int i = 0; i < R; i++) {
-                const int r = r0 + i;
-#pragma unroll
-                for (int t = 0; t < CPL; t++) {
-                    const int g = gbase + t * WAVE;
-                    if (g < C && r < rows) {
-                        const float *wr = W + (size_t)r * cols;
-                        float s = 0.0f;
-                        for (int k = 4 * g; k < 4 * g + 4 && k < cols; k++) s = fmaf(wr[k], job.xf[k], s);
-                        acc[i] += s;
-                    }
-                }
+                if (lane == 0 && r < rows) job.y[r] = job.bias ? v + job.bias[r] : v;
+                acc[i] = 0.0f;
             }
         }
     }
+}
 
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-        float v = wave_sum(acc[i]);
-        const int r = r0 + i;
-        if (lane == 0 && r < rows) job.y[r] = job.bias ? v + job.bias[r] : v;
+// f32 weights: tensor::matvec_bt (tensor.rs:56-79); lanes stride the row
+// four weights at a time, x read through the cache.
+__global__ __launch_bounds__(256) void gemv_f32_kernel(JobTable tab) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int blk = blockIdx.x;
+    int ji = 0;
+    for (int i = 1; i < tab.n; i++)
+        if (blk >= tab.j[i].wave0) ji = i;
+    const GemvJob &job = tab.j[ji];
+    const int rows = job.rows, cols = job.cols;
+    const int lw = (blk - job.wave0) * WAVES_PER_BLOCK + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const float *W = static_cast<const float *>(job.w);
+    for (int r = lw; r < rows; r += job.nwaves) {
+        const float *wr = W + (size_t)r * cols;
+        float s = 0.0f;
+        if ((cols & 3) == 0) {
+            for (int g = lane; g < cols / 4; g += WAVE) {
+                float4 a = reinterpret_cast<const float4 *>(wr)[g];
+                float4 b = reinterpret_cast<const float4 *>(job.xf)[g];
+                s = fmaf(a.x, b.x, s);
+                s = fmaf(a.y, b.y, s);
+                s = fmaf(a.z, b.z, s);
+                s = fmaf(a.w, b.w, s);
+            }
+        } else {
+            for (int k = lane; k < cols; k += WAVE) s = fmaf(wr[k], job.xf[k], s);
+        }
+        const float v = wave_sum(s);
+        if (lane == 0) job.y[r] = job.bias ? v + job.bias[r] : v;
     }
 }
 
-template <int PREC>
-int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC) {
+struct Plan {
+    int cpl, r;
+};
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+// Chunks per lane per segment (CPL) and rows per wave-step (R).
+Plan plan_for(int prec, int maxC, int rows_total, int cu_count) {
     int cpl = (maxC + WAVE - 1) / WAVE;
     if (cpl < 1) cpl = 1;
-    if (cpl > 8) cpl = 8;
-    static const int rows_for_cpl[9] = {8, 8, 4, 2, 2, 1, 1, 1, 1};
-    const int R = rows_for_cpl[cpl];
-    int waves = 0;
+    if (cpl > 8) cpl = 8;  // wider rows take several segments
+    int r = cpl == 1 || cpl == 2 ? 4 : cpl <= 4 ? 2 : 1;
+    // short matrices: fewer rows per wave, more waves
+    while (r > 1 && (rows_total + r - 1) / r < 8 * cu_count) r /= 2;
+    int forced = env_int("KVAD_GEMV_R", 0);  // tuning knob
+    if (forced == 1 || (forced == 2 && cpl <= 4) || (forced == 4 && cpl <= 2)) r = forced;
+    return {cpl, r};
+}
+
+template <int PREC, int CPL, int R>
+void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, bool dots) {
+    dim3 grid(blocks), block(WAVE * WPB);
+    if (dots)
+        hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, true>), grid, block, lds, ctx->stream, tab);
+    else
+        hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, false>), grid, block, lds, ctx->stream, tab);
+}
+
+template <int PREC>
+int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_total, bool dots) {
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    Plan p = plan_for(PREC, maxC, rows_total, cu);
     for (int i = 0; i < tab.n; i++) {
-        tab.j[i].wave0 = waves;
-        waves += (tab.j[i].rows + R - 1) / R;
+        size_t wb = (size_t)tab.j[i].rows * tab.j[i].cols;
+        if (wb >= 0xfff00000ull) return fail(KH_DECLINED, "matvec: weights of 4 GiB or more are not addressed here");
     }
-    if (waves == 0) return KH_OK;
-    dim3 grid((waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK), block(WAVE * WAVES_PER_BLOCK);
-    switch (cpl) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<PREC, 1, 8>), grid, block, 0, ctx->stream, tab); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<PREC, 2, 4>), grid, block, 0, ctx->stream, tab); break;
-        case 3: hipLaunchKernelGGL((gemv_kernel<PREC, 3, 2>), grid, block, 0, ctx->stream, tab); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<PREC, 4, 2>), grid, block, 0, ctx->stream, tab); break;
-        case 5: hipLaunchKernelGGL((gemv_kernel<PREC, 5, 1>), grid, block, 0, ctx->stream, tab); break;
-        case 6: hipLaunchKernelGGL((gemv_kernel<PREC, 6, 1>), grid, block, 0, ctx->stream, tab); break;
-        case 7: hipLaunchKernelGGL((gemv_kernel<PREC, 7, 1>), grid, block, 0, ctx->stream, tab); break;
-        default: hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1>), grid, block, 0, ctx->stream, tab); break;
+    // workgroups: about `wg_per_cu` per CU over the launch, shared out by rows
+    const int cap_wg = env_int("KVAD_GEMV_WG_PER_CU", 2) * cu;
+    int blocks = 0;
+    for (int i = 0; i < tab.n; i++) {
+        const int groups = (tab.j[i].rows + p.r - 1) / p.r;
+        const int want = (groups + WPB - 1) / WPB;
+        int share = (int)((long long)cap_wg * tab.j[i].rows / (rows_total > 0 ? rows_total : 1));
+        if (share < 1) share = 1;
+        const int nwg = want < share ? want : share;
+        tab.j[i].wave0 = blocks;  // first workgroup of the job
+        tab.j[i].nwaves = nwg * WPB;
+        blocks += nwg;
     }
+    if (blocks == 0) return KH_OK;
+    const int pb = padded_blocks(PREC, maxC, p.cpl);
+    const size_t lds = (size_t)pb * 32 + 8 * (size_t)pb;
+    if (lds > 64 * 1024) return fail(KH_DECLINED, "matvec: activation too wide for the LDS stage");
+#define KH_CASE(CPL, R)                                                       \
+    if (p.cpl == CPL && p.r == R) {                                           \
+        launch_one<PREC, CPL, R>(ctx, tab, blocks, lds, dots);                \
+        KH_HIP(hipGetLastError());                                            \
+        return KH_OK;                                                         \
+    }
+    KH_CASE(1, 4) KH_CASE(1, 2) KH_CASE(1, 1)
+    KH_CASE(2, 4) KH_CASE(2, 2) KH_CASE(2, 1)
+    KH_CASE(3, 2) KH_CASE(3, 1) KH_CASE(4, 2) KH_CASE(4, 1)
+    KH_CASE(5, 1) KH_CASE(6, 1) KH_CASE(7, 1) KH_CASE(8, 1)
+#undef KH_CASE
+    return fail(KH_EINVAL, "matvec: no kernel for this plan");
+}
+
+int launch_f32(kh_ctx *ctx, JobTable &tab) {
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    int blocks = 0;
+    for (int i = 0; i < tab.n; i++) {
+        int nw = tab.j[i].rows < 8 * cu ? tab.j[i].rows : 8 * cu;
+        tab.j[i].wave0 = blocks;
+        tab.j[i].nwaves = nw;
+        blocks += (nw + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+    }
+    if (blocks == 0) return KH_OK;
+    hipLaunchKernelGGL(gemv_f32_kernel, dim3(blocks), dim3(256), 0, ctx->stream, tab);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -383,10 +554,8 @@ __global__ void dequant_row_kernel(int prec, const void *qs, const float *scales
             sc = (s[j + 4] & 0xf) | ((s[j - 4] >> 6) << 4);
             mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
         }
-        unsigned short d16 = (unsigned short)(blk[0] | (blk[1] << 8));
-        unsigned short m16 = (unsigned short)(blk[2] | (blk[3] << 8));
-        float dl = half_bits_to_float(d16) * (float)sc;
-        float ml = half_bits_to_float(m16) * (float)mn;
+        float dl = half_bits_to_float(blk[0] | (blk[1] << 8)) * (float)sc;
+        float ml = half_bits_to_float(blk[2] | (blk[3] << 8)) * (float)mn;
         int q = (blk[16 + 32 * c + l] >> (4 * h)) & 0xf;
         float t = dl * (float)q;
         out[k] = t - ml;
@@ -411,18 +580,22 @@ int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
     for (int base = 0; base < njobs; base += MAX_JOBS) {
         JobTable tab{};
         tab.n = njobs - base < MAX_JOBS ? njobs - base : MAX_JOBS;
-        int maxC = 0;
+        int maxC = 0, maxCols = 0, rows_total = 0;
+        bool dots = false;
         for (int i = 0; i < tab.n; i++) {
             tab.j[i] = jobs[base + i];
             int c = chunks_per_row(precision, tab.j[i].cols);
             maxC = c > maxC ? c : maxC;
+            maxCols = tab.j[i].cols > maxCols ? tab.j[i].cols : maxCols;
+            rows_total += tab.j[i].rows;
+            dots = dots || tab.j[i].dots;
         }
         int rc;
         switch (precision) {
-            case KH_Q8: rc = launch_prec<KH_Q8>(ctx, tab, maxC); break;
-            case KH_Q4: rc = launch_prec<KH_Q4>(ctx, tab, maxC); break;
-            case KH_Q4K: rc = launch_prec<KH_Q4K>(ctx, tab, maxC); break;
-            case KH_F32: rc = launch_prec<KH_F32>(ctx, tab, maxC); break;
+            case KH_Q8: rc = launch_prec<KH_Q8>(ctx, tab, maxC, maxCols, rows_total, dots); break;
+            case KH_Q4: rc = launch_prec<KH_Q4>(ctx, tab, maxC, maxCols, rows_total, dots); break;
+            case KH_Q4K: rc = launch_prec<KH_Q4K>(ctx, tab, maxC, maxCols, rows_total, dots); break;
+            case KH_F32: rc = launch_f32(ctx, tab); break;
             default: return fail(KH_EINVAL, "unknown precision");
         }
         if (rc != KH_OK) return rc;
