@@ -1,44 +1,566 @@
-// Batched prefill: Weight::matmul_bt (crates/llm/src/quant.rs:751-907) and
-// tensor::gemm_bt (tensor.rs:102-186).
+// Batched prefill GEMM on CDNA4 matrix cores: Weight::matmul_bt
+// (crates/llm/src/quant.rs:751-907, x86 row_dot path) for q8 / q4 / Q4_K
+// weights, and tensor::gemm_bt (tensor.rs:102-186) for f32 weights.
+//
+// Quantised weights.  y[m, r] = sum_b ws[r,b] * xs[m,b] * D_b[r,m] where
+// D_b is the exact i32 dot of weight row r's 32-block b with token m's
+// quantised block (row_dot pass 1, quant.rs:876-897).  One
+// v_mfma_i32_32x32x32_i8 computes D_b for a 32x32 (rows x tokens) tile and
+// exactly one 32-wide block, so every block dot is the reference's integer;
+// the block's scaling (pass 2, quant.rs:899-905) is applied to the tile in
+// registers before the next block.  q4 nibbles are widened to (code - 8) in
+// LDS (the same integers as q4_row_dots, quant.rs:168-189); Q4_K codes are
+// widened unsigned and their sub-block scale/min terms applied as the GEMV
+// does (y += xs * (d*sc*dot - dmin*m*sum), mpp.rs:304-315).
+//
+// The per-block scaling costs three VALU operations per output per block
+// (convert, scale product, fused add) against one MFMA per 32x32 tile per
+// block: with 32-wide scale blocks on both operands this epilogue, not the
+// matrix core, bounds the kernel.
+//
+// Tiles.  A workgroup of 4 waves computes a BN x BM (weight rows x tokens)
+// tile; each wave WR/WT-splits it into RT x TT MFMA tiles of 32 x 32.  A
+// stage is 128 k-values (4 blocks): weight and activation bytes go global ->
+// registers (next stage, in flight during compute) -> LDS (rows padded by 16
+// bytes), with the stage's scales beside them.  Buffer loads return zeros
+// past the end of an array, so edge tiles need no branches on rows or
+// tokens; a k tail (K % 128 != 0) is masked explicitly.
+//
+// f32 weights use v_mfma_f32_32x32x2_f32 over 32-wide k stages with the same
+// tile map.  Sums are taken in a different order from the reference's
+// 4-lane register tiles, so results agree to rounding (1e-5 relative).
 #include "common.hpp"
 
 namespace kh {
+namespace {
 
-int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
-    // Row-at-a-time fallback: one GEMV job per activation row, all in as few
-    // launches as the job table allows.  Same per-element arithmetic as the
-    // reference's x86 row_dot (quant.rs:865-907).
-    const size_t rows = w->rows, cols = w->cols;
-    std::vector<GemvJob> jobs(m);
-    QAct a{};
-    if (w->precision != KH_F32) {
-        size_t qb = (m * cols + 255) / 256 * 256, sb = (4 * m * cols / BLOCK + 255) / 256 * 256;
-        int rc = ensure(ctx, ctx->ws, qb + 2 * sb);
-        if (rc) return rc;
-        char *p = static_cast<char *>(ctx->ws.ptr);
-        a.qs = reinterpret_cast<int8_t *>(p);
-        a.scales = reinterpret_cast<float *>(p + qb);
-        a.sums = reinterpret_cast<int32_t *>(p + qb + sb);
-        if ((rc = launch_qact(ctx, xs, m, cols, a))) return rc;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr unsigned RSRC_WORD3 = 0x00020000;  // raw buffer, gfx9 family
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes > 0xffffffffu ? 0xffffffffu : bytes), RSRC_WORD3);
+}
+__device__ __forceinline__ int4 ld16(const rsrc_t &r, unsigned off) {
+    return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float ldf(const rsrc_t &r, unsigned off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ int ldi(const rsrc_t &r, unsigned off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+__device__ __forceinline__ float half_bits_to_float(unsigned h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffff));
+}
+
+// Four nibble codes per byte lane -> signed (code - 8) bytes, no borrows.
+__device__ __forceinline__ int nib_minus8(int x) {
+    return (int)((((unsigned)x | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+}
+
+struct GemmArgs {
+    const void *w;          // q8 int8 / q4 packed / Q4_K blocks / f32 [N, K]
+    const float *ws;        // q8/q4 block scales [N, K/32]
+    const int8_t *xq;       // quantised activations [M, K]
+    const float *xs;        // activation block scales [M, K/32]
+    const int32_t *xsum;    // activation block sums [M, K/32] (Q4_K)
+    const float *xf;        // f32 activations [M, K] (f32 GEMM)
+    const float *bias;      // [N] or null
+    float *y;               // [M, N]
+    int M, N, K;
+};
+
+constexpr int THREADS = 256;
+constexpr int BK = 128;              // k per stage (bytes of int8)
+constexpr int NBS = BK / BLOCK;      // 32-blocks per stage
+constexpr int ASTR = BK + 16;        // LDS row stride, bytes
+
+// Writes a 32x32 accumulator tile (lane: token l&31, rows 8g + 4(l>>5) + e).
+template <int RT, int TT>
+__device__ __forceinline__ void store_tiles(const GemmArgs &a, const v16f (&acc)[RT][TT], int r_base, int t_base,
+                                            int lane) {
+    const bool vec = (a.N & 3) == 0;
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            const int tok = t_base + tt * 32 + (lane & 31);
+            if (tok >= a.M) continue;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int r = r_base + rt * 32 + 8 * g + 4 * (lane >> 5);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float add = a.bias && r + e < a.N ? a.bias[r + e] : 0.0f;  // finish, quant.rs:849-858
+                    v[e] = acc[rt][tt][4 * g + e] + add;
+                }
+                float *dst = a.y + (size_t)tok * a.N + r;
+                if (vec && r + 3 < a.N) {
+                    *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (r + e < a.N) dst[e] = v[e];
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// int8 MFMA GEMM for q8 / q4 / Q4_K weights
+// ---------------------------------------------------------------------------
+
+template <int PREC, int WR, int WT, int RT, int TT>
+__global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
+    static_assert(WR * WT == 4, "four waves");
+    constexpr int BN = WR * RT * 32, BM = WT * TT * 32;
+    // per-thread global chunk counts of one stage
+    constexpr int A_CH = PREC == KH_Q8 ? BN * (BK / 16) : BN * NBS;  // q4 / Q4_K: one 16-byte chunk per block
+    constexpr int A_PT = (A_CH + THREADS - 1) / THREADS;
+    constexpr int B_CH = BM * (BK / 16);
+    constexpr int B_PT = (B_CH + THREADS - 1) / THREADS;
+    constexpr int WS_PT = (BN * NBS + THREADS - 1) / THREADS;
+    constexpr int XS_PT = (BM * NBS + THREADS - 1) / THREADS;
+
+    __shared__ __align__(16) int8_t sA[BN * ASTR];
+    __shared__ __align__(16) int8_t sB[BM * ASTR];
+    __shared__ __align__(16) float sW[NBS][BN];   // ws (q8/q4) or d*sc (Q4_K)
+    __shared__ __align__(16) float sWm[NBS][BN];  // dmin*m (Q4_K)
+    __shared__ float sX[NBS][BM];                 // xs
+    __shared__ float sXs[NBS][BM];                // block sums as floats (Q4_K)
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr0 = (wave / WT) * RT * 32, wm0 = (wave % WT) * TT * 32;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int K = a.K, nb = K / BLOCK;
+
+    const size_t wbytes = PREC == KH_Q8 ? (size_t)a.N * K
+                          : PREC == KH_Q4 ? (size_t)a.N * K / 2
+                                          : (size_t)a.N * (K / QK_K) * Q4K_BYTES;
+    const rsrc_t W = rsrc(a.w, wbytes);
+    const rsrc_t WS = rsrc(a.ws, PREC == KH_Q4K ? 0 : (size_t)a.N * nb * 4);
+    const rsrc_t X = rsrc(a.xq, (size_t)a.M * K);
+    const rsrc_t XS = rsrc(a.xs, (size_t)a.M * nb * 4);
+    const rsrc_t XSUM = rsrc(a.xsum, PREC == KH_Q4K ? (size_t)a.M * nb * 4 : 0);
+
+    int4 ra[A_PT], rb[B_PT], rh;
+    float rws[WS_PT], rxs[XS_PT], rxsum[XS_PT];
+
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < A_PT; u++) {
+            const int c = tid + u * THREADS;
+            int4 v = {0, 0, 0, 0};
+            if (c < A_CH) {
+                if constexpr (PREC == KH_Q8) {
+                    const int row = c >> 3, kc = c & 7;
+                    if (k0 + 16 * kc < K) v = ld16(W, (unsigned)(n0 + row) * (unsigned)K + (unsigned)(k0 + 16 * kc));
+                } else if constexpr (PREC == KH_Q4) {
+                    const int row = c / NBS, blk = c % NBS;
+                    if (k0 / BLOCK + blk < nb)
+                        v = ld16(W, (unsigned)(n0 + row) * (unsigned)(K / 2) + (unsigned)((k0 / BLOCK + blk) * 16));
+                } else {
+                    const int row = c / NBS, q = c % NBS;
+                    const unsigned sb = (unsigned)(k0 / QK_K), h = (unsigned)((k0 % QK_K) / BK);
+                    v = ld16(W, (unsigned)(n0 + row) * (unsigned)(K / QK_K) * Q4K_BYTES + sb * Q4K_BYTES + 16 + 64 * h +
+                                    16 * q);
+                }
+            }
+            ra[u] = v;
+        }
+        if constexpr (PREC == KH_Q4K) {
+            rh = int4{0, 0, 0, 0};
+            if (tid < BN)
+                rh = ld16(W, (unsigned)(n0 + tid) * (unsigned)(K / QK_K) * Q4K_BYTES +
+                                 (unsigned)(k0 / QK_K) * Q4K_BYTES);
+        }
+#pragma unroll
+        for (int u = 0; u < B_PT; u++) {
+            const int c = tid + u * THREADS;
+            int4 v = {0, 0, 0, 0};
+            if (c < B_CH) {
+                const int tok = c >> 3, kc = c & 7;
+                if (k0 + 16 * kc < K) v = ld16(X, (unsigned)(m0 + tok) * (unsigned)K + (unsigned)(k0 + 16 * kc));
+            }
+            rb[u] = v;
+        }
+        if constexpr (PREC != KH_Q4K) {
+#pragma unroll
+            for (int u = 0; u < WS_PT; u++) {
+                const int c = tid + u * THREADS;
+                const int row = c / NBS, blk = c % NBS;
+                rws[u] = c < BN * NBS && k0 / BLOCK + blk < nb
+                             ? ldf(WS, ((unsigned)(n0 + row) * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u)
+                             : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < XS_PT; u++) {
+            const int c = tid + u * THREADS;
+            const int tok = c / NBS, blk = c % NBS;
+            const bool ok = c < BM * NBS && k0 / BLOCK + blk < nb;
+            const unsigned off = ((unsigned)(m0 + tok) * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u;
+            rxs[u] = ok ? ldf(XS, off) : 0.0f;
+            if constexpr (PREC == KH_Q4K) rxsum[u] = ok ? (float)ldi(XSUM, off) : 0.0f;
+        }
+    };
+
+    auto store_stage = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < A_PT; u++) {
+            const int c = tid + u * THREADS;
+            if (c >= A_CH) continue;
+            if constexpr (PREC == KH_Q8) {
+                const int row = c >> 3, kc = c & 7;
+                *reinterpret_cast<int4 *>(sA + row * ASTR + 16 * kc) = ra[u];
+            } else if constexpr (PREC == KH_Q4) {
+                // byte i of a block: weight i (low nibble), weight 16 + i (high), quant.rs:258-274
+                const int row = c / NBS, blk = c % NBS;
+                const int4 x = ra[u];
+                int4 lo = {nib_minus8(x.x & 0x0f0f0f0f), nib_minus8(x.y & 0x0f0f0f0f), nib_minus8(x.z & 0x0f0f0f0f),
+                           nib_minus8(x.w & 0x0f0f0f0f)};
+                int4 hi = {nib_minus8((x.x >> 4) & 0x0f0f0f0f), nib_minus8((x.y >> 4) & 0x0f0f0f0f),
+                           nib_minus8((x.z >> 4) & 0x0f0f0f0f), nib_minus8((x.w >> 4) & 0x0f0f0f0f)};
+                *reinterpret_cast<int4 *>(sA + row * ASTR + 32 * blk) = lo;
+                *reinterpret_cast<int4 *>(sA + row * ASTR + 32 * blk + 16) = hi;
+            } else {
+                // qs byte p of the super-block: sub-block 2(p/32) in the low
+                // nibble, 2(p/32)+1 in the high, weight p%32 (mpp.rs:308-313)
+                const int row = c / NBS, q = c % NBS;
+                const int4 x = ra[u];
+                int4 lo = {x.x & 0x0f0f0f0f, x.y & 0x0f0f0f0f, x.z & 0x0f0f0f0f, x.w & 0x0f0f0f0f};
+                int4 hi = {(x.x >> 4) & 0x0f0f0f0f, (x.y >> 4) & 0x0f0f0f0f, (x.z >> 4) & 0x0f0f0f0f,
+                           (x.w >> 4) & 0x0f0f0f0f};
+                const int base = 64 * (q >> 1) + 16 * (q & 1);
+                *reinterpret_cast<int4 *>(sA + row * ASTR + base) = lo;
+                *reinterpret_cast<int4 *>(sA + row * ASTR + base + 32) = hi;
+            }
+        }
+        if constexpr (PREC == KH_Q4K) {
+            if (tid < BN) {
+                // 6-bit scales and minimums of the stage's four sub-blocks
+                // (scale_min, mpp.rs:276-282)
+                const unsigned hb[4] = {(unsigned)rh.x, (unsigned)rh.y, (unsigned)rh.z, (unsigned)rh.w};
+                auto byte = [&](int i) { return (hb[i >> 2] >> (8 * (i & 3))) & 0xffu; };  // block byte i
+                const float d = half_bits_to_float(hb[0]), dmin = half_bits_to_float(hb[0] >> 16);
+                const int h = (k0 % QK_K) / BK;
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int j = 4 * h + jj;
+                    unsigned sc, mn;
+                    if (j < 4) {
+                        sc = byte(4 + j) & 63;
+                        mn = byte(4 + j + 4) & 63;
+                    } else {
+                        sc = (byte(4 + j + 4) & 0xf) | ((byte(4 + j - 4) >> 6) << 4);
+                        mn = (byte(4 + j + 4) >> 4) | ((byte(4 + j) >> 6) << 4);
+                    }
+                    sW[jj][tid] = d * (float)sc;
+                    sWm[jj][tid] = dmin * (float)mn;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < B_PT; u++) {
+            const int c = tid + u * THREADS;
+            if (c < B_CH) *reinterpret_cast<int4 *>(sB + (c >> 3) * ASTR + 16 * (c & 7)) = rb[u];
+        }
+        if constexpr (PREC != KH_Q4K) {
+#pragma unroll
+            for (int u = 0; u < WS_PT; u++) {
+                const int c = tid + u * THREADS;
+                if (c < BN * NBS) sW[c % NBS][c / NBS] = rws[u];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < XS_PT; u++) {
+            const int c = tid + u * THREADS;
+            if (c < BM * NBS) {
+                sX[c % NBS][c / NBS] = rxs[u];
+                if constexpr (PREC == KH_Q4K) sXs[c % NBS][c / NBS] = rxsum[u];
+            }
+        }
+    };
+
+    v16f acc[RT][TT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[rt][tt][v] = 0.0f;
+
+    const v16i zero = {};
+    load_stage(0);
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        __syncthreads();  // the previous stage's reads of LDS are done
+        store_stage(k0);
+        __syncthreads();
+        if (k0 + BK < K) load_stage(k0 + BK);  // in flight during this stage's MFMAs
+        const int nblk = min(NBS, (K - k0) / BLOCK);
+#pragma unroll
+        for (int b = 0; b < NBS; b++) {
+            if (b >= nblk) break;
+            v4i af[RT], bf[TT];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+                af[rt] = *reinterpret_cast<const v4i *>(sA + (wr0 + rt * 32 + (lane & 31)) * ASTR + b * 32 +
+                                                        16 * (lane >> 5));
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+                bf[tt] = *reinterpret_cast<const v4i *>(sB + (wm0 + tt * 32 + (lane & 31)) * ASTR + b * 32 +
+                                                        16 * (lane >> 5));
+            float4 wv[RT][4], wm[RT][4];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int r = wr0 + rt * 32 + 8 * g + 4 * (lane >> 5);
+                    wv[rt][g] = *reinterpret_cast<const float4 *>(&sW[b][r]);
+                    if constexpr (PREC == KH_Q4K) wm[rt][g] = *reinterpret_cast<const float4 *>(&sWm[b][r]);
+                }
+            float xv[TT], xsv[TT];
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++) {
+                xv[tt] = sX[b][wm0 + tt * 32 + (lane & 31)];
+                if constexpr (PREC == KH_Q4K) xsv[tt] = sXs[b][wm0 + tt * 32 + (lane & 31)];
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int tt = 0; tt < TT; tt++) {
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[rt], bf[tt], zero, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const float4 w4 = wv[rt][v >> 2];
+                        const float wsc = (v & 3) == 0 ? w4.x : (v & 3) == 1 ? w4.y : (v & 3) == 2 ? w4.z : w4.w;
+                        if constexpr (PREC == KH_Q4K) {
+                            const float4 m4 = wm[rt][v >> 2];
+                            const float mn = (v & 3) == 0 ? m4.x : (v & 3) == 1 ? m4.y : (v & 3) == 2 ? m4.z : m4.w;
+                            const float t2 = mn * xsv[tt];
+                            const float t = __builtin_fmaf(wsc, (float)d[v], -t2);  // d*sc*dot - dmin*m*sum
+                            acc[rt][tt][v] = __builtin_fmaf(xv[tt], t, acc[rt][tt][v]);
+                        } else {
+                            const float p = wsc * xv[tt];  // ws * xs, quant.rs:903
+                            acc[rt][tt][v] = __builtin_fmaf(p, (float)d[v], acc[rt][tt][v]);
+                        }
+                    }
+                }
+        }
     }
+    store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, lane);
+}
+
+// ---------------------------------------------------------------------------
+// f32 GEMM: v_mfma_f32_32x32x2_f32
+// ---------------------------------------------------------------------------
+
+constexpr int FK = 32;          // k per stage (floats)
+constexpr int FSTR = FK + 4;    // LDS row stride, floats
+
+template <int WR, int WT, int RT, int TT>
+__global__ __launch_bounds__(THREADS) void gemm_f32_kernel(GemmArgs a) {
+    constexpr int BN = WR * RT * 32, BM = WT * TT * 32;
+    constexpr int A_CH = BN * (FK / 4), B_CH = BM * (FK / 4);
+    constexpr int A_PT = (A_CH + THREADS - 1) / THREADS, B_PT = (B_CH + THREADS - 1) / THREADS;
+    __shared__ __align__(16) float sA[BN * FSTR];
+    __shared__ __align__(16) float sB[BM * FSTR];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr0 = (wave / WT) * RT * 32, wm0 = (wave % WT) * TT * 32;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int K = a.K;
+    const rsrc_t W = rsrc(a.w, (size_t)a.N * K * 4);
+    const rsrc_t X = rsrc(a.xf, (size_t)a.M * K * 4);
+
+    int4 ra[A_PT], rb[B_PT];
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < A_PT; u++) {
+            const int c = tid + u * THREADS, row = c / (FK / 4), kc = c % (FK / 4);
+            ra[u] = c < A_CH && k0 + 4 * kc < K ? ld16(W, ((unsigned)(n0 + row) * (unsigned)K + (unsigned)(k0 + 4 * kc)) * 4u)
+                                                 : int4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < B_PT; u++) {
+            const int c = tid + u * THREADS, tok = c / (FK / 4), kc = c % (FK / 4);
+            rb[u] = c < B_CH && k0 + 4 * kc < K ? ld16(X, ((unsigned)(m0 + tok) * (unsigned)K + (unsigned)(k0 + 4 * kc)) * 4u)
+                                                 : int4{0, 0, 0, 0};
+        }
+    };
+    auto store_stage = [&]() {
+#pragma unroll
+        for (int u = 0; u < A_PT; u++) {
+            const int c = tid + u * THREADS;
+            if (c < A_CH) *reinterpret_cast<int4 *>(sA + (c / (FK / 4)) * FSTR + 4 * (c % (FK / 4))) = ra[u];
+        }
+#pragma unroll
+        for (int u = 0; u < B_PT; u++) {
+            const int c = tid + u * THREADS;
+            if (c < B_CH) *reinterpret_cast<int4 *>(sB + (c / (FK / 4)) * FSTR + 4 * (c % (FK / 4))) = rb[u];
+        }
+    };
+
+    v16f acc[RT][TT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[rt][tt][v] = 0.0f;
+
+    load_stage(0);
+    for (int k0 = 0; k0 < K; k0 += FK) {
+        __syncthreads();
+        store_stage();
+        __syncthreads();
+        if (k0 + FK < K) load_stage(k0 + FK);
+        // lane half h takes k = 16h + 4q + e of the stage; A and B agree on it
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float4 af[RT], bf[TT];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+                af[rt] = *reinterpret_cast<const float4 *>(sA + (wr0 + rt * 32 + (lane & 31)) * FSTR +
+                                                           16 * (lane >> 5) + 4 * q);
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+                bf[tt] = *reinterpret_cast<const float4 *>(sB + (wm0 + tt * 32 + (lane & 31)) * FSTR +
+                                                           16 * (lane >> 5) + 4 * q);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int tt = 0; tt < TT; tt++) {
+                    acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[rt].x, bf[tt].x, acc[rt][tt], 0, 0, 0);
+                    acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[rt].y, bf[tt].y, acc[rt][tt], 0, 0, 0);
+                    acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[rt].z, bf[tt].z, acc[rt][tt], 0, 0, 0);
+                    acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[rt].w, bf[tt].w, acc[rt][tt], 0, 0, 0);
+                }
+        }
+    }
+    store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, lane);
+}
+
+// Tile shape for a problem: the largest tile that still gives every CU a
+// workgroup, else the smallest.
+enum Shape { T128x128, T128x64, T128x32 };
+
+Shape pick_shape(int M, int N, int cu) {
+    const long long nt = (N + 127) / 128;
+    if (nt * ((M + 127) / 128) >= cu) return T128x128;
+    if (nt * ((M + 63) / 64) >= cu) return T128x64;
+    return T128x32;
+}
+
+template <int PREC>
+int launch_i8(kh_ctx *ctx, const GemmArgs &a) {
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const unsigned gx = (unsigned)((a.N + 127) / 128);
+    switch (pick_shape(a.M, a.N, cu)) {
+        case T128x128:
+            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 2, 2>), dim3(gx, (a.M + 127) / 128), dim3(THREADS), 0,
+                               ctx->stream, a);
+            break;
+        case T128x64:
+            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 2, 1>), dim3(gx, (a.M + 63) / 64), dim3(THREADS), 0,
+                               ctx->stream, a);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 4, 1, 1, 1>), dim3(gx, (a.M + 31) / 32), dim3(THREADS), 0,
+                               ctx->stream, a);
+            break;
+    }
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+int launch_f32gemm(kh_ctx *ctx, const GemmArgs &a) {
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const unsigned gx = (unsigned)((a.N + 127) / 128);
+    switch (pick_shape(a.M, a.N, cu)) {
+        case T128x128:
+            hipLaunchKernelGGL((gemm_f32_kernel<2, 2, 2, 2>), dim3(gx, (a.M + 127) / 128), dim3(THREADS), 0,
+                               ctx->stream, a);
+            break;
+        case T128x64:
+            hipLaunchKernelGGL((gemm_f32_kernel<2, 2, 2, 1>), dim3(gx, (a.M + 63) / 64), dim3(THREADS), 0,
+                               ctx->stream, a);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm_f32_kernel<4, 1, 1, 1>), dim3(gx, (a.M + 31) / 32), dim3(THREADS), 0,
+                               ctx->stream, a);
+            break;
+    }
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+// Row-at-a-time path for shapes the tiled kernels do not take (f32 weights
+// whose width is not a multiple of 4): one GEMV job per activation row.
+int matmul_rows(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
+    std::vector<GemvJob> jobs(m);
     for (size_t i = 0; i < m; i++) {
         GemvJob &j = jobs[i];
         j = GemvJob{};
         j.w = w->qs;
-        j.ws = w->scales;
-        if (w->precision != KH_F32) {
-            j.xq = a.qs + i * cols;
-            j.xs = a.scales + i * (cols / BLOCK);
-            j.xsum = a.sums + i * (cols / BLOCK);
-        } else {
-            j.xf = xs + i * cols;
-        }
+        j.xf = xs + i * w->cols;
         j.bias = bias;
-        j.y = y + i * rows;
-        j.rows = (int)rows;
-        j.cols = (int)cols;
+        j.y = y + i * w->rows;
+        j.rows = (int)w->rows;
+        j.cols = (int)w->cols;
     }
     return launch_gemv(ctx, w->precision, jobs.data(), (int)m);
+}
+
+}  // namespace
+
+int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
+    const size_t rows = w->rows, cols = w->cols;
+    // 32-bit buffer offsets: the weights and activations (plus one tile of
+    // overhang) must stay below 4 GiB
+    const size_t wb = w->precision == KH_F32 ? 4 * rows * cols : rows * cols;
+    const size_t xb = w->precision == KH_F32 ? 4 * m * cols : m * cols;
+    if (wb + 4 * 128 * cols >= 0xffffffffull || xb + 4 * 128 * cols >= 0xffffffffull || rows > 0x7fffffff ||
+        m > 0x7fffffff)
+        return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
+    GemmArgs a{};
+    a.w = w->qs;
+    a.ws = w->scales;
+    a.bias = bias;
+    a.y = y;
+    a.M = (int)m;
+    a.N = (int)rows;
+    a.K = (int)cols;
+    if (w->precision == KH_F32) {
+        if (cols % 4) return matmul_rows(ctx, w, xs, m, bias, y);
+        a.xf = xs;
+        return launch_f32gemm(ctx, a);
+    }
+    // QActBatch::new (quant.rs:693-714): the activation rows quantised per block
+    const size_t qb = (m * cols + 255) / 256 * 256, sb = (4 * m * cols / BLOCK + 255) / 256 * 256;
+    int rc = ensure(ctx, ctx->ws, qb + 2 * sb);
+    if (rc) return rc;
+    char *p = static_cast<char *>(ctx->ws.ptr);
+    QAct q{reinterpret_cast<int8_t *>(p), reinterpret_cast<float *>(p + qb), reinterpret_cast<int32_t *>(p + qb + sb)};
+    if ((rc = launch_qact(ctx, xs, m, cols, q))) return rc;
+    a.xq = q.qs;
+    a.xs = q.scales;
+    a.xsum = q.sums;
+    switch (w->precision) {
+        case KH_Q8: return launch_i8<KH_Q8>(ctx, a);
+        case KH_Q4: return launch_i8<KH_Q4>(ctx, a);
+        case KH_Q4K: return launch_i8<KH_Q4K>(ctx, a);
+        default: return fail(KH_EINVAL, "matmul: unknown precision");
+    }
 }
 
 }  // namespace kh
