@@ -308,6 +308,8 @@ def secondary(torch, K, ctx, stream, dev, gen, args):
     log(f"q8 qwen: {out}")
     del g
 
+    out["prefill_gemm"] = prefill(torch, K, ctx, stream, dev, gen, args)
+
     spec = K.Spec(14, 2, 64)
     att = {}
     for L in (1024, 8192, 32768):
@@ -328,6 +330,39 @@ def secondary(torch, K, ctx, stream, dev, gen, args):
     out["attend_qwen05b"] = att
     log(f"attend: {att}")
     return out
+
+
+def prefill(torch, K, ctx, stream, dev, gen, args):
+    """batched-prefill GEMM, q8 (int8 MFMA) and f32
+    (f32 MFMA), at (M, K, N) = (512, 896, 4864) and (2048, 4096, 14336).
+    Each call is Weight::matmul_bt on device pointers: the activation
+    quantiser plus the GEMM, y[M, N] f32."""
+    res = {}
+    for (m, k, n) in ((512, 896, 4864), (2048, 4096, 14336)):
+        f = torch.randn(n, k, device=dev, generator=gen) * 0.02
+        xs = torch.randn(m, k, device=dev, generator=gen)
+        y = torch.empty(m, n, device=dev)
+        ops = 2 * m * n * k
+        for prec, code in (("q8", K.Q8), ("f32", K.F32)):
+            with torch.cuda.stream(stream):
+                w = K.Weight.quantize_dev(ctx, n, k, f.data_ptr(), code)
+            torch.cuda.synchronize()
+
+            def run():
+                for _ in range(4):
+                    w.matmul_bt_dev(xs.data_ptr(), m, y.data_ptr())
+
+            g = Graph(torch, ctx, stream, run)
+            s = g.time(max(3, args.steps // 10), 2) / 4
+            peak = 5000.0 if prec == "q8" else 157.3
+            tops = ops / s / 1e12
+            res[f"{prec}_{m}x{k}x{n}"] = {"us": round(s * 1e6, 2), "TOPS": round(tops, 2),
+                                          "frac_of_mfma_peak": round(tops / peak, 4),
+                                          "peak": f"{peak} T{'OP' if prec == 'q8' else 'FLOP'}/s"}
+            del g, w
+        del f, xs, y
+    log(f"prefill gemm: {res}")
+    return res
 
 
 def cpu_baseline(layers, budget_s: float):

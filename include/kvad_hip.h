@@ -88,6 +88,8 @@ int kh_weight_f32(kh_ctx *ctx, size_t rows, size_t cols, const float *data, kh_w
  * [rows, cols]: precision KH_Q8 or KH_Q4 as the reference quantises, KH_Q4K
  * with this library's packing of GGML's block (any valid packing; the GEMV
  * reads whatever bytes it is given).  Bit-identical to the CPU quantiser.
+ * KH_F32, and any width that does not divide into blocks, keeps the data as
+ * an f32 weight (quant.rs:211-213). 
  * `data` is a host pointer; the _dev form takes a device pointer. */
 int kh_weight_quantize(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision, kh_weight **out);
 int kh_weight_quantize_dev(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision,

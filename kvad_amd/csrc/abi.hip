@@ -292,10 +292,32 @@ static size_t qs_bytes_of(int precision, size_t rows, size_t cols) {
 static int quantize(kh_ctx *ctx, size_t rows, size_t cols, const float *data, int precision, bool host,
                     kh_weight **out) {
     if (!ctx || !out || !data) return fail(KH_EINVAL, "kh_weight_quantize: null argument");
-    if (precision != KH_Q8 && precision != KH_Q4 && precision != KH_Q4K)
-        return fail(KH_EINVAL, "kh_weight_quantize: precision must be KH_Q8, KH_Q4 or KH_Q4K");
-    if (shape_check(rows, cols, precision == KH_Q4K ? QK_K : BLOCK, "kh_weight_quantize")) return KH_EINVAL;
+    if (precision != KH_F32 && precision != KH_Q8 && precision != KH_Q4 && precision != KH_Q4K)
+        return fail(KH_EINVAL, "kh_weight_quantize: unknown precision");
+    if (shape_check(rows, cols, 1, "kh_weight_quantize")) return KH_EINVAL;
+    // A width that does not block stays f32, as Weight::quantize keeps it
+    // (quant.rs:211-213).
+    const size_t unit = precision == KH_Q4K ? QK_K : BLOCK;
+    if (cols % unit != 0 || cols < unit) precision = KH_F32;
     Guard g(ctx);
+    if (precision == KH_F32) {
+        std::unique_ptr<kh_weight> w(new kh_weight());
+        w->ctx = ctx;
+        w->precision = KH_F32;
+        w->rows = rows;
+        w->cols = cols;
+        w->bytes = 4 * rows * cols;
+        KH_HIP(hipMalloc(&w->qs, w->bytes));
+        hipError_t e = hipMemcpyAsync(w->qs, data, w->bytes, host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
+                                      ctx->stream);
+        if (e == hipSuccess && host) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(w->qs);
+            return hip_fail(e, "kh_weight_quantize: copy");
+        }
+        *out = w.release();
+        return KH_OK;
+    }
     std::unique_ptr<kh_weight> w(new kh_weight());
     w->ctx = ctx;
     w->precision = precision;

@@ -1,5 +1,6 @@
 // GQA decode attention over a device-resident KV cache, split along the
-// sequence, in one launch.
+// sequence: one launch computes per-split partial softmax sums, a second
+// merges them.
 //
 // Reference: model::attend (crates/llm/src/model/mod.rs:769-819) with
 // tensor::dot (tensor.rs:220-235) and softmax_inplace (tensor.rs:297-308).
@@ -8,31 +9,31 @@
 // and reads each key and value row once for the whole group -- the
 // restructuring the reference's notes ask for (docs/engine.md:783-791).
 //
-// Per workgroup (split j): all its K and V rows are loaded up front (16
-// lanes per row, 16 rows per pass); scores s = dot(q, k) * scale; local max
-// m_j, l_j = sum exp(s - m_j), acc_j = sum exp(s - m_j) v, and the smallest
-// score.  Splits are merged in two levels, each by the last workgroup to
-// arrive (an atomic counter per group, reset by that workgroup): chunks of
-// 16 splits, then the chunks.  A merge of parts (m_i, l_i, acc_i) is
-//   M = max m_i,  l = sum l_i exp(m_i - M),  acc = sum exp(m_i - M) acc_i,
-// and the output is acc * (1/S) with S the final l.
+// Split kernel, workgroup (split j, head group): all its K and V rows are
+// loaded up front (16 lanes per row, 16 rows per pass); scores s = dot(q, k)
+// * scale; local max m_j, l_j = sum exp(s - m_j), acc_j = sum exp(s - m_j) v,
+// and the smallest score.  When one split covers the whole sequence it
+// finishes the job itself with the reference's exact weights
+// w = exp(s - M) * (1/S), dropping w < 1e-8 (mod.rs:807).
 //
-// The reference skips weights w = exp(s - M) / S below 1e-8 (mod.rs:807).  A
-// split whose smallest score could fall under that threshold
-// (s < M + ln S + ln 1e-8, checked with a margin) has its positions scored
-// again by the final merger, and each skipped term w * v is taken back out.
-// Real scores never qualify (it takes a gap of about 18 + ln S), so the fast
-// path is the whole cost; the slow path keeps the reference's weights exact
-// when it does occur.  Every sum has a fixed order, so results are
-// deterministic run to run.
+// Merge kernel, one workgroup per query head:
+//   M = max m_j,  S = sum l_j exp(m_j - M),  acc = sum exp(m_j - M) acc_j,
+// and out = acc * (1/S).  The reference's skip of weights below 1e-8 can
+// only bite in a split whose smallest score is below M + ln S + ln 1e-8
+// (checked with a margin); such a split's positions are scored again,
+// identically, and each skipped term w * v is taken back out.  Real scores
+// never qualify (it takes a gap of about 18 + ln S), so the fast path is the
+// whole cost; the slow path keeps the reference's weights when it does occur.
+//
+// The two launches share nothing but the partials in device memory, so no
+// workgroup waits on another and no cross-XCD fence is needed.  Every sum has
+// a fixed order, so results are deterministic run to run.
 #include "common.hpp"
 
 namespace kh {
 namespace {
 
 constexpr unsigned RSRC_WORD3 = 0x00020000;
-constexpr int CH = 16;  // splits per first-level merge
-
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 __device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
@@ -87,19 +88,15 @@ struct AttnArgs {
     size_t kstride, vstride;  // floats between consecutive positions
     size_t kbytes, vbytes;    // readable bytes of the k and v arrays
     int n_head, group, gc;    // group = n_head / n_kv_head; gc = heads per workgroup
-    int L, P, nsplit, nchunk;
+    int L, P, nsplit;
     float scale;
     // per split, [nsplit][n_head]: local max, sum, smallest score; and acc
     float *pm, *pl, *pmin, *pacc;
-    // per chunk of CH splits, [nchunk][n_head] and [nchunk][n_head][hd]
-    float *cm, *cl, *cmin, *cacc;
-    unsigned *cnt_top;        // [n_head / gc]
-    unsigned *cnt_chunk;      // [n_head / gc][nchunk]
     float *out;               // [n_head][hd]
 };
 
-// The 16-lane row's scores of one position for the G heads: the same
-// arithmetic in the main pass and in the skip correction.
+// One position's scores for the G heads from the 16-lane row's slices: the
+// same arithmetic wherever a score is needed.
 template <int GM, int DPL>
 __device__ __forceinline__ void score_row(const float (&qr)[GM][DPL], const float (&kv)[DPL], float scale, int G,
                                           float (&s)[GM]) {
@@ -115,59 +112,17 @@ __device__ __forceinline__ void score_row(const float (&qr)[GM][DPL], const floa
     }
 }
 
-// Merges parts [first, first + np) of the head group's G heads into
-// dst (m, l, min, acc at index `slot`).  Run by a whole workgroup.
-template <int GM, int HD>
-__device__ void merge_parts(const float *pm, const float *pl, const float *pmin, const float *pacc, int first,
-                            int np, int n_head, int h0, int G, float *dm, float *dl, float *dmin, float *dacc,
-                            int slot, float (*s_w)[CH]) {
-    const int tid = threadIdx.x;
-    // per head: max, then the weights exp(m_i - M), sum and min
-    if (tid < G) {
-        const int h = tid;
-        float m[CH], l[CH], mn[CH];
+template <int DPL>
+__device__ __forceinline__ void load_row(const rsrc_t &R, unsigned off, float (&r)[DPL]) {
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const size_t o = (size_t)(first + (i < np ? i : 0)) * n_head + h0 + h;
-            m[i] = i < np ? pm[o] : -INFINITY;
-            l[i] = i < np ? pl[o] : 0.0f;
-            mn[i] = i < np ? pmin[o] : INFINITY;
-        }
-        float M = -INFINITY, lo = INFINITY;
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            M = fmaxf(M, m[i]);
-            lo = fminf(lo, mn[i]);
-        }
-        float sum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const float w = i < np ? expf(m[i] - M) : 0.0f;
-            s_w[h][i] = w;
-            sum = fmaf(l[i], w, sum);
-        }
-        const size_t od = (size_t)slot * n_head + h0 + h;
-        dm[od] = M;
-        dl[od] = sum;
-        dmin[od] = lo;
-    }
-    __syncthreads();
-    for (int i = tid; i < G * HD; i += 256) {
-        const int h = i / HD, d = i % HD;
-        float c[CH];
-#pragma unroll
-        for (int k = 0; k < CH; k++)
-            c[k] = k < np ? pacc[((size_t)(first + k) * n_head + h0 + h) * HD + d] : 0.0f;
-        float x = 0.0f;
-#pragma unroll
-        for (int k = 0; k < CH; k++)
-            if (k < np) x = fmaf(s_w[h][k], c[k], x);
-        dacc[((size_t)slot * n_head + h0 + h) * HD + d] = x;
+    for (int d = 0; d < DPL; d += 4) {
+        const float4 f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(R, off, d * 4, 0));
+        r[d] = f.x, r[d + 1] = f.y, r[d + 2] = f.z, r[d + 3] = f.w;
     }
 }
 
 template <int HD, int GM, int NP>  // NP: passes of 16 positions; P = 16 * NP
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;  // dims per lane
     constexpr int P = 16 * NP;
     const int split = blockIdx.x, hg = blockIdx.y;
@@ -177,27 +132,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int sub = lane & 15, pg = tid >> 4;  // dim slice, position within a pass
     const int t0 = split * P;
     const int n = min(a.L - t0, P);
+    const bool whole = a.nsplit == 1;
     const rsrc_t K = rsrc(a.k, a.kbytes), V = rsrc(a.v, a.vbytes);
 
-    __shared__ float s_p[GM][P];          // scores, then exp(s - m)
-    __shared__ float s_red[4][GM][HD];    // per-wave partial acc; merge output
-    __shared__ float s_w[GM][CH];
-    __shared__ int s_flag;
+    __shared__ float s_p[GM][P];          // scores, then exp(s - m) (or final weights)
+    __shared__ float s_red[4][GM][HD];    // per-wave partial acc
 
     // every K and V row of the split in flight at once
     float kr[NP][DPL], vr[NP][DPL];
 #pragma unroll
     for (int u = 0; u < NP; u++) {
-        const int t = t0 + u * 16 + pg;
-        const unsigned ko = (unsigned)(((size_t)t * a.kstride + (size_t)kvh * HD + sub * DPL) * 4);
-        const unsigned vo = (unsigned)(((size_t)t * a.vstride + (size_t)kvh * HD + sub * DPL) * 4);
-#pragma unroll
-        for (int d = 0; d < DPL; d += 4) {
-            float4 f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(K, ko, d * 4, 0));
-            kr[u][d] = f.x, kr[u][d + 1] = f.y, kr[u][d + 2] = f.z, kr[u][d + 3] = f.w;
-            f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(V, vo, d * 4, 0));
-            vr[u][d] = f.x, vr[u][d + 1] = f.y, vr[u][d + 2] = f.z, vr[u][d + 3] = f.w;
-        }
+        const size_t t = (size_t)(t0 + u * 16 + pg);
+        load_row<DPL>(K, (unsigned)((t * a.kstride + (size_t)kvh * HD + sub * DPL) * 4), kr[u]);
+        load_row<DPL>(V, (unsigned)((t * a.vstride + (size_t)kvh * HD + sub * DPL) * 4), vr[u]);
     }
     float qr[GM][DPL];
 #pragma unroll
@@ -217,7 +164,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // local softmax statistics; weights exp(s - m) in place
+    // local softmax statistics (softmax_inplace, tensor.rs:297-308); exp(s - m)
+    // in place, or, for a whole sequence, the final weights
     for (int h = wave; h < G; h += 4) {
         float mx = -INFINITY, mn = INFINITY;
         for (int i = lane; i < n; i += 64) {
@@ -233,7 +181,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             l += e;
         }
         l = wave_sum(l);
-        if (lane == 0) {
+        if (whole) {
+            const float inv = 1.0f / l;
+            for (int i = lane; i < P; i += 64) {
+                const float w = s_p[h][i] * inv;
+                s_p[h][i] = w < 1e-8f ? 0.0f : w;  // mod.rs:807
+            }
+        } else if (lane == 0) {
             const size_t o = (size_t)split * a.n_head + h0 + h;
             a.pm[o] = mx;
             a.pl[o] = l;
@@ -242,7 +196,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // acc[h][:] = sum_t exp(s_t - m) v_t over this lane's positions
+    // acc[h][:] = sum_t p_t v_t over this lane's positions
     float acc[GM][DPL];
 #pragma unroll
     for (int h = 0; h < GM; h++)
@@ -278,177 +232,135 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 for (int d = 0; d < DPL; d++) s_red[wave][h][sub * DPL + d] = acc[h][d];
     }
     __syncthreads();
+    float *dst = whole ? a.out + (size_t)h0 * HD : a.pacc + ((size_t)split * a.n_head + h0) * HD;
     for (int i = tid; i < G * HD; i += 256) {
         const int h = i / HD, d = i % HD;
         float x = s_red[0][h][d];
         x += s_red[1][h][d];
         x += s_red[2][h][d];
         x += s_red[3][h][d];
-        a.pacc[((size_t)split * a.n_head + h0 + h) * HD + d] = x;
+        dst[(size_t)h * HD + d] = x;
     }
+}
 
-    // ---- first level: the last split of a chunk merges the chunk -----------
-    const int chunk = split / CH, cfirst = chunk * CH, cn = min(CH, a.nsplit - cfirst);
-    __threadfence();
+// Fixed-order tree over the 256 threads' values; every thread gets the result.
+template <typename F>
+__device__ __forceinline__ float block_reduce(float v, float *s_red, F op) {
+    const int tid = threadIdx.x;
+    s_red[tid] = v;
     __syncthreads();
-    if (tid == 0) {
-        unsigned *c = &a.cnt_chunk[(size_t)hg * a.nchunk + chunk];
-        const unsigned prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_flag = prev == (unsigned)(cn - 1);
-        if (s_flag) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!s_flag) return;
-    __threadfence();
-    // a single chunk is the whole sequence: its merger is the final one
-    const float *fm = a.pm, *fl = a.pl, *fmin = a.pmin, *facc = a.pacc;
-    int nparts = a.nsplit;
-    if (a.nchunk > 1) {
-        merge_parts<GM, HD>(a.pm, a.pl, a.pmin, a.pacc, cfirst, cn, a.n_head, h0, G, a.cm, a.cl, a.cmin, a.cacc,
-                            chunk, s_w);
-        // ---- second level: the last chunk merges the chunks ----------------
-        __threadfence();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) s_red[tid] = op(s_red[tid], s_red[tid + w]);
         __syncthreads();
-        if (tid == 0) {
-            const unsigned prev =
-                __hip_atomic_fetch_add(&a.cnt_top[hg], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_flag = prev == (unsigned)(a.nchunk - 1);
-            if (s_flag) __hip_atomic_store(&a.cnt_top[hg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const float r = s_red[0];
+    __syncthreads();
+    return r;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+    constexpr int DPL = HD / 16, NG = 256 / HD;  // dim groups of the acc merge
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int ns = a.nsplit, n_head = a.n_head;
+    __shared__ float s_red[256];
+    __shared__ float s_acc[NG][HD];
+    __shared__ float s_fix[16][HD];
+    __shared__ int s_need;
+
+    // M and the smallest score over the splits
+    float mx = -INFINITY, lo = INFINITY;
+    for (int i = tid; i < ns; i += 256) {
+        mx = fmaxf(mx, a.pm[(size_t)i * n_head + h]);
+        lo = fminf(lo, a.pmin[(size_t)i * n_head + h]);
+    }
+    const float M = block_reduce(mx, s_red, [](float x, float y) { return fmaxf(x, y); });
+    lo = block_reduce(lo, s_red, [](float x, float y) { return fminf(x, y); });
+
+    // S = sum l_j exp(m_j - M)
+    float s = 0.0f;
+    for (int i = tid; i < ns; i += 256) {
+        const size_t o = (size_t)i * n_head + h;
+        s = fmaf(a.pl[o], expf(a.pm[o] - M), s);
+    }
+    const float S = block_reduce(s, s_red, [](float x, float y) { return x + y; });
+    const float inv = 1.0f / S;  // inv = 1 / sum, tensor.rs:304
+
+    // acc[d] = sum_j exp(m_j - M) acc_j[d]
+    {
+        const int g = tid / HD, d = tid % HD;
+        float x = 0.0f;
+        for (int i = g; i < ns; i += NG) {
+            const size_t o = (size_t)i * n_head + h;
+            x = fmaf(expf(a.pm[o] - M), a.pacc[o * HD + d], x);
         }
-        __syncthreads();
-        if (!s_flag) return;
-        __threadfence();
-        fm = a.cm, fl = a.cl, fmin = a.cmin, facc = a.cacc;
-        nparts = a.nchunk;
+        s_acc[g][d] = x;
     }
-    // the parts merged CH at a time, in order, into running (M, S, acc)
-    __shared__ float s_M[GM], s_S[GM], s_min[GM], s_alpha[GM], s_inv[GM];
-    if (tid < G) {
-        s_M[tid] = -INFINITY;
-        s_S[tid] = 0.0f;
-        s_min[tid] = INFINITY;
-    }
-    for (int i = tid; i < G * HD; i += 256) s_red[0][i / HD][i % HD] = 0.0f;
     __syncthreads();
-    for (int first = 0; first < nparts; first += CH) {
-        const int np = min(CH, nparts - first);
-        if (tid < G) {
-            const int h = tid;
-            float m[CH], l[CH], mn[CH];
-#pragma unroll
-            for (int i = 0; i < CH; i++) {
-                const size_t o = (size_t)(first + (i < np ? i : 0)) * a.n_head + h0 + h;
-                m[i] = i < np ? fm[o] : -INFINITY;
-                l[i] = i < np ? fl[o] : 0.0f;
-                mn[i] = i < np ? fmin[o] : INFINITY;
-            }
-            float M = s_M[h], lo = s_min[h];
-#pragma unroll
-            for (int i = 0; i < CH; i++) {
-                M = fmaxf(M, m[i]);
-                lo = fminf(lo, mn[i]);
-            }
-            const float alpha = s_M[h] == -INFINITY ? 0.0f : expf(s_M[h] - M);  // rescales the running sum
-            float sum = s_S[h] * alpha;
-#pragma unroll
-            for (int i = 0; i < CH; i++) {
-                const float w = i < np ? expf(m[i] - M) : 0.0f;
-                s_w[h][i] = w;
-                sum = fmaf(l[i], w, sum);
-            }
-            s_alpha[h] = alpha;
-            s_M[h] = M;
-            s_S[h] = sum;
-            s_min[h] = lo;
-        }
-        __syncthreads();
-        for (int i = tid; i < G * HD; i += 256) {
-            const int h = i / HD, d = i % HD;
-            float c[CH];
-#pragma unroll
-            for (int k = 0; k < CH; k++)
-                c[k] = k < np ? facc[((size_t)(first + k) * a.n_head + h0 + h) * HD + d] : 0.0f;
-            float x = s_red[0][h][d] * s_alpha[h];
-#pragma unroll
-            for (int k = 0; k < CH; k++)
-                if (k < np) x = fmaf(s_w[h][k], c[k], x);
-            s_red[0][h][d] = x;
-        }
-        __syncthreads();
-    }
-    if (tid < G) s_inv[tid] = 1.0f / s_S[tid];  // inv = 1 / sum, tensor.rs:304
-    __syncthreads();
-    for (int i = tid; i < G * HD; i += 256) s_red[0][i / HD][i % HD] *= s_inv[i / HD];
 
     // ---- skip correction: w = exp(s - M) * (1/S) < 1e-8 ---------------------
     // possible only where a score is below M + ln S + ln 1e-8 (with a margin)
-    if (tid == 0) {
-        int need = 0;
-        for (int h = 0; h < G; h++) need |= s_min[h] < s_M[h] + logf(s_S[h]) - 18.420681f + 1.0f;
-        s_flag = need;
-    }
-    __syncthreads();
-    if (s_flag) {
-        for (int j = 0; j < a.nsplit; j++) {
-            if (tid == 0) {
-                int need = 0;
-                for (int h = 0; h < G; h++)
-                    need |= a.pmin[(size_t)j * a.n_head + h0 + h] < s_M[h] + logf(s_S[h]) - 18.420681f + 1.0f;
-                s_flag = need;
-            }
+    const float thr = M + logf(S) - 18.420681f + 1.0f;
+    if (lo < thr) {
+        const int group16 = tid >> 4, sub = tid & 15, kvh = h / a.group;
+        const rsrc_t K = rsrc(a.k, a.kbytes), V = rsrc(a.v, a.vbytes);
+        float qr[1][DPL];
+#pragma unroll
+        for (int d = 0; d < DPL; d++) qr[0][d] = a.q[(size_t)h * HD + sub * DPL + d];
+        float fix[DPL];
+#pragma unroll
+        for (int d = 0; d < DPL; d++) fix[d] = 0.0f;
+        for (int j = 0; j < ns; j++) {
+            if (tid == 0) s_need = a.pmin[(size_t)j * n_head + h] < thr;
             __syncthreads();
-            if (!s_flag) continue;
-            const int tj = j * P, nj = min(a.L - tj, P);
+            const int need = s_need;
+            __syncthreads();
+            if (!need) continue;
+            const int tj = j * a.P, nj = min(a.L - tj, a.P);
             for (int base = 0; base < nj; base += 16) {
-                const int t = tj + base + pg;
-                const bool ok = base + pg < nj;
+                const int t = tj + base + group16;
+                if (base + group16 >= nj) continue;  // whole 16-lane rows drop out together
                 float kv[DPL], vv[DPL];
-                const unsigned ko = (unsigned)(((size_t)(ok ? t : tj) * a.kstride + (size_t)kvh * HD + sub * DPL) * 4);
-                const unsigned vo = (unsigned)(((size_t)(ok ? t : tj) * a.vstride + (size_t)kvh * HD + sub * DPL) * 4);
+                load_row<DPL>(K, (unsigned)(((size_t)t * a.kstride + (size_t)kvh * HD + sub * DPL) * 4), kv);
+                load_row<DPL>(V, (unsigned)(((size_t)t * a.vstride + (size_t)kvh * HD + sub * DPL) * 4), vv);
+                float sc[1];
+                score_row<1, DPL>(qr, kv, a.scale, 1, sc);
+                float w = expf(sc[0] - M);
+                w = w * inv;
+                if (w < 1e-8f) {
 #pragma unroll
-                for (int d = 0; d < DPL; d += 4) {
-                    float4 f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(K, ko, d * 4, 0));
-                    kv[d] = f.x, kv[d + 1] = f.y, kv[d + 2] = f.z, kv[d + 3] = f.w;
-                    f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(V, vo, d * 4, 0));
-                    vv[d] = f.x, vv[d + 1] = f.y, vv[d + 2] = f.z, vv[d + 3] = f.w;
-                }
-                float s[GM];
-                score_row<GM, DPL>(qr, kv, a.scale, G, s);
-                // positions taken out one at a time, in order
-                for (int r = 0; r < 16; r++) {
-                    if (pg == r && ok) {
-#pragma unroll
-                        for (int h = 0; h < GM; h++) {
-                            if (h < G) {
-                                float w = expf(s[h] - s_M[h]);
-                                w = w * s_inv[h];
-                                if (w < 1e-8f) {
-#pragma unroll
-                                    for (int d = 0; d < DPL; d++) s_red[0][h][sub * DPL + d] -= w * vv[d];
-                                }
-                            }
-                        }
-                    }
-                    __syncthreads();
+                    for (int d = 0; d < DPL; d++) fix[d] = fmaf(w, vv[d], fix[d]);
                 }
             }
         }
+#pragma unroll
+        for (int d = 0; d < DPL; d++) s_fix[group16][sub * DPL + d] = fix[d];
+        __syncthreads();
+        if (tid < HD) {
+            float f = 0.0f;
+            for (int g = 0; g < 16; g++) f += s_fix[g][tid];
+            s_fix[0][tid] = f;
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    for (int i = tid; i < G * HD; i += 256) {
-        const int h = i / HD, d = i % HD;
-        a.out[(size_t)(h0 + h) * HD + d] = s_red[0][h][d];
+    if (tid < HD) {
+        float x = s_acc[0][tid];
+#pragma unroll
+        for (int g = 1; g < NG; g++) x += s_acc[g][tid];
+        x = x * inv;
+        if (lo < thr) x -= s_fix[0][tid];
+        a.out[(size_t)h * HD + tid] = x;
     }
 }
 
 template <int HD, int GM>
-void launch_g(const AttnArgs &a, dim3 grid, hipStream_t stream) {
+void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
     switch (a.P / 16) {
-        case 1: hipLaunchKernelGGL((attn_kernel<HD, GM, 1>), grid, dim3(256), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((attn_kernel<HD, GM, 2>), grid, dim3(256), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((attn_kernel<HD, GM, 4>), grid, dim3(256), 0, stream, a); break;
-        case 8: hipLaunchKernelGGL((attn_kernel<HD, GM, 8>), grid, dim3(256), 0, stream, a); break;
-        default: hipLaunchKernelGGL((attn_kernel<HD, GM, (HD == 64 ? 16 : 8)>), grid, dim3(256), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 1>), grid, dim3(256), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 2>), grid, dim3(256), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 4>), grid, dim3(256), 0, stream, a); break;
+        case 8: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 8>), grid, dim3(256), 0, stream, a); break;
+        default: hipLaunchKernelGGL((attn_split_kernel<HD, GM, (HD == 64 ? 16 : 8)>), grid, dim3(256), 0, stream, a); break;
     }
 }
 
@@ -461,7 +373,8 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     if (head_dim != 64 && head_dim != 128)
         return fail(KH_DECLINED, "attend: head_dim other than 64 or 128 runs on the CPU");
     if (n_positions == 0) return launch_fill(ctx, out, (size_t)n_head * head_dim, 0.0f);
-    if ((n_positions * kstride + 4096) * 4 >= 0xffffffffull || (n_positions * vstride + 4096) * 4 >= 0xffffffffull)
+    // 32-bit buffer offsets, including a split's overhang past the last row
+    if ((n_positions + 256) * kstride * 4 >= 0xffffffffull || (n_positions + 256) * vstride * 4 >= 0xffffffffull)
         return fail(KH_DECLINED, "attend: caches of 4 GiB or more per layer are not addressed here");
 
     AttnArgs a{};
@@ -489,38 +402,37 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     while (P < pmax && (long long)((n_positions + P - 1) / P) * n_hg > cu) P *= 2;
     a.P = P;
     a.nsplit = (int)((n_positions + P - 1) / P);
-    a.nchunk = (a.nsplit + CH - 1) / CH;
     a.scale = 1.0f / sqrtf((float)head_dim);  // mod.rs:777
     a.out = out;
 
-    const size_t ns = (size_t)a.nsplit * n_head, nc = (size_t)a.nchunk * n_head;
-    const size_t bytes = 4 * (3 * ns + ns * head_dim + 3 * nc + nc * head_dim) + 1024;
-    int rc = ensure(ctx, ctx->ws, bytes);
-    if (rc) return rc;
-    float *p = static_cast<float *>(ctx->ws.ptr);
-    a.pm = p, p += ns;
-    a.pl = p, p += ns;
-    a.pmin = p, p += ns;
-    a.pacc = p, p += ns * head_dim;
-    a.cm = p, p += nc;
-    a.cl = p, p += nc;
-    a.cmin = p, p += nc;
-    a.cacc = p;
-    const size_t ncounters = (size_t)n_hg * (1 + a.nchunk);
-    if (ncounters * sizeof(unsigned) > ctx->counters.bytes)
-        return fail(KH_DECLINED, "attend: sequence too long for the counter block");
-    a.cnt_top = static_cast<unsigned *>(ctx->counters.ptr);
-    a.cnt_chunk = a.cnt_top + n_hg;
+    if (a.nsplit > 1) {
+        const size_t ns = (size_t)a.nsplit * n_head;
+        const size_t bytes = 4 * (3 * ns + ns * head_dim) + 1024;
+        int rc = ensure(ctx, ctx->ws, bytes);
+        if (rc) return rc;
+        float *p = static_cast<float *>(ctx->ws.ptr);
+        a.pm = p, p += ns;
+        a.pl = p, p += ns;
+        a.pmin = p, p += ns;
+        a.pacc = p;
+    }
 
     dim3 grid(a.nsplit, n_hg);
     if (head_dim == 64) {
-        if (gc <= 4) launch_g<64, 4>(a, grid, ctx->stream);
-        else launch_g<64, 8>(a, grid, ctx->stream);
+        if (gc <= 4) launch_split<64, 4>(a, grid, ctx->stream);
+        else launch_split<64, 8>(a, grid, ctx->stream);
     } else {
-        if (gc <= 4) launch_g<128, 4>(a, grid, ctx->stream);
-        else launch_g<128, 8>(a, grid, ctx->stream);
+        if (gc <= 4) launch_split<128, 4>(a, grid, ctx->stream);
+        else launch_split<128, 8>(a, grid, ctx->stream);
     }
     KH_HIP(hipGetLastError());
+    if (a.nsplit > 1) {
+        if (head_dim == 64)
+            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(n_head), dim3(256), 0, ctx->stream, a);
+        else
+            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(n_head), dim3(256), 0, ctx->stream, a);
+        KH_HIP(hipGetLastError());
+    }
     return KH_OK;
 }
 
