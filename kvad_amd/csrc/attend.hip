@@ -121,125 +121,219 @@ __device__ __forceinline__ void load_row(const rsrc_t &R, unsigned off, float (&
     }
 }
 
-template <int HD, int GM, int NP>  // NP: passes of 16 positions; P = 16 * NP
+// Sums (or maxima) over the wave's four rows of 16 lanes, by swapping
+// rows (v_permlane16_swap) and then halves (v_permlane32_swap) between two
+// copies of a value; every lane gets the total, in a fixed order.  Written
+// as inline assembly: the compiler folds the builtins' two results into one
+// when both inputs are the same value.
+__device__ __forceinline__ void swap16(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+template <typename F>
+__device__ __forceinline__ float rows_reduce(float x, F op) {
+    float a = x, b = x;
+    swap16(a, b);
+    x = op(a, b);
+    a = x, b = x;
+    swap32(a, b);
+    return op(a, b);
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    return rows_reduce(x, [](float u, float v) { return u + v; });
+}
+__device__ __forceinline__ float rows_max(float x) {
+    return rows_reduce(x, [](float u, float v) { return fmaxf(u, v); });
+}
+__device__ __forceinline__ float rows_min(float x) {
+    return rows_reduce(x, [](float u, float v) { return fminf(u, v); });
+}
+
+// Split kernel.  Lanes form 16-lane rows (16 per workgroup); row r takes
+// positions r, r + 16, ... of the split, lane `sub` of a row dims
+// [sub*DPL, sub*DPL + DPL).  Each wave reduces its four rows with lane swaps
+// against the wave's own maximum, and the four waves meet once in LDS.
+template <int HD, int G, int NP>  // G heads per workgroup; P = 16 * NP positions
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;  // dims per lane
     constexpr int P = 16 * NP;
     const int split = blockIdx.x, hg = blockIdx.y;
-    const int h0 = hg * a.gc, kvh = h0 / a.group, G = a.gc;
+    const int h0 = hg * G, kvh = h0 / a.group;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sub = lane & 15, pg = tid >> 4;  // dim slice, position within a pass
+    const int sub = lane & 15, row = tid >> 4;
     const int t0 = split * P;
     const int n = min(a.L - t0, P);
     const bool whole = a.nsplit == 1;
     const rsrc_t K = rsrc(a.k, a.kbytes), V = rsrc(a.v, a.vbytes);
 
-    __shared__ float s_p[GM][P];          // scores, then exp(s - m) (or final weights)
-    __shared__ float s_red[4][GM][HD];    // per-wave partial acc
+    __shared__ float s_acc[4][G][HD];  // per-wave totals
+    __shared__ float s_st[3][4][G];    // per-wave max, sum, smallest score
 
     // every K and V row of the split in flight at once
     float kr[NP][DPL], vr[NP][DPL];
 #pragma unroll
     for (int u = 0; u < NP; u++) {
-        const size_t t = (size_t)(t0 + u * 16 + pg);
+        const size_t t = (size_t)(t0 + u * 16 + row);
         load_row<DPL>(K, (unsigned)((t * a.kstride + (size_t)kvh * HD + sub * DPL) * 4), kr[u]);
         load_row<DPL>(V, (unsigned)((t * a.vstride + (size_t)kvh * HD + sub * DPL) * 4), vr[u]);
     }
-    float qr[GM][DPL];
+    float qr[G][DPL];
 #pragma unroll
-    for (int h = 0; h < GM; h++)
+    for (int h = 0; h < G; h++)
 #pragma unroll
-        for (int d = 0; d < DPL; d++) qr[h][d] = h < G ? a.q[(size_t)(h0 + h) * HD + sub * DPL + d] : 0.0f;
+        for (int d = 0; d < DPL; d += 4) {
+            const float4 f = *reinterpret_cast<const float4 *>(a.q + (size_t)(h0 + h) * HD + sub * DPL + d);
+            qr[h][d] = f.x, qr[h][d + 1] = f.y, qr[h][d + 2] = f.z, qr[h][d + 3] = f.w;
+        }
 
-    // scores
+    // scores (the same in all 16 lanes of a row), the row's extremes
+    float s[NP][G], mx[G], mn[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) mx[h] = -INFINITY, mn[h] = INFINITY;
 #pragma unroll
     for (int u = 0; u < NP; u++) {
-        float s[GM];
-        score_row<GM, DPL>(qr, kr[u], a.scale, G, s);
-        const int tt = u * 16 + pg;
+        score_row<G, DPL>(qr, kr[u], a.scale, G, s[u]);
+        const bool ok = u * 16 + row < n;
 #pragma unroll
-        for (int h = 0; h < GM; h++)
-            if (sub == h && h < G) s_p[h][tt] = tt < n ? s[h] : -INFINITY;
+        for (int h = 0; h < G; h++) {
+            s[u][h] = ok ? s[u][h] : -INFINITY;
+            mx[h] = fmaxf(mx[h], s[u][h]);
+            mn[h] = ok ? fminf(mn[h], s[u][h]) : mn[h];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        mx[h] = rows_max(mx[h]);
+        mn[h] = rows_min(mn[h]);
+    }
+
+    // exp(s - m) against the wave's max; the wave's sum and weighted values
+    float l[G], acc[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        l[h] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DPL; d++) acc[h][d] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < NP; u++)
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float e = s[u][h] == -INFINITY ? 0.0f : expf(s[u][h] - mx[h]);
+            l[h] += e;
+#pragma unroll
+            for (int d = 0; d < DPL; d++) acc[h][d] = fmaf(e, vr[u][d], acc[h][d]);
+        }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        l[h] = rows_sum(l[h]);
+#pragma unroll
+        for (int d = 0; d < DPL; d++) acc[h][d] = rows_sum(acc[h][d]);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int d = 0; d < DPL; d++) s_acc[wave][h][sub * DPL + d] = acc[h][d];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            s_st[0][wave][h] = mx[h];
+            s_st[1][wave][h] = l[h];
+            s_st[2][wave][h] = mn[h];
+        }
     }
     __syncthreads();
 
-    // local softmax statistics (softmax_inplace, tensor.rs:297-308); exp(s - m)
-    // in place, or, for a whole sequence, the final weights
-    for (int h = wave; h < G; h += 4) {
-        float mx = -INFINITY, mn = INFINITY;
-        for (int i = lane; i < n; i += 64) {
-            mx = fmaxf(mx, s_p[h][i]);
-            mn = fminf(mn, s_p[h][i]);
-        }
-        mx = wave_max(mx);
-        mn = wave_min(mn);
-        float l = 0.0f;
-        for (int i = lane; i < P; i += 64) {
-            const float e = i < n ? expf(s_p[h][i] - mx) : 0.0f;
-            s_p[h][i] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (whole) {
-            const float inv = 1.0f / l;
-            for (int i = lane; i < P; i += 64) {
-                const float w = s_p[h][i] * inv;
-                s_p[h][i] = w < 1e-8f ? 0.0f : w;  // mod.rs:807
+    if (!whole) {
+        // the split's statistics: M over the waves, each wave rescaled to it
+        for (int i = tid; i < G * HD; i += 256) {
+            const int h = i / HD, d = i % HD;
+            const float M = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
+            float x = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float c = s_st[0][w][h] == -INFINITY ? 0.0f : expf(s_st[0][w][h] - M);
+                x = fmaf(c, s_acc[w][h][d], x);
             }
-        } else if (lane == 0) {
-            const size_t o = (size_t)split * a.n_head + h0 + h;
-            a.pm[o] = mx;
-            a.pl[o] = l;
-            a.pmin[o] = mn;
+            a.pacc[((size_t)split * a.n_head + h0 + h) * HD + d] = x;
         }
+        if (tid < G) {
+            const int h = tid;
+            const float M = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
+            float L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float c = s_st[0][w][h] == -INFINITY ? 0.0f : expf(s_st[0][w][h] - M);
+                L = fmaf(c, s_st[1][w][h], L);
+            }
+            const size_t o = (size_t)split * a.n_head + h0 + h;
+            a.pm[o] = M;
+            a.pl[o] = L;
+            a.pmin[o] = fminf(fminf(s_st[2][0][h], s_st[2][1][h]), fminf(s_st[2][2][h], s_st[2][3][h]));
+        }
+        return;
+    }
+
+    // One split is the whole sequence: the reference's own weights
+    // w = exp(s - M) * (1/S), S = sum exp(s - M), dropping w < 1e-8
+    // (softmax_inplace, tensor.rs:297-308; mod.rs:805-812).
+    float M[G];
+#pragma unroll
+    for (int h = 0; h < G; h++)
+        M[h] = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
+    float e[NP][G];
+#pragma unroll
+    for (int h = 0; h < G; h++) l[h] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NP; u++)
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            e[u][h] = s[u][h] == -INFINITY ? 0.0f : expf(s[u][h] - M[h]);
+            l[h] += e[u][h];
+        }
+#pragma unroll
+    for (int h = 0; h < G; h++) l[h] = rows_sum(l[h]);
+    __syncthreads();  // everyone has read s_st
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < G; h++) s_st[1][wave][h] = l[h];
     }
     __syncthreads();
-
-    // acc[h][:] = sum_t p_t v_t over this lane's positions
-    float acc[GM][DPL];
+    float inv[G];
 #pragma unroll
-    for (int h = 0; h < GM; h++)
+    for (int h = 0; h < G; h++) inv[h] = 1.0f / (((s_st[1][0][h] + s_st[1][1][h]) + s_st[1][2][h]) + s_st[1][3][h]);
+#pragma unroll
+    for (int h = 0; h < G; h++)
 #pragma unroll
         for (int d = 0; d < DPL; d++) acc[h][d] = 0.0f;
 #pragma unroll
-    for (int u = 0; u < NP; u++) {
-        const int tt = u * 16 + pg;
+    for (int u = 0; u < NP; u++)
 #pragma unroll
-        for (int h = 0; h < GM; h++) {
-            if (h < G) {
-                const float p = s_p[h][tt];
+        for (int h = 0; h < G; h++) {
+            float w = e[u][h] * inv[h];
+            w = w < 1e-8f ? 0.0f : w;
 #pragma unroll
-                for (int d = 0; d < DPL; d++) acc[h][d] = fmaf(p, vr[u][d], acc[h][d]);
-            }
+            for (int d = 0; d < DPL; d++) acc[h][d] = fmaf(w, vr[u][d], acc[h][d]);
         }
-    }
-    // the wave's four rows (lanes 16 and 32 apart), then the four waves
 #pragma unroll
-    for (int h = 0; h < GM; h++)
+    for (int h = 0; h < G; h++)
 #pragma unroll
-        for (int d = 0; d < DPL; d++) {
-            float x = acc[h][d];
-            x += __shfl_xor(x, 16);
-            x += __shfl_xor(x, 32);
-            acc[h][d] = x;
-        }
+        for (int d = 0; d < DPL; d++) acc[h][d] = rows_sum(acc[h][d]);
     if (lane < 16) {
 #pragma unroll
-        for (int h = 0; h < GM; h++)
-            if (h < G)
+        for (int h = 0; h < G; h++)
 #pragma unroll
-                for (int d = 0; d < DPL; d++) s_red[wave][h][sub * DPL + d] = acc[h][d];
+            for (int d = 0; d < DPL; d++) s_acc[wave][h][sub * DPL + d] = acc[h][d];
     }
     __syncthreads();
-    float *dst = whole ? a.out + (size_t)h0 * HD : a.pacc + ((size_t)split * a.n_head + h0) * HD;
     for (int i = tid; i < G * HD; i += 256) {
         const int h = i / HD, d = i % HD;
-        float x = s_red[0][h][d];
-        x += s_red[1][h][d];
-        x += s_red[2][h][d];
-        x += s_red[3][h][d];
-        dst[(size_t)h * HD + d] = x;
+        a.out[(size_t)(h0 + h) * HD + d] = ((s_acc[0][h][d] + s_acc[1][h][d]) + s_acc[2][h][d]) + s_acc[3][h][d];
     }
 }
 
@@ -258,17 +352,21 @@ __device__ __forceinline__ float block_reduce(float v, float *s_red, F op) {
     return r;
 }
 
+constexpr int MAX_SPLITS = 4096;
+
 template <int HD>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
-    constexpr int DPL = HD / 16, NG = 256 / HD;  // dim groups of the acc merge
+    constexpr int DPL = HD / 16;
+    constexpr int NQ = HD / 4, NSG = 256 / NQ;  // float4 slices of a row; split groups
     const int h = blockIdx.x, tid = threadIdx.x;
     const int ns = a.nsplit, n_head = a.n_head;
     __shared__ float s_red[256];
-    __shared__ float s_acc[NG][HD];
+    __shared__ float s_c[MAX_SPLITS];           // exp(m_j - M)
+    __shared__ __align__(16) float s_acc[NSG][HD];
     __shared__ float s_fix[16][HD];
     __shared__ int s_need;
 
-    // M and the smallest score over the splits
+    // the splits' statistics, all loads in flight together
     float mx = -INFINITY, lo = INFINITY;
     for (int i = tid; i < ns; i += 256) {
         mx = fmaxf(mx, a.pm[(size_t)i * n_head + h]);
@@ -277,24 +375,42 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     const float M = block_reduce(mx, s_red, [](float x, float y) { return fmaxf(x, y); });
     lo = block_reduce(lo, s_red, [](float x, float y) { return fminf(x, y); });
 
-    // S = sum l_j exp(m_j - M)
+    // c_j = exp(m_j - M);  S = sum l_j c_j
     float s = 0.0f;
     for (int i = tid; i < ns; i += 256) {
         const size_t o = (size_t)i * n_head + h;
-        s = fmaf(a.pl[o], expf(a.pm[o] - M), s);
+        const float c = expf(a.pm[o] - M);
+        s_c[i] = c;
+        s = fmaf(a.pl[o], c, s);
     }
-    const float S = block_reduce(s, s_red, [](float x, float y) { return x + y; });
+    const float S = block_reduce(s, s_red, [](float x, float y) { return x + y; });  // syncs s_c too
     const float inv = 1.0f / S;  // inv = 1 / sum, tensor.rs:304
 
-    // acc[d] = sum_j exp(m_j - M) acc_j[d]
+    // acc[d] = sum_j c_j acc_j[d]: thread (split group sg, float4 slice dq)
+    // walks splits sg, sg + NSG, ... eight loads at a time
     {
-        const int g = tid / HD, d = tid % HD;
-        float x = 0.0f;
-        for (int i = g; i < ns; i += NG) {
-            const size_t o = (size_t)i * n_head + h;
-            x = fmaf(expf(a.pm[o] - M), a.pacc[o * HD + d], x);
+        const int sg = tid / NQ, dq = tid % NQ;
+        const rsrc_t PA = rsrc(a.pacc, (size_t)ns * n_head * HD * 4);
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int i0 = sg; i0 < ns; i0 += 8 * NSG) {
+            float4 v[8];
+            float c[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + u * NSG;
+                v[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      PA, (unsigned)((((size_t)i * n_head + h) * HD + 4 * dq) * 4), 0, 0));
+                c[u] = i < ns ? s_c[i] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                x.x = fmaf(c[u], v[u].x, x.x);
+                x.y = fmaf(c[u], v[u].y, x.y);
+                x.z = fmaf(c[u], v[u].z, x.z);
+                x.w = fmaf(c[u], v[u].w, x.w);
+            }
         }
-        s_acc[g][d] = x;
+        *reinterpret_cast<float4 *>(&s_acc[sg][4 * dq]) = x;
     }
     __syncthreads();
 
@@ -346,21 +462,39 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     if (tid < HD) {
         float x = s_acc[0][tid];
 #pragma unroll
-        for (int g = 1; g < NG; g++) x += s_acc[g][tid];
+        for (int g = 1; g < NSG; g++) x += s_acc[g][tid];
         x = x * inv;
         if (lo < thr) x -= s_fix[0][tid];
         a.out[(size_t)h * HD + tid] = x;
     }
 }
 
-template <int HD, int GM>
+// P ladders: 16, 64, 128 positions for hd 64; 16, 32, 64 for hd 128.
+template <int HD, int G>
+void launch_split_g(const AttnArgs &a, dim3 grid, hipStream_t stream) {
+    const int np = a.P / 16;
+    if (np == 1) {
+        hipLaunchKernelGGL((attn_split_kernel<HD, G, 1>), grid, dim3(256), 0, stream, a);
+    } else if constexpr (HD == 64) {
+        if (np == 4) hipLaunchKernelGGL((attn_split_kernel<64, G, 4>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((attn_split_kernel<64, G, 8>), grid, dim3(256), 0, stream, a);
+    } else {
+        if (np == 2) hipLaunchKernelGGL((attn_split_kernel<128, G, 2>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((attn_split_kernel<128, G, 4>), grid, dim3(256), 0, stream, a);
+    }
+}
+
+template <int HD>
 void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
-    switch (a.P / 16) {
-        case 1: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 1>), grid, dim3(256), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 2>), grid, dim3(256), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 4>), grid, dim3(256), 0, stream, a); break;
-        case 8: hipLaunchKernelGGL((attn_split_kernel<HD, GM, 8>), grid, dim3(256), 0, stream, a); break;
-        default: hipLaunchKernelGGL((attn_split_kernel<HD, GM, (HD == 64 ? 16 : 8)>), grid, dim3(256), 0, stream, a); break;
+    switch (a.gc) {
+        case 1: launch_split_g<HD, 1>(a, grid, stream); break;
+        case 2: launch_split_g<HD, 2>(a, grid, stream); break;
+        case 3: launch_split_g<HD, 3>(a, grid, stream); break;
+        case 4: launch_split_g<HD, 4>(a, grid, stream); break;
+        case 5: launch_split_g<HD, 5>(a, grid, stream); break;
+        case 6: launch_split_g<HD, 6>(a, grid, stream); break;
+        case 7: launch_split_g<HD, 7>(a, grid, stream); break;
+        default: launch_split_g<HD, 8>(a, grid, stream); break;
     }
 }
 
@@ -393,13 +527,17 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     a.gc = gc;
     const int n_hg = n_head / gc;
     a.L = (int)n_positions;
-    // positions per split: a power-of-two count of 16-row passes, growing
-    // until the launch is about one workgroup per CU (at most 256 rows for
-    // hd 64, 128 for hd 128)
+    // positions per split, from a short ladder: 16 rows, or the middle rung
+    // when that would give more than about four workgroups per CU, or the
+    // top rung when the merge's split limit needs it
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const int pmax = head_dim == 64 ? 256 : 128;
-    int P = 16;
-    while (P < pmax && (long long)((n_positions + P - 1) / P) * n_hg > cu) P *= 2;
+    const int ladder[3] = {16, head_dim == 64 ? 64 : 32, head_dim == 64 ? 128 : 64};
+    int step = 0;
+    while (step < 1 && (long long)((n_positions + ladder[step] - 1) / ladder[step]) * n_hg > 4 * cu) step++;
+    while (step < 2 && (n_positions + ladder[step] - 1) / ladder[step] > (size_t)MAX_SPLITS) step++;
+    const int P = ladder[step];
+    if ((n_positions + P - 1) / P > (size_t)MAX_SPLITS)
+        return fail(KH_DECLINED, "attend: sequence longer than the split merge takes");
     a.P = P;
     a.nsplit = (int)((n_positions + P - 1) / P);
     a.scale = 1.0f / sqrtf((float)head_dim);  // mod.rs:777
@@ -418,13 +556,8 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     }
 
     dim3 grid(a.nsplit, n_hg);
-    if (head_dim == 64) {
-        if (gc <= 4) launch_split<64, 4>(a, grid, ctx->stream);
-        else launch_split<64, 8>(a, grid, ctx->stream);
-    } else {
-        if (gc <= 4) launch_split<128, 4>(a, grid, ctx->stream);
-        else launch_split<128, 8>(a, grid, ctx->stream);
-    }
+    if (head_dim == 64) launch_split<64>(a, grid, ctx->stream);
+    else launch_split<128>(a, grid, ctx->stream);
     KH_HIP(hipGetLastError());
     if (a.nsplit > 1) {
         if (head_dim == 64)
