@@ -178,6 +178,43 @@ int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t 
 int kh_attend_dev(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
                   const float *k, const float *v, size_t n_positions, float *out);
 
+/* ---- mixture of experts ----------------------------------------------- */
+
+/* Router scoring (Scoring, model/ffn.rs:173-177) and selection (Select, ffn.rs:179-195). */
+#define KH_SOFTMAX 0
+#define KH_SIGMOID 1
+#define KH_GREEDY 0
+#define KH_GROUP_LIMITED 1
+#define KH_NOAUX_TC 2
+
+typedef struct kh_moe kh_moe;
+
+/* Moe (model/ffn.rs:474-506) and its Router (ffn.rs:197-252): n_experts
+ * routed experts of width `inter` over `hidden`, top_k picks per token,
+ * scoring/select/n_group/topk_group/norm_topk/scale as the router's config,
+ * bias (n_experts floats, host) the selection bias of noaux_tc or NULL.
+ * The weights are set below as borrowed handles that must outlive the layer. */
+int kh_moe_new(kh_ctx *ctx, size_t n_experts, size_t top_k, size_t hidden, size_t inter, int scoring, int select,
+               size_t n_group, size_t topk_group, int norm_topk, float scale, const float *bias, kh_moe **out);
+int kh_moe_free(kh_moe *moe);
+/* The router's gate, [n_experts, hidden], any precision (Moe's gate, ffn.rs:474-506). */
+int kh_moe_set_router(kh_moe *moe, const kh_weight *router);
+/* Expert `expert`'s Ffn (ffn.rs:355-388): gate/up [inter, hidden], down
+ * [hidden, inter]; every expert in one quantised precision. */
+int kh_moe_set_expert(kh_moe *moe, size_t expert, const kh_weight *gate, const kh_weight *up, const kh_weight *down);
+/* The shared expert (SharedExpert, ffn.rs:413-451; DeepSeek's fused
+ * shared experts): gate/up [width, hidden], down [hidden, width]. */
+int kh_moe_set_shared(kh_moe *moe, const kh_weight *gate, const kh_weight *up, const kh_weight *down);
+/* Moe::run (ffn.rs:615-708): out[m, hidden] for hs[m, hidden].  One token runs
+ * as decode_together (ffn.rs:820-842), a batch grouped by expert; both add
+ * the experts in expert order after the shared expert, as mix() does. */
+int kh_moe_run(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out);
+int kh_moe_run_dev(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out);
+/* Router::route (ffn.rs:256-309) for m tokens' logits [m, n_experts]:
+ * experts/weights [m, top_k] in pick order (unused slots -1 / 0), count [m]. */
+int kh_moe_route(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
+                 int32_t *count);
+
 #ifdef __cplusplus
 }
 #endif

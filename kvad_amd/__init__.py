@@ -24,10 +24,12 @@ import numpy as np
 
 __all__ = [
     "F32", "Q8", "Q4", "Q4K", "KvadError", "Declined", "lib", "Context", "Weight", "matvec_many",
-    "KvCache", "Spec", "attend", "LIB_PATH",
+    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
 ]
 
 F32, Q8, Q4, Q4K = 0, 1, 2, 3
+SOFTMAX, SIGMOID = 0, 1                   # Scoring, model/ffn.rs:173-177
+GREEDY, GROUP_LIMITED, NOAUX_TC = 0, 1, 2  # Select, model/ffn.rs:179-195
 OK, DECLINED = 0, 1
 
 LIB_PATH = Path(os.environ.get("KVAD_HIP_LIB", Path(__file__).resolve().parent / "libkvad_hip.so"))
@@ -95,6 +97,15 @@ _SIGS = {
     "kh_kv_layer_ptrs": (C.c_int, [_p, _sz, C.POINTER(_p), C.POINTER(_p)]),
     "kh_attend": (C.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "kh_attend_dev": (C.c_int, [_p, _sz, _sz, _sz, _p, _p, _p, _sz, _p]),
+    "kh_moe_new": (C.c_int, [_p, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, C.c_float, _p,
+                             C.POINTER(_p)]),
+    "kh_moe_free": (C.c_int, [_p]),
+    "kh_moe_set_router": (C.c_int, [_p, _p]),
+    "kh_moe_set_expert": (C.c_int, [_p, _sz, _p, _p, _p]),
+    "kh_moe_set_shared": (C.c_int, [_p, _p, _p, _p]),
+    "kh_moe_run": (C.c_int, [_p, _p, _p, _sz, _p]),
+    "kh_moe_run_dev": (C.c_int, [_p, _p, _p, _sz, _p]),
+    "kh_moe_route": (C.c_int, [_p, _p, _p, _sz, _p, _p, _p]),
 }
 
 
@@ -407,3 +418,63 @@ def attend_dev(ctx: Context, spec: Spec, q_ptr: int, k_ptr: int, v_ptr: int, n_p
                out_ptr: int) -> None:
     _check(lib.kh_attend_dev(ctx.h, spec.n_head, spec.n_kv_head, spec.head_dim, q_ptr, k_ptr, v_ptr,
                              n_positions, out_ptr))
+
+
+class Moe:
+    """kvad's Moe (model/ffn.rs:474-708) on the device: a router and n_experts
+    SwiGLU experts (plus an optional shared expert).  The Weight objects are
+    kept referenced here, since the layer borrows their device arrays."""
+
+    def __init__(self, ctx: Context, n_experts: int, top_k: int, hidden: int, inter: int, scoring: int = SOFTMAX,
+                 select: int = GREEDY, n_group: int = 1, topk_group: int = 1, norm_topk: bool = False,
+                 scale: float = 1.0, bias=None):
+        self.ctx, self.n_experts, self.top_k, self.hidden, self.inter = ctx, n_experts, top_k, hidden, inter
+        b = None if bias is None else _f32(bias)
+        self.h = C.c_void_p()
+        _check(lib.kh_moe_new(ctx.h, n_experts, top_k, hidden, inter, scoring, select, n_group, topk_group,
+                              int(norm_topk), scale, _ptr(b), C.byref(self.h)))
+        self._keep = {}
+
+    def set_router(self, w: Weight) -> None:
+        _check(lib.kh_moe_set_router(self.h, w.h))
+        self._keep["router"] = w
+
+    def set_expert(self, x: int, gate: Weight, up: Weight, down: Weight) -> None:
+        _check(lib.kh_moe_set_expert(self.h, x, gate.h, up.h, down.h))
+        self._keep[x] = (gate, up, down)
+
+    def set_shared(self, gate: Weight, up: Weight, down: Weight) -> None:
+        _check(lib.kh_moe_set_shared(self.h, gate.h, up.h, down.h))
+        self._keep["shared"] = (gate, up, down)
+
+    def run(self, hs, m: int) -> np.ndarray:
+        """Moe::run: out [m * hidden] for hs [m * hidden]."""
+        hs = _f32(hs)
+        assert hs.size == m * self.hidden, "moe shape mismatch"
+        out = np.empty(m * self.hidden, np.float32)
+        _check(lib.kh_moe_run(self.ctx.h, self.h, _ptr(hs), m, _ptr(out)))
+        return out
+
+    def run_dev(self, hs_ptr: int, m: int, out_ptr: int) -> None:
+        _check(lib.kh_moe_run_dev(self.ctx.h, self.h, hs_ptr, m, out_ptr))
+
+    def route(self, logits, m: int):
+        """Router::route per token: a list of [(expert, weight), ...] in pick order."""
+        logits = _f32(logits)
+        e = np.empty(m * self.top_k, np.int32)
+        w = np.empty(m * self.top_k, np.float32)
+        c = np.empty(m, np.int32)
+        _check(lib.kh_moe_route(self.ctx.h, self.h, _ptr(logits), m, _ptr(e), _ptr(w), _ptr(c)))
+        k = self.top_k
+        return [[(int(e[i * k + j]), float(w[i * k + j])) for j in range(int(c[i]))] for i in range(m)]
+
+    def free(self) -> None:
+        if self.h:
+            lib.kh_moe_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

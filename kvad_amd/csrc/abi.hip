@@ -125,6 +125,8 @@ int make_jobs(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *con
     return KH_OK;
 }
 
+}  // namespace
+
 // matvec on device pointers.
 int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots) {
     std::vector<GemvJob> jobs;
@@ -158,6 +160,7 @@ int matmul_device(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     return launch_matmul(ctx, w, xs, m, bias, y);
 }
 
+namespace {
 }  // namespace
 }  // namespace kh
 
@@ -181,9 +184,6 @@ int kh_init(int device, kh_ctx **out) {
     KH_HIP(hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device));
     KH_HIP(hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking));
     ctx->stream = ctx->own;
-    KH_HIP(hipMalloc(&ctx->counters.ptr, 65536));
-    ctx->counters.bytes = 65536;
-    KH_HIP(hipMemset(ctx->counters.ptr, 0, 65536));
     KH_HIP(hipDeviceSynchronize());
     *out = ctx.release();
     return KH_OK;
@@ -196,7 +196,7 @@ int kh_free(kh_ctx *ctx) {
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->ws.ptr) (void)hipFree(ctx->ws.ptr);
         if (ctx->io.ptr) (void)hipFree(ctx->io.ptr);
-        if (ctx->counters.ptr) (void)hipFree(ctx->counters.ptr);
+        if (ctx->moe.ptr) (void)hipFree(ctx->moe.ptr);
         if (ctx->own) (void)hipStreamDestroy(ctx->own);
     }
     delete ctx;
@@ -720,6 +720,147 @@ int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t 
                        kv->v_dim, n_positions, dout);
     if (rc) return rc;
     KH_HIP(hipMemcpyAsync(out, dout, 4 * nq, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+// ---- mixture of experts ------------------------------------------------------
+
+int kh_moe_new(kh_ctx *ctx, size_t n_experts, size_t top_k, size_t hidden, size_t inter, int scoring, int select,
+               size_t n_group, size_t topk_group, int norm_topk, float scale, const float *bias, kh_moe **out) {
+    if (!ctx || !out) return fail(KH_EINVAL, "kh_moe_new: null argument");
+    *out = nullptr;
+    if (n_experts == 0 || top_k == 0 || top_k > n_experts || hidden == 0 || inter == 0)
+        return fail(KH_EINVAL, "kh_moe_new: needs experts, 0 < top_k <= experts, and widths");
+    if (n_experts > 512 || top_k > 16 || n_group > 64)
+        return fail(KH_DECLINED, "kh_moe_new: more than 512 experts, 16 picks or 64 groups");
+    if (scoring < 0 || scoring > 1 || select < 0 || select > 2)
+        return fail(KH_EINVAL, "kh_moe_new: unknown scoring or selection");
+    if (n_group == 0 || n_experts % n_group != 0)
+        return fail(KH_EINVAL, "kh_moe_new: experts must divide into n_group groups");
+    Guard g(ctx);
+    std::unique_ptr<kh_moe> m(new kh_moe());
+    m->ctx = ctx;
+    m->n_experts = n_experts;
+    m->top_k = top_k;
+    m->hidden = hidden;
+    m->inter = inter;
+    m->scoring = scoring;
+    m->select = select;
+    m->n_group = n_group;
+    m->topk_group = topk_group;
+    m->norm_topk = norm_topk;
+    m->scale = scale;
+    m->gate.assign(n_experts, nullptr);
+    m->up.assign(n_experts, nullptr);
+    m->down.assign(n_experts, nullptr);
+    KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->tab), sizeof(void *) * 3 * n_experts));
+    KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->stab), sizeof(float *) * 3 * n_experts));
+    if (bias) {
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->bias), 4 * n_experts));
+        KH_HIP(hipMemcpy(m->bias, bias, 4 * n_experts, hipMemcpyHostToDevice));
+    }
+    *out = m.release();
+    return KH_OK;
+}
+
+int kh_moe_free(kh_moe *moe) {
+    if (!moe) return KH_OK;
+    {
+        Guard g(moe->ctx);
+        (void)hipStreamSynchronize(moe->ctx->stream);
+        if (moe->tab) (void)hipFree(moe->tab);
+        if (moe->stab) (void)hipFree(moe->stab);
+        if (moe->bias) (void)hipFree(moe->bias);
+    }
+    delete moe;
+    return KH_OK;
+}
+
+int kh_moe_set_router(kh_moe *moe, const kh_weight *router) {
+    if (!moe || check_weight(router)) return fail(KH_EINVAL, "kh_moe_set_router: null argument");
+    if (router->rows != moe->n_experts || router->cols != moe->hidden)
+        return fail(KH_EINVAL, "kh_moe_set_router: the router is [n_experts, hidden]");
+    moe->router = router;
+    return KH_OK;
+}
+
+int kh_moe_set_expert(kh_moe *moe, size_t expert, const kh_weight *gate, const kh_weight *up,
+                      const kh_weight *down) {
+    if (!moe || check_weight(gate) || check_weight(up) || check_weight(down))
+        return fail(KH_EINVAL, "kh_moe_set_expert: null argument");
+    if (expert >= moe->n_experts) return fail(KH_EINVAL, "kh_moe_set_expert: no such expert");
+    if (gate->rows != moe->inter || gate->cols != moe->hidden || up->rows != moe->inter ||
+        up->cols != moe->hidden || down->rows != moe->hidden || down->cols != moe->inter)
+        return fail(KH_EINVAL, "kh_moe_set_expert: gate/up are [inter, hidden], down [hidden, inter]");
+    const int p = gate->precision;
+    if (p == KH_F32 || up->precision != p || down->precision != p)
+        return fail(KH_DECLINED, "kh_moe_set_expert: an expert's three weights must share one quantised precision");
+    if (moe->precision >= 0 && moe->precision != p)
+        return fail(KH_DECLINED, "kh_moe_set_expert: every expert must have the same precision");
+    moe->precision = p;
+    moe->gate[expert] = gate;
+    moe->up[expert] = up;
+    moe->down[expert] = down;
+    moe->dirty = true;
+    return KH_OK;
+}
+
+int kh_moe_set_shared(kh_moe *moe, const kh_weight *gate, const kh_weight *up, const kh_weight *down) {
+    if (!moe || check_weight(gate) || check_weight(up) || check_weight(down))
+        return fail(KH_EINVAL, "kh_moe_set_shared: null argument");
+    if (gate->cols != moe->hidden || up->cols != moe->hidden || up->rows != gate->rows ||
+        down->rows != moe->hidden || down->cols != gate->rows || gate->rows % BLOCK)
+        return fail(KH_EINVAL, "kh_moe_set_shared: gate/up are [width, hidden], down [hidden, width]");
+    if (gate->precision == KH_F32 || up->precision == KH_F32 || down->precision == KH_F32 ||
+        gate->precision != up->precision)
+        return fail(KH_DECLINED, "kh_moe_set_shared: the shared expert must be quantised");
+    moe->sgate = gate;
+    moe->sup = up;
+    moe->sdown = down;
+    return KH_OK;
+}
+
+int kh_moe_run_dev(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out) {
+    if (!ctx || !moe || !hs || !out) return fail(KH_EINVAL, "kh_moe_run_dev: null argument");
+    Guard g(ctx);
+    return moe_run_device(ctx, moe, hs, m, out);
+}
+
+int kh_moe_run(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out) {
+    if (!ctx || !moe || !hs || !out) return fail(KH_EINVAL, "kh_moe_run: null argument");
+    if (m == 0) return KH_OK;
+    Guard g(ctx);
+    const size_t n = m * moe->hidden;
+    int rc = ensure(ctx, ctx->io, 2 * up(4 * n));
+    if (rc) return rc;
+    float *dx = static_cast<float *>(ctx->io.ptr);
+    float *dy = reinterpret_cast<float *>(static_cast<char *>(ctx->io.ptr) + up(4 * n));
+    KH_HIP(hipMemcpyAsync(dx, hs, 4 * n, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = moe_run_device(ctx, moe, dx, m, dy))) return rc;
+    KH_HIP(hipMemcpyAsync(out, dy, 4 * n, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
+int kh_moe_route(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
+                 int32_t *count) {
+    if (!ctx || !moe || !logits || !experts || !weights || !count) return fail(KH_EINVAL, "kh_moe_route: null argument");
+    if (m == 0) return KH_OK;
+    Guard g(ctx);
+    const size_t nl = m * moe->n_experts, np = m * moe->top_k;
+    int rc = ensure(ctx, ctx->io, up(4 * nl) + 2 * up(4 * np) + up(4 * m));
+    if (rc) return rc;
+    char *p = static_cast<char *>(ctx->io.ptr);
+    float *dl = reinterpret_cast<float *>(p);
+    int32_t *de = reinterpret_cast<int32_t *>(p + up(4 * nl));
+    float *dw = reinterpret_cast<float *>(p + up(4 * nl) + up(4 * np));
+    int32_t *dc = reinterpret_cast<int32_t *>(p + up(4 * nl) + 2 * up(4 * np));
+    KH_HIP(hipMemcpyAsync(dl, logits, 4 * nl, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = route_device(ctx, moe, dl, m, de, dw, dc))) return rc;
+    KH_HIP(hipMemcpyAsync(experts, de, 4 * np, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipMemcpyAsync(weights, dw, 4 * np, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipMemcpyAsync(count, dc, 4 * m, hipMemcpyDeviceToHost, ctx->stream));
     KH_HIP(hipStreamSynchronize(ctx->stream));
     return KH_OK;
 }

@@ -57,7 +57,7 @@ struct kh_ctx {
     std::recursive_mutex mu;
     kh::Workspace ws;        // per-call scratch (activations, partials)
     kh::Workspace io;        // staging for host-pointer calls
-    kh::Workspace counters;  // zeroed once; kernels that use them leave them zero
+    kh::Workspace moe;       // mixture-of-experts intermediates
 };
 
 struct kh_weight {
@@ -67,6 +67,24 @@ struct kh_weight {
     void *qs = nullptr;        // q8: int8[rows*cols]; q4: uint8[rows*cols/2]; q4k: blocks; f32: float[rows*cols]
     float *scales = nullptr;   // q8/q4: float[rows*cols/32]
     size_t bytes = 0;          // bytes held on the device
+};
+
+// A mixture-of-experts layer (model/ffn.rs:555-708): router settings and
+// device tables of the experts' weights.  The weights are borrowed handles.
+struct kh_moe {
+    kh_ctx *ctx = nullptr;
+    size_t n_experts = 0, top_k = 0, hidden = 0, inter = 0;
+    int scoring = 0, select = 0, norm_topk = 0;
+    size_t n_group = 1, topk_group = 1;
+    float scale = 1.0f;
+    float *bias = nullptr;                     // device [n_experts] or null
+    const kh_weight *router = nullptr;
+    std::vector<const kh_weight *> gate, up, down;
+    const kh_weight *sgate = nullptr, *sup = nullptr, *sdown = nullptr;
+    int precision = -1;                        // of every expert weight
+    void **tab = nullptr;                      // device: [gate qs | up qs | down qs] x n_experts
+    float **stab = nullptr;                    // device: the same for scales
+    bool dirty = true;                         // tables need uploading
 };
 
 struct kh_kv {
@@ -99,6 +117,12 @@ struct GemvJob {
     const float *bias;      // or null
     float *y;
     int32_t *dots;          // optional: pass-1 integers, [rows * cols/32]
+    // Expert indirection (MoE decode): when wtab is set the weight is
+    // wtab[*sel] (scales wstab[*sel]), read from device memory by the kernel.
+    const void *const *wtab;
+    const float *const *wstab;
+    const int32_t *sel;
+    const float *xf2;       // with xf: the staged activation is swiglu(xf, xf2)
     int rows;
     int cols;
     int wave0;              // set by the launcher: first workgroup of the job
@@ -110,6 +134,66 @@ int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs);
 
 // Batched prefill y[m, rows] = xs[m, cols] W^T (+bias), m > 1 (device pointers).
 int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
+
+// GEMM over activations already quantised (QActBatch form), optionally
+// grouped by expert: with `tiles` set, workgroup row y of the grid takes tile
+// tiles[1 + 3y .. 3 + 3y] = (expert, first row, rows) of tiles[0] tiles, its
+// weight is wtab[expert], and activation row r of the tile is gather[r]
+// (or r).  Output row r is y + r * N.
+struct GemmArgs {
+    const void *w;          // q8 int8 / q4 packed / Q4_K blocks / f32 [N, K]
+    const float *ws;        // q8/q4 block scales [N, K/32]
+    const int8_t *xq;       // quantised activations [M, K]
+    const float *xs;        // activation block scales [M, K/32]
+    const int32_t *xsum;    // activation block sums [M, K/32] (Q4_K)
+    const float *xf;        // f32 activations [M, K] (f32 GEMM)
+    const float *bias;      // [N] or null
+    float *y;               // [M, N]
+    int M, N, K;
+    const int32_t *tiles;
+    const int32_t *gather;
+    const void *const *wtab;
+    const float *const *wstab;
+};
+int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m);
+
+// Operator bodies on device pointers (abi.hip), for the layers built on them.
+int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots);
+int matvec_many_device(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x, float *const *y);
+int matmul_device(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
+// QActBatch::new of swiglu(g, u) (gemv.hip): m rows of k values.
+int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, size_t k, const QAct &out);
+// Moe::run on device pointers, and Router::route alone (moe.hip).
+int moe_run_device(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out);
+int route_device(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
+                 int32_t *count);
+
+// ---- mixture of experts (moe.hip) ----
+// Router::route for m tokens (logits [m, n]): experts/weights [m, top_k] in
+// pick order, count [m]; with `sorted` set, the picks of each token are
+// reordered by expert index (the order mix() adds them in).
+struct RouteArgs {
+    const float *logits;
+    const float *bias;      // [n] or null
+    int n, top_k, scoring, select, n_group, topk_group, norm_topk, always_scale;
+    float scale;
+    int32_t *experts;
+    float *weights;
+    int32_t *count;
+    int32_t *sorted_experts;  // optional, [m, top_k]
+    float *sorted_weights;
+};
+int launch_route(kh_ctx *ctx, const RouteArgs &r, int m);
+// Groups m tokens' picks by expert (expert order, then token order): rows
+// [m*top_k] of (token, weight), each token's k-th pick's row in pos, and the
+// grouped-GEMM tile table for tiles of tile_m rows.
+int launch_moe_group(kh_ctx *ctx, const int32_t *experts, const float *weights, const int32_t *count, int m,
+                     int top_k, int n_exp, int tile_m, int32_t *row_token, float *row_weight, int32_t *pos,
+                     int32_t *tiles);
+// out[i] = base[i] (or 0) + sum over token i's picks in expert order of w * y[pos].
+int launch_moe_combine(kh_ctx *ctx, const float *base, const float *y, const int32_t *experts,
+                       const float *weights, const int32_t *count, const int32_t *pos, int m, int top_k,
+                       int hidden, float *out);
 
 // Split decode attention over one layer's cache, device pointers.
 int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,

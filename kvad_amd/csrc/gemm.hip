@@ -64,17 +64,6 @@ __device__ __forceinline__ int nib_minus8(int x) {
     return (int)((((unsigned)x | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
 }
 
-struct GemmArgs {
-    const void *w;          // q8 int8 / q4 packed / Q4_K blocks / f32 [N, K]
-    const float *ws;        // q8/q4 block scales [N, K/32]
-    const int8_t *xq;       // quantised activations [M, K]
-    const float *xs;        // activation block scales [M, K/32]
-    const int32_t *xsum;    // activation block sums [M, K/32] (Q4_K)
-    const float *xf;        // f32 activations [M, K] (f32 GEMM)
-    const float *bias;      // [N] or null
-    float *y;               // [M, N]
-    int M, N, K;
-};
 
 constexpr int THREADS = 256;
 constexpr int BK = 128;              // k per stage (bytes of int8)
@@ -84,14 +73,14 @@ constexpr int ASTR = BK + 16;        // LDS row stride, bytes
 // Writes a 32x32 accumulator tile (lane: token l&31, rows 8g + 4(l>>5) + e).
 template <int RT, int TT>
 __device__ __forceinline__ void store_tiles(const GemmArgs &a, const v16f (&acc)[RT][TT], int r_base, int t_base,
-                                            int lane) {
+                                            int t_end, int lane) {
     const bool vec = (a.N & 3) == 0;
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) {
             const int tok = t_base + tt * 32 + (lane & 31);
-            if (tok >= a.M) continue;
+            if (tok >= t_end) continue;
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const int r = r_base + rt * 32 + 8 * g + 4 * (lane >> 5);
@@ -139,17 +128,47 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr0 = (wave / WT) * RT * 32, wm0 = (wave % WT) * TT * 32;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
     const int K = a.K, nb = K / BLOCK;
+
+    // the workgroup's rows of activations (and, grouped, its expert)
+    int m0, m_end;
+    const void *wp = a.w;
+    const float *wsp = a.ws;
+    if (a.tiles) {
+        const int t = blockIdx.y;
+        if (t >= a.tiles[0]) return;  // the grid is sized for the most tiles grouping can make
+        const int x = a.tiles[1 + 3 * t];
+        m0 = a.tiles[2 + 3 * t];
+        m_end = m0 + a.tiles[3 + 3 * t];
+        wp = a.wtab[x];
+        wsp = a.wstab[x];
+    } else {
+        m0 = blockIdx.y * BM;
+        m_end = a.M;
+    }
 
     const size_t wbytes = PREC == KH_Q8 ? (size_t)a.N * K
                           : PREC == KH_Q4 ? (size_t)a.N * K / 2
                                           : (size_t)a.N * (K / QK_K) * Q4K_BYTES;
-    const rsrc_t W = rsrc(a.w, wbytes);
-    const rsrc_t WS = rsrc(a.ws, PREC == KH_Q4K ? 0 : (size_t)a.N * nb * 4);
+    const rsrc_t W = rsrc(wp, wbytes);
+    const rsrc_t WS = rsrc(wsp, PREC == KH_Q4K ? 0 : (size_t)a.N * nb * 4);
     const rsrc_t X = rsrc(a.xq, (size_t)a.M * K);
     const rsrc_t XS = rsrc(a.xs, (size_t)a.M * nb * 4);
     const rsrc_t XSUM = rsrc(a.xsum, PREC == KH_Q4K ? (size_t)a.M * nb * 4 : 0);
+
+    // source activation row of each of this thread's chunks (-1: none)
+    int brow[B_PT], srow[XS_PT];
+#pragma unroll
+    for (int u = 0; u < B_PT; u++) {
+        const int r = m0 + ((tid + u * THREADS) >> 3);
+        brow[u] = tid + u * THREADS < B_CH && r < m_end ? (a.gather ? a.gather[r] : r) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < XS_PT; u++) {
+        const int r = m0 + (tid + u * THREADS) / NBS;
+        srow[u] = tid + u * THREADS < BM * NBS && r < m_end ? (a.gather ? a.gather[r] : r) : -1;
+    }
 
     int4 ra[A_PT], rb[B_PT], rh;
     float rws[WS_PT], rxs[XS_PT], rxsum[XS_PT];
@@ -184,12 +203,10 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < B_PT; u++) {
-            const int c = tid + u * THREADS;
+            const int kc = (tid + u * THREADS) & 7;
             int4 v = {0, 0, 0, 0};
-            if (c < B_CH) {
-                const int tok = c >> 3, kc = c & 7;
-                if (k0 + 16 * kc < K) v = ld16(X, (unsigned)(m0 + tok) * (unsigned)K + (unsigned)(k0 + 16 * kc));
-            }
+            if (brow[u] >= 0 && k0 + 16 * kc < K)
+                v = ld16(X, (unsigned)brow[u] * (unsigned)K + (unsigned)(k0 + 16 * kc));
             rb[u] = v;
         }
         if constexpr (PREC != KH_Q4K) {
@@ -204,10 +221,9 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < XS_PT; u++) {
-            const int c = tid + u * THREADS;
-            const int tok = c / NBS, blk = c % NBS;
-            const bool ok = c < BM * NBS && k0 / BLOCK + blk < nb;
-            const unsigned off = ((unsigned)(m0 + tok) * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u;
+            const int blk = (tid + u * THREADS) % NBS;
+            const bool ok = srow[u] >= 0 && k0 / BLOCK + blk < nb;
+            const unsigned off = ((unsigned)srow[u] * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u;
             rxs[u] = ok ? ldf(XS, off) : 0.0f;
             if constexpr (PREC == KH_Q4K) rxsum[u] = ok ? (float)ldi(XSUM, off) : 0.0f;
         }
@@ -356,7 +372,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
                 }
         }
     }
-    store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, lane);
+    store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -447,7 +463,7 @@ __global__ __launch_bounds__(THREADS) void gemm_f32_kernel(GemmArgs a) {
                 }
         }
     }
-    store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, lane);
+    store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, a.M, lane);
 }
 
 // Tile shape for a problem: the largest tile that still gives every CU a
@@ -462,21 +478,19 @@ Shape pick_shape(int M, int N, int cu) {
 }
 
 template <int PREC>
-int launch_i8(kh_ctx *ctx, const GemmArgs &a) {
-    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m) {
     const unsigned gx = (unsigned)((a.N + 127) / 128);
-    switch (pick_shape(a.M, a.N, cu)) {
-        case T128x128:
-            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 2, 2>), dim3(gx, (a.M + 127) / 128), dim3(THREADS), 0,
-                               ctx->stream, a);
+    const unsigned gy = a.tiles ? (unsigned)max_tiles : (unsigned)((a.M + tile_m - 1) / tile_m);
+    if (gy == 0) return KH_OK;
+    switch (tile_m) {
+        case 128:
+            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 2, 2>), dim3(gx, gy), dim3(THREADS), 0, ctx->stream, a);
             break;
-        case T128x64:
-            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 2, 1>), dim3(gx, (a.M + 63) / 64), dim3(THREADS), 0,
-                               ctx->stream, a);
+        case 64:
+            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 2, 1>), dim3(gx, gy), dim3(THREADS), 0, ctx->stream, a);
             break;
         default:
-            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 4, 1, 1, 1>), dim3(gx, (a.M + 31) / 32), dim3(THREADS), 0,
-                               ctx->stream, a);
+            hipLaunchKernelGGL((gemm_i8_kernel<PREC, 4, 1, 1, 1>), dim3(gx, gy), dim3(THREADS), 0, ctx->stream, a);
             break;
     }
     KH_HIP(hipGetLastError());
@@ -555,11 +569,18 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     a.xq = q.qs;
     a.xs = q.scales;
     a.xsum = q.sums;
-    switch (w->precision) {
-        case KH_Q8: return launch_i8<KH_Q8>(ctx, a);
-        case KH_Q4: return launch_i8<KH_Q4>(ctx, a);
-        case KH_Q4K: return launch_i8<KH_Q4K>(ctx, a);
-        default: return fail(KH_EINVAL, "matmul: unknown precision");
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const Shape sh = pick_shape(a.M, a.N, cu);
+    return launch_gemm_q(ctx, w->precision, a, 0, sh == T128x128 ? 128 : sh == T128x64 ? 64 : 32);
+}
+
+int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m) {
+    if (a.tiles && (!a.wtab || !a.wstab)) return fail(KH_EINVAL, "gemm: grouped launch without weight tables");
+    switch (precision) {
+        case KH_Q8: return launch_i8<KH_Q8>(ctx, a, max_tiles, tile_m);
+        case KH_Q4: return launch_i8<KH_Q4>(ctx, a, max_tiles, tile_m);
+        case KH_Q4K: return launch_i8<KH_Q4K>(ctx, a, max_tiles, tile_m);
+        default: return fail(KH_EINVAL, "gemm: the grouped kernel takes quantised weights");
     }
 }
 

@@ -101,6 +101,13 @@ __host__ __device__ inline int chunks_per_row(int prec, int cols) {
 
 __host__ __device__ inline int align16(int n) { return (n + 15) & ~15; }
 
+// silu(g) * u with silu(g) = g / (1 + exp(-g)), as swiglu_inplace computes
+// it (tensor.rs:344-350): one divide, one product.
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    const float silu = g / (1.0f + expf(-g));
+    return silu * u;
+}
+
 // ---------------------------------------------------------------------------
 // activation quantisation: 8 lanes per 32-block, 4 values each
 // ---------------------------------------------------------------------------
@@ -141,6 +148,32 @@ __global__ __launch_bounds__(256) void qact_kernel(const float *__restrict__ x, 
     int sub = threadIdx.x & 7;
     bool ok = b < nblocks;
     float4 v = ok ? reinterpret_cast<const float4 *>(x)[b * 8 + sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float scale;
+    int s;
+    int packed = quantize4(v, &scale, &s);
+    if (ok) {
+        reinterpret_cast<int *>(qs)[b * 8 + sub] = packed;
+        if (sub == 0) {
+            scales[b] = scale;
+            sums[b] = s;
+        }
+    }
+}
+
+// QActBatch::new of h = swiglu(g, u) (tensor.rs:344-350, quant.rs:693-714).
+__global__ __launch_bounds__(256) void swiglu_qact_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                                         size_t nblocks, int8_t *__restrict__ qs,
+                                                         float *__restrict__ scales, int32_t *__restrict__ sums) {
+    size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t b = tid >> 3;
+    int sub = threadIdx.x & 7;
+    bool ok = b < nblocks;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (ok) {
+        const float4 a = reinterpret_cast<const float4 *>(g)[b * 8 + sub];
+        const float4 c = reinterpret_cast<const float4 *>(u)[b * 8 + sub];
+        v = make_float4(swiglu1(a.x, c.x), swiglu1(a.y, c.y), swiglu1(a.z, c.z), swiglu1(a.w, c.w));
+    }
     float scale;
     int s;
     int packed = quantize4(v, &scale, &s);
@@ -335,8 +368,15 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     size_t wbytes = PREC == KH_Q8 ? (size_t)rows * cols
                     : PREC == KH_Q4 ? (size_t)rows * cols / 2
                                     : (size_t)rows * (cols / QK_K) * Q4K_BYTES;
-    const rsrc_t W = rsrc(job.w, wbytes);
-    const rsrc_t WS = rsrc(job.ws, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
+    const void *wp = job.w;
+    const float *wsp = job.ws;
+    if (job.wtab) {  // an expert chosen on the device (MoE decode)
+        const int x = *job.sel;
+        wp = job.wtab[x];
+        wsp = job.wstab[x];
+    }
+    const rsrc_t W = rsrc(wp, wbytes);
+    const rsrc_t WS = rsrc(wsp, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
 
     // the wave's work: its row groups, each cut into nseg segments, walked in
     // order with the next piece's loads in flight while this one computes
@@ -353,6 +393,10 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
         for (int base = 0; base < PB * 8; base += WAVE * WPB) {
             const int i = base + tid, b = i >> 3;
             float4 v = b < nb ? reinterpret_cast<const float4 *>(job.xf)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (job.xf2) {  // swiglu(gate, up) first (tensor.rs:344-350)
+                const float4 u = b < nb ? reinterpret_cast<const float4 *>(job.xf2)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                v = make_float4(swiglu1(v.x, u.x), swiglu1(v.y, u.y), swiglu1(v.z, u.z), swiglu1(v.w, u.w));
+            }
             float scale;
             int s;
             const int packed = quantize4(v, &scale, &s);
@@ -572,6 +616,16 @@ int launch_qact(kh_ctx *ctx, const float *x, size_t m, size_t k, const QAct &out
     size_t threads = nblocks * 8;
     dim3 grid((unsigned)((threads + 255) / 256)), block(256);
     hipLaunchKernelGGL(qact_kernel, grid, block, 0, ctx->stream, x, nblocks, out.qs, out.scales, out.sums);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, size_t k, const QAct &out) {
+    size_t nblocks = m * k / BLOCK;
+    if (nblocks == 0) return KH_OK;
+    size_t threads = nblocks * 8;
+    hipLaunchKernelGGL(swiglu_qact_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, g, u,
+                       nblocks, out.qs, out.scales, out.sums);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }

@@ -1,0 +1,542 @@
+// A mixture-of-experts layer on the device: Moe::run (crates/llm/src/model/
+// ffn.rs:615-708) with Router::route (ffn.rs:256-349), mix (ffn.rs:744-806),
+// decode_together (ffn.rs:820-842) and SharedExpert::run (ffn.rs:437-451).
+//
+// Decode (one token) is four launches and no host round trip: (1) one GEMV
+// launch for the router and the shared expert's gate and up, which read the
+// same input; (2) the router, one wave, which writes the chosen experts in
+// expert order; (3) one GEMV launch for every chosen expert's gate and up,
+// each job reading its weight through a device table indexed by the router's
+// pick; (4) one GEMV launch for every down projection, the shared expert's
+// included, each staging swiglu(gate, up) as its input; then the combine,
+// which adds the weighted expert outputs to the shared expert's in expert
+// order -- the order mix() adds them, so the sum rounds as the reference's.
+//
+// Prefill groups the tokens by expert (expert order, then token order, as
+// by_expert is filled, ffn.rs:627-640), runs each expert's gate/up and down as
+// one grouped int8 GEMM over tiles of its rows, and combines per token in
+// expert order after the shared expert (which runs on every token).
+#include "common.hpp"
+
+namespace kh {
+namespace {
+
+constexpr int MAX_EXPERTS = 512;
+constexpr int MAX_TOPK = 16;
+constexpr int MAX_GROUPS = 64;
+
+// f32::total_cmp as an integer key (-0.0 < +0.0; a total order).
+__device__ __forceinline__ int total_key(float f) {
+    const int b = __builtin_bit_cast(int, f);
+    return b ^ (int)(((unsigned)(b >> 31)) >> 1);
+}
+
+// Router::route for one token per wave (ffn.rs:256-309).  The softmax's sum
+// and the normalisation run in one lane in index order, as the reference
+// sums them; the top-k picks the largest choice, the lowest index on ties.
+__global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
+    const int tok = blockIdx.x, lane = threadIdx.x, n = r.n;
+    __shared__ float s_score[MAX_EXPERTS], s_choice[MAX_EXPERTS];
+    __shared__ float s_inv;
+    __shared__ int s_order[MAX_GROUPS];
+    __shared__ float s_str[MAX_GROUPS];
+    __shared__ int s_pick_e[MAX_TOPK];
+    __shared__ float s_pick_w[MAX_TOPK];
+    __shared__ int s_best;
+    const float *lg = r.logits + (size_t)tok * n;
+
+    if (r.scoring == 0) {  // softmax_inplace (tensor.rs:297-308)
+        float mx = -INFINITY;
+        for (int i = lane; i < n; i += 64) mx = fmaxf(mx, lg[i]);
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        for (int i = lane; i < n; i += 64) s_score[i] = expf(lg[i] - mx);
+        __syncthreads();
+        if (lane == 0) {
+            float sum = 0.0f;
+            for (int i = 0; i < n; i++) sum += s_score[i];
+            s_inv = 1.0f / sum;
+        }
+        __syncthreads();
+        for (int i = lane; i < n; i += 64) s_score[i] *= s_inv;
+    } else {  // sigmoid (ffn.rs:262-266)
+        for (int i = lane; i < n; i += 64) s_score[i] = 1.0f / (1.0f + expf(-lg[i]));
+    }
+    __syncthreads();
+    for (int i = lane; i < n; i += 64) s_choice[i] = r.bias ? s_score[i] + r.bias[i] : s_score[i];
+    __syncthreads();
+
+    // mask_to_best_groups (ffn.rs:312-349)
+    if (r.select != 0 && r.n_group > 1) {
+        const int per = n / r.n_group;
+        if (lane < r.n_group) {
+            const float *grp = s_choice + lane * per;
+            float st;
+            if (r.select == 1) {
+                st = -INFINITY;
+                for (int i = 0; i < per; i++) st = fmaxf(st, grp[i]);
+            } else {
+                float a = -INFINITY, b = -INFINITY;
+                for (int i = 0; i < per; i++) {
+                    const float v = grp[i];
+                    if (v > a) {
+                        b = a;
+                        a = v;
+                    } else if (v > b) {
+                        b = v;
+                    }
+                }
+                st = a + b;
+            }
+            s_str[lane] = st;
+        }
+        __syncthreads();
+        if (lane == 0) {  // stable sort, descending by total_cmp
+            for (int g = 0; g < r.n_group; g++) s_order[g] = g;
+            for (int i = 1; i < r.n_group; i++) {
+                const int x = s_order[i];
+                int j = i;
+                while (j > 0 && total_key(s_str[s_order[j - 1]]) < total_key(s_str[x])) {
+                    s_order[j] = s_order[j - 1];
+                    j--;
+                }
+                s_order[j] = x;
+            }
+        }
+        __syncthreads();
+        const int keep = r.topk_group < r.n_group ? r.topk_group : r.n_group;
+        for (int o = keep; o < r.n_group; o++)
+            for (int i = lane; i < per; i += 64) s_choice[s_order[o] * per + i] = -INFINITY;
+        __syncthreads();
+    }
+
+    // the picks, one at a time (ffn.rs:279-293)
+    const int k = r.top_k < n ? r.top_k : n;
+    int got = 0;
+    for (int p = 0; p < k; p++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int i = lane; i < n; i += 64) {
+            const float v = s_choice[i];
+            if (v > -INFINITY && (bi == 0x7fffffff || v > bv)) bv = v, bi = i;
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) bv = ov, bi = oi;
+        }
+        if (lane == 0) s_best = bi;
+        __syncthreads();
+        const int best = s_best;
+        if (best == 0x7fffffff) break;
+        if (lane == 0) {
+            s_pick_e[got] = best;
+            s_pick_w[got] = s_score[best];
+            s_choice[best] = -INFINITY;
+        }
+        got++;
+        __syncthreads();
+    }
+
+    if (lane == 0) {
+        const bool normalised = r.norm_topk && r.top_k > 1;
+        if (normalised) {  // ffn.rs:296-302
+            float total = 0.0f;
+            for (int i = 0; i < got; i++) total += s_pick_w[i];
+            total += 1e-20f;
+            for (int i = 0; i < got; i++) s_pick_w[i] /= total;
+        }
+        if (r.always_scale || !normalised)
+            for (int i = 0; i < got; i++) s_pick_w[i] *= r.scale;
+        int32_t *e = r.experts + (size_t)tok * r.top_k;
+        float *w = r.weights + (size_t)tok * r.top_k;
+        for (int i = 0; i < r.top_k; i++) {
+            e[i] = i < got ? s_pick_e[i] : -1;
+            w[i] = i < got ? s_pick_w[i] : 0.0f;
+        }
+        r.count[tok] = got;
+        if (r.sorted_experts) {
+            // the picks in expert order; unused slots name expert 0 with
+            // weight 0, so a kernel that reads every slot stays in bounds
+            int se[MAX_TOPK];
+            float sw[MAX_TOPK];
+            for (int i = 0; i < got; i++) {
+                int j = i;
+                while (j > 0 && se[j - 1] > s_pick_e[i]) {
+                    se[j] = se[j - 1];
+                    sw[j] = sw[j - 1];
+                    j--;
+                }
+                se[j] = s_pick_e[i];
+                sw[j] = s_pick_w[i];
+            }
+            for (int i = 0; i < r.top_k; i++) {
+                r.sorted_experts[(size_t)tok * r.top_k + i] = i < got ? se[i] : 0;
+                r.sorted_weights[(size_t)tok * r.top_k + i] = i < got ? sw[i] : 0.0f;
+            }
+        }
+    }
+}
+
+// by_expert (ffn.rs:627-640): rows in expert order, tokens in order within an
+// expert.  One workgroup; thread x walks the picks for expert x.
+constexpr int GROUP_CHUNK = 8192;
+
+__global__ __launch_bounds__(256) void group_kernel(const int32_t *experts, const float *weights,
+                                                   const int32_t *count, int m, int top_k, int n_exp, int tile_m,
+                                                   int32_t *row_token, float *row_weight, int32_t *pos,
+                                                   int32_t *tiles) {
+    __shared__ int s_cnt[MAX_EXPERTS], s_off[MAX_EXPERTS];
+    __shared__ int s_e[GROUP_CHUNK];
+    const int tid = threadIdx.x, total = m * top_k;
+    for (int x = tid; x < n_exp; x += 256) s_cnt[x] = 0;
+    __syncthreads();
+    for (int i = tid; i < total; i += 256) {
+        const int t = i / top_k, k = i % top_k;
+        if (k < count[t]) atomicAdd(&s_cnt[experts[i]], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int off = 0, nt = 0;
+        for (int x = 0; x < n_exp; x++) {
+            s_off[x] = off;
+            const int c = s_cnt[x];
+            for (int r0 = 0; r0 < c; r0 += tile_m) {
+                tiles[1 + 3 * nt] = x;
+                tiles[2 + 3 * nt] = off + r0;
+                tiles[3 + 3 * nt] = c - r0 < tile_m ? c - r0 : tile_m;
+                nt++;
+            }
+            off += c;
+        }
+        tiles[0] = nt;
+    }
+    __syncthreads();
+    int next[(MAX_EXPERTS + 255) / 256];
+#pragma unroll
+    for (int j = 0; j < (MAX_EXPERTS + 255) / 256; j++) next[j] = tid + 256 * j < n_exp ? s_off[tid + 256 * j] : 0;
+    for (int c0 = 0; c0 < total; c0 += GROUP_CHUNK) {
+        const int cn = total - c0 < GROUP_CHUNK ? total - c0 : GROUP_CHUNK;
+        __syncthreads();
+        for (int i = tid; i < cn; i += 256) {
+            const int t = (c0 + i) / top_k, k = (c0 + i) % top_k;
+            s_e[i] = k < count[t] ? experts[c0 + i] : -1;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < (MAX_EXPERTS + 255) / 256; j++) {
+            const int x = tid + 256 * j;
+            if (x >= n_exp) continue;
+            for (int i = 0; i < cn; i++) {
+                if (s_e[i] != x) continue;
+                const int row = next[j]++;
+                row_token[row] = (c0 + i) / top_k;
+                row_weight[row] = weights[c0 + i];
+                pos[c0 + i] = row;
+            }
+        }
+    }
+}
+
+// out[t] = base[t] (or 0), then + w * y[row] over token t's picks in expert
+// order (the mix order, ffn.rs:775-805).  `pos` null: pick k's row is
+// t * top_k + k of picks already in expert order.
+__global__ __launch_bounds__(256) void combine_kernel(const float *base, const float *y, const int32_t *experts,
+                                                     const float *weights, const int32_t *count,
+                                                     const int32_t *pos, int top_k, int hidden, float *out) {
+    const int t = blockIdx.x;
+    const int n = count[t];
+    int pe[MAX_TOPK], pr[MAX_TOPK];
+    float pw[MAX_TOPK];
+    for (int k = 0; k < n; k++) {  // insertion sort by expert
+        const int e = experts[(size_t)t * top_k + k];
+        const int r = pos ? pos[(size_t)t * top_k + k] : t * top_k + k;
+        const float w = weights[(size_t)t * top_k + k];
+        int j = k;
+        while (j > 0 && pe[j - 1] > e) {
+            pe[j] = pe[j - 1];
+            pr[j] = pr[j - 1];
+            pw[j] = pw[j - 1];
+            j--;
+        }
+        pe[j] = e, pr[j] = r, pw[j] = w;
+    }
+    for (int i = threadIdx.x; i < hidden; i += 256) {
+        float v = base ? base[(size_t)t * hidden + i] : 0.0f;
+        for (int k = 0; k < n; k++) {
+            const float p = pw[k] * y[(size_t)pr[k] * hidden + i];
+            v = v + p;
+        }
+        out[(size_t)t * hidden + i] = v;
+    }
+}
+
+size_t up256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Bump allocator over the context's MoE workspace.
+struct Carve {
+    char *base;
+    size_t used = 0;
+    template <typename T>
+    T *take(size_t n) {
+        T *p = reinterpret_cast<T *>(base + used);
+        used += up256(n * sizeof(T));
+        return p;
+    }
+};
+
+QAct take_qact(Carve &c, size_t m, size_t k) {
+    QAct q;
+    q.qs = c.take<int8_t>(m * k);
+    q.scales = c.take<float>(m * k / BLOCK);
+    q.sums = c.take<int32_t>(m * k / BLOCK);
+    return q;
+}
+
+int upload_tables(kh_ctx *ctx, kh_moe *moe) {
+    if (!moe->dirty) return KH_OK;
+    const size_t n = moe->n_experts;
+    std::vector<void *> tab(3 * n);
+    std::vector<float *> stab(3 * n);
+    for (size_t x = 0; x < n; x++) {
+        const kh_weight *w[3] = {moe->gate[x], moe->up[x], moe->down[x]};
+        for (int j = 0; j < 3; j++) {
+            tab[j * n + x] = w[j]->qs;
+            stab[j * n + x] = w[j]->scales;
+        }
+    }
+    KH_HIP(hipMemcpyAsync(moe->tab, tab.data(), sizeof(void *) * 3 * n, hipMemcpyHostToDevice, ctx->stream));
+    KH_HIP(hipMemcpyAsync(moe->stab, stab.data(), sizeof(float *) * 3 * n, hipMemcpyHostToDevice, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    moe->dirty = false;
+    return KH_OK;
+}
+
+RouteArgs route_args(const kh_moe *moe, const float *logits, int32_t *experts, float *weights, int32_t *count) {
+    RouteArgs r{};
+    r.logits = logits;
+    r.bias = moe->bias;
+    r.n = (int)moe->n_experts;
+    r.top_k = (int)moe->top_k;
+    r.scoring = moe->scoring;
+    r.select = moe->select;
+    r.n_group = (int)moe->n_group;
+    r.topk_group = (int)moe->topk_group;
+    r.norm_topk = moe->norm_topk;
+    r.always_scale = moe->select == 2;  // noaux_tc scales always (ffn.rs:251)
+    r.scale = moe->scale;
+    r.experts = experts;
+    r.weights = weights;
+    r.count = count;
+    return r;
+}
+
+GemvJob expert_job(const kh_moe *moe, int which, const int32_t *sel, const float *xf, const float *xf2, float *y) {
+    const size_t n = moe->n_experts;
+    const kh_weight *w0 = which == 0 ? moe->gate[0] : which == 1 ? moe->up[0] : moe->down[0];
+    GemvJob j{};
+    j.wtab = const_cast<const void *const *>(moe->tab + which * n);
+    j.wstab = const_cast<const float *const *>(moe->stab + which * n);
+    j.sel = sel;
+    j.xf = xf;
+    j.xf2 = xf2;
+    j.y = y;
+    j.rows = (int)w0->rows;
+    j.cols = (int)w0->cols;
+    return j;
+}
+
+GemvJob plain_job(const kh_weight *w, const float *xf, const float *xf2, float *y) {
+    GemvJob j{};
+    j.w = w->qs;
+    j.ws = w->scales;
+    j.xf = xf;
+    j.xf2 = xf2;
+    j.y = y;
+    j.rows = (int)w->rows;
+    j.cols = (int)w->cols;
+    return j;
+}
+
+// One token: decode_together (ffn.rs:820-842) after early() (ffn.rs:556-612).
+int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
+    const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
+    const size_t sh = moe->sgate ? moe->sgate->rows : 0;
+    Carve c{static_cast<char *>(ctx->moe.ptr)};
+    float *logits = c.take<float>(n);
+    float *sg = c.take<float>(sh ? sh : 1), *su = c.take<float>(sh ? sh : 1);
+    int32_t *pe = c.take<int32_t>(k), *cnt = c.take<int32_t>(1), *se = c.take<int32_t>(k);
+    float *pw = c.take<float>(k), *sw = c.take<float>(k);
+    float *g = c.take<float>(k * inter), *u = c.take<float>(k * inter);
+    float *y = c.take<float>(k * hid), *ys = c.take<float>(hid);
+
+    // (1) the router and the shared expert's gate and up read x together
+    std::vector<const kh_weight *> w{moe->router};
+    std::vector<const float *> xs{x};
+    std::vector<float *> ys1{logits};
+    if (sh) {
+        w.push_back(moe->sgate), xs.push_back(x), ys1.push_back(sg);
+        w.push_back(moe->sup), xs.push_back(x), ys1.push_back(su);
+    }
+    int rc;
+    if (moe->router->precision == KH_F32) {  // matvec_many declines f32: run the router alone
+        if ((rc = matvec_device(ctx, moe->router, x, nullptr, logits, nullptr))) return rc;
+        if (sh && (rc = matvec_many_device(ctx, w.size() - 1, w.data() + 1, xs.data() + 1, ys1.data() + 1)))
+            return rc;
+    } else if ((rc = matvec_many_device(ctx, w.size(), w.data(), xs.data(), ys1.data()))) {
+        return rc;
+    }
+    // (2) the router
+    RouteArgs r = route_args(moe, logits, pe, pw, cnt);
+    r.sorted_experts = se;
+    r.sorted_weights = sw;
+    if ((rc = launch_route(ctx, r, 1))) return rc;
+    // (3) every chosen expert's gate and up, through the device tables
+    std::vector<GemvJob> jobs;
+    for (size_t i = 0; i < k; i++) {
+        jobs.push_back(expert_job(moe, 0, se + i, x, nullptr, g + i * inter));
+        jobs.push_back(expert_job(moe, 1, se + i, x, nullptr, u + i * inter));
+    }
+    if ((rc = launch_gemv(ctx, moe->precision, jobs.data(), (int)jobs.size()))) return rc;
+    // (4) every down projection, input swiglu(gate, up) staged by the kernel
+    jobs.clear();
+    for (size_t i = 0; i < k; i++) jobs.push_back(expert_job(moe, 2, se + i, g + i * inter, u + i * inter, y + i * hid));
+    if (sh && moe->sdown->precision == moe->precision) jobs.push_back(plain_job(moe->sdown, sg, su, ys));
+    if ((rc = launch_gemv(ctx, moe->precision, jobs.data(), (int)jobs.size()))) return rc;
+    if (sh && moe->sdown->precision != moe->precision) {
+        GemvJob j = plain_job(moe->sdown, sg, su, ys);
+        if ((rc = launch_gemv(ctx, moe->sdown->precision, &j, 1))) return rc;
+    }
+    // (5) out = shared, then + w * y in expert order
+    hipLaunchKernelGGL(combine_kernel, dim3(1), dim3(256), 0, ctx->stream, sh ? ys : nullptr, y, se, sw, cnt,
+                       nullptr, (int)k, (int)hid, out);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+// Ffn::run over pre-quantised rows with a plain (ungrouped) weight set.
+int ffn_rows(kh_ctx *ctx, const kh_weight *gate, const kh_weight *up, const kh_weight *down, const QAct &xq,
+             size_t m, float *g, float *u, const QAct &hq, float *y) {
+    GemmArgs a{};
+    a.xq = xq.qs, a.xs = xq.scales, a.xsum = xq.sums;
+    a.M = (int)m, a.K = (int)gate->cols;
+    const int tm = m >= 128 ? 128 : m >= 64 ? 64 : 32;
+    int rc;
+    a.w = gate->qs, a.ws = gate->scales, a.N = (int)gate->rows, a.y = g;
+    if ((rc = launch_gemm_q(ctx, gate->precision, a, 0, tm))) return rc;
+    a.w = up->qs, a.ws = up->scales, a.N = (int)up->rows, a.y = u;
+    if ((rc = launch_gemm_q(ctx, up->precision, a, 0, tm))) return rc;
+    if ((rc = launch_swiglu_qact(ctx, g, u, m, gate->rows, hq))) return rc;
+    GemmArgs d{};
+    d.xq = hq.qs, d.xs = hq.scales, d.xsum = hq.sums;
+    d.M = (int)m, d.K = (int)down->cols, d.N = (int)down->rows;
+    d.w = down->qs, d.ws = down->scales, d.y = y;
+    return launch_gemm_q(ctx, down->precision, d, 0, tm);
+}
+
+// A batch: Moe::run for m > 1 (ffn.rs:615-708, mix ffn.rs:788-805).
+int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out) {
+    const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
+    const size_t sh = moe->sgate ? moe->sgate->rows : 0;
+    const size_t total = m * k;
+    const int tile_m = total / n >= 64 ? 64 : 32;
+    const size_t max_tiles = (total + tile_m - 1) / tile_m + n;
+    Carve c{static_cast<char *>(ctx->moe.ptr)};
+    float *logits = c.take<float>(m * n);
+    int32_t *pe = c.take<int32_t>(total), *cnt = c.take<int32_t>(m), *pos = c.take<int32_t>(total);
+    float *pw = c.take<float>(total);
+    int32_t *row_token = c.take<int32_t>(total), *tiles = c.take<int32_t>(1 + 3 * max_tiles);
+    float *row_weight = c.take<float>(total);
+    QAct hq = take_qact(c, m, hid);
+    float *g = c.take<float>(total * inter), *u = c.take<float>(total * inter);
+    QAct rq = take_qact(c, total, inter);
+    float *y = c.take<float>(total * hid);
+    float *base = nullptr, *sg = nullptr, *su = nullptr;
+    QAct sq{};
+    if (sh) {
+        base = c.take<float>(m * hid);
+        sg = c.take<float>(m * sh);
+        su = c.take<float>(m * sh);
+        sq = take_qact(c, m, sh);
+    }
+    int rc;
+    // router logits (any precision), then the routes
+    if ((rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits))) return rc;
+    if ((rc = launch_route(ctx, route_args(moe, logits, pe, pw, cnt), (int)m))) return rc;
+    // by_expert, and the tiles of the grouped GEMMs
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(256), 0, ctx->stream, pe, pw, cnt, (int)m, (int)k, (int)n,
+                       tile_m, row_token, row_weight, pos, tiles);
+    KH_HIP(hipGetLastError());
+    // the activations, quantised once for every expert and the shared one
+    if ((rc = launch_qact(ctx, hs, m, hid, hq))) return rc;
+    // the shared expert on every token (SharedExpert::run, ffn.rs:437-451)
+    if (sh && (rc = ffn_rows(ctx, moe->sgate, moe->sup, moe->sdown, hq, m, sg, su, sq, base))) return rc;
+    // each expert's gate and up over its own rows
+    GemmArgs a{};
+    a.xq = hq.qs, a.xs = hq.scales, a.xsum = hq.sums;
+    a.M = (int)m, a.K = (int)hid, a.N = (int)inter;
+    a.tiles = tiles, a.gather = row_token;
+    a.wtab = const_cast<const void *const *>(moe->tab);
+    a.wstab = const_cast<const float *const *>(moe->stab);
+    a.y = g;
+    if ((rc = launch_gemm_q(ctx, moe->precision, a, (int)max_tiles, tile_m))) return rc;
+    a.wtab = const_cast<const void *const *>(moe->tab + n);
+    a.wstab = const_cast<const float *const *>(moe->stab + n);
+    a.y = u;
+    if ((rc = launch_gemm_q(ctx, moe->precision, a, (int)max_tiles, tile_m))) return rc;
+    if ((rc = launch_swiglu_qact(ctx, g, u, total, inter, rq))) return rc;
+    // each expert's down over its rows of swiglu(gate, up)
+    GemmArgs d{};
+    d.xq = rq.qs, d.xs = rq.scales, d.xsum = rq.sums;
+    d.M = (int)total, d.K = (int)inter, d.N = (int)hid;
+    d.tiles = tiles;
+    d.wtab = const_cast<const void *const *>(moe->tab + 2 * n);
+    d.wstab = const_cast<const float *const *>(moe->stab + 2 * n);
+    d.y = y;
+    if ((rc = launch_gemm_q(ctx, moe->precision, d, (int)max_tiles, tile_m))) return rc;
+    // out = shared, then + w * y per token in expert order
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)m), dim3(256), 0, ctx->stream, base, y, pe, pw, cnt, pos,
+                       (int)k, (int)hid, out);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+size_t workspace_bytes(const kh_moe *moe, size_t m) {
+    const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
+    const size_t sh = moe->sgate ? moe->sgate->rows : 0;
+    const size_t total = m * k, max_tiles = total / 32 + 1 + n;
+    auto q = [](size_t a, size_t b) { return up256(a * b) + 2 * up256(4 * a * b / BLOCK); };
+    size_t b = up256(4 * m * n) + 5 * up256(4 * total) + up256(4 * m) + up256(4 * (1 + 3 * max_tiles));
+    b += q(m, hid) + 2 * up256(4 * total * inter) + q(total, inter) + up256(4 * total * hid);
+    b += sh ? up256(4 * m * hid) + 2 * up256(4 * m * sh) + q(m, sh) : 0;
+    b += up256(4 * hid) + 2 * up256(4 * (sh ? sh : 1)) + 4 * up256(4 * k) + up256(4 * k * hid);  // decode extras
+    return b + 4096;
+}
+
+}  // namespace
+
+int launch_route(kh_ctx *ctx, const RouteArgs &r, int m) {
+    if (r.n > MAX_EXPERTS || r.top_k > MAX_TOPK || r.n_group > MAX_GROUPS)
+        return fail(KH_DECLINED, "route: more experts, picks or groups than the device router takes");
+    if (m == 0) return KH_OK;
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)m), dim3(64), 0, ctx->stream, r);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+int moe_run_device(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out) {
+    if (!moe->router) return fail(KH_EINVAL, "moe: no router set");
+    for (size_t x = 0; x < moe->n_experts; x++)
+        if (!moe->gate[x] || !moe->up[x] || !moe->down[x]) return fail(KH_EINVAL, "moe: an expert is not set");
+    if (m == 0) return KH_OK;
+    int rc = upload_tables(ctx, moe);
+    if (rc) return rc;
+    if ((rc = ensure(ctx, ctx->moe, workspace_bytes(moe, m)))) return rc;
+    return m == 1 ? moe_decode(ctx, moe, hs, out) : moe_prefill(ctx, moe, hs, m, out);
+}
+
+int route_device(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
+                 int32_t *count) {
+    return launch_route(ctx, route_args(moe, logits, experts, weights, count), (int)m);
+}
+
+}  // namespace kh

@@ -73,6 +73,8 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         "kvo_rope_apply": (None, [_p, _p, _sz, _p, _sz]),
         "kvo_attend": (None, [_sz, _sz, _sz, _p, _p, _p, _sz, _p]),
         "kvo_route": (C.c_int, [_p, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, _f, _p, _p, _p]),
+        "kvo_moe_run_q8": (None, [_p, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, _f, _p]
+                           + [_p] * 8 + [_sz] + [_p] * 7),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -338,3 +340,27 @@ def route(logits, top_k: int, scoring: int = 0, select: int = 0, n_group: int = 
     got = lib.kvo_route(P(logits), n, top_k, scoring, select, n_group, topk_group, int(norm_topk), scale, P(b),
                         P(e), P(w))
     return [(int(e[i]), float(w[i])) for i in range(got)]
+
+
+def moe_run_q8(hs, m: int, hidden: int, inter: int, n_exp: int, top_k: int, router, gate, up, down,
+               shared=None, scoring: int = 0, select: int = 0, n_group: int = 1, topk_group: int = 1,
+               norm_topk: bool = False, scale: float = 1.0, bias=None, L=None) -> np.ndarray:
+    """Moe::run (model/ffn.rs:615-708) with every weight q8.  router, gate, up,
+    down and the shared (gate, up, down) are (scales, qs) pairs; gate/up hold
+    every expert's rows stacked ([n_exp*inter, hidden]), down likewise
+    ([n_exp*hidden, inter]); shared is None or ((s, q), (s, q), (s, q), width)."""
+    L = L or lib
+    out = np.empty(m * hidden, np.float32)
+    f = lambda a: _c(a, np.float32)
+    i8 = lambda a: _c(a, np.int8)
+    if shared is None:
+        sh = [None] * 6
+        sh_inter = 0
+    else:
+        (sgs, sgq), (sus, suq), (sds, sdq), sh_inter = shared
+        sh = [f(sgs), i8(sgq), f(sus), i8(suq), f(sds), i8(sdq)]
+    b = None if bias is None else f(bias)
+    args = [f(router[0]), i8(router[1]), f(gate[0]), i8(gate[1]), f(up[0]), i8(up[1]), f(down[0]), i8(down[1])]
+    L.kvo_moe_run_q8(P(f(hs)), m, hidden, inter, n_exp, top_k, scoring, select, n_group, topk_group,
+                     int(norm_topk), scale, P(b), *[P(a) for a in args], sh_inter, *[P(a) for a in sh], P(out))
+    return out

@@ -856,6 +856,14 @@ void kvo_attend(size_t n_head, size_t n_kv_head, size_t hd, const float *q, cons
 /* router                                                                     */
 /* ------------------------------------------------------------------------- */
 
+/* f32::total_cmp as an integer key: the IEEE bits with the magnitude bits
+ * flipped for negatives, so -0.0 < +0.0 and the order is total. */
+static int32_t total_key(float f) {
+    int32_t b;
+    memcpy(&b, &f, sizeof b);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
 int kvo_route(const float *logits, size_t n, size_t top_k, int scoring, int select, size_t n_group,
               size_t topk_group, int norm_topk, float scale, const float *bias, int32_t *experts,
               float *weights) {
@@ -898,10 +906,10 @@ int kvo_route(const float *logits, size_t n, size_t top_k, int scoring, int sele
             }
             order[g] = g;
         }
-        for (size_t i = 1; i < n_group; i++) { /* stable insertion sort, descending */
+        for (size_t i = 1; i < n_group; i++) { /* stable insertion sort, descending by total_cmp */
             size_t x = order[i];
             size_t j = i;
-            while (j > 0 && strength[order[j - 1]] < strength[x]) {
+            while (j > 0 && total_key(strength[order[j - 1]]) < total_key(strength[x])) {
                 order[j] = order[j - 1];
                 j--;
             }
@@ -938,4 +946,79 @@ int kvo_route(const float *logits, size_t n, size_t top_k, int scoring, int sele
     free(scores);
     free(choice);
     return got;
+}
+
+/* ------------------------------------------------------------------------- */
+/* mixture of experts                                                         */
+/* ------------------------------------------------------------------------- */
+
+/* Ffn::run / Ffn::run_one (model/ffn.rs:370-388): gate and up, SwiGLU, down.
+ * m == 1 goes through matvec, as matmul_bt does (quant.rs:767-769). */
+static void ffn_q8(const float *xs, size_t m, size_t hidden, size_t inter, const float *gs, const int8_t *gq,
+                   const float *us, const int8_t *uq, const float *ds, const int8_t *dq, float *y) {
+    float *g = (float *)malloc(sizeof(float) * m * inter);
+    float *u = (float *)malloc(sizeof(float) * m * inter);
+    kvo_matmul_q8(gs, gq, inter, hidden, xs, m, NULL, g);
+    kvo_matmul_q8(us, uq, inter, hidden, xs, m, NULL, u);
+    kvo_swiglu(g, u, m * inter);
+    kvo_matmul_q8(ds, dq, hidden, inter, g, m, NULL, y);
+    free(g);
+    free(u);
+}
+
+void kvo_moe_run_q8(const float *hs, size_t m, size_t hidden, size_t inter, size_t n_exp, size_t top_k,
+                    int scoring, int select, size_t n_group, size_t topk_group, int norm_topk, float scale,
+                    const float *bias, const float *r_s, const int8_t *r_q, const float *g_s, const int8_t *g_q,
+                    const float *u_s, const int8_t *u_q, const float *d_s, const int8_t *d_q, size_t sh_inter,
+                    const float *sg_s, const int8_t *sg_q, const float *su_s, const int8_t *su_q,
+                    const float *sd_s, const int8_t *sd_q, float *out) {
+    /* Moe::run (ffn.rs:615-708) with mix (:744-806) and decode_together
+     * (:820-842).  Expert x's gate/up are rows [x*inter, (x+1)*inter) of
+     * g/u, its down rows [x*hidden, (x+1)*hidden) of d; scales alike. */
+    const size_t gsz = inter * hidden, gsb = gsz / KVO_BLOCK;
+    float *logits = (float *)malloc(sizeof(float) * m * n_exp);
+    kvo_matmul_q8(r_s, r_q, n_exp, hidden, hs, m, NULL, logits);
+    int32_t *pe = (int32_t *)malloc(sizeof(int32_t) * m * (top_k ? top_k : 1));
+    float *pw = (float *)malloc(sizeof(float) * m * (top_k ? top_k : 1));
+    int *np = (int *)malloc(sizeof(int) * m);
+    for (size_t i = 0; i < m; i++)
+        np[i] = kvo_route(logits + i * n_exp, n_exp, top_k, scoring, select, n_group, topk_group, norm_topk, scale,
+                          bias, pe + i * top_k, pw + i * top_k);
+    /* the shared expert first: out starts as its output (ffn.rs:675-681, 775-785) */
+    if (sh_inter)
+        ffn_q8(hs, m, hidden, sh_inter, sg_s, sg_q, su_s, su_q, sd_s, sd_q, out);
+    else
+        memset(out, 0, sizeof(float) * m * hidden);
+    /* then each chosen expert in index order, its tokens in token order */
+    float *rows = (float *)malloc(sizeof(float) * m * hidden);
+    float *y = (float *)malloc(sizeof(float) * m * hidden);
+    size_t *tok = (size_t *)malloc(sizeof(size_t) * m);
+    float *wt = (float *)malloc(sizeof(float) * m);
+    for (size_t x = 0; x < n_exp; x++) {
+        size_t cnt = 0;
+        for (size_t i = 0; i < m; i++)
+            for (int k = 0; k < np[i]; k++)
+                if ((size_t)pe[i * top_k + k] == x) {
+                    tok[cnt] = i;
+                    wt[cnt] = pw[i * top_k + k];
+                    memcpy(rows + cnt * hidden, hs + i * hidden, sizeof(float) * hidden);
+                    cnt++;
+                }
+        if (!cnt) continue;
+        ffn_q8(rows, cnt, hidden, inter, g_s + x * gsb, g_q + x * gsz, u_s + x * gsb, u_q + x * gsz,
+               d_s + x * gsb, d_q + x * gsz, y);
+        for (size_t j = 0; j < cnt; j++)
+            for (size_t e = 0; e < hidden; e++) {
+                float p = wt[j] * y[j * hidden + e];
+                out[tok[j] * hidden + e] = out[tok[j] * hidden + e] + p;
+            }
+    }
+    free(rows);
+    free(y);
+    free(tok);
+    free(wt);
+    free(logits);
+    free(pe);
+    free(pw);
+    free(np);
 }

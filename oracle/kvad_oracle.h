@@ -110,6 +110,17 @@ int kvo_route(const float *logits, size_t n_experts, size_t top_k, int scoring, 
               size_t n_group, size_t topk_group, int norm_topk, float scale, const float *bias,
               int32_t *experts, float *weights);
 
+/* ---- MoE layer: Moe::run (model/ffn.rs:615-708), every weight q8 ---- */
+/* Expert x's gate/up occupy rows [x*inter, (x+1)*inter) of g/u ([n_exp*inter, hidden]),
+ * its down rows [x*hidden, (x+1)*hidden) of d ([n_exp*hidden, inter]); scales alike.
+ * sh_inter == 0 means no shared expert.  out is [m, hidden]. */
+void kvo_moe_run_q8(const float *hs, size_t m, size_t hidden, size_t inter, size_t n_exp, size_t top_k,
+                    int scoring, int select, size_t n_group, size_t topk_group, int norm_topk, float scale,
+                    const float *bias, const float *r_s, const int8_t *r_q, const float *g_s, const int8_t *g_q,
+                    const float *u_s, const int8_t *u_q, const float *d_s, const int8_t *d_q, size_t sh_inter,
+                    const float *sg_s, const int8_t *sg_q, const float *su_s, const int8_t *su_q,
+                    const float *sd_s, const int8_t *sd_q, float *out);
+
 #ifdef __cplusplus
 }
 #endif

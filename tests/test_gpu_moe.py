@@ -1,0 +1,143 @@
+"""GPU parity of the mixture-of-experts layer (Moe::run, model/ffn.rs:615-708)
+and its router (Router::route, ffn.rs:256-309) against the CPU oracle, through
+the C ABI.
+
+Bar.  The router on the same logits picks the same experts in the same order,
+with weights within 1e-6 (its exp and divide are the device's).  The layer's
+output agrees within 2e-3 x max|ref|: each of its GEMVs agrees with the
+oracle's to 1e-5, but the SwiGLU hidden is quantised again before the down
+projection, and a hidden value within rounding of a quantisation boundary
+takes the neighbouring int8 code on one side (about 1e-3 of codes at these
+shapes), a difference of one code step in that term.  The device's own
+decode and batched paths, and repeated runs, are compared as well.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+import kvad_amd as K  # noqa: E402
+
+from test_gpu_gemv import say  # noqa: E402
+
+MOE_RTOL = 2e-3
+
+
+def close(got, want, rtol):
+    scale = max(float(np.max(np.abs(want))), 1e-30)
+    err = float(np.max(np.abs(got.astype(np.float64) - want)))
+    assert err <= rtol * scale, f"max err {err:.3e} vs scale {scale:.3e} (rel {err / scale:.2e})"
+    return err / scale
+
+
+def route_cases():
+    lg = O.normal(50, 64)
+    bias = O.normal(51, 64, 0.1)
+    return {
+        "kat": (np.array([0, 3, 1, -1, 2, 0.5, -2, 4], np.float32), dict(top_k=4, norm_topk=True)),
+        "v2lite": (lg, dict(top_k=6)),
+        "noaux": (lg, dict(top_k=8, scoring=K.SIGMOID, select=K.NOAUX_TC, n_group=8, topk_group=4,
+                           norm_topk=True, scale=2.5, bias=bias)),
+        "group": (lg, dict(top_k=6, select=K.GROUP_LIMITED, n_group=8, topk_group=3, scale=1.5)),
+        "starved": (lg[:16], dict(top_k=4, select=K.GROUP_LIMITED, n_group=8, topk_group=1)),
+    }
+
+
+@pytest.mark.parametrize("case", sorted(route_cases()))
+def test_router_matches_the_oracle(ctx, case):
+    logits, kw = route_cases()[case]
+    say("route", case)
+    n = logits.size
+    cfg = {k: v for k, v in kw.items() if k != "top_k"}
+    moe = K.Moe(ctx, n, kw["top_k"], 64, 32, **cfg)
+    got = moe.route(logits, 1)[0]
+    want = O.route(logits, **kw)
+    assert [e for e, _ in got] == [e for e, _ in want]
+    np.testing.assert_allclose([w for _, w in got], [w for _, w in want], rtol=1e-6, atol=0)
+    if case == "kat":  # ffn.rs:1128-1147
+        assert [e for e, _ in got] == [7, 1, 4, 2]
+    # many tokens at once, each its own route
+    m = 37
+    many = np.concatenate([np.roll(logits, i) for i in range(m)])
+    for i, picks in enumerate(moe.route(many, m)):
+        ref = O.route(np.roll(logits, i), **kw)
+        assert [e for e, _ in picks] == [e for e, _ in ref]
+
+
+def build(ctx, hidden, inter, n_exp, top_k, seed, sh_inter=0, **kw):
+    """A q8 MoE layer with weights ~ N(0, 0.02) (router N(0, 0.5) so routes are decisive)."""
+    q = lambda s, r, c, sc: O.quantize_q8(O.normal(s, r * c, sc), r, c)
+    router = q(seed, n_exp, hidden, 0.5)
+    gate = q(seed + 1, n_exp * inter, hidden, 0.02)
+    up = q(seed + 2, n_exp * inter, hidden, 0.02)
+    down = q(seed + 3, n_exp * hidden, inter, 0.02)
+    shared = None
+    moe = K.Moe(ctx, n_exp, top_k, hidden, inter, **kw)
+    moe.set_router(K.Weight.from_q8(ctx, n_exp, hidden, *router))
+    gs, gq = gate[0].reshape(n_exp, -1), gate[1].reshape(n_exp, -1)
+    us, uq = up[0].reshape(n_exp, -1), up[1].reshape(n_exp, -1)
+    ds, dq = down[0].reshape(n_exp, -1), down[1].reshape(n_exp, -1)
+    for x in range(n_exp):
+        moe.set_expert(x, K.Weight.from_q8(ctx, inter, hidden, gs[x], gq[x]),
+                       K.Weight.from_q8(ctx, inter, hidden, us[x], uq[x]),
+                       K.Weight.from_q8(ctx, hidden, inter, ds[x], dq[x]))
+    if sh_inter:
+        sg, su, sd = q(seed + 4, sh_inter, hidden, 0.02), q(seed + 5, sh_inter, hidden, 0.02), \
+            q(seed + 6, hidden, sh_inter, 0.02)
+        moe.set_shared(K.Weight.from_q8(ctx, sh_inter, hidden, *sg), K.Weight.from_q8(ctx, sh_inter, hidden, *su),
+                       K.Weight.from_q8(ctx, hidden, sh_inter, *sd))
+        shared = (sg, su, sd, sh_inter)
+
+    def oracle(hs, m):
+        return O.moe_run_q8(hs, m, hidden, inter, n_exp, top_k, router, gate, up, down, shared, **kw)
+
+    return moe, oracle
+
+
+SMALL = dict(hidden=256, inter=128, n_exp=16, top_k=4, sh_inter=256)
+
+
+@pytest.mark.parametrize("m", [1, 2, 33, 200])
+def test_moe_matches_the_oracle(ctx, m):
+    say("moe small", m)
+    moe, oracle = build(ctx, seed=100, **SMALL)
+    hs = O.normal(7 + m, m * SMALL["hidden"])
+    close(moe.run(hs, m), oracle(hs, m), MOE_RTOL)
+
+
+def test_moe_without_a_shared_expert_and_with_starved_groups(ctx):
+    # group-limited routing that leaves fewer than top_k experts standing:
+    # unused pick slots must neither read out of bounds nor count
+    say("moe starved")
+    kw = dict(select=K.GROUP_LIMITED, n_group=8, topk_group=1, norm_topk=True)
+    moe, oracle = build(ctx, hidden=128, inter=64, n_exp=16, top_k=4, seed=200, **kw)
+    for m in (1, 9):
+        hs = O.normal(300 + m, m * 128)
+        close(moe.run(hs, m), oracle(hs, m), MOE_RTOL)
+
+
+def test_moe_decode_and_batch_agree_and_repeat(ctx):
+    say("moe decode vs batch")
+    moe, _ = build(ctx, seed=400, **SMALL)
+    m, h = 6, SMALL["hidden"]
+    hs = O.normal(9, m * h)
+    batch = moe.run(hs, m).reshape(m, h)
+    for i in range(m):
+        close(batch[i], moe.run(hs[i * h:(i + 1) * h], 1), MOE_RTOL)
+    np.testing.assert_array_equal(moe.run(hs, m).reshape(m, h), batch)
+    one = moe.run(hs[:h], 1)
+    np.testing.assert_array_equal(moe.run(hs[:h], 1), one)
+
+
+@pytest.mark.parametrize("m", [1, 512])
+def test_deepseek_v2_lite_layer(ctx, m):
+    # hidden 2048, 64 routed experts + 2 shared (one
+    # SwiGLU of width 2816), expert width 1408, top-6 softmax, no
+    # renormalisation, scale 1 -- decode (one token) and prefill (512)
+    say("moe deepseek", m)
+    moe, oracle = build(ctx, hidden=2048, inter=1408, n_exp=64, top_k=6, seed=500, sh_inter=2816)
+    hs = O.normal(600 + m, m * 2048)
+    rel = close(moe.run(hs, m), oracle(hs, m), MOE_RTOL)
+    say("moe deepseek rel err", m, f"{rel:.2e}")

@@ -581,3 +581,64 @@ def test_without_normalisation_the_weights_are_the_softmaxs_own():
 def test_route_ties_pick_the_first_index():
     picks = O.route(np.array([1.0, 2.0, 2.0, 0.0], np.float32), 2)
     assert [e for e, _ in picks] == [1, 2]
+
+
+def _moe_weights(hidden, inter, n_exp, seed, sh_inter=0):
+    q = lambda s, r, c, sc: O.quantize_q8(O.normal(s, r * c, sc), r, c)
+    router = q(seed, n_exp, hidden, 0.5)
+    gate = q(seed + 1, n_exp * inter, hidden, 0.05)
+    up = q(seed + 2, n_exp * inter, hidden, 0.05)
+    down = q(seed + 3, n_exp * hidden, inter, 0.05)
+    shared = None
+    if sh_inter:
+        shared = (q(seed + 4, sh_inter, hidden, 0.05), q(seed + 5, sh_inter, hidden, 0.05),
+                  q(seed + 6, hidden, sh_inter, 0.05), sh_inter)
+    return router, gate, up, down, shared
+
+
+def test_moe_tokens_together_equal_tokens_alone():
+    # prefill (grouped by expert, matmul_bt) against decode (matvec), bit for
+    # bit: matmul_bt's x86 row_dot is the same arithmetic as matvec's qrow
+    # (quant.rs:410-452, 865-907), and the mix adds in expert order either way
+    hidden, inter, n_exp, k, m = 64, 32, 8, 3, 5
+    r, g, u, d, sh = _moe_weights(hidden, inter, n_exp, 60, sh_inter=64)
+    hs = O.normal(70, m * hidden)
+    together = O.moe_run_q8(hs, m, hidden, inter, n_exp, k, r, g, u, d, sh).reshape(m, hidden)
+    for i in range(m):
+        alone = O.moe_run_q8(hs[i * hidden:(i + 1) * hidden], 1, hidden, inter, n_exp, k, r, g, u, d, sh)
+        np.testing.assert_array_equal(together[i], alone)
+
+
+def test_moe_is_the_weighted_sum_of_the_chosen_experts():
+    # y = shared(x) + sum_x w_x ffn_x(x) over the router's picks, in float64
+    # from the dequantised weights and the quantised activations
+    hidden, inter, n_exp, k = 64, 32, 8, 3
+    r, g, u, d, sh = _moe_weights(hidden, inter, n_exp, 80, sh_inter=32)
+    x = O.normal(90, hidden)
+    got = O.moe_run_q8(x, 1, hidden, inter, n_exp, k, r, g, u, d, sh)
+
+    def deq(sq, rows, cols):
+        s, q = sq
+        return (q.reshape(rows, cols).astype(np.float64) * np.repeat(s.reshape(rows, cols // 32), 32, axis=1))
+
+    def qx(v):
+        q, s, _ = O.qact(v.astype(np.float32))
+        return q.astype(np.float64) * np.repeat(s.astype(np.float64), 32)
+
+    def ffn(G, U, D, width, v):
+        a = qx(v)
+        gg, uu = G @ a, U @ a
+        h = gg / (1.0 + np.exp(-gg)) * uu
+        return D @ qx(h)
+
+    logits = deq(r, n_exp, hidden) @ qx(x)
+    picks = O.route(logits.astype(np.float32), k)
+    want = ffn(deq(sh[0], 32, hidden), deq(sh[1], 32, hidden), deq(sh[2], hidden, 32), 32, x)
+    Gs, Us, Ds = deq(g, n_exp * inter, hidden), deq(u, n_exp * inter, hidden), deq(d, n_exp * hidden, inter)
+    for e, w in sorted(picks):
+        want = want + w * ffn(Gs[e * inter:(e + 1) * inter], Us[e * inter:(e + 1) * inter],
+                              Ds[e * hidden:(e + 1) * hidden], inter, x)
+    scale = float(np.max(np.abs(want)))
+    # rounding only (measured 2e-7); a code of h landing on the other side of
+    # a rounding boundary between the two paths would show as ~1e-3
+    assert float(np.max(np.abs(got - want))) <= 1e-4 * scale
