@@ -309,6 +309,7 @@ def secondary(torch, K, ctx, stream, dev, gen, args):
     del g
 
     out["prefill_gemm"] = prefill(torch, K, ctx, stream, dev, gen, args)
+    out["moe_deepseek_v2_lite"] = moe(torch, K, ctx, stream, dev, gen, args)
 
     spec = K.Spec(14, 2, 64)
     att = {}
@@ -362,6 +363,62 @@ def prefill(torch, K, ctx, stream, dev, gen, args):
             del g, w
         del f, xs, y
     log(f"prefill gemm: {res}")
+    return res
+
+
+def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8):
+    """a DeepSeek-V2-Lite MoE layer at q8 (hidden 2048,
+    64 experts of width 1408 + a fused shared expert of width 2816, top-6
+    softmax routing).  Decode: one token through n_layers distinct layers
+    (weights ~ N(0, 0.02), router ~ N(0, 0.5), x ~ N(0, 1) per layer), HIP
+    graph; bytes = the router, the shared expert and the six chosen experts'
+    weights read once.  Prefill: 512 tokens through one layer, 2*M*N*K ops."""
+    hidden, inter, n_exp, k, sh = 2048, 1408, 64, 6, 2816
+    res = {}
+
+    def q8(rows, cols, sd=0.02):
+        f = torch.randn(rows, cols, device=dev, generator=gen) * sd
+        return K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8)
+
+    layers = []
+    with torch.cuda.stream(stream):
+        for _ in range(n_layers):
+            m = K.Moe(ctx, n_exp, k, hidden, inter)
+            m.set_router(q8(n_exp, hidden, 0.5))
+            for x in range(n_exp):
+                m.set_expert(x, q8(inter, hidden), q8(inter, hidden), q8(hidden, inter))
+            m.set_shared(q8(sh, hidden), q8(sh, hidden), q8(hidden, sh))
+            layers.append((m, torch.randn(hidden, device=dev, generator=gen), torch.empty(hidden, device=dev)))
+    torch.cuda.synchronize()
+
+    def q8b(r, c):
+        return r * c + 4 * r * c // 32
+
+    tok_bytes = q8b(n_exp, hidden) + 3 * q8b(sh, hidden) + k * 3 * q8b(inter, hidden) + 8 * hidden
+
+    def decode():
+        for m, x, y in layers:
+            m.run_dev(x.data_ptr(), 1, y.data_ptr())
+
+    g = Graph(torch, ctx, stream, decode)
+    s = g.time(max(5, args.steps // 5), 2) / n_layers
+    res["decode_1tok"] = {"us_per_layer": round(s * 1e6, 2), "GBps": round(tok_bytes / s / 1e9, 1),
+                          "bytes_per_layer": tok_bytes, "launches_per_layer": 5}
+    del g
+    m0 = layers[0][0]
+    M = 512
+    hs = torch.randn(M, hidden, device=dev, generator=gen)
+    ys = torch.empty(M, hidden, device=dev)
+
+    def pre():
+        m0.run_dev(hs.data_ptr(), M, ys.data_ptr())
+
+    g = Graph(torch, ctx, stream, pre)
+    s = g.time(max(3, args.steps // 10), 2)
+    ops = 2 * M * k * 3 * inter * hidden + 2 * M * 3 * sh * hidden
+    res["prefill_512tok"] = {"us": round(s * 1e6, 1), "TOPS": round(ops / s / 1e12, 2), "ops": ops}
+    del g
+    log(f"moe: {res}")
     return res
 
 

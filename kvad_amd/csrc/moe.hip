@@ -109,33 +109,28 @@ __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
         __syncthreads();
     }
 
-    // the picks, one at a time (ffn.rs:279-293)
+    // the picks (ffn.rs:279-293): the reference takes the largest choice,
+    // the lowest index on ties, until top_k are taken or none is left; that
+    // is the order of each valid expert's rank among the valid choices
     const int k = r.top_k < n ? r.top_k : n;
-    int got = 0;
-    for (int p = 0; p < k; p++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int i = lane; i < n; i += 64) {
-            const float v = s_choice[i];
-            if (v > -INFINITY && (bi == 0x7fffffff || v > bv)) bv = v, bi = i;
+    if (lane == 0) s_best = 0;
+    __syncthreads();
+    for (int i = lane; i < n; i += 64) {
+        const float v = s_choice[i];
+        if (!(v > -INFINITY)) continue;
+        int rank = 0;
+        for (int j = 0; j < n; j++) {
+            const float u = s_choice[j];
+            rank += u > -INFINITY && (u > v || (u == v && j < i));
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) bv = ov, bi = oi;
+        if (rank < k) {
+            s_pick_e[rank] = i;
+            s_pick_w[rank] = s_score[i];
+            atomicAdd(&s_best, 1);
         }
-        if (lane == 0) s_best = bi;
-        __syncthreads();
-        const int best = s_best;
-        if (best == 0x7fffffff) break;
-        if (lane == 0) {
-            s_pick_e[got] = best;
-            s_pick_w[got] = s_score[best];
-            s_choice[best] = -INFINITY;
-        }
-        got++;
-        __syncthreads();
     }
+    __syncthreads();
+    const int got = s_best;
 
     if (lane == 0) {
         const bool normalised = r.norm_topk && r.top_k > 1;
@@ -178,96 +173,118 @@ __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
 }
 
 // by_expert (ffn.rs:627-640): rows in expert order, tokens in order within an
-// expert.  One workgroup; thread x walks the picks for expert x.
-constexpr int GROUP_CHUNK = 8192;
+// expert.  One workgroup of 1024 threads.  The tokens fall into at most 64
+// runs; (1) each run's count per expert (LDS atomics: order
+// free), (2) each (expert, run)'s first row by a prefix over experts then
+// runs, (3) each pick's row = its run's first row for that expert plus the
+// picks of that expert by earlier tokens of the same run.
+constexpr int GROUP_THREADS = 1024;
+constexpr int GROUP_CELLS = 16384;  // runs x experts counters in LDS
 
-__global__ __launch_bounds__(256) void group_kernel(const int32_t *experts, const float *weights,
-                                                   const int32_t *count, int m, int top_k, int n_exp, int tile_m,
-                                                   int32_t *row_token, float *row_weight, int32_t *pos,
-                                                   int32_t *tiles) {
-    __shared__ int s_cnt[MAX_EXPERTS], s_off[MAX_EXPERTS];
-    __shared__ int s_e[GROUP_CHUNK];
-    const int tid = threadIdx.x, total = m * top_k;
-    for (int x = tid; x < n_exp; x += 256) s_cnt[x] = 0;
+__global__ __launch_bounds__(GROUP_THREADS) void group_kernel(const int32_t *experts, const float *weights,
+                                                             const int32_t *count, int m, int top_k, int n_exp,
+                                                             int tile_m, int nrun, int run_len,
+                                                             int32_t *row_token, float *row_weight, int32_t *pos,
+                                                             int32_t *tiles) {
+    __shared__ int s_cnt[GROUP_CELLS];  // [run][expert], then each cell's first row
+    __shared__ int s_tot[MAX_EXPERTS];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < nrun * n_exp; i += GROUP_THREADS) s_cnt[i] = 0;
     __syncthreads();
-    for (int i = tid; i < total; i += 256) {
+    for (int i = tid; i < m * top_k; i += GROUP_THREADS) {
         const int t = i / top_k, k = i % top_k;
-        if (k < count[t]) atomicAdd(&s_cnt[experts[i]], 1);
+        if (k < count[t]) atomicAdd(&s_cnt[(t / run_len) * n_exp + experts[i]], 1);
     }
     __syncthreads();
-    if (tid == 0) {
+    for (int x = tid; x < n_exp; x += GROUP_THREADS) {
+        int c = 0;
+        for (int r = 0; r < nrun; r++) c += s_cnt[r * n_exp + x];
+        s_tot[x] = c;
+    }
+    __syncthreads();
+    if (tid == 0) {  // expert offsets and the tile table, in expert order
         int off = 0, nt = 0;
         for (int x = 0; x < n_exp; x++) {
-            s_off[x] = off;
-            const int c = s_cnt[x];
+            const int c = s_tot[x];
             for (int r0 = 0; r0 < c; r0 += tile_m) {
                 tiles[1 + 3 * nt] = x;
                 tiles[2 + 3 * nt] = off + r0;
                 tiles[3 + 3 * nt] = c - r0 < tile_m ? c - r0 : tile_m;
                 nt++;
             }
+            s_tot[x] = off;
             off += c;
         }
         tiles[0] = nt;
     }
     __syncthreads();
-    int next[(MAX_EXPERTS + 255) / 256];
-#pragma unroll
-    for (int j = 0; j < (MAX_EXPERTS + 255) / 256; j++) next[j] = tid + 256 * j < n_exp ? s_off[tid + 256 * j] : 0;
-    for (int c0 = 0; c0 < total; c0 += GROUP_CHUNK) {
-        const int cn = total - c0 < GROUP_CHUNK ? total - c0 : GROUP_CHUNK;
-        __syncthreads();
-        for (int i = tid; i < cn; i += 256) {
-            const int t = (c0 + i) / top_k, k = (c0 + i) % top_k;
-            s_e[i] = k < count[t] ? experts[c0 + i] : -1;
+    for (int x = tid; x < n_exp; x += GROUP_THREADS) {  // first row of each (run, expert)
+        int row = s_tot[x];
+        for (int r = 0; r < nrun; r++) {
+            const int c = s_cnt[r * n_exp + x];
+            s_cnt[r * n_exp + x] = row;
+            row += c;
         }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < (MAX_EXPERTS + 255) / 256; j++) {
-            const int x = tid + 256 * j;
-            if (x >= n_exp) continue;
-            for (int i = 0; i < cn; i++) {
-                if (s_e[i] != x) continue;
-                const int row = next[j]++;
-                row_token[row] = (c0 + i) / top_k;
-                row_weight[row] = weights[c0 + i];
-                pos[c0 + i] = row;
-            }
+    }
+    __syncthreads();
+    for (int t = tid; t < m; t += GROUP_THREADS) {
+        const int run = t / run_len, t0 = run * run_len, n = count[t];
+        for (int k = 0; k < n; k++) {
+            const int x = experts[(size_t)t * top_k + k];
+            int rank = 0;
+            for (int u = t0; u < t; u++)
+                for (int j = 0; j < count[u]; j++) rank += experts[(size_t)u * top_k + j] == x;
+            const int row = s_cnt[run * n_exp + x] + rank;
+            row_token[row] = t;
+            row_weight[row] = weights[(size_t)t * top_k + k];
+            pos[(size_t)t * top_k + k] = row;
         }
     }
 }
 
 // out[t] = base[t] (or 0), then + w * y[row] over token t's picks in expert
-// order (the mix order, ffn.rs:775-805).  `pos` null: pick k's row is
-// t * top_k + k of picks already in expert order.
+// order (the mix order, ffn.rs:775-805).  `pos` null: the picks are already
+// in expert order and pick k's row is t * top_k + k.  Grid: (hidden / 256,
+// tokens); every load of a thread is independent, so they fly together.
 __global__ __launch_bounds__(256) void combine_kernel(const float *base, const float *y, const int32_t *experts,
                                                      const float *weights, const int32_t *count,
                                                      const int32_t *pos, int top_k, int hidden, float *out) {
-    const int t = blockIdx.x;
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
     const int n = count[t];
     int pe[MAX_TOPK], pr[MAX_TOPK];
     float pw[MAX_TOPK];
-    for (int k = 0; k < n; k++) {  // insertion sort by expert
-        const int e = experts[(size_t)t * top_k + k];
-        const int r = pos ? pos[(size_t)t * top_k + k] : t * top_k + k;
-        const float w = weights[(size_t)t * top_k + k];
-        int j = k;
-        while (j > 0 && pe[j - 1] > e) {
-            pe[j] = pe[j - 1];
-            pr[j] = pr[j - 1];
-            pw[j] = pw[j - 1];
-            j--;
-        }
-        pe[j] = e, pr[j] = r, pw[j] = w;
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; k++) {
+        const bool ok = k < n;
+        pe[k] = ok ? experts[(size_t)t * top_k + k] : 0x7fffffff;
+        pr[k] = ok ? (pos ? pos[(size_t)t * top_k + k] : t * top_k + k) : 0;
+        pw[k] = ok ? weights[(size_t)t * top_k + k] : 0.0f;
     }
-    for (int i = threadIdx.x; i < hidden; i += 256) {
-        float v = base ? base[(size_t)t * hidden + i] : 0.0f;
-        for (int k = 0; k < n; k++) {
-            const float p = pw[k] * y[(size_t)pr[k] * hidden + i];
+    if (pos) {  // into expert order: a fixed network, so the arrays stay in registers
+#pragma unroll
+        for (int a = 0; a < MAX_TOPK - 1; a++)
+#pragma unroll
+            for (int b = 0; b < MAX_TOPK - 1 - a; b++) {
+                const bool sw = pe[b] > pe[b + 1];
+                const int e0 = pe[b], r0 = pr[b];
+                const float w0 = pw[b];
+                pe[b] = sw ? pe[b + 1] : e0, pr[b] = sw ? pr[b + 1] : r0, pw[b] = sw ? pw[b + 1] : w0;
+                pe[b + 1] = sw ? e0 : pe[b + 1], pr[b + 1] = sw ? r0 : pr[b + 1], pw[b + 1] = sw ? w0 : pw[b + 1];
+            }
+    }
+    if (i >= hidden) return;
+    float yv[MAX_TOPK];
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; k++) yv[k] = k < n ? y[(size_t)pr[k] * hidden + i] : 0.0f;
+    float v = base ? base[(size_t)t * hidden + i] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; k++) {
+        if (k < n) {
+            const float p = pw[k] * yv[k];
             v = v + p;
         }
-        out[(size_t)t * hidden + i] = v;
     }
+    out[(size_t)t * hidden + i] = v;
 }
 
 size_t up256(size_t n) { return (n + 255) / 256 * 256; }
@@ -407,8 +424,8 @@ int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
         if ((rc = launch_gemv(ctx, moe->sdown->precision, &j, 1))) return rc;
     }
     // (5) out = shared, then + w * y in expert order
-    hipLaunchKernelGGL(combine_kernel, dim3(1), dim3(256), 0, ctx->stream, sh ? ys : nullptr, y, se, sw, cnt,
-                       nullptr, (int)k, (int)hid, out);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((hid + 255) / 256), 1), dim3(256), 0, ctx->stream,
+                       sh ? ys : nullptr, y, se, sw, cnt, nullptr, (int)k, (int)hid, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -463,8 +480,11 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     if ((rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits))) return rc;
     if ((rc = launch_route(ctx, route_args(moe, logits, pe, pw, cnt), (int)m))) return rc;
     // by_expert, and the tiles of the grouped GEMMs
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(256), 0, ctx->stream, pe, pw, cnt, (int)m, (int)k, (int)n,
-                       tile_m, row_token, row_weight, pos, tiles);
+    const int nrun_max = (int)(GROUP_CELLS / n) < 64 ? (int)(GROUP_CELLS / n) : 64;
+    const int run_len = (int)((m + nrun_max - 1) / nrun_max);
+    const int nrun = (int)((m + run_len - 1) / run_len);
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), 0, ctx->stream, pe, pw, cnt, (int)m, (int)k,
+                       (int)n, tile_m, nrun, run_len, row_token, row_weight, pos, tiles);
     KH_HIP(hipGetLastError());
     // the activations, quantised once for every expert and the shared one
     if ((rc = launch_qact(ctx, hs, m, hid, hq))) return rc;
@@ -494,8 +514,8 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     d.y = y;
     if ((rc = launch_gemm_q(ctx, moe->precision, d, (int)max_tiles, tile_m))) return rc;
     // out = shared, then + w * y per token in expert order
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)m), dim3(256), 0, ctx->stream, base, y, pe, pw, cnt, pos,
-                       (int)k, (int)hid, out);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((hid + 255) / 256), (unsigned)m), dim3(256), 0, ctx->stream,
+                       base, y, pe, pw, cnt, pos, (int)k, (int)hid, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
