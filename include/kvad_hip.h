@@ -178,6 +178,22 @@ int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t 
 int kh_attend_dev(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
                   const float *k, const float *v, size_t n_positions, float *out);
 
+/* ---- decode glue (device pointers, asynchronous on the context's stream) */
+
+/* tensor::rms_norm (tensor.rs:329-333) over m rows of n:
+ * out = x * (1 / sqrt(mean(x^2) + eps)) * w. */
+int kh_rms_norm_dev(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out);
+/* Rope::apply (tensor.rs:463-472; interleaved = 0, pairs i and i+half) or
+ * Rope::apply_interleaved (tensor.rs:437-446; pairs 2i and 2i+1), in place on
+ * x [m][n_vec][2*half], row r at position pos0 + r.  cos_t/sin_t are the
+ * caller's tables [max_pos][half] (Rope::tables, tensor.rs:377-387). */
+int kh_rope_dev(kh_ctx *ctx, const float *cos_t, const float *sin_t, size_t half, float *x, size_t m,
+                size_t n_vec, size_t pos0, int interleaved);
+/* swiglu_inplace (tensor.rs:344-350): gate[i] = silu(gate[i]) * up[i]. */
+int kh_swiglu_dev(kh_ctx *ctx, float *gate, const float *up, size_t n);
+/* softmax_inplace (tensor.rs:297-308) over each of m rows of n, in place. */
+int kh_softmax_dev(kh_ctx *ctx, float *x, size_t m, size_t n);
+
 /* ---- mixture of experts ----------------------------------------------- */
 
 /* Router scoring (Scoring, model/ffn.rs:173-177) and selection (Select, ffn.rs:179-195). */

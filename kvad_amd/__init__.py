@@ -48,6 +48,14 @@ def _load() -> C.CDLL:
         raise ImportError(
             f"{LIB_PATH} is missing: build it with `python kvad_amd/build.py` "
             "(there is no CPU fallback for this path)")
+    # torch ships its own HIP runtime under the same soname.  Loaded first, it
+    # serves this library too, so a process that also uses torch for device
+    # memory has one runtime; loaded second, it would start a second runtime
+    # beside the system one and find no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     return C.CDLL(str(LIB_PATH))
 
 
@@ -97,6 +105,10 @@ _SIGS = {
     "kh_kv_layer_ptrs": (C.c_int, [_p, _sz, C.POINTER(_p), C.POINTER(_p)]),
     "kh_attend": (C.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "kh_attend_dev": (C.c_int, [_p, _sz, _sz, _sz, _p, _p, _p, _sz, _p]),
+    "kh_rms_norm_dev": (C.c_int, [_p, _p, _p, _sz, _sz, C.c_float, _p]),
+    "kh_rope_dev": (C.c_int, [_p, _p, _p, _sz, _p, _sz, _sz, _sz, C.c_int]),
+    "kh_swiglu_dev": (C.c_int, [_p, _p, _p, _sz]),
+    "kh_softmax_dev": (C.c_int, [_p, _p, _sz, _sz]),
     "kh_moe_new": (C.c_int, [_p, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, C.c_float, _p,
                              C.POINTER(_p)]),
     "kh_moe_free": (C.c_int, [_p]),
@@ -478,3 +490,22 @@ class Moe:
             self.free()
         except Exception:
             pass
+
+
+# ---- decode glue on device pointers (tensor.rs:297-472) ----------------------
+
+def rms_norm_dev(ctx: Context, x_ptr: int, w_ptr: int, m: int, n: int, eps: float, out_ptr: int) -> None:
+    _check(lib.kh_rms_norm_dev(ctx.h, x_ptr, w_ptr, m, n, eps, out_ptr))
+
+
+def rope_dev(ctx: Context, cos_ptr: int, sin_ptr: int, half: int, x_ptr: int, m: int, n_vec: int, pos0: int,
+             interleaved: bool = False) -> None:
+    _check(lib.kh_rope_dev(ctx.h, cos_ptr, sin_ptr, half, x_ptr, m, n_vec, pos0, int(interleaved)))
+
+
+def swiglu_dev(ctx: Context, gate_ptr: int, up_ptr: int, n: int) -> None:
+    _check(lib.kh_swiglu_dev(ctx.h, gate_ptr, up_ptr, n))
+
+
+def softmax_dev(ctx: Context, x_ptr: int, m: int, n: int) -> None:
+    _check(lib.kh_softmax_dev(ctx.h, x_ptr, m, n))

@@ -71,6 +71,7 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         "kvo_swiglu": (None, [_p, _p, _sz]),
         "kvo_rope_tables": (None, [_sz, _sz, _f, _p, _p]),
         "kvo_rope_apply": (None, [_p, _p, _sz, _p, _sz]),
+        "kvo_rope_apply_interleaved": (None, [_p, _p, _sz, _p, _sz]),
         "kvo_attend": (None, [_sz, _sz, _sz, _p, _p, _p, _sz, _p]),
         "kvo_route": (C.c_int, [_p, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, _f, _p, _p, _p]),
         "kvo_moe_run_q8": (None, [_p, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, _f, _p]
@@ -318,6 +319,12 @@ def rope_tables(head_dim: int, max_pos: int, theta: float):
 def rope_apply(cos_t, sin_t, half: int, x, pos: int) -> np.ndarray:
     x = _c(x, np.float32).copy()
     lib.kvo_rope_apply(P(cos_t), P(sin_t), half, P(x), pos)
+    return x
+
+
+def rope_apply_interleaved(cos_t, sin_t, half: int, x, pos: int) -> np.ndarray:
+    x = _c(x, np.float32).copy()
+    lib.kvo_rope_apply_interleaved(P(cos_t), P(sin_t), half, P(x), pos)
     return x
 
 

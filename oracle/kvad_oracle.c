@@ -814,6 +814,19 @@ void kvo_rope_apply(const float *cos_t, const float *sin_t, size_t half, float *
     }
 }
 
+void kvo_rope_apply_interleaved(const float *cos_t, const float *sin_t, size_t half, float *x, size_t pos) {
+    /* tensor.rs:437-446: pairs 2i and 2i + 1 */
+    size_t base = pos * half;
+    for (size_t i = 0; i < half; i++) {
+        float c = cos_t[base + i], s = sin_t[base + i];
+        float a = x[2 * i], b = x[2 * i + 1];
+        float p1 = a * c, p2 = b * s;
+        x[2 * i] = p1 - p2;
+        float p3 = b * c, p4 = a * s;
+        x[2 * i + 1] = p3 + p4;
+    }
+}
+
 /* ------------------------------------------------------------------------- */
 /* attention                                                                  */
 /* ------------------------------------------------------------------------- */

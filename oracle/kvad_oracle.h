@@ -97,6 +97,7 @@ void kvo_rms_norm(const float *x, const float *w, size_t n, float eps, float *ou
 void kvo_swiglu(float *gate, const float *up, size_t n);              /* tensor.rs:344-350 */
 void kvo_rope_tables(size_t head_dim, size_t max_pos, float theta, float *cos_t, float *sin_t); /* :390-407 */
 void kvo_rope_apply(const float *cos_t, const float *sin_t, size_t half, float *x, size_t pos); /* :463-472 */
+void kvo_rope_apply_interleaved(const float *cos_t, const float *sin_t, size_t half, float *x, size_t pos); /* :437-446 */
 
 /* ---- decode attention: model::attend (model/mod.rs:769-819) ---- */
 /* k_cache/v_cache rows are n_kv_head*head_dim wide; out is n_head*head_dim. */

@@ -642,3 +642,16 @@ def test_moe_is_the_weighted_sum_of_the_chosen_experts():
     # rounding only (measured 2e-7); a code of h landing on the other side of
     # a rounding boundary between the two paths would show as ~1e-3
     assert float(np.max(np.abs(got - want))) <= 1e-4 * scale
+
+
+def test_interleaved_rope_is_the_half_split_rope_a_permutation_apart():
+    # tensor.rs:430-436: the two conventions differ by a permutation of the
+    # coordinates, applied to the vector before and undone after
+    hd = 64
+    c, s = O.rope_tables(hd, 20, 1e6)
+    x = O.normal(3, hd)
+    perm = np.r_[0:hd:2, 1:hd:2]  # interleaved pair (2i, 2i+1) -> (i, i + half)
+    for pos in (0, 1, 7, 19):
+        inter = O.rope_apply_interleaved(c, s, hd // 2, x, pos)
+        split = O.rope_apply(c, s, hd // 2, x[perm], pos)
+        np.testing.assert_array_equal(inter[perm], split)
