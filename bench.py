@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary (q8, attention) figures")
+    ap.add_argument("--counters", type=int, default=0, metavar="MIB",
+                    help="only run a MIB-sized copy and two eager steps of the GEMV kernels (for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -162,10 +164,6 @@ def main() -> int:
             many([L["gate"], L["up"]], [L["h"].data_ptr()] * 2, [L["y_gate"].data_ptr(), L["y_up"].data_ptr()])
             L["down"].matvec_bt_dev(L["m"].data_ptr(), L["y_down"].data_ptr())
 
-    g_step = Graph(torch, ctx, stream, step)
-    sec = g_step.time(args.steps, args.warmup)
-    log(f"step: {sec * 1e3:.3f} ms, {step_bytes / sec / 1e9:.1f} GB/s")
-
     # ---- the GEMV kernels alone: down's input pre-quantised ---------------
     with torch.cuda.stream(stream):
         for L in layers:
@@ -182,6 +180,29 @@ def main() -> int:
             L["o"].matvec_bt_dev(L["a"].data_ptr(), L["y_o"].data_ptr())
             many([L["gate"], L["up"]], [L["h"].data_ptr()] * 2, [L["y_gate"].data_ptr(), L["y_up"].data_ptr()])
             L["down"].matvec_q_dev(*[t.data_ptr() for t in L["mq"]], L["y_down"].data_ptr())
+
+    if args.counters:
+        # a workload for rocprofv3 --pmc: a streaming kernel of known traffic
+        # (dst = 2 * src over MIB MiB each way, far past the 256 MB cache: the
+        # counters' calibration), then the GEMV kernels launched eagerly
+        n = args.counters << 18  # MiB -> floats
+        src = torch.ones(n, device=dev)
+        dst = torch.empty(n, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                kernels()
+        torch.cuda.synchronize()
+        print(json.dumps({"counters_run": {"calibration_bytes_each_way": 4 * n, "calibration_runs": 3, "gemv_steps": 2,
+                                           "launches_per_step": launches, "bytes_per_step": step_bytes}}))
+        return 0
+
+    g_step = Graph(torch, ctx, stream, step)
+    sec = g_step.time(args.steps, args.warmup)
+    log(f"step: {sec * 1e3:.3f} ms, {step_bytes / sec / 1e9:.1f} GB/s")
 
     g_k = Graph(torch, ctx, stream, kernels)
     ksec = g_k.time(args.steps, args.warmup)
@@ -231,7 +252,7 @@ def main() -> int:
                                 "down 4096x14336", "launches_per_step": launches,
                    "bytes_per_step": step_bytes, "launch": "hip graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "kernel": "gemv_kernel<Q4K,*>", "avg_launch_us": round(avg_launch * 1e6, 3),
                      "bytes_per_launch": step_bytes // launches},
         "cpu_baseline": cpu,
@@ -240,6 +261,20 @@ def main() -> int:
     print(json.dumps(result), flush=True)
     ctx.set_stream(None)
     return 0
+
+
+TRAFFIC = ROOT / "profiles" / "gemv_q4k_llama3_8b_traffic.json"
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch of this workload, from the rocprofv3 --pmc
+    passes recorded in profiles/ (FETCH_SIZE + WRITE_SIZE per dispatch, each
+    scaled by what the counter reads for a plain copy of known size); null
+    until those passes exist."""
+    try:
+        return json.loads(TRAFFIC.read_text())["bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def secondary(torch, K, ctx, stream, dev, gen, args):
