@@ -478,7 +478,7 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(JobTable tab) {
 }
 
 struct Plan {
-    int cpl, r;
+    int cpl, r, wg;  // chunks per lane per segment, rows per wave-step, workgroups per CU
 };
 
 int env_int(const char *name, int dflt) {
@@ -486,17 +486,27 @@ int env_int(const char *name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-// Chunks per lane per segment (CPL) and rows per wave-step (R).
-Plan plan_for(int prec, int maxC, int rows_total, int cu_count) {
+// Launch shape from a sweep over Llama-3-8B and Qwen2.5-0.5B shapes with
+// weights far larger than the cache: R = 4 rows per wave-step for short rows
+// (1 for very tall launches of rows two chunks per lane or wider, where
+// balance across waves matters more), fewer for short matrices so there are
+// enough waves; one workgroup per CU for Q4_K with a wide activation (each
+// workgroup stages it in LDS), three for very tall launches, else two.
+Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
     int cpl = (maxC + WAVE - 1) / WAVE;
     if (cpl < 1) cpl = 1;
     if (cpl > 8) cpl = 8;  // wider rows take several segments
+    const bool tall = rows_total >= 16384 && cpl >= 2;
     int r = cpl == 1 || cpl == 2 ? 4 : cpl <= 4 ? 2 : 1;
+    if (tall) r = 1;
     // short matrices: fewer rows per wave, more waves
     while (r > 1 && (rows_total + r - 1) / r < 8 * cu_count) r /= 2;
-    int forced = env_int("KVAD_GEMV_R", 0);  // tuning knob
+    int forced = env_int("KVAD_GEMV_R", 0);  // tuning knobs
     if (forced == 1 || (forced == 2 && cpl <= 4) || (forced == 4 && cpl <= 2)) r = forced;
-    return {cpl, r};
+    int wg = maxCols >= 8192 && prec == KH_Q4K ? 1 : tall ? 3 : 2;
+    const int fw = env_int("KVAD_GEMV_WG_PER_CU", 0);
+    if (fw > 0) wg = fw;
+    return {cpl, r, wg};
 }
 
 template <int PREC, int CPL, int R>
@@ -511,13 +521,13 @@ void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, bool d
 template <int PREC>
 int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_total, bool dots) {
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    Plan p = plan_for(PREC, maxC, rows_total, cu);
+    Plan p = plan_for(PREC, maxC, maxCols, rows_total, cu);
     for (int i = 0; i < tab.n; i++) {
         size_t wb = (size_t)tab.j[i].rows * tab.j[i].cols;
         if (wb >= 0xfff00000ull) return fail(KH_DECLINED, "matvec: weights of 4 GiB or more are not addressed here");
     }
     // workgroups: about `wg_per_cu` per CU over the launch, shared out by rows
-    const int cap_wg = env_int("KVAD_GEMV_WG_PER_CU", 2) * cu;
+    const int cap_wg = p.wg * cu;
     int blocks = 0;
     for (int i = 0; i < tab.n; i++) {
         const int groups = (tab.j[i].rows + p.r - 1) / p.r;
