@@ -231,6 +231,48 @@ int kh_moe_run_dev(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *o
 int kh_moe_route(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
                  int32_t *count);
 
+/* ---- a device-resident decoder (Llama family) ------------------------- */
+
+/* Spec (model/mod.rs:286-330) of a Llama-family decoder: Qwen2/2.5, Llama,
+ * Qwen3 dense (llama.rs).  n_ctx bounds the device KV cache. */
+typedef struct {
+    size_t n_layer, n_embd, n_head, n_kv_head, head_dim, n_ff, vocab, n_ctx;
+    float eps;
+    int rope_interleaved; /* 0: Rope::apply (HF half split), 1: apply_interleaved */
+} kh_llm_spec;
+
+typedef struct kh_llm kh_llm;
+
+/* A session over the model (the Session trait's device-resident backend,
+ * model/mod.rs:839-976): weights as borrowed handles, the KV cache in HBM,
+ * the greedy next token chosen on the device. */
+int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out);
+int kh_llm_free(kh_llm *m);
+/* Block l (llama.rs:139-200): q [n_head*hd, n_embd], k/v [n_kv*hd, n_embd],
+ * o [n_embd, n_head*hd], gate/up [n_ff, n_embd], down [n_embd, n_ff]; norms
+ * and biases are host vectors, copied (biases and q/k norms may be NULL). */
+int kh_llm_set_layer(kh_llm *m, size_t l, const kh_weight *q, const kh_weight *k, const kh_weight *v,
+                     const kh_weight *o, const kh_weight *gate, const kh_weight *up, const kh_weight *down,
+                     const float *attn_norm, const float *mlp_norm, const float *q_b, const float *k_b,
+                     const float *v_b, const float *q_norm, const float *k_norm);
+/* The ends (llama.rs:384-415): embedding [vocab, n_embd], final norm (host),
+ * lm_head or NULL when tied to the embedding. */
+int kh_llm_set_ends(kh_llm *m, const kh_weight *embed, const float *final_norm, const kh_weight *lm_head);
+/* RoPE tables from Rope::tables (tensor.rs:377-387), host [max_pos, hd/2]. */
+int kh_llm_set_rope(kh_llm *m, const float *cos_t, const float *sin_t, size_t max_pos);
+/* Session::forward for one token at the next position: logits [vocab] (host,
+ * may be NULL) and the greedy next token (sampler::argmax, sampler.rs:217). */
+int kh_llm_forward(kh_ctx *ctx, kh_llm *m, int32_t token, float *logits, int32_t *next);
+/* n greedy steps from `token`, one captured HIP graph replayed per token;
+ * tokens[n] receives the tokens generated. */
+int kh_llm_generate(kh_ctx *ctx, kh_llm *m, int32_t token, size_t n, int32_t *tokens);
+/* n more replays of the captured step from the device state as it stands,
+ * asynchronous, nothing copied back (for timing after kh_llm_generate). */
+int kh_llm_generate_launch(kh_ctx *ctx, kh_llm *m, size_t n);
+/* Session::cached / truncate (model/mod.rs:860-880; KvCache::truncate keeps a prefix). */
+int kh_llm_len(const kh_llm *m, size_t *len);
+int kh_llm_truncate(kh_llm *m, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,7 @@ import numpy as np
 
 __all__ = [
     "F32", "Q8", "Q4", "Q4K", "KvadError", "Declined", "lib", "Context", "Weight", "matvec_many",
-    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
+    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "Llm", "LlmSpec", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
 ]
 
 F32, Q8, Q4, Q4K = 0, 1, 2, 3
@@ -109,6 +109,16 @@ _SIGS = {
     "kh_rope_dev": (C.c_int, [_p, _p, _p, _sz, _p, _sz, _sz, _sz, C.c_int]),
     "kh_swiglu_dev": (C.c_int, [_p, _p, _p, _sz]),
     "kh_softmax_dev": (C.c_int, [_p, _p, _sz, _sz]),
+    "kh_llm_new": (C.c_int, [_p, _p, C.POINTER(_p)]),
+    "kh_llm_free": (C.c_int, [_p]),
+    "kh_llm_set_layer": (C.c_int, [_p, _sz] + [_p] * 14),
+    "kh_llm_set_ends": (C.c_int, [_p, _p, _p, _p]),
+    "kh_llm_set_rope": (C.c_int, [_p, _p, _p, _sz]),
+    "kh_llm_forward": (C.c_int, [_p, _p, C.c_int32, _p, _p]),
+    "kh_llm_generate": (C.c_int, [_p, _p, C.c_int32, _sz, _p]),
+    "kh_llm_generate_launch": (C.c_int, [_p, _p, _sz]),
+    "kh_llm_len": (C.c_int, [_p, C.POINTER(_sz)]),
+    "kh_llm_truncate": (C.c_int, [_p, _sz]),
     "kh_moe_new": (C.c_int, [_p, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, C.c_float, _p,
                              C.POINTER(_p)]),
     "kh_moe_free": (C.c_int, [_p]),
@@ -509,3 +519,70 @@ def swiglu_dev(ctx: Context, gate_ptr: int, up_ptr: int, n: int) -> None:
 
 def softmax_dev(ctx: Context, x_ptr: int, m: int, n: int) -> None:
     _check(lib.kh_softmax_dev(ctx.h, x_ptr, m, n))
+
+
+class LlmSpec(C.Structure):
+    """kh_llm_spec: a Llama-family decoder's sizes (model/mod.rs:286-330)."""
+    _fields_ = [(n, C.c_size_t) for n in ("n_layer", "n_embd", "n_head", "n_kv_head", "head_dim", "n_ff", "vocab",
+                                         "n_ctx")] + [("eps", C.c_float), ("rope_interleaved", C.c_int)]
+
+
+class Llm:
+    """A device-resident decoder session (the Session trait's device backend,
+    model/mod.rs:839-976) over borrowed Weight handles (kept referenced here)."""
+
+    def __init__(self, ctx: Context, **spec):
+        self.ctx = ctx
+        self.spec = LlmSpec(**spec)
+        self.h = C.c_void_p()
+        _check(lib.kh_llm_new(ctx.h, C.byref(self.spec), C.byref(self.h)))
+        self._keep = {}
+
+    def set_layer(self, l: int, q, k, v, o, gate, up, down, attn_norm, mlp_norm, q_b=None, k_b=None, v_b=None,
+                  q_norm=None, k_norm=None) -> None:
+        vec = [None if a is None else _f32(a) for a in (attn_norm, mlp_norm, q_b, k_b, v_b, q_norm, k_norm)]
+        _check(lib.kh_llm_set_layer(self.h, l, q.h, k.h, v.h, o.h, gate.h, up.h, down.h, *[_ptr(a) for a in vec]))
+        self._keep[l] = (q, k, v, o, gate, up, down)
+
+    def set_ends(self, embed, final_norm, lm_head=None) -> None:
+        fn = _f32(final_norm)
+        _check(lib.kh_llm_set_ends(self.h, embed.h, _ptr(fn), None if lm_head is None else lm_head.h))
+        self._keep["ends"] = (embed, lm_head)
+
+    def set_rope(self, cos_t, sin_t, max_pos: int) -> None:
+        c, s = _f32(cos_t), _f32(sin_t)
+        _check(lib.kh_llm_set_rope(self.h, _ptr(c), _ptr(s), max_pos))
+
+    def forward(self, token: int, want_logits: bool = True):
+        """(logits or None, next token) for one token at the next position."""
+        logits = np.empty(self.spec.vocab, np.float32) if want_logits else None
+        nxt = C.c_int32()
+        _check(lib.kh_llm_forward(self.ctx.h, self.h, token, _ptr(logits), C.byref(nxt)))
+        return logits, nxt.value
+
+    def generate(self, token: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.int32)
+        _check(lib.kh_llm_generate(self.ctx.h, self.h, token, n, _ptr(out)))
+        return out
+
+    def generate_launch(self, n: int) -> None:
+        _check(lib.kh_llm_generate_launch(self.ctx.h, self.h, n))
+
+    def __len__(self) -> int:
+        n = _sz()
+        _check(lib.kh_llm_len(self.h, C.byref(n)))
+        return n.value
+
+    def truncate(self, n: int) -> None:
+        _check(lib.kh_llm_truncate(self.h, n))
+
+    def free(self) -> None:
+        if self.h:
+            lib.kh_llm_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -89,6 +89,10 @@ struct AttnArgs {
     size_t kbytes, vbytes;    // readable bytes of the k and v arrays
     int n_head, group, gc;    // group = n_head / n_kv_head; gc = heads per workgroup
     int L, P, nsplit;
+    // when set, the length is read here (+ plus_one) and L/nsplit above are
+    // the launch's maxima; splits past the length return at once
+    const int32_t *len_dev;
+    int plus_one;
     float scale;
     // per split, [nsplit][n_head]: local max, sum, smallest score; and acc
     float *pm, *pl, *pmin, *pacc;
@@ -164,10 +168,13 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane & 15, row = tid >> 4;
+    const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
+    const int nsplit = (L + P - 1) / P;
+    if (split >= nsplit) return;
     const int t0 = split * P;
-    const int n = min(a.L - t0, P);
-    const bool whole = a.nsplit == 1;
-    const rsrc_t K = rsrc(a.k, a.kbytes), V = rsrc(a.v, a.vbytes);
+    const int n = min(L - t0, P);
+    const bool whole = nsplit == 1;
+    const rsrc_t K = rsrc(a.k, (size_t)L * a.kstride * 4), V = rsrc(a.v, (size_t)L * a.vstride * 4);
 
     __shared__ float s_acc[4][G][HD];  // per-wave totals
     __shared__ float s_st[3][4][G];    // per-wave max, sum, smallest score
@@ -359,7 +366,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     constexpr int DPL = HD / 16;
     constexpr int NQ = HD / 4, NSG = 256 / NQ;  // float4 slices of a row; split groups
     const int h = blockIdx.x, tid = threadIdx.x;
-    const int ns = a.nsplit, n_head = a.n_head;
+    const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
+    const int ns = (L + a.P - 1) / a.P, n_head = a.n_head;
+    if (ns <= 1) return;  // the split kernel finished a single split itself
     __shared__ float s_red[256];
     __shared__ float s_c[MAX_SPLITS];           // exp(m_j - M)
     __shared__ __align__(16) float s_acc[NSG][HD];
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     const float thr = M + logf(S) - 18.420681f + 1.0f;
     if (lo < thr) {
         const int group16 = tid >> 4, sub = tid & 15, kvh = h / a.group;
-        const rsrc_t K = rsrc(a.k, a.kbytes), V = rsrc(a.v, a.vbytes);
+        const rsrc_t K = rsrc(a.k, (size_t)L * a.kstride * 4), V = rsrc(a.v, (size_t)L * a.vstride * 4);
         float qr[1][DPL];
 #pragma unroll
         for (int d = 0; d < DPL; d++) qr[0][d] = a.q[(size_t)h * HD + sub * DPL + d];
@@ -432,7 +441,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
             const int need = s_need;
             __syncthreads();
             if (!need) continue;
-            const int tj = j * a.P, nj = min(a.L - tj, a.P);
+            const int tj = j * a.P, nj = min(L - tj, a.P);
             for (int base = 0; base < nj; base += 16) {
                 const int t = tj + base + group16;
                 if (base + group16 >= nj) continue;  // whole 16-lane rows drop out together
@@ -500,18 +509,20 @@ void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
 
 }  // namespace
 
-int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
-                  const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out) {
+namespace {
+
+// The launch for n_positions (or, with a device length, for at most that
+// many): split size, partial buffers carved from ws.
+int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
+          const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out) {
     if (n_kv_head <= 0 || n_head <= 0 || n_head % n_kv_head != 0)
         return fail(KH_EINVAL, "attend: n_head must be a positive multiple of n_kv_head");
     if (head_dim != 64 && head_dim != 128)
         return fail(KH_DECLINED, "attend: head_dim other than 64 or 128 runs on the CPU");
-    if (n_positions == 0) return launch_fill(ctx, out, (size_t)n_head * head_dim, 0.0f);
     // 32-bit buffer offsets, including a split's overhang past the last row
     if ((n_positions + 256) * kstride * 4 >= 0xffffffffull || (n_positions + 256) * vstride * 4 >= 0xffffffffull)
         return fail(KH_DECLINED, "attend: caches of 4 GiB or more per layer are not addressed here");
-
-    AttnArgs a{};
+    a = AttnArgs{};
     a.q = q;
     a.k = k;
     a.v = v;
@@ -542,31 +553,71 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     a.nsplit = (int)((n_positions + P - 1) / P);
     a.scale = 1.0f / sqrtf((float)head_dim);  // mod.rs:777
     a.out = out;
+    return KH_OK;
+}
 
-    if (a.nsplit > 1) {
-        const size_t ns = (size_t)a.nsplit * n_head;
-        const size_t bytes = 4 * (3 * ns + ns * head_dim) + 1024;
-        int rc = ensure(ctx, ctx->ws, bytes);
-        if (rc) return rc;
-        float *p = static_cast<float *>(ctx->ws.ptr);
-        a.pm = p, p += ns;
-        a.pl = p, p += ns;
-        a.pmin = p, p += ns;
-        a.pacc = p;
-    }
+void carve(AttnArgs &a, void *ws, int head_dim) {
+    const size_t ns = (size_t)a.nsplit * a.n_head;
+    float *p = static_cast<float *>(ws);
+    a.pm = p, p += ns;
+    a.pl = p, p += ns;
+    a.pmin = p, p += ns;
+    a.pacc = p;
+    (void)head_dim;
+}
 
-    dim3 grid(a.nsplit, n_hg);
+int run(kh_ctx *ctx, const AttnArgs &a, int head_dim) {
+    dim3 grid(a.nsplit, a.n_head / a.gc);
     if (head_dim == 64) launch_split<64>(a, grid, ctx->stream);
     else launch_split<128>(a, grid, ctx->stream);
     KH_HIP(hipGetLastError());
     if (a.nsplit > 1) {
         if (head_dim == 64)
-            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(n_head), dim3(256), 0, ctx->stream, a);
+            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(a.n_head), dim3(256), 0, ctx->stream, a);
         else
-            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(n_head), dim3(256), 0, ctx->stream, a);
+            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(a.n_head), dim3(256), 0, ctx->stream, a);
         KH_HIP(hipGetLastError());
     }
     return KH_OK;
+}
+
+}  // namespace
+
+size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions) {
+    (void)n_kv_head;
+    const size_t ns = (max_positions + 15) / 16 * (size_t)n_head;  // the smallest split size bounds the count
+    return 4 * (3 * ns + ns * head_dim) + 1024;
+}
+
+int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
+                  const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out) {
+    if (n_positions == 0) {
+        if (n_kv_head <= 0 || n_head <= 0 || n_head % n_kv_head != 0)
+            return fail(KH_EINVAL, "attend: n_head must be a positive multiple of n_kv_head");
+        return launch_fill(ctx, out, (size_t)n_head * head_dim, 0.0f);
+    }
+    AttnArgs a;
+    int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, k, v, kstride, vstride, n_positions, out);
+    if (rc) return rc;
+    if (a.nsplit > 1) {
+        const size_t ns = (size_t)a.nsplit * n_head;
+        if ((rc = ensure(ctx, ctx->ws, 4 * (3 * ns + ns * head_dim) + 1024))) return rc;
+        carve(a, ctx->ws.ptr, head_dim);
+    }
+    return run(ctx, a, head_dim);
+}
+
+int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
+                         const float *v, size_t kstride, size_t vstride, const int32_t *len_dev, int plus_one,
+                         size_t max_positions, float *out, void *ws) {
+    if (max_positions == 0) return fail(KH_EINVAL, "attend: no positions");
+    AttnArgs a;
+    int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, k, v, kstride, vstride, max_positions, out);
+    if (rc) return rc;
+    a.len_dev = len_dev;
+    a.plus_one = plus_one;
+    carve(a, ws, head_dim);
+    return run(ctx, a, head_dim);
 }
 
 }  // namespace kh

@@ -87,6 +87,35 @@ struct kh_moe {
     bool dirty = true;                         // tables need uploading
 };
 
+// A device-resident Llama-family decoder (crates/llm/src/model/llama.rs).
+struct kh_llm {
+    kh_ctx *ctx = nullptr;
+    kh_llm_spec spec{};
+    struct Layer {
+        const kh_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+        const kh_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+        float *attn_norm = nullptr, *mlp_norm = nullptr;     // device [n_embd]
+        float *q_b = nullptr, *k_b = nullptr, *v_b = nullptr;  // device biases or null
+        float *q_norm = nullptr, *k_norm = nullptr;          // device [head_dim] or null
+    };
+    std::vector<Layer> layers;
+    const kh_weight *embed = nullptr, *head = nullptr;       // head null: tied to embed
+    float *final_norm = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;          // [n_ctx, head_dim/2]
+    std::vector<float *> kc, vc;                             // per layer [n_ctx, kv_dim]
+    float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *u = nullptr,
+          *logits = nullptr;
+    kh::QAct hq{};
+    int32_t *state = nullptr;                                // token, pos, step
+    int32_t *token = nullptr, *pos = nullptr, *steps = nullptr;
+    int32_t *out = nullptr;                                  // generated tokens
+    int out_cap = 0;
+    void *attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    size_t len = 0;                                          // positions in the cache
+    hipGraphExec_t graph = nullptr;                          // one captured step
+};
+
 struct kh_kv {
     kh_ctx *ctx = nullptr;
     size_t n_layer = 0, k_dim = 0, v_dim = 0;
@@ -123,6 +152,7 @@ struct GemvJob {
     const float *const *wstab;
     const int32_t *sel;
     const float *xf2;       // with xf: the staged activation is swiglu(xf, xf2)
+    int accumulate;         // y[r] = y[r] + (x W^T + bias)[r]: the residual add
     int rows;
     int cols;
     int wave0;              // set by the launcher: first workgroup of the job
@@ -205,5 +235,15 @@ int launch_quantize(kh_ctx *ctx, const float *w, size_t rows, size_t cols, int p
 // Small helpers.
 int launch_fill(kh_ctx *ctx, float *p, size_t n, float value);
 int launch_dequant_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out);
+// The same with the row index read from device memory (an embedding lookup).
+int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out);
+// tensor::rms_norm over m rows of n (glue.hip).
+int launch_rms_norm(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out);
+// Attention whose length is read from device memory: n_positions = *len_dev
+// (+1 when plus_one), at most max_positions; partials in `ws` (attend_ws_bytes).
+int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
+                         const float *v, size_t kv_stride_k, size_t kv_stride_v, const int32_t *len_dev, int plus_one,
+                         size_t max_positions, float *out, void *ws);
+size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions);
 
 }  // namespace kh

@@ -438,7 +438,11 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
             for (int i = 0; i < R; i++) {
                 const float v = wave_sum(acc[i]);
                 const int r = r0 + i;
-                if (lane == 0 && r < rows) job.y[r] = job.bias ? v + job.bias[r] : v;
+                if (lane == 0 && r < rows) {
+                    float out = job.bias ? v + job.bias[r] : v;
+                    if (job.accumulate) out = job.y[r] + out;  // x += proj (llama.rs:273-276)
+                    job.y[r] = out;
+                }
                 acc[i] = 0.0f;
             }
         }
@@ -473,7 +477,11 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(JobTable tab) {
             for (int k = lane; k < cols; k += WAVE) s = fmaf(wr[k], job.xf[k], s);
         }
         const float v = wave_sum(s);
-        if (lane == 0) job.y[r] = job.bias ? v + job.bias[r] : v;
+        if (lane == 0) {
+            float out = job.bias ? v + job.bias[r] : v;
+            if (job.accumulate) out = job.y[r] + out;
+            job.y[r] = out;
+        }
     }
 }
 
@@ -582,8 +590,10 @@ __global__ void fill_kernel(float *p, size_t n, float value) {
 }
 
 // Weight::row (quant.rs:374-402) and the Q4_K decoder (mpp.rs:304-315).
-__global__ void dequant_row_kernel(int prec, const void *qs, const float *scales, size_t cols, size_t r,
+__global__ void dequant_row_kernel(int prec, const void *qs, const float *scales, size_t cols, size_t r_host,
+                                   const int32_t *r_dev,
                                    float *out) {
+    const size_t r = r_dev ? (size_t)*r_dev : r_host;
     size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= cols) return;
     const size_t nb = cols / BLOCK;
@@ -676,7 +686,15 @@ int launch_fill(kh_ctx *ctx, float *p, size_t n, float value) {
 
 int launch_dequant_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out) {
     hipLaunchKernelGGL(dequant_row_kernel, dim3((unsigned)((w->cols + 255) / 256)), dim3(256), 0, ctx->stream,
-                       w->precision, (const void *)w->qs, (const float *)w->scales, w->cols, r, out);
+                       w->precision, (const void *)w->qs, (const float *)w->scales, w->cols, r,
+                       (const int32_t *)nullptr, out);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out) {
+    hipLaunchKernelGGL(dequant_row_kernel, dim3((unsigned)((w->cols + 255) / 256)), dim3(256), 0, ctx->stream,
+                       w->precision, (const void *)w->qs, (const float *)w->scales, w->cols, (size_t)0, r, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }

@@ -104,6 +104,14 @@ __global__ __launch_bounds__(256) void softmax_kernel(float *x, int n) {
 }
 
 }  // namespace
+
+int launch_rms_norm(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out) {
+    if (m == 0 || n == 0) return KH_OK;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)m), dim3(256), 0, ctx->stream, x, w, (int)n, eps, out);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
 }  // namespace kh
 
 using namespace kh;

@@ -1,0 +1,459 @@
+// A device-resident decoder session for the Llama family (Qwen2/2.5/3 dense,
+// Llama): the forward of one token (crates/llm/src/model/llama.rs:224-289
+// run_rows with m = 1, embed and head at :384-415) with every operator on
+// the device, the KV cache in HBM, and the greedy next token chosen on the
+// device (sampler::argmax, crates/llm/src/sampler.rs:217-226).
+//
+// The position and the token live in device memory, so one token's launches
+// are the same every step: `kh_llm_generate` captures them once as a HIP
+// graph and replays it per token.  Per layer: RMSNorm; q/k/v (+bias) as one
+// GEMV launch; RoPE of q and k (per-head RMSNorm first where the model has
+// q/k norms) with k and v written into the cache row at the position, one
+// launch; attention over the cache, its length read from the device; o as a
+// GEMV that adds into the residual; RMSNorm; gate and up as one launch; down
+// with swiglu(gate, up) staged by the GEMV and added into the residual.
+#include <memory>
+
+#include "common.hpp"
+
+namespace kh {
+namespace {
+
+// One workgroup per head of q or k (then the v copy): optional per-head
+// RMSNorm (norm_heads, llama.rs:122-127), RoPE at the device position,
+// and k and v into the cache row.
+__global__ __launch_bounds__(128) void rope_push_kernel(float *qkv, int n_head, int n_kv, int hd,
+                                                       const float *cos_t, const float *sin_t, int interleaved,
+                                                       const float *q_norm, const float *k_norm, float eps,
+                                                       float *kc, float *vc, const int32_t *pos_dev) {
+    const int h = blockIdx.x, t = threadIdx.x, half = hd / 2;
+    const int pos = *pos_dev;
+    const int kv_dim = n_kv * hd;
+    __shared__ float s_x[256];
+    __shared__ float s_red[128];
+    if (h == n_head + n_kv) {  // the values: straight into the cache
+        for (int i = t; i < kv_dim; i += 128) vc[(size_t)pos * kv_dim + i] = qkv[(size_t)(n_head + n_kv) * hd + i];
+        return;
+    }
+    const bool is_q = h < n_head;
+    float *x = qkv + (size_t)h * hd;
+    for (int i = t; i < hd; i += 128) s_x[i] = x[i];
+    __syncthreads();
+    const float *nw = is_q ? q_norm : k_norm;
+    if (nw) {  // rms_norm of the head (tensor.rs:329-333), tree sum
+        float s = 0.0f;
+        for (int i = t; i < hd; i += 128) {
+            const float sq = s_x[i] * s_x[i];
+            s = s + sq;
+        }
+        s_red[t] = s;
+        __syncthreads();
+        for (int w = 64; w > 0; w >>= 1) {
+            if (t < w) s_red[t] = s_red[t] + s_red[t + w];
+            __syncthreads();
+        }
+        const float inv = 1.0f / sqrtf(s_red[0] / (float)hd + eps);
+        __syncthreads();
+        for (int i = t; i < hd; i += 128) {
+            const float u = s_x[i] * inv;
+            s_x[i] = u * nw[i];
+        }
+        __syncthreads();
+    }
+    // Rope::apply / apply_interleaved (tensor.rs:437-472)
+    float *dst = is_q ? x : kc + (size_t)pos * kv_dim + (size_t)(h - n_head) * hd;
+    for (int i = t; i < half; i += 128) {
+        const float c = cos_t[(size_t)pos * half + i], s = sin_t[(size_t)pos * half + i];
+        const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + half;
+        const float a = s_x[ia], b = s_x[ib];
+        const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+        dst[ia] = ac - bs;
+        dst[ib] = bc + as;
+    }
+}
+
+// sampler::argmax (sampler.rs:217-226): the first of equal maxima; a NaN
+// never wins, and a NaN first entry keeps index 0.  Then the next token
+// becomes the input, the position advances and the step's token is recorded.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *v, int n, int32_t *token, int32_t *pos,
+                                                     int32_t *step, int32_t *out, int out_cap) {
+    __shared__ float s_v[1024];
+    __shared__ int s_i[1024];
+    const int t = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int i = 1 + t; i < n; i += 1024) {
+        const float x = v[i];
+        if (x == x && (bi < 0 || x > bv)) bv = x, bi = i;
+    }
+    s_v[t] = bv;
+    s_i[t] = bi;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if (t < w) {
+            const float ov = s_v[t + w];
+            const int oi = s_i[t + w];
+            if (oi >= 0 && (s_i[t] < 0 || ov > s_v[t] || (ov == s_v[t] && oi < s_i[t]))) s_v[t] = ov, s_i[t] = oi;
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        const float first = n > 0 ? v[0] : 0.0f;
+        int best = 0;
+        if (n > 1 && first == first && s_i[0] >= 0 && s_v[0] > first) best = s_i[0];
+        *token = best;
+        *pos = *pos + 1;
+        const int k = *step;
+        if (out && k < out_cap) out[k] = best;
+        *step = k + 1;
+    }
+}
+
+template <typename T>
+int dev_alloc(T **p, size_t n) {
+    KH_HIP(hipMalloc(reinterpret_cast<void **>(p), sizeof(T) * (n ? n : 1)));
+    return KH_OK;
+}
+
+int dev_vector(float **p, const float *host, size_t n) {
+    if (!host) {
+        *p = nullptr;
+        return KH_OK;
+    }
+    int rc = dev_alloc(p, n);
+    if (rc) return rc;
+    KH_HIP(hipMemcpy(*p, host, 4 * n, hipMemcpyHostToDevice));
+    return KH_OK;
+}
+
+GemvJob gemv_job(const kh_weight *w, const float *x, const float *x2, const float *bias, float *y, int acc) {
+    GemvJob j{};
+    j.w = w->qs;
+    j.ws = w->scales;
+    j.xf = x;
+    j.xf2 = x2;
+    j.bias = bias;
+    j.y = y;
+    j.rows = (int)w->rows;
+    j.cols = (int)w->cols;
+    j.accumulate = acc;
+    return j;
+}
+
+// Jobs of one precision in one launch; mixed precisions in as many.
+int run_jobs(kh_ctx *ctx, const std::vector<std::pair<const kh_weight *, GemvJob>> &jobs) {
+    for (int prec : {KH_Q8, KH_Q4, KH_Q4K, KH_F32}) {
+        std::vector<GemvJob> js;
+        for (auto &j : jobs)
+            if (j.first->precision == prec) js.push_back(j.second);
+        if (!js.empty()) {
+            int rc = launch_gemv(ctx, prec, js.data(), (int)js.size());
+            if (rc) return rc;
+        }
+    }
+    return KH_OK;
+}
+
+bool fusable(const kh_weight *w) { return w->precision == KH_F32 || w->cols <= 8192; }
+
+// One token's launches, all on the context's stream.
+int step(kh_ctx *ctx, kh_llm *m) {
+    const kh_llm_spec &s = m->spec;
+    const size_t qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
+    int rc;
+    if ((rc = launch_dequant_row_dev(ctx, m->embed, m->token, m->x))) return rc;  // embed (llama.rs:384-391)
+    for (size_t l = 0; l < s.n_layer; l++) {
+        const kh_llm::Layer &L = m->layers[l];
+        // ---- attention sub-block (llama.rs:241-276)
+        if ((rc = launch_rms_norm(ctx, m->x, L.attn_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+        std::vector<std::pair<const kh_weight *, GemvJob>> jobs;
+        jobs.push_back({L.q, gemv_job(L.q, m->h, nullptr, L.q_b, m->qkv, 0)});
+        jobs.push_back({L.k, gemv_job(L.k, m->h, nullptr, L.k_b, m->qkv + qd, 0)});
+        jobs.push_back({L.v, gemv_job(L.v, m->h, nullptr, L.v_b, m->qkv + qd + kvd, 0)});
+        if ((rc = run_jobs(ctx, jobs))) return rc;
+        hipLaunchKernelGGL(rope_push_kernel, dim3((unsigned)(s.n_head + s.n_kv_head + 1)), dim3(128), 0,
+                           ctx->stream, m->qkv, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, m->rope_cos,
+                           m->rope_sin, s.rope_interleaved, L.q_norm, L.k_norm, s.eps, m->kc[l], m->vc[l], m->pos);
+        KH_HIP(hipGetLastError());
+        if ((rc = launch_attend_devlen(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, m->qkv, m->kc[l],
+                                       m->vc[l], kvd, kvd, m->pos, 1, s.n_ctx, m->att, m->attn_ws)))
+            return rc;
+        jobs.clear();
+        jobs.push_back({L.o, gemv_job(L.o, m->att, nullptr, nullptr, m->x, 1)});
+        if ((rc = run_jobs(ctx, jobs))) return rc;
+        // ---- MLP sub-block (llama.rs:278-285, Ffn::run ffn.rs:370-375)
+        if ((rc = launch_rms_norm(ctx, m->x, L.mlp_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+        jobs.clear();
+        jobs.push_back({L.gate, gemv_job(L.gate, m->h, nullptr, nullptr, m->g, 0)});
+        jobs.push_back({L.up, gemv_job(L.up, m->h, nullptr, nullptr, m->u, 0)});
+        if ((rc = run_jobs(ctx, jobs))) return rc;
+        jobs.clear();
+        if (fusable(L.down)) {
+            jobs.push_back({L.down, gemv_job(L.down, m->g, m->u, nullptr, m->x, 1)});
+        } else {  // too wide to stage in LDS: quantise swiglu(gate, up) first
+            if ((rc = launch_swiglu_qact(ctx, m->g, m->u, 1, s.n_ff, m->hq))) return rc;
+            GemvJob j = gemv_job(L.down, nullptr, nullptr, nullptr, m->x, 1);
+            j.xq = m->hq.qs, j.xs = m->hq.scales, j.xsum = m->hq.sums;
+            jobs.push_back({L.down, j});
+        }
+        if ((rc = run_jobs(ctx, jobs))) return rc;
+    }
+    // ---- head (llama.rs:404-411)
+    if ((rc = launch_rms_norm(ctx, m->x, m->final_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+    const kh_weight *head = m->head ? m->head : m->embed;
+    std::vector<std::pair<const kh_weight *, GemvJob>> jobs{{head, gemv_job(head, m->h, nullptr, nullptr, m->logits, 0)}};
+    if ((rc = run_jobs(ctx, jobs))) return rc;
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, ctx->stream, m->logits, (int)s.vocab, m->token, m->pos,
+                       m->steps, m->out, m->out_cap);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+int ready(const kh_llm *m) {
+    if (!m->embed || !m->final_norm || !m->rope_cos) return fail(KH_EINVAL, "llm: ends or rope tables not set");
+    for (auto &L : m->layers)
+        if (!L.q || !L.attn_norm) return fail(KH_EINVAL, "llm: a layer is not set");
+    return KH_OK;
+}
+
+int check_weight_shape(const kh_weight *w, size_t rows, size_t cols, const char *what) {
+    if (!w) return fail(KH_EINVAL, std::string("kh_llm_set_layer: ") + what + " is null");
+    if (w->rows != rows || w->cols != cols)
+        return fail(KH_EINVAL, std::string("kh_llm_set_layer: ") + what + " has the wrong shape");
+    if (w->precision != KH_F32 && w->cols > 0x7fffffff) return fail(KH_EINVAL, "too wide");
+    return KH_OK;
+}
+
+}  // namespace
+}  // namespace kh
+
+using namespace kh;
+
+extern "C" {
+
+int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out) {
+    if (!ctx || !spec || !out) return fail(KH_EINVAL, "kh_llm_new: null argument");
+    *out = nullptr;
+    const kh_llm_spec &s = *spec;
+    if (!s.n_layer || !s.n_embd || !s.n_head || !s.n_kv_head || !s.head_dim || !s.n_ff || !s.vocab || !s.n_ctx ||
+        s.n_head % s.n_kv_head)
+        return fail(KH_EINVAL, "kh_llm_new: every size must be positive and n_kv_head divide n_head");
+    if ((s.head_dim != 64 && s.head_dim != 128) || s.n_ctx > (1u << 20) || s.n_head + s.n_kv_head + 1 > 65535)
+        return fail(KH_DECLINED, "kh_llm_new: head_dim 64 or 128 and a context up to 2^20 positions");
+    if (s.n_ff % BLOCK || s.n_embd % 4) return fail(KH_EINVAL, "kh_llm_new: n_ff % 32 and n_embd % 4 must be 0");
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    std::unique_ptr<kh_llm> m(new kh_llm());
+    m->ctx = ctx;
+    m->spec = s;
+    m->layers.assign(s.n_layer, kh_llm::Layer{});
+    const size_t kvd = s.n_kv_head * s.head_dim, qd = s.n_head * s.head_dim;
+    int rc;
+    m->kc.assign(s.n_layer, nullptr);
+    m->vc.assign(s.n_layer, nullptr);
+    for (size_t l = 0; l < s.n_layer; l++) {
+        if ((rc = dev_alloc(&m->kc[l], s.n_ctx * kvd)) || (rc = dev_alloc(&m->vc[l], s.n_ctx * kvd))) return rc;
+    }
+    if ((rc = dev_alloc(&m->x, s.n_embd)) || (rc = dev_alloc(&m->h, s.n_embd)) ||
+        (rc = dev_alloc(&m->qkv, qd + 2 * kvd)) || (rc = dev_alloc(&m->att, qd)) || (rc = dev_alloc(&m->g, s.n_ff)) ||
+        (rc = dev_alloc(&m->u, s.n_ff)) || (rc = dev_alloc(&m->logits, s.vocab)) ||
+        (rc = dev_alloc(&m->hq.qs, s.n_ff)) || (rc = dev_alloc(&m->hq.scales, s.n_ff / BLOCK)) ||
+        (rc = dev_alloc(&m->hq.sums, s.n_ff / BLOCK)) || (rc = dev_alloc(&m->state, 3)))
+        return rc;
+    m->token = m->state, m->pos = m->state + 1, m->steps = m->state + 2;
+    KH_HIP(hipMemset(m->state, 0, 3 * sizeof(int32_t)));
+    m->attn_ws_bytes = attend_ws_bytes((int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, s.n_ctx);
+    KH_HIP(hipMalloc(&m->attn_ws, m->attn_ws_bytes));
+    *out = m.release();
+    return KH_OK;
+}
+
+int kh_llm_free(kh_llm *m) {
+    if (!m) return KH_OK;
+    {
+        std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipStreamSynchronize(m->ctx->stream);
+        if (m->graph) (void)hipGraphExecDestroy(m->graph);
+        for (auto p : m->kc) (void)hipFree(p);
+        for (auto p : m->vc) (void)hipFree(p);
+        for (auto &L : m->layers)
+            for (float *p : {L.attn_norm, L.mlp_norm, L.q_b, L.k_b, L.v_b, L.q_norm, L.k_norm})
+                if (p) (void)hipFree(p);
+        for (void *p : {(void *)m->x, (void *)m->h, (void *)m->qkv, (void *)m->att, (void *)m->g, (void *)m->u,
+                        (void *)m->logits, (void *)m->hq.qs, (void *)m->hq.scales, (void *)m->hq.sums,
+                        (void *)m->state, (void *)m->final_norm, (void *)m->rope_cos, (void *)m->rope_sin,
+                        m->attn_ws, (void *)m->out})
+            if (p) (void)hipFree(p);
+    }
+    delete m;
+    return KH_OK;
+}
+
+int kh_llm_set_layer(kh_llm *m, size_t l, const kh_weight *q, const kh_weight *k, const kh_weight *v,
+                     const kh_weight *o, const kh_weight *gate, const kh_weight *up, const kh_weight *down,
+                     const float *attn_norm, const float *mlp_norm, const float *q_b, const float *k_b,
+                     const float *v_b, const float *q_norm, const float *k_norm) {
+    if (!m || !attn_norm || !mlp_norm) return fail(KH_EINVAL, "kh_llm_set_layer: null argument");
+    const kh_llm_spec &s = m->spec;
+    if (l >= s.n_layer) return fail(KH_EINVAL, "kh_llm_set_layer: no such layer");
+    const size_t qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
+    int rc;
+    if ((rc = check_weight_shape(q, qd, s.n_embd, "q")) || (rc = check_weight_shape(k, kvd, s.n_embd, "k")) ||
+        (rc = check_weight_shape(v, kvd, s.n_embd, "v")) || (rc = check_weight_shape(o, s.n_embd, qd, "o")) ||
+        (rc = check_weight_shape(gate, s.n_ff, s.n_embd, "gate")) ||
+        (rc = check_weight_shape(up, s.n_ff, s.n_embd, "up")) ||
+        (rc = check_weight_shape(down, s.n_embd, s.n_ff, "down")))
+        return rc;
+    std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+    (void)hipSetDevice(m->ctx->device);
+    kh_llm::Layer &L = m->layers[l];
+    for (float *p : {L.attn_norm, L.mlp_norm, L.q_b, L.k_b, L.v_b, L.q_norm, L.k_norm})
+        if (p) (void)hipFree(p);
+    L = kh_llm::Layer{};
+    L.q = q, L.k = k, L.v = v, L.o = o, L.gate = gate, L.up = up, L.down = down;
+    if ((rc = dev_vector(&L.attn_norm, attn_norm, s.n_embd)) || (rc = dev_vector(&L.mlp_norm, mlp_norm, s.n_embd)) ||
+        (rc = dev_vector(&L.q_b, q_b, qd)) || (rc = dev_vector(&L.k_b, k_b, kvd)) ||
+        (rc = dev_vector(&L.v_b, v_b, kvd)) || (rc = dev_vector(&L.q_norm, q_norm, s.head_dim)) ||
+        (rc = dev_vector(&L.k_norm, k_norm, s.head_dim)))
+        return rc;
+    if (m->graph) {
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
+    return KH_OK;
+}
+
+int kh_llm_set_ends(kh_llm *m, const kh_weight *embed, const float *final_norm, const kh_weight *lm_head) {
+    if (!m || !embed || !final_norm) return fail(KH_EINVAL, "kh_llm_set_ends: null argument");
+    const kh_llm_spec &s = m->spec;
+    if (embed->rows != s.vocab || embed->cols != s.n_embd)
+        return fail(KH_EINVAL, "kh_llm_set_ends: the embedding is [vocab, n_embd]");
+    if (lm_head && (lm_head->rows != s.vocab || lm_head->cols != s.n_embd))
+        return fail(KH_EINVAL, "kh_llm_set_ends: the head is [vocab, n_embd]");
+    std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+    (void)hipSetDevice(m->ctx->device);
+    if (m->final_norm) (void)hipFree(m->final_norm);
+    int rc = dev_vector(&m->final_norm, final_norm, s.n_embd);
+    if (rc) return rc;
+    m->embed = embed;
+    m->head = lm_head;
+    if (m->graph) {
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
+    return KH_OK;
+}
+
+int kh_llm_set_rope(kh_llm *m, const float *cos_t, const float *sin_t, size_t max_pos) {
+    if (!m || !cos_t || !sin_t) return fail(KH_EINVAL, "kh_llm_set_rope: null argument");
+    if (max_pos < m->spec.n_ctx) return fail(KH_EINVAL, "kh_llm_set_rope: the tables must cover n_ctx positions");
+    std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+    (void)hipSetDevice(m->ctx->device);
+    const size_t n = m->spec.n_ctx * (m->spec.head_dim / 2);
+    if (m->rope_cos) (void)hipFree(m->rope_cos);
+    if (m->rope_sin) (void)hipFree(m->rope_sin);
+    m->rope_cos = m->rope_sin = nullptr;
+    int rc;
+    if ((rc = dev_vector(&m->rope_cos, cos_t, n)) || (rc = dev_vector(&m->rope_sin, sin_t, n))) return rc;
+    return KH_OK;
+}
+
+int kh_llm_len(const kh_llm *m, size_t *len) {
+    if (!m || !len) return fail(KH_EINVAL, "kh_llm_len: null argument");
+    *len = m->len;
+    return KH_OK;
+}
+
+int kh_llm_truncate(kh_llm *m, size_t len) {
+    if (!m) return fail(KH_EINVAL, "kh_llm_truncate: null argument");
+    std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+    (void)hipSetDevice(m->ctx->device);
+    if (len < m->len) m->len = len;  // KvCache::truncate keeps a prefix, never extends (mod.rs:709-725)
+    const int32_t p = (int32_t)m->len;
+    KH_HIP(hipMemcpyAsync(m->pos, &p, 4, hipMemcpyHostToDevice, m->ctx->stream));
+    KH_HIP(hipStreamSynchronize(m->ctx->stream));
+    return KH_OK;
+}
+
+int kh_llm_forward(kh_ctx *ctx, kh_llm *m, int32_t token, float *logits, int32_t *next) {
+    if (!ctx || !m || m->ctx != ctx) return fail(KH_EINVAL, "kh_llm_forward: null argument or foreign context");
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = ready(m);
+    if (rc) return rc;
+    if (token < 0 || (size_t)token >= m->spec.vocab) return fail(KH_EINVAL, "kh_llm_forward: token out of range");
+    if (m->len >= m->spec.n_ctx) return fail(KH_EINVAL, "kh_llm_forward: the context window is full");
+    const int32_t st[3] = {token, (int32_t)m->len, 0};
+    KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = step(ctx, m))) return rc;
+    if (logits) KH_HIP(hipMemcpyAsync(logits, m->logits, 4 * m->spec.vocab, hipMemcpyDeviceToHost, ctx->stream));
+    int32_t nt = 0;
+    KH_HIP(hipMemcpyAsync(&nt, m->token, 4, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    m->len += 1;
+    if (next) *next = nt;
+    return KH_OK;
+}
+
+int kh_llm_generate(kh_ctx *ctx, kh_llm *m, int32_t token, size_t n, int32_t *tokens) {
+    if (!ctx || !m || m->ctx != ctx || (n && !tokens)) return fail(KH_EINVAL, "kh_llm_generate: null argument");
+    if (n == 0) return KH_OK;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = ready(m);
+    if (rc) return rc;
+    if (token < 0 || (size_t)token >= m->spec.vocab) return fail(KH_EINVAL, "kh_llm_generate: token out of range");
+    if (m->len + n > m->spec.n_ctx) return fail(KH_EINVAL, "kh_llm_generate: the steps would overrun the context");
+    if (m->out_cap < n) {  // the record of generated tokens
+        if (m->out) {
+            KH_HIP(hipStreamSynchronize(ctx->stream));
+            (void)hipFree(m->out);
+            m->out = nullptr;
+        }
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+        KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->out), 4 * n));
+        m->out_cap = (int)n;
+    }
+    const int32_t st[3] = {token, (int32_t)m->len, 0};
+    KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
+    if (!m->graph) {  // one token's launches, captured once (they read pos and token from the device)
+        KH_HIP(hipStreamSynchronize(ctx->stream));
+        hipGraph_t g = nullptr;
+        KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        rc = step(ctx, m);
+        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+        e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            m->graph = nullptr;
+            return hip_fail(e, "hipGraphInstantiate");
+        }
+    }
+    for (size_t i = 0; i < n; i++) KH_HIP(hipGraphLaunch(m->graph, ctx->stream));
+    KH_HIP(hipMemcpyAsync(tokens, m->out, 4 * n, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    m->len += n;
+    return KH_OK;
+}
+
+int kh_llm_generate_launch(kh_ctx *ctx, kh_llm *m, size_t n) {
+    // Replays n more steps of an already-captured graph from the device state
+    // as it stands, without copying anything back (for timing).
+    if (!ctx || !m || !m->graph) return fail(KH_EINVAL, "kh_llm_generate_launch: no captured step");
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (m->len + n > m->spec.n_ctx) return fail(KH_EINVAL, "kh_llm_generate_launch: the steps would overrun the context");
+    for (size_t i = 0; i < n; i++) KH_HIP(hipGraphLaunch(m->graph, ctx->stream));
+    m->len += n;
+    return KH_OK;
+}
+
+}  // extern "C"

@@ -371,3 +371,64 @@ def moe_run_q8(hs, m: int, hidden: int, inter: int, n_exp: int, top_k: int, rout
     L.kvo_moe_run_q8(P(f(hs)), m, hidden, inter, n_exp, top_k, scoring, select, n_group, topk_group,
                      int(norm_topk), scale, P(b), *[P(a) for a in args], sh_inter, *[P(a) for a in sh], P(out))
     return out
+
+
+class Llm:
+    """A Llama-family decoder on the CPU for one token at a time: the forward
+    of crates/llm/src/model/llama.rs:224-289 (run_rows, m = 1) between the
+    embedding and the head (llama.rs:384-415), every operator the oracle's.
+    Weights are q8 (scales, qs) pairs; norms and biases f32 arrays."""
+
+    def __init__(self, spec: dict, layers: list, embed, final_norm, lm_head=None, cos_t=None, sin_t=None):
+        self.s, self.layers, self.embed, self.final_norm = spec, layers, embed, final_norm
+        self.head = lm_head if lm_head is not None else embed
+        self.cos, self.sin = cos_t, sin_t
+        kvd = spec["n_kv_head"] * spec["head_dim"]
+        self.kc = [np.zeros((spec["n_ctx"], kvd), np.float32) for _ in layers]
+        self.vc = [np.zeros((spec["n_ctx"], kvd), np.float32) for _ in layers]
+        self.len = 0
+
+    def forward(self, token: int) -> np.ndarray:
+        s = self.s
+        e, hd, nh, nkv, eps = s["n_embd"], s["head_dim"], s["n_head"], s["n_kv_head"], s["eps"]
+        qd, kvd, half = nh * hd, nkv * hd, hd // 2
+        pos = self.len
+        x = row_q8(*self.embed, e, token)                       # Weight::row, llama.rs:384-391
+        rope = rope_apply_interleaved if s.get("rope_interleaved") else rope_apply
+        for l, L in enumerate(self.layers):
+            h = rms_norm(x, L["attn_norm"], eps)
+            q = matvec_q8(*L["q"], qd, e, h, L.get("q_b"))
+            k = matvec_q8(*L["k"], kvd, e, h, L.get("k_b"))
+            v = matvec_q8(*L["v"], kvd, e, h, L.get("v_b"))
+            for head in range(nh):
+                seg = q[head * hd:(head + 1) * hd]
+                if L.get("q_norm") is not None:
+                    seg = rms_norm(seg, L["q_norm"], eps)
+                q[head * hd:(head + 1) * hd] = rope(self.cos, self.sin, half, seg, pos)
+            for head in range(nkv):
+                seg = k[head * hd:(head + 1) * hd]
+                if L.get("k_norm") is not None:
+                    seg = rms_norm(seg, L["k_norm"], eps)
+                k[head * hd:(head + 1) * hd] = rope(self.cos, self.sin, half, seg, pos)
+            self.kc[l][pos], self.vc[l][pos] = k, v             # KvCache::push
+            a = attend(nh, nkv, hd, q, self.kc[l][:pos + 1].ravel(), self.vc[l][:pos + 1].ravel(), pos + 1)
+            x = (x + matvec_q8(*L["o"], e, qd, a)).astype(np.float32)
+            h = rms_norm(x, L["mlp_norm"], eps)
+            g = matvec_q8(*L["gate"], s["n_ff"], e, h)
+            u = matvec_q8(*L["up"], s["n_ff"], e, h)
+            x = (x + matvec_q8(*L["down"], e, s["n_ff"], swiglu(g, u))).astype(np.float32)
+        self.len += 1
+        return matvec_q8(*self.head, s["vocab"], e, rms_norm(x, self.final_norm, eps))
+
+
+def argmax(v) -> int:
+    """sampler::argmax (crates/llm/src/sampler.rs:217-226): the first of equal
+    maxima; NaN never replaces the running best."""
+    v = np.asarray(v)
+    if v.size == 0:
+        return 0
+    best, top = 0, v[0]
+    for i in range(1, v.size):
+        if v[i] > top:
+            best, top = i, v[i]
+    return best
