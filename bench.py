@@ -31,6 +31,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -345,6 +347,7 @@ def secondary(torch, K, ctx, stream, dev, gen, args):
 
     out["prefill_gemm"] = prefill(torch, K, ctx, stream, dev, gen, args)
     out["moe_deepseek_v2_lite"] = moe(torch, K, ctx, stream, dev, gen, args)
+    out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args)
 
     spec = K.Spec(14, 2, 64)
     att = {}
@@ -454,6 +457,54 @@ def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8):
     res["prefill_512tok"] = {"us": round(s * 1e6, 1), "TOPS": round(ops / s / 1e12, 2), "ops": ops}
     del g
     log(f"moe: {res}")
+    return res
+
+
+def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256):
+    """The second half of BASELINE.json's metric: Qwen2.5-0.5B-shaped q8
+    decode, tokens per second, on the device-resident session (24 layers,
+    n_embd 896, 14/2 heads of 64, ffn 4864, vocab 151936, tied embedding,
+    q/k/v biases; weights ~ N(0, 0.02), norms 1).  Greedy tokens, one HIP
+    graph replay per token; `warm` tokens first, then `timed` tokens timed with
+    HIP events on the session's stream (context warm..warm+timed)."""
+    spec = dict(n_layer=24, n_embd=896, n_head=14, n_kv_head=2, head_dim=64, n_ff=4864, vocab=151936,
+                n_ctx=n_ctx, eps=1e-6, rope_interleaved=0)
+    e, qd, kvd, ff = 896, 896, 128, 4864
+
+    def q8(rows, cols):
+        f = torch.randn(rows, cols, device=dev, generator=gen) * 0.02
+        return K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8)
+
+    ones = np.ones(e, np.float32)
+    with torch.cuda.stream(stream):
+        m = K.Llm(ctx, **spec)
+        rng = np.random.default_rng(0)
+        for l in range(24):
+            m.set_layer(l, q8(qd, e), q8(kvd, e), q8(kvd, e), q8(e, qd), q8(ff, e), q8(ff, e), q8(e, ff), ones, ones,
+                        (rng.standard_normal(qd) * 0.02).astype(np.float32),
+                        (rng.standard_normal(kvd) * 0.02).astype(np.float32),
+                        (rng.standard_normal(kvd) * 0.02).astype(np.float32))
+        m.set_ends(q8(151936, e), ones)
+        half = 32
+        inv = 1.0 / (1e6 ** (np.arange(half, dtype=np.float32) * 2.0 / 64))  # Rope::new, tensor.rs:390-407
+        ang = np.arange(n_ctx, dtype=np.float32)[:, None] * inv[None, :].astype(np.float32)
+        m.set_rope(np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32), n_ctx)
+    torch.cuda.synchronize()
+    first = m.generate(1, warm)  # captures the step's graph
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        m.generate_launch(timed)
+        e1.record(stream)
+        e1.synchronize()
+    s = e0.elapsed_time(e1) / 1e3
+    tps = timed / s
+    res = {"tok_per_s": round(tps, 1), "ms_per_token": round(s / timed * 1e3, 4), "context": [warm, warm + timed],
+           "launches_per_token": 24 * 9 + 4, "vs_reference_cpu_q8_112tps": round(tps / 112.0, 2),
+           "vs_reference_metal_q8_191tps": round(tps / 191.0, 2), "first_tokens": [int(t) for t in first[:4]]}
+    log(f"qwen0.5b q8 decode: {res}")
+    m.free()
     return res
 
 
