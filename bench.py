@@ -13,10 +13,11 @@ the 128 GEMV launches of one token, each with its activation quantisation,
 replayed from a HIP graph.  Inputs are resident in HBM.
 
 value = algorithmic bytes per step / step time (GB/s), the bytes being
-144*rows*cols/256 + 4*cols + 4*rows per GEMV.  roofline = the GEMV kernels
-alone (the same launches on pre-quantised activations), timed with HIP
-events on the stream they run on.  cpu_baseline = the C oracle's Q4_K GEMV
-on the host's cores over layer 0's matrices.
+144*rows*cols/256 + 4*cols + 4*rows per GEMV.  roofline: every launch of the
+step is the GEMV kernel (it quantises its own input), so its average launch
+duration is the step time over the 128 launches, timed with HIP events on
+the stream they run on.  cpu_baseline = the C oracle's Q4_K GEMV on the
+host's cores over layer 0's matrices.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -166,23 +167,6 @@ def main() -> int:
             many([L["gate"], L["up"]], [L["h"].data_ptr()] * 2, [L["y_gate"].data_ptr(), L["y_up"].data_ptr()])
             L["down"].matvec_bt_dev(L["m"].data_ptr(), L["y_down"].data_ptr())
 
-    # ---- the GEMV kernels alone: down's input pre-quantised ---------------
-    with torch.cuda.stream(stream):
-        for L in layers:
-            n = 14336
-            L["mq"] = (torch.empty(n, dtype=torch.int8, device=dev), torch.empty(n // 32, device=dev),
-                       torch.empty(n // 32, dtype=torch.int32, device=dev))
-            K.qact_dev(ctx, L["m"].data_ptr(), 1, n, *[t.data_ptr() for t in L["mq"]])
-    torch.cuda.synchronize()
-
-    def kernels():
-        for L in layers:
-            many([L["q"], L["k"], L["v"]], [L["x"].data_ptr()] * 3,
-                 [L["y_q"].data_ptr(), L["y_k"].data_ptr(), L["y_v"].data_ptr()])
-            L["o"].matvec_bt_dev(L["a"].data_ptr(), L["y_o"].data_ptr())
-            many([L["gate"], L["up"]], [L["h"].data_ptr()] * 2, [L["y_gate"].data_ptr(), L["y_up"].data_ptr()])
-            L["down"].matvec_q_dev(*[t.data_ptr() for t in L["mq"]], L["y_down"].data_ptr())
-
     if args.counters:
         # a workload for rocprofv3 --pmc: a streaming kernel of known traffic
         # (dst = 2 * src over MIB MiB each way, far past the 256 MB cache: the
@@ -196,21 +180,19 @@ def main() -> int:
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
             for _ in range(2):
-                kernels()
+                step()
         torch.cuda.synchronize()
         print(json.dumps({"counters_run": {"calibration_bytes_each_way": 4 * n, "calibration_runs": 3, "gemv_steps": 2,
                                            "launches_per_step": launches, "bytes_per_step": step_bytes}}))
         return 0
 
+    # every launch of the step is a GEMV kernel (each quantises its own
+    # input), so the step's events time the kernel: avg launch = step / launches
     g_step = Graph(torch, ctx, stream, step)
     sec = g_step.time(args.steps, args.warmup)
-    log(f"step: {sec * 1e3:.3f} ms, {step_bytes / sec / 1e9:.1f} GB/s")
-
-    g_k = Graph(torch, ctx, stream, kernels)
-    ksec = g_k.time(args.steps, args.warmup)
-    avg_launch = ksec / launches
-    achieved = step_bytes / ksec / 1e9
-    log(f"gemv kernels: {avg_launch * 1e6:.2f} us/launch avg, {achieved:.1f} GB/s")
+    avg_launch = sec / launches
+    achieved = step_bytes / sec / 1e9
+    log(f"step: {sec * 1e3:.3f} ms, {achieved:.1f} GB/s, {avg_launch * 1e6:.2f} us per GEMV launch")
 
     # ---- each config shape as its own launch ------------------------------
     per_shape = {}

@@ -86,23 +86,13 @@ GemvJob job_for(const kh_weight *w, const QAct *a, const float *xf, const float 
     return j;
 }
 
-// Rows wider than this quantise their input in a separate launch: past it,
-// every workgroup re-quantising x in LDS costs more than one small launch.
-size_t fuse_max_cols() {
-    static const size_t v = [] {
-        const char *e = getenv("KVAD_FUSE_MAX_COLS");
-        return e && *e ? (size_t)atol(e) : (size_t)8192;
-    }();
-    return v;
-}
-
 // The GEMV jobs for n matvecs on device pointers, quantising into ws the
 // inputs of wide rows (once per distinct input, quant.rs:634-644).
 int make_jobs(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x, const float *const *bias,
               float *const *y, int32_t *dots, std::vector<GemvJob> &jobs) {
     size_t total = 0;
     for (size_t i = 0; i < n; i++)
-        if (w[i]->precision != KH_F32 && w[i]->cols > fuse_max_cols()) total += qact_bytes(1, w[i]->cols);
+        if (w[i]->precision != KH_F32 && w[i]->cols > fuse_max_cols(w[i]->precision)) total += qact_bytes(1, w[i]->cols);
     int rc = total ? ensure(ctx, ctx->ws, total) : KH_OK;
     if (rc) return rc;
     char *p = static_cast<char *>(ctx->ws.ptr);
@@ -110,7 +100,7 @@ int make_jobs(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *con
     jobs.clear();
     for (size_t i = 0; i < n; i++) {
         const float *b = bias ? bias[i] : nullptr;
-        if (w[i]->precision == KH_F32 || w[i]->cols <= fuse_max_cols()) {
+        if (w[i]->precision == KH_F32 || w[i]->cols <= fuse_max_cols(w[i]->precision)) {
             jobs.push_back(job_for(w[i], nullptr, x[i], b, y[i], dots));
             continue;
         }

@@ -109,6 +109,8 @@ struct kh_llm {
     int32_t *state = nullptr;                                // token, pos, step
     int32_t *token = nullptr, *pos = nullptr, *steps = nullptr;
     int32_t *out = nullptr;                                  // generated tokens
+    float *arg_v = nullptr;                                  // argmax partials
+    int *arg_i = nullptr;
     int out_cap = 0;
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -153,13 +155,19 @@ struct GemvJob {
     const int32_t *sel;
     const float *xf2;       // with xf: the staged activation is swiglu(xf, xf2)
     int accumulate;         // y[r] = y[r] + (x W^T + bias)[r]: the residual add
+    const float *norm_w;    // with xf: the staged activation is rms_norm(xf, norm_w, norm_eps)
+    float norm_eps;
     int rows;
     int cols;
     int wave0;              // set by the launcher: first workgroup of the job
     int nwaves;             // set by the launcher: waves working on the job
 };
 
-// Runs every job in one launch (all jobs share `precision`).
+// Widest rows whose GEMV quantises its f32 input itself (each workgroup
+// stages it in LDS); wider inputs are quantised once in a launch of their own.
+size_t fuse_max_cols(int precision);
+
+// Runs every job in one launch per input kind (all jobs share `precision`).
 int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs);
 
 // Batched prefill y[m, rows] = xs[m, cols] W^T (+bias), m > 1 (device pointers).

@@ -6,7 +6,7 @@
 // QActivation::new (quant.rs:1044-1066), tensor::matvec_bt (tensor.rs:56-79),
 // Q4_K decoding (crates/gpu/src/mpp.rs:241-315).
 //
-// Shape of the kernel.  A workgroup (4 waves) first stages the activation in
+// Shape of the kernel.  A workgroup (8 waves) first stages the activation in
 // LDS as int8 codes, per-32 scales and code sums -- quantising the f32 input
 // itself (QActivation::new, fused into the GEMV so a matvec is one launch),
 // or copying codes a producer already made.  Each wave then owns R weight
@@ -29,6 +29,8 @@
 // same row computed alone, to the bit.
 #include "common.hpp"
 
+#include <vector>
+
 namespace kh {
 namespace {
 
@@ -48,6 +50,15 @@ __device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
                                              (int)(bytes > 0xffffffffu ? 0xffffffffu : bytes), RSRC_WORD3);
 }
+// A pointer every lane holds alike, moved to scalar registers.
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+    const unsigned long long v = reinterpret_cast<unsigned long long>(p);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return reinterpret_cast<T *>(((unsigned long long)hi << 32) | lo);
+}
+
 __device__ __forceinline__ int4 bld16(rsrc_t r, unsigned off) {
     return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
@@ -341,12 +352,156 @@ __device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, fl
     }
 }
 
+// Activation staging.  A thread's first batch of activation loads is issued
+// before the workgroup's first weight loads: vector loads complete in order,
+// so an activation load issued after them would wait for HBM.  Later batches
+// (wide activations only) follow as they are needed.  The input kind is a
+// template parameter so that a launch holds registers only for what it loads.
+constexpr int IN_F32 = 0;       // f32 x
+constexpr int IN_SWIGLU = 1;    // swiglu(xf, xf2)
+constexpr int IN_CODES = 2;     // int8 codes, scales and sums made elsewhere
+constexpr int IN_NORM = 3;      // rms_norm(xf) * norm_w
+
+// SB float4s (or code int4s) per thread per batch: 4, or 8 where the
+// kernel's weight registers leave room (one batch then covers 16384 columns).
+template <int KIND, int SB>
+struct Stage {
+    float4 v[SB];                    // f32 input, or int4 codes
+    float4 u[KIND == IN_F32 ? 1 : SB];  // swiglu's second input, norm weights, or (scale, sum)
+};
+
+__device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// Batch `bat` of the thread's loads: float4 c = (bat * SB + k) * T + tid
+// of the f32 input (block c >> 3), or int4 c of the codes and, on batch 0,
+// scale and sum k * T + tid.
+template <int KIND, int SB>
+__device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &st, int bat, int nb, int tid) {
+    constexpr int T = WAVE * WPB;
+    // buffer loads: past the input's end they return zeros, with no branch
+    if constexpr (KIND == IN_CODES) {
+        const rsrc_t Q = rsrc(job.xq, (size_t)nb * BLOCK), S = rsrc(job.xs, (size_t)nb * 4),
+                     M = rsrc(job.xsum, (size_t)nb * 4);
+#pragma unroll
+        for (int k = 0; k < SB; k++) {
+            const unsigned c = (unsigned)((bat * SB + k) * T + tid);
+            st.v[k] = __builtin_bit_cast(float4, bld16(Q, c * 16));
+            const unsigned j = (unsigned)(k * T + tid);
+            st.u[k] = bat == 0 ? make_float4(bldf(S, j * 4), __builtin_bit_cast(float, bldi(M, j * 4)), 0.f, 0.f)
+                               : zero4();
+        }
+    } else {
+        const rsrc_t X = rsrc(job.xf, (size_t)nb * BLOCK * 4);
+        const void *x2 = KIND == IN_SWIGLU ? (const void *)job.xf2 : KIND == IN_NORM ? (const void *)job.norm_w : job.xf;
+        const rsrc_t X2 = rsrc(x2, (size_t)nb * BLOCK * 4);
+#pragma unroll
+        for (int k = 0; k < SB; k++) {
+            const unsigned c = (unsigned)((bat * SB + k) * T + tid);
+            st.v[k] = __builtin_bit_cast(float4, bld16(X, c * 16));
+            if constexpr (KIND != IN_F32) st.u[k] = __builtin_bit_cast(float4, bld16(X2, c * 16));
+        }
+    }
+}
+
+// Stages the activation of `job` in LDS for a workgroup: int8 codes, scales
+// and code sums of PB blocks (blocks past nb are zero).  From f32 input it
+// quantises as QActivation::new (quant.rs:1044-1066), first applying
+// rms_norm (tensor.rs:329-333) for IN_NORM or swiglu(xf, xf2)
+// (tensor.rs:344-350) for IN_SWIGLU; codes made elsewhere are copied.  `st` holds batch 0,
+// loaded by stage_load.  Every workgroup computes the same values.
+template <int KIND, int SB>
+__device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND, SB> &st, int8_t *sq, float *ssc,
+                                                 int *ssum, int PB, int nb, int cols, int tid, int lane, int wv) {
+    constexpr int T = WAVE * WPB;
+    if constexpr (KIND == IN_CODES) {
+        const int nbat = (PB * 2 + T * SB - 1) / (T * SB);
+        for (int bat = 0; bat < nbat; bat++) {
+            if (bat > 0) stage_load(job, st, bat, nb, tid);
+#pragma unroll
+            for (int k = 0; k < SB; k++) {
+                const int c = (bat * SB + k) * T + tid;
+                if (c < PB * 2) reinterpret_cast<int4 *>(sq)[c] = __builtin_bit_cast(int4, st.v[k]);
+                const int j = k * T + tid;
+                if (bat == 0 && j < PB) {
+                    ssc[j] = st.u[k].x;
+                    ssum[j] = __builtin_bit_cast(int, st.u[k].y);
+                }
+            }
+        }
+        return;
+    } else {
+        constexpr bool nw = KIND == IN_NORM;
+        const int total = PB * 8;  // float4s, padding included
+        const int nbat = (total + T * SB - 1) / (T * SB);
+        __shared__ float s_ss[WPB];
+        float inv = 1.0f;
+        // Sum of squares over the thread's float4s in index order, then over
+        // the wave, then over the waves in order: every workgroup gets the
+        // same sum.
+        auto sumsq = [](float ss, float4 v) {
+            const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+            return ss + ((a + b) + (c + d));
+        };
+        if constexpr (nw) {
+            float ss = 0.0f;
+            if (nbat == 1) {
+#pragma unroll
+                for (int k = 0; k < SB; k++) ss = sumsq(ss, st.v[k]);
+            } else {  // wide activations: a pass of its own
+                for (int bat = 0; bat < nbat; bat++) {
+                    Stage<KIND, SB> t;
+                    stage_load(job, t, bat, nb, tid);
+#pragma unroll
+                    for (int k = 0; k < SB; k++) ss = sumsq(ss, t.v[k]);
+                }
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) s_ss[wv] = ss;
+            __syncthreads();
+            float t = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WPB; w++) t = t + s_ss[w];
+            inv = 1.0f / sqrtf(t / (float)cols + job.norm_eps);
+        }
+        for (int bat = 0; bat < nbat; bat++) {
+            if (bat > 0) stage_load(job, st, bat, nb, tid);
+#pragma unroll
+            for (int k = 0; k < SB; k++) {
+                const int i = (bat * SB + k) * T + tid, b = i >> 3;
+                if (b >= PB) break;  // uniform per 8-lane block group, and past every later k
+                float4 x = st.v[k];
+                if constexpr (nw) {
+                    const float4 w = st.u[k];  // zeros past the end, like x
+                    x = make_float4((x.x * inv) * w.x, (x.y * inv) * w.y, (x.z * inv) * w.z, (x.w * inv) * w.w);
+                }
+                if constexpr (KIND == IN_SWIGLU) {
+                    const float4 u = st.u[k];
+                    x = make_float4(swiglu1(x.x, u.x), swiglu1(x.y, u.y), swiglu1(x.z, u.z), swiglu1(x.w, u.w));
+                }
+                float scale;
+                int s;
+                const int packed = quantize4(x, &scale, &s);
+                reinterpret_cast<int *>(sq)[i] = packed;
+                if ((tid & 7) == 0) {
+                    ssc[b] = scale;
+                    ssum[b] = s;
+                }
+            }
+        }
+    }
+}
+
+// The input kind of a job.
+__host__ __device__ inline int input_kind(const GemvJob &j) {
+    return j.xf ? (j.xf2 ? IN_SWIGLU : j.norm_w ? IN_NORM : IN_F32) : IN_CODES;
+}
+
 // One launch runs every job of the table.  Workgroups are spread over the
 // jobs in proportion to their rows; each wave walks the row groups
 // lw, lw + nw, ... of its job, loading the next group's weights before it
 // computes the current one.  The first group's loads are issued before the
 // activation is staged, so they fly while the workgroup quantises.
-template <int PREC, int CPL, int R, bool DOTS>
+template <int PREC, int CPL, int R, int KIND, bool DOTS>
 __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
@@ -371,9 +526,10 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     const void *wp = job.w;
     const float *wsp = job.ws;
     if (job.wtab) {  // an expert chosen on the device (MoE decode)
-        const int x = *job.sel;
-        wp = job.wtab[x];
-        wsp = job.wstab[x];
+        // one address for the wave: the buffer descriptors stay in scalar registers
+        const int x = __builtin_amdgcn_readfirstlane(*job.sel);
+        wp = uniform_ptr(job.wtab[x]);
+        wsp = uniform_ptr(job.wstab[x]);
     }
     const rsrc_t W = rsrc(wp, wbytes);
     const rsrc_t WS = rsrc(wsp, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
@@ -382,41 +538,19 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     // order with the next piece's loads in flight while this one computes
     const int my_groups = lw < ngroups ? (ngroups - lw + nw - 1) / nw : 0;
     const int steps = my_groups * nseg;
+    Stage<KIND, (CPL >= 4 ? 8 : 4)> st;
+    stage_load(job, st, 0, nb, tid);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    // (unconditional: a wave with no rows reads past the end, which returns
+    // zeros, and the wait for the activation then never covers these loads)
     Chunks<PREC, CPL, R> cur;
-    if (steps > 0) load_chunks<PREC, CPL, R>(cur, W, WS, lw * R, cols, nb, 0, lane);
+    load_chunks<PREC, CPL, R>(cur, W, WS, lw * R, cols, nb, 0, lane);
 
     // ---- stage the activation in LDS (zero blocks pad the tail) ---------
     int8_t *sq = reinterpret_cast<int8_t *>(lds);
     float *ssc = reinterpret_cast<float *>(lds + (size_t)PB * 32);
     int *ssum = reinterpret_cast<int *>(ssc + PB);
-    if (job.xf) {  // quantise the f32 input (QActivation::new, quant.rs:1044-1066)
-        for (int base = 0; base < PB * 8; base += WAVE * WPB) {
-            const int i = base + tid, b = i >> 3;
-            float4 v = b < nb ? reinterpret_cast<const float4 *>(job.xf)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (job.xf2) {  // swiglu(gate, up) first (tensor.rs:344-350)
-                const float4 u = b < nb ? reinterpret_cast<const float4 *>(job.xf2)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                v = make_float4(swiglu1(v.x, u.x), swiglu1(v.y, u.y), swiglu1(v.z, u.z), swiglu1(v.w, u.w));
-            }
-            float scale;
-            int s;
-            const int packed = quantize4(v, &scale, &s);
-            if (b < PB) {
-                reinterpret_cast<int *>(sq)[i] = packed;
-                if ((tid & 7) == 0) {
-                    ssc[b] = scale;
-                    ssum[b] = s;
-                }
-            }
-        }
-    } else {  // codes made elsewhere
-        for (int i = tid; i < PB * 2; i += WAVE * WPB)
-            reinterpret_cast<int4 *>(sq)[i] =
-                i < nb * 2 ? reinterpret_cast<const int4 *>(job.xq)[i] : int4{0, 0, 0, 0};
-        for (int i = tid; i < PB; i += WAVE * WPB) {
-            ssc[i] = i < nb ? job.xs[i] : 0.0f;
-            ssum[i] = i < nb ? job.xsum[i] : 0;
-        }
-    }
+    stage_activation(job, st, sq, ssc, ssum, PB, nb, cols, tid, lane, wv);
     __syncthreads();
 
     float acc[R];
@@ -506,30 +640,35 @@ Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
     if (cpl > 8) cpl = 8;  // wider rows take several segments
     const bool tall = rows_total >= 16384 && cpl >= 2;
     int r = cpl == 1 || cpl == 2 ? 4 : cpl <= 4 ? 2 : 1;
-    if (tall) r = 1;
+    if (tall || (prec == KH_Q4K && cpl >= 2 && rows_total >= 6144)) r = 1;
     // short matrices: fewer rows per wave, more waves
     while (r > 1 && (rows_total + r - 1) / r < 8 * cu_count) r /= 2;
     int forced = env_int("KVAD_GEMV_R", 0);  // tuning knobs
     if (forced == 1 || (forced == 2 && cpl <= 4) || (forced == 4 && cpl <= 2)) r = forced;
-    int wg = maxCols >= 8192 && prec == KH_Q4K ? 1 : tall ? 3 : 2;
+    int wg = maxCols >= 8192 && prec == KH_Q4K ? 1 : tall || (prec == KH_Q4K && rows_total >= 6144) ? 3 : 2;
     const int fw = env_int("KVAD_GEMV_WG_PER_CU", 0);
     if (fw > 0) wg = fw;
     return {cpl, r, wg};
 }
 
+template <int PREC, int CPL, int R, int KIND>
+void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds) {
+    hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, KIND, false>), dim3(blocks), dim3(WAVE * WPB), lds, ctx->stream, tab);
+}
+
 template <int PREC, int CPL, int R>
-void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, bool dots) {
-    dim3 grid(blocks), block(WAVE * WPB);
-    if (dots)
-        hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, true>), grid, block, lds, ctx->stream, tab);
-    else
-        hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, false>), grid, block, lds, ctx->stream, tab);
+void launch_kind(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int kind) {
+    if (kind == IN_F32) launch_one<PREC, CPL, R, IN_F32>(ctx, tab, blocks, lds);
+    else if (kind == IN_SWIGLU) launch_one<PREC, CPL, R, IN_SWIGLU>(ctx, tab, blocks, lds);
+    else if (kind == IN_NORM) launch_one<PREC, CPL, R, IN_NORM>(ctx, tab, blocks, lds);
+    else launch_one<PREC, CPL, R, IN_CODES>(ctx, tab, blocks, lds);
 }
 
 template <int PREC>
-int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_total, bool dots) {
+int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_total, bool dots, int kind) {
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     Plan p = plan_for(PREC, maxC, maxCols, rows_total, cu);
+    if (dots) p = {1, 1, 2};  // block dots (a debugging aid): one kernel shape serves every width
     for (int i = 0; i < tab.n; i++) {
         size_t wb = (size_t)tab.j[i].rows * tab.j[i].cols;
         if (wb >= 0xfff00000ull) return fail(KH_DECLINED, "matvec: weights of 4 GiB or more are not addressed here");
@@ -551,9 +690,20 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     const int pb = padded_blocks(PREC, maxC, p.cpl);
     const size_t lds = (size_t)pb * 32 + 8 * (size_t)pb;
     if (lds > 64 * 1024) return fail(KH_DECLINED, "matvec: activation too wide for the LDS stage");
+    if (dots) {
+        dim3 grid(blocks), block(WAVE * WPB);
+        if (kind == IN_CODES)
+            hipLaunchKernelGGL((gemv_kernel<PREC, 1, 1, IN_CODES, true>), grid, block, lds, ctx->stream, tab);
+        else if (kind == IN_F32)
+            hipLaunchKernelGGL((gemv_kernel<PREC, 1, 1, IN_F32, true>), grid, block, lds, ctx->stream, tab);
+        else
+            return fail(KH_EINVAL, "matvec: block dots are offered for plain and pre-quantised inputs only");
+        KH_HIP(hipGetLastError());
+        return KH_OK;
+    }
 #define KH_CASE(CPL, R)                                                       \
     if (p.cpl == CPL && p.r == R) {                                           \
-        launch_one<PREC, CPL, R>(ctx, tab, blocks, lds, dots);                \
+        launch_kind<PREC, CPL, R>(ctx, tab, blocks, lds, kind);               \
         KH_HIP(hipGetLastError());                                            \
         return KH_OK;                                                         \
     }
@@ -651,30 +801,48 @@ int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, si
 }
 
 int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
-    for (int base = 0; base < njobs; base += MAX_JOBS) {
-        JobTable tab{};
-        tab.n = njobs - base < MAX_JOBS ? njobs - base : MAX_JOBS;
-        int maxC = 0, maxCols = 0, rows_total = 0;
-        bool dots = false;
-        for (int i = 0; i < tab.n; i++) {
-            tab.j[i] = jobs[base + i];
-            int c = chunks_per_row(precision, tab.j[i].cols);
-            maxC = c > maxC ? c : maxC;
-            maxCols = tab.j[i].cols > maxCols ? tab.j[i].cols : maxCols;
-            rows_total += tab.j[i].rows;
-            dots = dots || tab.j[i].dots;
+    // one launch per input kind present (a kernel stages one kind), in table order
+    for (int i = 0; i < njobs; i++)
+        if (jobs[i].xf2 && jobs[i].norm_w) return fail(KH_EINVAL, "matvec: rms_norm and swiglu inputs do not combine");
+    for (int kind : {IN_F32, IN_NORM, IN_SWIGLU, IN_CODES}) {
+        std::vector<GemvJob> js;
+        for (int i = 0; i < njobs; i++)
+            if (precision == KH_F32 || input_kind(jobs[i]) == kind) js.push_back(jobs[i]);
+        for (int base = 0; base < (int)js.size(); base += MAX_JOBS) {
+            JobTable tab{};
+            tab.n = (int)js.size() - base < MAX_JOBS ? (int)js.size() - base : MAX_JOBS;
+            int maxC = 0, maxCols = 0, rows_total = 0;
+            bool dots = false;
+            for (int i = 0; i < tab.n; i++) {
+                tab.j[i] = js[base + i];
+                int c = chunks_per_row(precision, tab.j[i].cols);
+                maxC = c > maxC ? c : maxC;
+                maxCols = tab.j[i].cols > maxCols ? tab.j[i].cols : maxCols;
+                rows_total += tab.j[i].rows;
+                dots = dots || tab.j[i].dots;
+            }
+            int rc;
+            switch (precision) {
+                case KH_Q8: rc = launch_prec<KH_Q8>(ctx, tab, maxC, maxCols, rows_total, dots, kind); break;
+                case KH_Q4: rc = launch_prec<KH_Q4>(ctx, tab, maxC, maxCols, rows_total, dots, kind); break;
+                case KH_Q4K: rc = launch_prec<KH_Q4K>(ctx, tab, maxC, maxCols, rows_total, dots, kind); break;
+                case KH_F32: rc = launch_f32(ctx, tab); break;
+                default: return fail(KH_EINVAL, "unknown precision");
+            }
+            if (rc != KH_OK) return rc;
         }
-        int rc;
-        switch (precision) {
-            case KH_Q8: rc = launch_prec<KH_Q8>(ctx, tab, maxC, maxCols, rows_total, dots); break;
-            case KH_Q4: rc = launch_prec<KH_Q4>(ctx, tab, maxC, maxCols, rows_total, dots); break;
-            case KH_Q4K: rc = launch_prec<KH_Q4K>(ctx, tab, maxC, maxCols, rows_total, dots); break;
-            case KH_F32: rc = launch_f32(ctx, tab); break;
-            default: return fail(KH_EINVAL, "unknown precision");
-        }
-        if (rc != KH_OK) return rc;
+        if (precision == KH_F32) break;
     }
     return KH_OK;
+}
+
+size_t fuse_max_cols(int precision) {
+    static const size_t forced = [] {
+        const char *e = getenv("KVAD_FUSE_MAX_COLS");
+        return e && *e ? (size_t)atol(e) : (size_t)0;
+    }();
+    if (forced) return forced;
+    return precision == KH_Q4K ? 16384 : 8192;
 }
 
 int launch_fill(kh_ctx *ctx, float *p, size_t n, float value) {

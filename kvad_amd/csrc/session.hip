@@ -73,34 +73,60 @@ __global__ __launch_bounds__(128) void rope_push_kernel(float *qkv, int n_head, 
 }
 
 // sampler::argmax (sampler.rs:217-226): the first of equal maxima; a NaN
-// never wins, and a NaN first entry keeps index 0.  Then the next token
-// becomes the input, the position advances and the step's token is recorded.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float *v, int n, int32_t *token, int32_t *pos,
-                                                     int32_t *step, int32_t *out, int out_cap) {
-    __shared__ float s_v[1024];
-    __shared__ int s_i[1024];
+// never wins, and a NaN first entry keeps index 0.  Two launches: each
+// workgroup reduces a run of entries 1.. (largest, then lowest index), then
+// one workgroup reduces the runs, compares with entry 0, and makes the next
+// token the input, advances the position and records the step's token.
+constexpr int ARGMAX_BLOCKS = 256;
+
+__device__ __forceinline__ void better(float &bv, int &bi, float ov, int oi) {
+    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) bv = ov, bi = oi;
+}
+
+__device__ void block_best(float &bv, int &bi, float *s_v, int *s_i) {
     const int t = threadIdx.x;
-    float bv = -INFINITY;
-    int bi = -1;
-    for (int i = 1 + t; i < n; i += 1024) {
-        const float x = v[i];
-        if (x == x && (bi < 0 || x > bv)) bv = x, bi = i;
-    }
     s_v[t] = bv;
     s_i[t] = bi;
     __syncthreads();
-    for (int w = 512; w > 0; w >>= 1) {
+    for (int w = 128; w > 0; w >>= 1) {
         if (t < w) {
-            const float ov = s_v[t + w];
-            const int oi = s_i[t + w];
-            if (oi >= 0 && (s_i[t] < 0 || ov > s_v[t] || (ov == s_v[t] && oi < s_i[t]))) s_v[t] = ov, s_i[t] = oi;
+            float v = s_v[t];
+            int i = s_i[t];
+            better(v, i, s_v[t + w], s_i[t + w]);
+            s_v[t] = v, s_i[t] = i;
         }
         __syncthreads();
     }
-    if (t == 0) {
+    bv = s_v[0], bi = s_i[0];
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int n, float *pv, int *pi) {
+    __shared__ float s_v[256];
+    __shared__ int s_i[256];
+    const int per = (n - 1 + ARGMAX_BLOCKS - 1) / ARGMAX_BLOCKS;
+    const int lo = 1 + blockIdx.x * per, hi = min(n, lo + per);
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int i = lo + threadIdx.x; i < hi; i += 256) {
+        const float x = v[i];
+        if (x == x) better(bv, bi, x, i);
+    }
+    block_best(bv, bi, s_v, s_i);
+    if (threadIdx.x == 0) pv[blockIdx.x] = bv, pi[blockIdx.x] = bi;
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float *v, int n, const float *pv, const int *pi,
+                                                          int32_t *token, int32_t *pos, int32_t *step, int32_t *out,
+                                                          int out_cap) {
+    __shared__ float s_v[256];
+    __shared__ int s_i[256];
+    float bv = pv[threadIdx.x];
+    int bi = pi[threadIdx.x];
+    block_best(bv, bi, s_v, s_i);
+    if (threadIdx.x == 0) {
         const float first = n > 0 ? v[0] : 0.0f;
         int best = 0;
-        if (n > 1 && first == first && s_i[0] >= 0 && s_v[0] > first) best = s_i[0];
+        if (n > 1 && first == first && bi >= 0 && bv > first) best = bi;
         *token = best;
         *pos = *pos + 1;
         const int k = *step;
@@ -154,7 +180,15 @@ int run_jobs(kh_ctx *ctx, const std::vector<std::pair<const kh_weight *, GemvJob
     return KH_OK;
 }
 
-bool fusable(const kh_weight *w) { return w->precision == KH_F32 || w->cols <= 8192; }
+bool fusable(const kh_weight *w) { return w->precision == KH_F32 || w->cols <= fuse_max_cols(w->precision); }
+
+// The GEMV can take rms_norm(x) as its input when it stages x itself.
+bool norm_fusable(const kh_weight *w) { return w->precision != KH_F32 && w->cols <= fuse_max_cols(w->precision); }
+
+GemvJob normed(GemvJob j, bool fuse, const float *w, float eps) {
+    if (fuse) j.norm_w = w, j.norm_eps = eps;
+    return j;
+}
 
 // One token's launches, all on the context's stream.
 int step(kh_ctx *ctx, kh_llm *m) {
@@ -165,11 +199,14 @@ int step(kh_ctx *ctx, kh_llm *m) {
     for (size_t l = 0; l < s.n_layer; l++) {
         const kh_llm::Layer &L = m->layers[l];
         // ---- attention sub-block (llama.rs:241-276)
-        if ((rc = launch_rms_norm(ctx, m->x, L.attn_norm, 1, s.n_embd, s.eps, m->h))) return rc;
         std::vector<std::pair<const kh_weight *, GemvJob>> jobs;
-        jobs.push_back({L.q, gemv_job(L.q, m->h, nullptr, L.q_b, m->qkv, 0)});
-        jobs.push_back({L.k, gemv_job(L.k, m->h, nullptr, L.k_b, m->qkv + qd, 0)});
-        jobs.push_back({L.v, gemv_job(L.v, m->h, nullptr, L.v_b, m->qkv + qd + kvd, 0)});
+        const bool fq = norm_fusable(L.q) && norm_fusable(L.k) && norm_fusable(L.v);
+        const float *qin = fq ? m->x : m->h;
+        if (!fq && (rc = launch_rms_norm(ctx, m->x, L.attn_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+        jobs.push_back({L.q, normed(gemv_job(L.q, qin, nullptr, L.q_b, m->qkv, 0), fq, L.attn_norm, s.eps)});
+        jobs.push_back({L.k, normed(gemv_job(L.k, qin, nullptr, L.k_b, m->qkv + qd, 0), fq, L.attn_norm, s.eps)});
+        jobs.push_back(
+            {L.v, normed(gemv_job(L.v, qin, nullptr, L.v_b, m->qkv + qd + kvd, 0), fq, L.attn_norm, s.eps)});
         if ((rc = run_jobs(ctx, jobs))) return rc;
         hipLaunchKernelGGL(rope_push_kernel, dim3((unsigned)(s.n_head + s.n_kv_head + 1)), dim3(128), 0,
                            ctx->stream, m->qkv, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, m->rope_cos,
@@ -182,10 +219,12 @@ int step(kh_ctx *ctx, kh_llm *m) {
         jobs.push_back({L.o, gemv_job(L.o, m->att, nullptr, nullptr, m->x, 1)});
         if ((rc = run_jobs(ctx, jobs))) return rc;
         // ---- MLP sub-block (llama.rs:278-285, Ffn::run ffn.rs:370-375)
-        if ((rc = launch_rms_norm(ctx, m->x, L.mlp_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+        const bool fm = norm_fusable(L.gate) && norm_fusable(L.up);
+        const float *min_ = fm ? m->x : m->h;
+        if (!fm && (rc = launch_rms_norm(ctx, m->x, L.mlp_norm, 1, s.n_embd, s.eps, m->h))) return rc;
         jobs.clear();
-        jobs.push_back({L.gate, gemv_job(L.gate, m->h, nullptr, nullptr, m->g, 0)});
-        jobs.push_back({L.up, gemv_job(L.up, m->h, nullptr, nullptr, m->u, 0)});
+        jobs.push_back({L.gate, normed(gemv_job(L.gate, min_, nullptr, nullptr, m->g, 0), fm, L.mlp_norm, s.eps)});
+        jobs.push_back({L.up, normed(gemv_job(L.up, min_, nullptr, nullptr, m->u, 0), fm, L.mlp_norm, s.eps)});
         if ((rc = run_jobs(ctx, jobs))) return rc;
         jobs.clear();
         if (fusable(L.down)) {
@@ -199,12 +238,17 @@ int step(kh_ctx *ctx, kh_llm *m) {
         if ((rc = run_jobs(ctx, jobs))) return rc;
     }
     // ---- head (llama.rs:404-411)
-    if ((rc = launch_rms_norm(ctx, m->x, m->final_norm, 1, s.n_embd, s.eps, m->h))) return rc;
     const kh_weight *head = m->head ? m->head : m->embed;
-    std::vector<std::pair<const kh_weight *, GemvJob>> jobs{{head, gemv_job(head, m->h, nullptr, nullptr, m->logits, 0)}};
+    const bool fh = norm_fusable(head);
+    if (!fh && (rc = launch_rms_norm(ctx, m->x, m->final_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+    std::vector<std::pair<const kh_weight *, GemvJob>> jobs{
+        {head, normed(gemv_job(head, fh ? m->x : m->h, nullptr, nullptr, m->logits, 0), fh, m->final_norm, s.eps)}};
     if ((rc = run_jobs(ctx, jobs))) return rc;
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, ctx->stream, m->logits, (int)s.vocab, m->token, m->pos,
-                       m->steps, m->out, m->out_cap);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(ARGMAX_BLOCKS), dim3(256), 0, ctx->stream, m->logits,
+                       (int)s.vocab, m->arg_v, m->arg_i);
+    KH_HIP(hipGetLastError());
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, ctx->stream, m->logits, (int)s.vocab, m->arg_v,
+                       m->arg_i, m->token, m->pos, m->steps, m->out, m->out_cap);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -258,7 +302,8 @@ int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out) {
         (rc = dev_alloc(&m->qkv, qd + 2 * kvd)) || (rc = dev_alloc(&m->att, qd)) || (rc = dev_alloc(&m->g, s.n_ff)) ||
         (rc = dev_alloc(&m->u, s.n_ff)) || (rc = dev_alloc(&m->logits, s.vocab)) ||
         (rc = dev_alloc(&m->hq.qs, s.n_ff)) || (rc = dev_alloc(&m->hq.scales, s.n_ff / BLOCK)) ||
-        (rc = dev_alloc(&m->hq.sums, s.n_ff / BLOCK)) || (rc = dev_alloc(&m->state, 3)))
+        (rc = dev_alloc(&m->hq.sums, s.n_ff / BLOCK)) || (rc = dev_alloc(&m->state, 3)) ||
+        (rc = dev_alloc(&m->arg_v, ARGMAX_BLOCKS)) || (rc = dev_alloc(&m->arg_i, ARGMAX_BLOCKS)))
         return rc;
     m->token = m->state, m->pos = m->state + 1, m->steps = m->state + 2;
     KH_HIP(hipMemset(m->state, 0, 3 * sizeof(int32_t)));
@@ -283,7 +328,7 @@ int kh_llm_free(kh_llm *m) {
         for (void *p : {(void *)m->x, (void *)m->h, (void *)m->qkv, (void *)m->att, (void *)m->g, (void *)m->u,
                         (void *)m->logits, (void *)m->hq.qs, (void *)m->hq.scales, (void *)m->hq.sums,
                         (void *)m->state, (void *)m->final_norm, (void *)m->rope_cos, (void *)m->rope_sin,
-                        m->attn_ws, (void *)m->out})
+                        m->attn_ws, (void *)m->out, (void *)m->arg_v, (void *)m->arg_i})
             if (p) (void)hipFree(p);
     }
     delete m;
