@@ -50,6 +50,11 @@ __device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
                                              (int)(bytes > 0xffffffffu ? 0xffffffffu : bytes), RSRC_WORD3);
 }
+// f32 read through the scalar cache (constant address space): for values a
+// kernel only reads, at wave-uniform addresses.  Such loads are counted apart
+// from vector loads, so they never wait for weight loads in flight.
+typedef const __attribute__((address_space(4))) float const_f32;
+
 // A pointer every lane holds alike, moved to scalar registers.
 template <typename T>
 __device__ __forceinline__ T *uniform_ptr(T *p) {
@@ -352,10 +357,9 @@ __device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, fl
     }
 }
 
-// Activation staging.  A thread's first batch of activation loads is issued
-// before the workgroup's first weight loads: vector loads complete in order,
-// so an activation load issued after them would wait for HBM.  Later batches
-// (wide activations only) follow as they are needed.  The input kind is a
+// Activation staging.  A thread's activation loads are issued before the
+// workgroup's first weight loads: vector loads complete in order, so an
+// activation load issued after them would wait for HBM.  The input kind is a
 // template parameter so that a launch holds registers only for what it loads.
 constexpr int IN_F32 = 0;       // f32 x
 constexpr int IN_SWIGLU = 1;    // swiglu(xf, xf2)
@@ -372,11 +376,11 @@ struct Stage {
 
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
-// Batch `bat` of the thread's loads: float4 c = (bat * SB + k) * T + tid
-// of the f32 input (block c >> 3), or int4 c of the codes and, on batch 0,
-// scale and sum k * T + tid.
+// The thread's loads: float4 c = k * T + tid of the f32 input (block c >> 3),
+// or int4 c of the codes and scale and sum c.  One such batch covers the
+// whole activation (the launcher checks it: stage_fits).
 template <int KIND, int SB>
-__device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &st, int bat, int nb, int tid) {
+__device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &st, int nb, int tid) {
     constexpr int T = WAVE * WPB;
     // buffer loads: past the input's end they return zeros, with no branch
     if constexpr (KIND == IN_CODES) {
@@ -384,11 +388,9 @@ __device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &
                      M = rsrc(job.xsum, (size_t)nb * 4);
 #pragma unroll
         for (int k = 0; k < SB; k++) {
-            const unsigned c = (unsigned)((bat * SB + k) * T + tid);
+            const unsigned c = (unsigned)(k * T + tid);
             st.v[k] = __builtin_bit_cast(float4, bld16(Q, c * 16));
-            const unsigned j = (unsigned)(k * T + tid);
-            st.u[k] = bat == 0 ? make_float4(bldf(S, j * 4), __builtin_bit_cast(float, bldi(M, j * 4)), 0.f, 0.f)
-                               : zero4();
+            st.u[k] = make_float4(bldf(S, c * 4), __builtin_bit_cast(float, bldi(M, c * 4)), 0.f, 0.f);
         }
     } else {
         const rsrc_t X = rsrc(job.xf, (size_t)nb * BLOCK * 4);
@@ -396,7 +398,7 @@ __device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &
         const rsrc_t X2 = rsrc(x2, (size_t)nb * BLOCK * 4);
 #pragma unroll
         for (int k = 0; k < SB; k++) {
-            const unsigned c = (unsigned)((bat * SB + k) * T + tid);
+            const unsigned c = (unsigned)(k * T + tid);
             st.v[k] = __builtin_bit_cast(float4, bld16(X, c * 16));
             if constexpr (KIND != IN_F32) st.u[k] = __builtin_bit_cast(float4, bld16(X2, c * 16));
         }
@@ -414,46 +416,30 @@ __device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND,
                                                  int *ssum, int PB, int nb, int cols, int tid, int lane, int wv) {
     constexpr int T = WAVE * WPB;
     if constexpr (KIND == IN_CODES) {
-        const int nbat = (PB * 2 + T * SB - 1) / (T * SB);
-        for (int bat = 0; bat < nbat; bat++) {
-            if (bat > 0) stage_load(job, st, bat, nb, tid);
 #pragma unroll
-            for (int k = 0; k < SB; k++) {
-                const int c = (bat * SB + k) * T + tid;
-                if (c < PB * 2) reinterpret_cast<int4 *>(sq)[c] = __builtin_bit_cast(int4, st.v[k]);
-                const int j = k * T + tid;
-                if (bat == 0 && j < PB) {
-                    ssc[j] = st.u[k].x;
-                    ssum[j] = __builtin_bit_cast(int, st.u[k].y);
-                }
+        for (int k = 0; k < SB; k++) {
+            const int c = k * T + tid;
+            if (c < PB * 2) reinterpret_cast<int4 *>(sq)[c] = __builtin_bit_cast(int4, st.v[k]);
+            if (c < PB) {
+                ssc[c] = st.u[k].x;
+                ssum[c] = __builtin_bit_cast(int, st.u[k].y);
             }
         }
         return;
     } else {
         constexpr bool nw = KIND == IN_NORM;
-        const int total = PB * 8;  // float4s, padding included
-        const int nbat = (total + T * SB - 1) / (T * SB);
-        __shared__ float s_ss[WPB];
         float inv = 1.0f;
-        // Sum of squares over the thread's float4s in index order, then over
-        // the wave, then over the waves in order: every workgroup gets the
-        // same sum.
-        auto sumsq = [](float ss, float4 v) {
-            const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
-            return ss + ((a + b) + (c + d));
-        };
         if constexpr (nw) {
+            // Sum of squares over the thread's float4s in index order, then
+            // over the wave, then over the waves in order: every workgroup
+            // gets the same sum.
+            __shared__ float s_ss[WPB];
             float ss = 0.0f;
-            if (nbat == 1) {
 #pragma unroll
-                for (int k = 0; k < SB; k++) ss = sumsq(ss, st.v[k]);
-            } else {  // wide activations: a pass of its own
-                for (int bat = 0; bat < nbat; bat++) {
-                    Stage<KIND, SB> t;
-                    stage_load(job, t, bat, nb, tid);
-#pragma unroll
-                    for (int k = 0; k < SB; k++) ss = sumsq(ss, t.v[k]);
-                }
+            for (int k = 0; k < SB; k++) {
+                const float4 v = st.v[k];
+                const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+                ss = ss + ((a + b) + (c + d));
             }
             ss = wave_sum(ss);
             if (lane == 0) s_ss[wv] = ss;
@@ -463,32 +449,38 @@ __device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND,
             for (int w = 0; w < WPB; w++) t = t + s_ss[w];
             inv = 1.0f / sqrtf(t / (float)cols + job.norm_eps);
         }
-        for (int bat = 0; bat < nbat; bat++) {
-            if (bat > 0) stage_load(job, st, bat, nb, tid);
 #pragma unroll
-            for (int k = 0; k < SB; k++) {
-                const int i = (bat * SB + k) * T + tid, b = i >> 3;
-                if (b >= PB) break;  // uniform per 8-lane block group, and past every later k
-                float4 x = st.v[k];
-                if constexpr (nw) {
-                    const float4 w = st.u[k];  // zeros past the end, like x
-                    x = make_float4((x.x * inv) * w.x, (x.y * inv) * w.y, (x.z * inv) * w.z, (x.w * inv) * w.w);
-                }
-                if constexpr (KIND == IN_SWIGLU) {
-                    const float4 u = st.u[k];
-                    x = make_float4(swiglu1(x.x, u.x), swiglu1(x.y, u.y), swiglu1(x.z, u.z), swiglu1(x.w, u.w));
-                }
-                float scale;
-                int s;
-                const int packed = quantize4(x, &scale, &s);
-                reinterpret_cast<int *>(sq)[i] = packed;
-                if ((tid & 7) == 0) {
-                    ssc[b] = scale;
-                    ssum[b] = s;
-                }
+        for (int k = 0; k < SB; k++) {
+            const int i = k * T + tid, b = i >> 3;
+            if (b >= PB) break;  // uniform per 8-lane block group, and past every later k
+            float4 x = st.v[k];
+            if constexpr (nw) {
+                const float4 w = st.u[k];  // zeros past the end, like x
+                x = make_float4((x.x * inv) * w.x, (x.y * inv) * w.y, (x.z * inv) * w.z, (x.w * inv) * w.w);
+            }
+            if constexpr (KIND == IN_SWIGLU) {
+                const float4 u = st.u[k];
+                x = make_float4(swiglu1(x.x, u.x), swiglu1(x.y, u.y), swiglu1(x.z, u.z), swiglu1(x.w, u.w));
+            }
+            float scale;
+            int s;
+            const int packed = quantize4(x, &scale, &s);
+            reinterpret_cast<int *>(sq)[i] = packed;
+            if ((tid & 7) == 0) {
+                ssc[b] = scale;
+                ssum[b] = s;
             }
         }
     }
+}
+
+// Whether one staging batch (SB loads per thread) covers PB blocks.
+// A kernel stages 8 loads per thread where its weight registers leave room
+// (CPL >= 4) or where it is built WIDE (rows of several segments), else 4.
+__host__ __device__ constexpr int stage_batch(int cpl, bool wide) { return cpl >= 4 || wide ? 8 : 4; }
+__host__ __device__ inline bool stage_fits(int kind, int PB, int sb) {
+    const int cap = sb * WAVE * WPB;
+    return kind == IN_CODES ? PB * 2 <= cap : PB * 8 <= cap;
 }
 
 // The input kind of a job.
@@ -501,7 +493,7 @@ __host__ __device__ inline int input_kind(const GemvJob &j) {
 // lw, lw + nw, ... of its job, loading the next group's weights before it
 // computes the current one.  The first group's loads are issued before the
 // activation is staged, so they fly while the workgroup quantises.
-template <int PREC, int CPL, int R, int KIND, bool DOTS>
+template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false>
 __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
@@ -535,16 +527,37 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     const rsrc_t WS = rsrc(wsp, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
 
     // the wave's work: its row groups, each cut into nseg segments, walked in
-    // order with the next piece's loads in flight while this one computes
+    // order; step s is group lw + (s / nseg) * nw, segment s % nseg.  Two
+    // register buffers take even and odd steps: a step's loads are issued
+    // just before the other buffer's step computes.  Every pass of the loop
+    // issues the same loads (a step past the wave's work reads past the end
+    // of the weights, which returns zeros), so each wait covers only the
+    // loads it needs.  Step 0's loads fly while the workgroup stages the
+    // activation.
     const int my_groups = lw < ngroups ? (ngroups - lw + nw - 1) / nw : 0;
     const int steps = my_groups * nseg;
-    Stage<KIND, (CPL >= 4 ? 8 : 4)> st;
-    stage_load(job, st, 0, nb, tid);
+    auto load_step = [&](Chunks<PREC, CPL, R> &c, int s) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunks<PREC, CPL, R>(c, W, WS, (lw + (s / nseg) * nw) * R, cols, nb, s % nseg, lane);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    Stage<KIND, stage_batch(CPL, WIDE)> st;
+    stage_load(job, st, nb, tid);
+    // The bias and residual values of the wave's rows, lane k * R + i holding
+    // those of row (lw + k * nw) * R + i, also ahead of the weights (a load in
+    // the epilogue would wait for every weight load in flight).
+    const int my_rows = my_groups * R;
+    const bool pre = my_rows <= WAVE;
+    float pbias = 0.0f, pres = 0.0f;
+    if (pre && (job.bias || job.accumulate)) {
+        const int r = (lw + (lane / R) * nw) * R + lane % R;
+        const unsigned off = lane < my_rows && r < rows ? (unsigned)r * 4u : 0xffffffffu;  // past the end: zero
+        if (job.bias) pbias = bldf(rsrc(job.bias, (size_t)rows * 4), off);
+        if (job.accumulate) pres = bldf(rsrc(job.y, (size_t)rows * 4), off);
+    }
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
-    // (unconditional: a wave with no rows reads past the end, which returns
-    // zeros, and the wait for the activation then never covers these loads)
-    Chunks<PREC, CPL, R> cur;
-    load_chunks<PREC, CPL, R>(cur, W, WS, lw * R, cols, nb, 0, lane);
+    Chunks<PREC, CPL, R> ca, cb;
+    load_step(ca, 0);
 
     // ---- stage the activation in LDS (zero blocks pad the tail) ---------
     int8_t *sq = reinterpret_cast<int8_t *>(lds);
@@ -556,30 +569,43 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     float acc[R];
 #pragma unroll
     for (int i = 0; i < R; i++) acc[i] = 0.0f;
-    for (int step = 0; step < steps; step++) {
-        const int grp = lw + (step / nseg) * nw, seg = step % nseg;
-        const int r0 = grp * R;
-        Chunks<PREC, CPL, R> nxt;
-        const bool more = step + 1 < steps;
-        if (more) {
-            const int ngrp = lw + ((step + 1) / nseg) * nw, nseg_i = (step + 1) % nseg;
-            load_chunks<PREC, CPL, R>(nxt, W, WS, ngrp * R, cols, nb, nseg_i, lane);
-        }
-        compute_chunks<PREC, CPL, R, DOTS>(cur, acc, sq, ssc, ssum, seg, lane, r0, rows, nb, C, job.dots);
-        if (more) cur = nxt;
+    // one step: the dot products of `c`, then (at a row group's last
+    // segment) the rows' sums written out
+    auto run_step = [&](const Chunks<PREC, CPL, R> &c, int step) {
+        const int k = step / nseg, seg = step % nseg;
+        const int r0 = (lw + k * nw) * R;
+        compute_chunks<PREC, CPL, R, DOTS>(c, acc, sq, ssc, ssum, seg, lane, r0, rows, nb, C, job.dots);
         if (seg == nseg - 1) {
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const float v = wave_sum(acc[i]);
                 const int r = r0 + i;
+                float b = 0.0f, y0 = 0.0f;
+                if (pre) {
+                    b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pbias), k * R + i));
+                    y0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pres), k * R + i));
+                } else if (r < rows) {  // scalar loads: they wait on no weight load
+                    if (job.bias) b = ((const_f32 *)job.bias)[r];
+                    if (job.accumulate) y0 = ((const_f32 *)job.y)[r];
+                }
                 if (lane == 0 && r < rows) {
-                    float out = job.bias ? v + job.bias[r] : v;
-                    if (job.accumulate) out = job.y[r] + out;  // x += proj (llama.rs:273-276)
+                    float out = job.bias ? v + b : v;
+                    if (job.accumulate) out = y0 + out;  // x += proj (llama.rs:273-276)
                     job.y[r] = out;
                 }
                 acc[i] = 0.0f;
             }
         }
+    };
+    // Every way back to the top of the loop has issued the same loads in the
+    // same order (the steps' loads in flight are always even, then odd), so
+    // each step waits only for its own loads; the last steps leave the loop
+    // by paths of their own and issue nothing past the wave's work.
+    for (int step = 0; step < steps; step += 2) {
+        load_step(cb, step + 1);
+        run_step(ca, step);
+        load_step(ca, step + 2);
+        if (step + 1 < steps) run_step(cb, step + 1);
     }
 }
 
@@ -628,47 +654,60 @@ int env_int(const char *name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-// Launch shape from a sweep over Llama-3-8B and Qwen2.5-0.5B shapes with
-// weights far larger than the cache: R = 4 rows per wave-step for short rows
-// (1 for very tall launches of rows two chunks per lane or wider, where
-// balance across waves matters more), fewer for short matrices so there are
-// enough waves; one workgroup per CU for Q4_K with a wide activation (each
-// workgroup stages it in LDS), three for very tall launches, else two.
+// Launch shape from sweeps over Llama-3-8B and Qwen2.5-0.5B shapes with
+// weights far larger than the cache.  Q4_K: short steps pipeline best -- one
+// chunk per lane (two segments per 4096-wide row) and two rows per step, or
+// two chunks per lane and one row for wide rows, three workgroups per CU (one
+// for wide activations, which every workgroup stages).  q8/q4: a row per
+// segment, R = 4 rows per step for short rows (1 for very tall launches,
+// where balance across waves matters more), fewer for short matrices so
+// there are enough waves, two workgroups per CU (three when very tall).
 Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
     int cpl = (maxC + WAVE - 1) / WAVE;
     if (cpl < 1) cpl = 1;
     if (cpl > 8) cpl = 8;  // wider rows take several segments
-    const bool tall = rows_total >= 16384 && cpl >= 2;
-    int r = cpl == 1 || cpl == 2 ? 4 : cpl <= 4 ? 2 : 1;
-    if (tall || (prec == KH_Q4K && cpl >= 2 && rows_total >= 6144)) r = 1;
+    int r, wg;
+    if (prec == KH_Q4K) {
+        cpl = cpl <= 2 ? 1 : 2;
+        r = cpl == 1 ? 2 : 1;
+        wg = maxCols >= 8192 ? 1 : 3;
+    } else {
+        const bool tall = rows_total >= 16384 && cpl >= 2;
+        r = cpl == 1 || cpl == 2 ? 4 : cpl <= 4 ? 2 : 1;
+        if (tall) r = 1;
+        wg = tall ? 3 : 2;
+    }
     // short matrices: fewer rows per wave, more waves
     while (r > 1 && (rows_total + r - 1) / r < 8 * cu_count) r /= 2;
-    int forced = env_int("KVAD_GEMV_R", 0);  // tuning knobs
+    // tuning knobs
+    const int fc = env_int("KVAD_GEMV_CPL", 0);  // chunks per lane (more segments when fewer)
+    if (fc > 0 && fc <= 8) cpl = fc;
+    const int forced = env_int("KVAD_GEMV_R", 0);
     if (forced == 1 || (forced == 2 && cpl <= 4) || (forced == 4 && cpl <= 2)) r = forced;
-    int wg = maxCols >= 8192 && prec == KH_Q4K ? 1 : tall || (prec == KH_Q4K && rows_total >= 6144) ? 3 : 2;
     const int fw = env_int("KVAD_GEMV_WG_PER_CU", 0);
     if (fw > 0) wg = fw;
     return {cpl, r, wg};
 }
 
-template <int PREC, int CPL, int R, int KIND>
+template <int PREC, int CPL, int R, int KIND, bool WIDE>
 void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds) {
-    hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, KIND, false>), dim3(blocks), dim3(WAVE * WPB), lds, ctx->stream, tab);
+    hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, KIND, false, WIDE>), dim3(blocks), dim3(WAVE * WPB), lds,
+                       ctx->stream, tab);
 }
 
-template <int PREC, int CPL, int R>
+template <int PREC, int CPL, int R, bool WIDE>
 void launch_kind(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int kind) {
-    if (kind == IN_F32) launch_one<PREC, CPL, R, IN_F32>(ctx, tab, blocks, lds);
-    else if (kind == IN_SWIGLU) launch_one<PREC, CPL, R, IN_SWIGLU>(ctx, tab, blocks, lds);
-    else if (kind == IN_NORM) launch_one<PREC, CPL, R, IN_NORM>(ctx, tab, blocks, lds);
-    else launch_one<PREC, CPL, R, IN_CODES>(ctx, tab, blocks, lds);
+    if (kind == IN_F32) launch_one<PREC, CPL, R, IN_F32, WIDE>(ctx, tab, blocks, lds);
+    else if (kind == IN_SWIGLU) launch_one<PREC, CPL, R, IN_SWIGLU, WIDE>(ctx, tab, blocks, lds);
+    else if (kind == IN_NORM) launch_one<PREC, CPL, R, IN_NORM, WIDE>(ctx, tab, blocks, lds);
+    else launch_one<PREC, CPL, R, IN_CODES, WIDE>(ctx, tab, blocks, lds);
 }
 
 template <int PREC>
 int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_total, bool dots, int kind) {
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     Plan p = plan_for(PREC, maxC, maxCols, rows_total, cu);
-    if (dots) p = {1, 1, 2};  // block dots (a debugging aid): one kernel shape serves every width
+    if (dots) p = {8, 1, 2};  // block dots (a debugging aid): one kernel shape serves every width
     for (int i = 0; i < tab.n; i++) {
         size_t wb = (size_t)tab.j[i].rows * tab.j[i].cols;
         if (wb >= 0xfff00000ull) return fail(KH_DECLINED, "matvec: weights of 4 GiB or more are not addressed here");
@@ -690,20 +729,30 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     const int pb = padded_blocks(PREC, maxC, p.cpl);
     const size_t lds = (size_t)pb * 32 + 8 * (size_t)pb;
     if (lds > 64 * 1024) return fail(KH_DECLINED, "matvec: activation too wide for the LDS stage");
+    // rows of several segments with R == 1 and CPL < 4 have a WIDE build
+    const bool wide = !stage_fits(kind, pb, stage_batch(p.cpl, false));
+    if (wide && !(p.cpl >= 4 || (p.r == 1 && stage_fits(kind, pb, stage_batch(p.cpl, true)))))
+        return fail(KH_DECLINED, "matvec: an f32 activation this wide is quantised in a launch of its own");
     if (dots) {
         dim3 grid(blocks), block(WAVE * WPB);
         if (kind == IN_CODES)
-            hipLaunchKernelGGL((gemv_kernel<PREC, 1, 1, IN_CODES, true>), grid, block, lds, ctx->stream, tab);
+            hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_CODES, true>), grid, block, lds, ctx->stream, tab);
         else if (kind == IN_F32)
-            hipLaunchKernelGGL((gemv_kernel<PREC, 1, 1, IN_F32, true>), grid, block, lds, ctx->stream, tab);
+            hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_F32, true>), grid, block, lds, ctx->stream, tab);
         else
             return fail(KH_EINVAL, "matvec: block dots are offered for plain and pre-quantised inputs only");
         KH_HIP(hipGetLastError());
         return KH_OK;
     }
 #define KH_CASE(CPL, R)                                                       \
-    if (p.cpl == CPL && p.r == R) {                                           \
-        launch_kind<PREC, CPL, R>(ctx, tab, blocks, lds, kind);               \
+    if (p.cpl == CPL && p.r == R && !wide) {                                  \
+        launch_kind<PREC, CPL, R, false>(ctx, tab, blocks, lds, kind);        \
+        KH_HIP(hipGetLastError());                                            \
+        return KH_OK;                                                         \
+    }
+#define KH_WIDE(CPL)                                                          \
+    if (p.cpl == CPL && p.r == 1 && wide) {                                   \
+        launch_kind<PREC, CPL, 1, true>(ctx, tab, blocks, lds, kind);         \
         KH_HIP(hipGetLastError());                                            \
         return KH_OK;                                                         \
     }
@@ -711,7 +760,9 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     KH_CASE(2, 4) KH_CASE(2, 2) KH_CASE(2, 1)
     KH_CASE(3, 2) KH_CASE(3, 1) KH_CASE(4, 2) KH_CASE(4, 1)
     KH_CASE(5, 1) KH_CASE(6, 1) KH_CASE(7, 1) KH_CASE(8, 1)
+    KH_WIDE(1) KH_WIDE(2) KH_WIDE(3)
 #undef KH_CASE
+#undef KH_WIDE
     return fail(KH_EINVAL, "matvec: no kernel for this plan");
 }
 
