@@ -209,7 +209,28 @@ def main() -> int:
         del g
     log(f"per shape: {per_shape}")
 
-    extra = {"q4k_gemv_per_shape": per_shape, "weight_bytes_resident": weight_bytes}
+    # ---- batched decode (forward_each, llama.rs:418-434): m tokens through
+    # the same 32 layers, one matmul_bt per projection (each quantises its m
+    # rows, then one multi-token GEMV streams the weights once) -------------
+    batched = {}
+    xs_m = torch.randn(8 * 14336, device=dev, generator=gen)
+    ys_m = torch.empty(8 * 14336, device=dev)
+    for m in (2, 4, 8):
+        def bstep(m=m):
+            for L in layers:
+                for name in LLAMA_LAYER:
+                    L[name].matmul_bt_dev(xs_m.data_ptr(), m, ys_m.data_ptr())
+
+        g = Graph(torch, ctx, stream, bstep)
+        s = g.time(max(3, args.steps // 2), args.warmup)
+        bb = args.layers * sum(144 * r * c // 256 + 4 * m * (r + c) for r, c in LLAMA_LAYER.values())
+        batched[str(m)] = {"ms_per_step": round(s * 1e3, 4), "GBps": round(bb / s / 1e9, 1),
+                           "token_rows_per_s": round(m / s, 1), "launches_per_step": 2 * 7 * args.layers}
+        del g
+    log(f"batched decode q4k: {batched}")
+
+    extra = {"q4k_gemv_per_shape": per_shape, "weight_bytes_resident": weight_bytes,
+             "q4k_batched_decode_llama3_8b": batched}
     if not args.no_extra:
         extra.update(secondary(torch, K, ctx, stream, dev, gen, args))
 

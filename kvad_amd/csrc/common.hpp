@@ -170,6 +170,11 @@ size_t fuse_max_cols(int precision);
 // Runs every job in one launch per input kind (all jobs share `precision`).
 int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs);
 
+// y[m, rows] = x W^T (+bias) for a few quantised token rows (m small): the
+// weights stream once for all of them.  x holds the rows' codes.
+constexpr int MULTI_TOKENS = 8;  // launch_matmul takes this path up to here
+int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, const float *bias, float *y);
+
 // Batched prefill y[m, rows] = xs[m, cols] W^T (+bias), m > 1 (device pointers).
 int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
 

@@ -537,6 +537,17 @@ int matmul_rows(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, cons
 
 }  // namespace
 
+namespace {
+// KVAD_MATMUL_GEMM=1 sends every m > 1 to the MFMA GEMM (for comparisons).
+bool matmul_force_gemm() {
+    static const bool v = [] {
+        const char *e = getenv("KVAD_MATMUL_GEMM");
+        return e && *e == '1';
+    }();
+    return v;
+}
+}  // namespace
+
 int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
     const size_t rows = w->rows, cols = w->cols;
     // 32-bit buffer offsets: the weights and activations (plus one tile of
@@ -566,6 +577,8 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     char *p = static_cast<char *>(ctx->ws.ptr);
     QAct q{reinterpret_cast<int8_t *>(p), reinterpret_cast<float *>(p + qb), reinterpret_cast<int32_t *>(p + qb + sb)};
     if ((rc = launch_qact(ctx, xs, m, cols, q))) return rc;
+    // a few tokens: stream the weights once through the multi-token GEMV
+    if (m <= (size_t)MULTI_TOKENS && !matmul_force_gemm()) return launch_gemv_multi(ctx, w, q, m, bias, y);
     a.xq = q.qs;
     a.xs = q.scales;
     a.xsum = q.sums;

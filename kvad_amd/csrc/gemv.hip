@@ -645,6 +645,203 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(JobTable tab) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Several tokens at once: matmul_bt for m <= MULTI_MAX rows (batched decode,
+// quant.rs:751-907).  The weights stream from HBM once for all m tokens; each
+// chunk's weight codes and scales are decoded once and dotted with every
+// token's codes, staged side by side in LDS.  Per token the arithmetic is the
+// single-token kernel's, term for term, so token t's row equals a GEMV of
+// that token to the bit.
+// ---------------------------------------------------------------------------
+
+
+struct MultiArgs {
+    const void *w;
+    const float *ws;
+    const int8_t *xq;     // [m][cols] codes
+    const float *xs;      // [m][cols / 32]
+    const int32_t *xsum;  // [m][cols / 32]
+    const float *bias;    // [rows] or null
+    float *y;             // [m][rows]
+    int rows, cols, m, nwaves;
+};
+
+// The chunks' contribution to each token's accumulator (one row per step).
+template <int PREC, int CPL, int T>
+__device__ __forceinline__ void compute_multi(const Chunks<PREC, CPL, 1> &c, float (&acc)[T], const int8_t *sq,
+                                              const float *ssc, const int *ssum, int PB, int seg, int lane) {
+    const int gl = seg * WAVE * CPL + lane;
+    if constexpr (PREC == KH_Q8) {
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int4 w = c.w[0][t];
+#pragma unroll
+            for (int k = 0; k < T; k++) {
+                const int4 a = *reinterpret_cast<const int4 *>(sq + (size_t)k * PB * 32 + g * 16);
+                const float as = ssc[k * PB + (g >> 1)];
+                int d = dot4(w.x, a.x, 0);
+                d = dot4(w.y, a.y, d);
+                d = dot4(w.z, a.z, d);
+                d = dot4(w.w, a.w, d);
+                d += dpp<DPP_XOR1>(d);
+                float sc = c.s[0][t] * as;
+                sc = sc * (float)d;
+                acc[k] += (lane & 1) ? 0.0f : sc;
+            }
+        }
+    } else if constexpr (PREC == KH_Q4) {
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int4 q = c.w[0][t];
+            const int4 lo4 = {q.x & 0x0f0f0f0f, q.y & 0x0f0f0f0f, q.z & 0x0f0f0f0f, q.w & 0x0f0f0f0f};
+            const int4 hi4 = {(q.x >> 4) & 0x0f0f0f0f, (q.y >> 4) & 0x0f0f0f0f, (q.z >> 4) & 0x0f0f0f0f,
+                              (q.w >> 4) & 0x0f0f0f0f};
+#pragma unroll
+            for (int k = 0; k < T; k++) {
+                const int8_t *sk = sq + (size_t)k * PB * 32;
+                const int4 alo = *reinterpret_cast<const int4 *>(sk + g * 32);
+                const int4 ahi = *reinterpret_cast<const int4 *>(sk + g * 32 + 16);
+                const float as = ssc[k * PB + g];
+                const int asum = ssum[k * PB + g];
+                int lo = dot4(lo4.x, alo.x, 0);
+                lo = dot4(lo4.y, alo.y, lo);
+                lo = dot4(lo4.z, alo.z, lo);
+                lo = dot4(lo4.w, alo.w, lo);
+                int hi = dot4(hi4.x, ahi.x, 0);
+                hi = dot4(hi4.y, ahi.y, hi);
+                hi = dot4(hi4.z, ahi.z, hi);
+                hi = dot4(hi4.w, ahi.w, hi);
+                const int d = lo + hi - 8 * asum;  // quant.rs:187
+                float sc = c.s[0][t] * as;
+                sc = sc * (float)d;
+                acc[k] += sc;
+            }
+        }
+    } else {
+        const int half = lane & 1, cc = (lane & 7) >> 1, j = 2 * cc + half;
+        const int sh = 8 * (j & 3);
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int b0 = (g >> 3) * 8 + 2 * cc;
+            const int4 q = c.w[0][t];
+            const int4 lo4 = {q.x & 0x0f0f0f0f, q.y & 0x0f0f0f0f, q.z & 0x0f0f0f0f, q.w & 0x0f0f0f0f};
+            const int4 hi4 = {(q.x >> 4) & 0x0f0f0f0f, (q.y >> 4) & 0x0f0f0f0f, (q.z >> 4) & 0x0f0f0f0f,
+                              (q.w >> 4) & 0x0f0f0f0f};
+            const int4 h = c.h[0][t];
+            const unsigned A = (unsigned)h.y >> sh, B = (unsigned)h.z >> sh, Cw = (unsigned)h.w >> sh;
+            const unsigned scb = j < 4 ? (A & 63) : ((Cw & 0xf) | ((A >> 2) & 0x30));
+            const unsigned mnb = j < 4 ? (B & 63) : (((Cw >> 4) & 0xf) | ((B >> 2) & 0x30));
+            const float dl = half_bits_to_float((unsigned)h.x) * (float)scb;
+            const float ml = half_bits_to_float((unsigned)h.x >> 16) * (float)mnb;
+#pragma unroll
+            for (int k = 0; k < T; k++) {
+                const int8_t *sk = sq + (size_t)k * PB * 32;
+                const int4 alo = *reinterpret_cast<const int4 *>(sk + b0 * 32 + 16 * half);
+                const int4 ahi = *reinterpret_cast<const int4 *>(sk + (b0 + 1) * 32 + 16 * half);
+                const float as = ssc[k * PB + b0 + half];
+                const int asum = ssum[k * PB + b0 + half];
+                int lo = dot4(lo4.x, alo.x, 0);
+                lo = dot4(lo4.y, alo.y, lo);
+                lo = dot4(lo4.z, alo.z, lo);
+                lo = dot4(lo4.w, alo.w, lo);
+                int hi = dot4(hi4.x, ahi.x, 0);
+                hi = dot4(hi4.y, ahi.y, hi);
+                hi = dot4(hi4.z, ahi.z, hi);
+                hi = dot4(hi4.w, ahi.w, hi);
+                lo += dpp<DPP_XOR1>(lo);
+                hi += dpp<DPP_XOR1>(hi);
+                const int d = half ? hi : lo;
+                float t1 = dl * (float)d;
+                float t2 = ml * (float)asum;
+                float sc = t1 - t2;
+                sc = as * sc;
+                acc[k] += sc;
+            }
+        }
+    }
+}
+
+// One wave per row at a time, rows lw, lw + nw, ...; each row in nseg
+// segments of CPL chunks per lane.  T >= m token slots (unused ones meet
+// zero codes).  The workgroup stages every token's codes first (the weights
+// of its first step are requested right after, so they fly while the
+// workgroup waits on the stage).
+template <int PREC, int CPL, int T>
+__global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rows = a.rows, cols = a.cols, nb = cols / BLOCK;
+    const int C = chunks_per_row(PREC, cols);
+    const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
+    const int PB = padded_blocks(PREC, C, CPL);
+    const int nw = a.nwaves, lw = blockIdx.x * WPB + wv;
+    const int my_rows = lw < rows ? (rows - lw + nw - 1) / nw : 0;
+    const int steps = my_rows * nseg;
+
+    int8_t *sq = reinterpret_cast<int8_t *>(lds);
+    float *ssc = reinterpret_cast<float *>(lds + (size_t)T * PB * 32);
+    int *ssum = reinterpret_cast<int *>(ssc + (size_t)T * PB);
+    {
+        const rsrc_t Q = rsrc(a.xq, (size_t)a.m * cols), S = rsrc(a.xs, (size_t)a.m * nb * 4),
+                     M = rsrc(a.xsum, (size_t)a.m * nb * 4);
+        for (int i = tid; i < T * PB * 2; i += WAVE * WPB) {  // int4 i: token i / (2 PB), 16 bytes
+            const int k = i / (PB * 2), c = i % (PB * 2);
+            const bool ok = k < a.m && c < nb * 2;
+            const int4 v = bld16(Q, ok ? (unsigned)(k * cols + c * 16) : 0xffffffffu);
+            reinterpret_cast<int4 *>(sq)[i] = v;
+        }
+        for (int i = tid; i < T * PB; i += WAVE * WPB) {
+            const int k = i / PB, b = i % PB;
+            const bool ok = k < a.m && b < nb;
+            const unsigned off = ok ? (unsigned)((k * nb + b) * 4) : 0xffffffffu;
+            ssc[i] = bldf(S, off);
+            ssum[i] = bldi(M, off);
+        }
+    }
+
+    const size_t wbytes = PREC == KH_Q8 ? (size_t)rows * cols
+                          : PREC == KH_Q4 ? (size_t)rows * cols / 2
+                                          : (size_t)rows * (cols / QK_K) * Q4K_BYTES;
+    const rsrc_t W = rsrc(a.w, wbytes);
+    const rsrc_t WS = rsrc(a.ws, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
+    auto load_step = [&](Chunks<PREC, CPL, 1> &c, int s) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunks<PREC, CPL, 1>(c, W, WS, lw + (s / nseg) * nw, cols, nb, s % nseg, lane);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    Chunks<PREC, CPL, 1> ca, cb;
+    load_step(ca, 0);
+    __syncthreads();
+
+    float acc[T];
+#pragma unroll
+    for (int k = 0; k < T; k++) acc[k] = 0.0f;
+    auto run_step = [&](const Chunks<PREC, CPL, 1> &c, int step) {
+        const int r = lw + (step / nseg) * nw, seg = step % nseg;
+        compute_multi<PREC, CPL, T>(c, acc, sq, ssc, ssum, PB, seg, lane);
+        if (seg == nseg - 1) {
+            const float b = a.bias && r < rows ? ((const_f32 *)a.bias)[r] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < T; k++) {
+                const float v = wave_sum(acc[k]);
+                if (lane == 0 && r < rows && k < a.m) a.y[(size_t)k * rows + r] = a.bias ? v + b : v;
+                acc[k] = 0.0f;
+            }
+        }
+    };
+    // the single-token kernel's loop: the same loads on every pass
+    for (int step = 0; step < steps; step += 2) {
+        load_step(cb, step + 1);
+        run_step(ca, step);
+        load_step(ca, step + 2);
+        if (step + 1 < steps) run_step(cb, step + 1);
+    }
+}
+
 struct Plan {
     int cpl, r, wg;  // chunks per lane per segment, rows per wave-step, workgroups per CU
 };
@@ -851,6 +1048,48 @@ int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, si
     return KH_OK;
 }
 
+template <int PREC, int T>
+int launch_multi_t(kh_ctx *ctx, const MultiArgs &a, int cpl, int blocks, size_t lds) {
+    dim3 grid(blocks), block(WAVE * WPB);
+    if (cpl == 1)
+        hipLaunchKernelGGL((gemv_multi_kernel<PREC, 1, T>), grid, block, lds, ctx->stream, a);
+    else
+        hipLaunchKernelGGL((gemv_multi_kernel<PREC, 2, T>), grid, block, lds, ctx->stream, a);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+template <int PREC>
+int launch_multi_p(kh_ctx *ctx, MultiArgs a) {
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int C = chunks_per_row(PREC, a.cols);
+    const int cpl = C <= 2 * WAVE ? 1 : 2;  // short steps: a row in segments of one or two chunks per lane
+    const int PB = padded_blocks(PREC, C, cpl);
+    int nwg = (a.rows + WPB - 1) / WPB;
+    if (nwg > 2 * cu) nwg = 2 * cu;
+    a.nwaves = nwg * WPB;
+    // token slots: the smallest of 2, 4, 8 that holds m, in as many launches
+    // as the LDS stage needs (each launch streams the weights once)
+    for (int t0 = 0; t0 < a.m;) {
+        int T = a.m - t0 <= 2 ? 2 : a.m - t0 <= 4 ? 4 : 8;
+        while (T > 2 && (size_t)T * PB * 40 > 64 * 1024) T /= 2;
+        if ((size_t)T * PB * 40 > 64 * 1024) return fail(KH_DECLINED, "matmul: activation too wide for the LDS stage");
+        MultiArgs b = a;
+        b.m = a.m - t0 < T ? a.m - t0 : T;
+        b.xq = a.xq + (size_t)t0 * a.cols;
+        b.xs = a.xs + (size_t)t0 * (a.cols / BLOCK);
+        b.xsum = a.xsum + (size_t)t0 * (a.cols / BLOCK);
+        b.y = a.y + (size_t)t0 * a.rows;
+        const size_t lds = (size_t)T * PB * 40;
+        int rc = T == 2 ? launch_multi_t<PREC, 2>(ctx, b, cpl, nwg, lds)
+                 : T == 4 ? launch_multi_t<PREC, 4>(ctx, b, cpl, nwg, lds)
+                          : launch_multi_t<PREC, 8>(ctx, b, cpl, nwg, lds);
+        if (rc) return rc;
+        t0 += b.m;
+    }
+    return KH_OK;
+}
+
 int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
     // one launch per input kind present (a kernel stages one kind), in table order
     for (int i = 0; i < njobs; i++)
@@ -885,6 +1124,29 @@ int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
         if (precision == KH_F32) break;
     }
     return KH_OK;
+}
+
+int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, const float *bias, float *y) {
+    if (m == 0) return KH_OK;
+    if ((size_t)w->rows * w->cols >= 0xfff00000ull || m * w->cols >= 0xfff00000ull)
+        return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
+    MultiArgs a{};
+    a.w = w->qs;
+    a.ws = w->scales;
+    a.xq = x.qs;
+    a.xs = x.scales;
+    a.xsum = x.sums;
+    a.bias = bias;
+    a.y = y;
+    a.rows = (int)w->rows;
+    a.cols = (int)w->cols;
+    a.m = (int)m;
+    switch (w->precision) {
+        case KH_Q8: return launch_multi_p<KH_Q8>(ctx, a);
+        case KH_Q4: return launch_multi_p<KH_Q4>(ctx, a);
+        case KH_Q4K: return launch_multi_p<KH_Q4K>(ctx, a);
+        default: return fail(KH_EINVAL, "matmul: the multi-token GEMV takes quantised weights");
+    }
 }
 
 size_t fuse_max_cols(int precision) {
