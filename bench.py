@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary (q8, attention) figures")
+    ap.add_argument("--only", choices=SECTIONS, default=None,
+                    help="run one secondary workload alone (for per-kernel rocprofv3 summaries) and print its figures")
     ap.add_argument("--counters", type=int, default=0, metavar="MIB",
                     help="only run a MIB-sized copy and two eager steps of the GEMV kernels (for rocprofv3 --pmc)")
     return ap.parse_args()
@@ -131,6 +133,12 @@ def main() -> int:
     ctx.reserve(64 << 20)
     gen = torch.Generator(device=dev)
     gen.manual_seed(20251201)
+
+    if args.only:
+        res = secondary(torch, K, ctx, stream, dev, gen, args, only=args.only)
+        print(json.dumps({"section": args.only, "n_gpus": 1, "data": "synthetic", "extra": res}), flush=True)
+        ctx.set_stream(None)
+        return 0
 
     # ---- weights: Q4_K quantised on the device from f32 ~ N(0, 0.02) ------
     t0 = time.time()
@@ -282,9 +290,31 @@ def measured_traffic():
         return None
 
 
-def secondary(torch, K, ctx, stream, dev, gen, args):
-    """BASELINE configs[0] (Q8 GEMV at Qwen2.5-0.5B FFN shapes, 24 layers) and
-    configs[3] (decode attention, Qwen geometry) as extra figures."""
+SECTIONS = ("q8", "prefill", "moe", "decode", "attend")
+
+
+def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
+    """The other configs as extra figures: BASELINE configs[0] (Q8 GEMV at
+    Qwen2.5-0.5B shapes), [2] (prefill GEMM), [3] (decode attention), [4]
+    (MoE) and the Qwen2.5-0.5B q8 decode session.  `only` picks one."""
+    out = {}
+    want = lambda name: only is None or only == name
+    if want("q8"):
+        out.update(q8_qwen(torch, K, ctx, stream, dev, gen, args))
+    if want("prefill"):
+        out["prefill_gemm"] = prefill(torch, K, ctx, stream, dev, gen, args)
+    if want("moe"):
+        out["moe_deepseek_v2_lite"] = moe(torch, K, ctx, stream, dev, gen, args)
+    if want("decode"):
+        out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args)
+    if want("attend"):
+        out["attend_qwen05b"] = attend(torch, K, ctx, stream, dev, gen, args)
+    return out
+
+
+def q8_qwen(torch, K, ctx, stream, dev, gen, args):
+    """Q8 GEMV at Qwen2.5-0.5B decode shapes, 24 layers
+    of distinct weights plus the 151936x896 lm_head."""
     out = {}
     qwen = {"q": (896, 896), "k": (128, 896), "v": (128, 896), "o": (896, 896),
             "gate": (4864, 896), "up": (4864, 896), "down": (896, 4864)}
@@ -347,11 +377,13 @@ def secondary(torch, K, ctx, stream, dev, gen, args):
     out["q8_qwen05b_ffn_single_launches"] = {"GBps": round(fb / s / 1e9, 1), "us_per_gemv": round(s / 48 * 1e6, 2)}
     log(f"q8 qwen: {out}")
     del g
+    return out
 
-    out["prefill_gemm"] = prefill(torch, K, ctx, stream, dev, gen, args)
-    out["moe_deepseek_v2_lite"] = moe(torch, K, ctx, stream, dev, gen, args)
-    out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args)
 
+def attend(torch, K, ctx, stream, dev, gen, args):
+    """GQA decode attention at Qwen2.5-0.5B geometry
+    (14 query heads, 2 KV heads, head_dim 64) over 24 layers of distinct f32
+    caches ~ N(0, 1); bytes = each K and V row read once, plus q and out."""
     spec = K.Spec(14, 2, 64)
     att = {}
     for L in (1024, 8192, 32768):
@@ -369,9 +401,8 @@ def secondary(torch, K, ctx, stream, dev, gen, args):
         b = 4 * L * 256 + 8 * 14 * 64
         att[str(L)] = {"us_per_layer": round(s * 1e6, 2), "GBps": round(b / s / 1e9, 1)}
         del g, kv
-    out["attend_qwen05b"] = att
     log(f"attend: {att}")
-    return out
+    return att
 
 
 def prefill(torch, K, ctx, stream, dev, gen, args):
