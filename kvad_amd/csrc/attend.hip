@@ -155,19 +155,40 @@ __device__ __forceinline__ float rows_min(float x) {
     return rows_reduce(x, [](float u, float v) { return fminf(u, v); });
 }
 
-// Split kernel.  Lanes form 16-lane rows (16 per workgroup); row r takes
-// positions r, r + 16, ... of the split, lane `sub` of a row dims
-// [sub*DPL, sub*DPL + DPL).  Each wave reduces its four rows with lane swaps
-// against the wave's own maximum, and the four waves meet once in LDS.
-template <int HD, int G, int NP>  // G heads per workgroup; P = 16 * NP positions
+// Split kernel, on matrix cores (v_mfma_f32_16x16x4_f32).  A workgroup of
+// four waves owns one KV head's G <= 16 query heads and P = 64 R positions;
+// wave w takes R tiles of 16 consecutive positions.  Per tile:
+//   scores  S = K Q^T: A = 16 positions x 4 k-slots, B = 4 k-slots x 16
+//           heads; k-slot c of lane (c, i) covers the head dims
+//           [c HD/4, (c+1) HD/4), one product per dim, so lane (c, i) reads
+//           HD bytes of key row i contiguously; the 16 columns are the G
+//           query heads (the rest zero).
+//   S lands as lane (c, j) holding positions 4c .. 4c+3 of head j: after
+//   exp, exactly the A operand of the value product for the four position
+//   groups r = 0..3 (position 4c + r in k-slot c).
+//   values  O += P V: B = V rows 4c + r, lane (c, j) holding dims
+//           4j .. 4j+3 (+64): one float4 of a row per lane, four rows of
+//           256 contiguous bytes per load instruction.
+// Every K and V row of the workgroup is loaded up front.  Statistics per
+// head are reduced over the wave's four lane rows with lane swaps; the four
+// waves meet once in LDS, as partial (m, l, acc) per split, or, when one
+// split covers the whole sequence, as the reference's exact weights
+// w = exp(s - M) * (1/S) with w < 1e-8 dropped (mod.rs:805-812).
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <int HD, int R>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
-    constexpr int DPL = HD / 16;  // dims per lane
-    constexpr int P = 16 * NP;
+    constexpr int HQ = HD / 4;   // dims per k-slot of the score product
+    constexpr int NQ4 = HQ / 4;  // float4s per lane of a key row
+    constexpr int VT = HD / 64;  // float4s per lane of a value row
+    constexpr int NT = HD / 16;  // 16-column tiles of the output
+    constexpr int P = 64 * R;
     const int split = blockIdx.x, hg = blockIdx.y;
+    const int G = a.gc;
     const int h0 = hg * G, kvh = h0 / a.group;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sub = lane & 15, row = tid >> 4;
+    const int j16 = lane & 15, c4 = lane >> 4;
     const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
     const int nsplit = (L + P - 1) / P;
     if (split >= nsplit) return;
@@ -175,88 +196,113 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     const int n = min(L - t0, P);
     const bool whole = nsplit == 1;
     const rsrc_t K = rsrc(a.k, (size_t)L * a.kstride * 4), V = rsrc(a.v, (size_t)L * a.vstride * 4);
+    const int pw = wave * 16 * R;  // the wave's first position in the split
 
-    __shared__ float s_acc[4][G][HD];  // per-wave totals
-    __shared__ float s_st[3][4][G];    // per-wave max, sum, smallest score
+    __shared__ __align__(16) float s_acc[4][16][HD];  // per-wave totals
+    __shared__ float s_st[3][4][16];                  // per-wave max, sum, smallest score
 
-    // every K and V row of the split in flight at once
-    float kr[NP][DPL], vr[NP][DPL];
+    // q first (the score products wait on it before any key), then keys,
+    // then values: loads complete in issue order
+    const bool hv = j16 < G;
+    f4v qb4[NQ4];
+    {
+        const float *qh = a.q + (size_t)(h0 + (hv ? j16 : 0)) * HD + HQ * c4;
 #pragma unroll
-    for (int u = 0; u < NP; u++) {
-        const size_t t = (size_t)(t0 + u * 16 + row);
-        load_row<DPL>(K, (unsigned)((t * a.kstride + (size_t)kvh * HD + sub * DPL) * 4), kr[u]);
-        load_row<DPL>(V, (unsigned)((t * a.vstride + (size_t)kvh * HD + sub * DPL) * 4), vr[u]);
-    }
-    float qr[G][DPL];
-#pragma unroll
-    for (int h = 0; h < G; h++)
-#pragma unroll
-        for (int d = 0; d < DPL; d += 4) {
-            const float4 f = *reinterpret_cast<const float4 *>(a.q + (size_t)(h0 + h) * HD + sub * DPL + d);
-            qr[h][d] = f.x, qr[h][d + 1] = f.y, qr[h][d + 2] = f.z, qr[h][d + 3] = f.w;
-        }
-
-    // scores (the same in all 16 lanes of a row), the row's extremes
-    float s[NP][G], mx[G], mn[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) mx[h] = -INFINITY, mn[h] = INFINITY;
-#pragma unroll
-    for (int u = 0; u < NP; u++) {
-        score_row<G, DPL>(qr, kr[u], a.scale, G, s[u]);
-        const bool ok = u * 16 + row < n;
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            s[u][h] = ok ? s[u][h] : -INFINITY;
-            mx[h] = fmaxf(mx[h], s[u][h]);
-            mn[h] = ok ? fminf(mn[h], s[u][h]) : mn[h];
+        for (int m = 0; m < NQ4; m++) {
+            const float4 f = *reinterpret_cast<const float4 *>(qh + 4 * m);
+            qb4[m] = hv ? f4v{f.x, f.y, f.z, f.w} : f4v{0.f, 0.f, 0.f, 0.f};
         }
     }
+    f4v kq[R][NQ4];
+    f4v vv[R][4][VT];
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        mx[h] = rows_max(mx[h]);
-        mn[h] = rows_min(mn[h]);
-    }
-
-    // exp(s - m) against the wave's max; the wave's sum and weighted values
-    float l[G], acc[G][DPL];
+    for (int u = 0; u < R; u++) {
+        const size_t t = (size_t)(t0 + pw + 16 * u + j16);
+        const unsigned off = (unsigned)((t * a.kstride + (size_t)kvh * HD + HQ * c4) * 4);
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        l[h] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < DPL; d++) acc[h][d] = 0.0f;
+        for (int m = 0; m < NQ4; m++)
+            kq[u][m] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(K, off, 16 * m, 0));
     }
 #pragma unroll
-    for (int u = 0; u < NP; u++)
+    for (int u = 0; u < R; u++)
 #pragma unroll
-        for (int h = 0; h < G; h++) {
-            const float e = s[u][h] == -INFINITY ? 0.0f : expf(s[u][h] - mx[h]);
-            l[h] += e;
+        for (int r = 0; r < 4; r++) {
+            const size_t t = (size_t)(t0 + pw + 16 * u + 4 * c4 + r);
+            const unsigned off = (unsigned)((t * a.vstride + (size_t)kvh * HD + 4 * j16) * 4);
 #pragma unroll
-            for (int d = 0; d < DPL; d++) acc[h][d] = fmaf(e, vr[u][d], acc[h][d]);
+            for (int v = 0; v < VT; v++)
+                vv[u][r][v] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(V, off, 256 * v, 0));
         }
+
+    // scores: lane (c4, j16) holds positions pw + 16u + 4c4 + r of head j16
+    f4v s[R];
+    float mx = -INFINITY, mn = INFINITY;
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        l[h] = rows_sum(l[h]);
+    for (int u = 0; u < R; u++) {
+        f4v d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int d = 0; d < DPL; d++) acc[h][d] = rows_sum(acc[h][d]);
-    }
-    if (lane < 16) {
+        for (int m = 0; m < NQ4; m++)
 #pragma unroll
-        for (int h = 0; h < G; h++)
+            for (int c = 0; c < 4; c++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(kq[u][m][c], qb4[m][c], d, 0, 0, 0);
 #pragma unroll
-            for (int d = 0; d < DPL; d++) s_acc[wave][h][sub * DPL + d] = acc[h][d];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            s_st[0][wave][h] = mx[h];
-            s_st[1][wave][h] = l[h];
-            s_st[2][wave][h] = mn[h];
+        for (int r = 0; r < 4; r++) {
+            const bool ok = hv && pw + 16 * u + 4 * c4 + r < n;
+            const float sc = d[r] * a.scale;  // dot(q, k) * scale, mod.rs:802
+            s[u][r] = ok ? sc : -INFINITY;
+            mx = fmaxf(mx, s[u][r]);
+            mn = ok ? fminf(mn, sc) : mn;
         }
     }
-    __syncthreads();
+    mx = rows_max(mx);
+    mn = rows_min(mn);
 
+    // O = sum_t p_t v_t over the wave's tiles, p given in the score layout
+    auto values = [&](const f4v (&p)[R], f4v (&acc)[NT]) {
+#pragma unroll
+        for (int q = 0; q < NT; q++) acc[q] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < R; u++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int q = 0; q < NT; q++)
+                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[u][r], vv[u][r][q >> 2][q & 3], acc[q], 0, 0, 0);
+    };
+    // acc[q][i] is head 4 c4 + i, dim 4 j16 + (q & 3) + 64 (q >> 2)
+    auto store_acc = [&](const f4v (&acc)[NT]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * c4 + i;
+            if (h < G) {
+#pragma unroll
+                for (int v = 0; v < VT; v++)
+                    *reinterpret_cast<float4 *>(&s_acc[wave][h][64 * v + 4 * j16]) =
+                        make_float4(acc[4 * v][i], acc[4 * v + 1][i], acc[4 * v + 2][i], acc[4 * v + 3][i]);
+            }
+        }
+    };
+
+    // exp(s - m) against the wave's max
+    f4v e[R];
+    float l = 0.0f;
+#pragma unroll
+    for (int u = 0; u < R; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            e[u][r] = s[u][r] == -INFINITY ? 0.0f : expf(s[u][r] - mx);
+            l += e[u][r];
+        }
+    l = rows_sum(l);
     if (!whole) {
+        f4v acc[NT];
+        values(e, acc);
+        store_acc(acc);
+        if (c4 == 0 && hv) {
+            s_st[0][wave][j16] = mx;
+            s_st[1][wave][j16] = l;
+            s_st[2][wave][j16] = mn;
+        }
+        __syncthreads();
         // the split's statistics: M over the waves, each wave rescaled to it
         for (int i = tid; i < G * HD; i += 256) {
             const int h = i / HD, d = i % HD;
@@ -272,15 +318,15 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         if (tid < G) {
             const int h = tid;
             const float M = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
-            float L = 0.0f;
+            float Ls = 0.0f;
 #pragma unroll
             for (int w = 0; w < 4; w++) {
                 const float c = s_st[0][w][h] == -INFINITY ? 0.0f : expf(s_st[0][w][h] - M);
-                L = fmaf(c, s_st[1][w][h], L);
+                Ls = fmaf(c, s_st[1][w][h], Ls);
             }
             const size_t o = (size_t)split * a.n_head + h0 + h;
             a.pm[o] = M;
-            a.pl[o] = L;
+            a.pl[o] = Ls;
             a.pmin[o] = fminf(fminf(s_st[2][0][h], s_st[2][1][h]), fminf(s_st[2][2][h], s_st[2][3][h]));
         }
         return;
@@ -289,54 +335,32 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     // One split is the whole sequence: the reference's own weights
     // w = exp(s - M) * (1/S), S = sum exp(s - M), dropping w < 1e-8
     // (softmax_inplace, tensor.rs:297-308; mod.rs:805-812).
-    float M[G];
-#pragma unroll
-    for (int h = 0; h < G; h++)
-        M[h] = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
-    float e[NP][G];
-#pragma unroll
-    for (int h = 0; h < G; h++) l[h] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < NP; u++)
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            e[u][h] = s[u][h] == -INFINITY ? 0.0f : expf(s[u][h] - M[h]);
-            l[h] += e[u][h];
-        }
-#pragma unroll
-    for (int h = 0; h < G; h++) l[h] = rows_sum(l[h]);
-    __syncthreads();  // everyone has read s_st
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < G; h++) s_st[1][wave][h] = l[h];
-    }
+    if (c4 == 0 && hv) s_st[0][wave][j16] = mx;
     __syncthreads();
-    float inv[G];
+    const int hj = hv ? j16 : 0;
+    const float M = fmaxf(fmaxf(s_st[0][0][hj], s_st[0][1][hj]), fmaxf(s_st[0][2][hj], s_st[0][3][hj]));
+    l = 0.0f;
 #pragma unroll
-    for (int h = 0; h < G; h++) inv[h] = 1.0f / (((s_st[1][0][h] + s_st[1][1][h]) + s_st[1][2][h]) + s_st[1][3][h]);
+    for (int u = 0; u < R; u++)
 #pragma unroll
-    for (int h = 0; h < G; h++)
-#pragma unroll
-        for (int d = 0; d < DPL; d++) acc[h][d] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < NP; u++)
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            float w = e[u][h] * inv[h];
-            w = w < 1e-8f ? 0.0f : w;
-#pragma unroll
-            for (int d = 0; d < DPL; d++) acc[h][d] = fmaf(w, vr[u][d], acc[h][d]);
+        for (int r = 0; r < 4; r++) {
+            e[u][r] = s[u][r] == -INFINITY ? 0.0f : expf(s[u][r] - M);
+            l += e[u][r];
         }
+    l = rows_sum(l);
+    if (c4 == 0 && hv) s_st[1][wave][j16] = l;
+    __syncthreads();
+    const float inv = 1.0f / (((s_st[1][0][hj] + s_st[1][1][hj]) + s_st[1][2][hj]) + s_st[1][3][hj]);
 #pragma unroll
-    for (int h = 0; h < G; h++)
+    for (int u = 0; u < R; u++)
 #pragma unroll
-        for (int d = 0; d < DPL; d++) acc[h][d] = rows_sum(acc[h][d]);
-    if (lane < 16) {
-#pragma unroll
-        for (int h = 0; h < G; h++)
-#pragma unroll
-            for (int d = 0; d < DPL; d++) s_acc[wave][h][sub * DPL + d] = acc[h][d];
-    }
+        for (int r = 0; r < 4; r++) {
+            const float w = e[u][r] * inv;
+            e[u][r] = w < 1e-8f ? 0.0f : w;
+        }
+    f4v acc[NT];
+    values(e, acc);
+    store_acc(acc);
     __syncthreads();
     for (int i = tid; i < G * HD; i += 256) {
         const int h = i / HD, d = i % HD;
@@ -478,33 +502,13 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     }
 }
 
-// P ladders: 16, 64, 128 positions for hd 64; 16, 32, 64 for hd 128.
-template <int HD, int G>
-void launch_split_g(const AttnArgs &a, dim3 grid, hipStream_t stream) {
-    const int np = a.P / 16;
-    if (np == 1) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, G, 1>), grid, dim3(256), 0, stream, a);
-    } else if constexpr (HD == 64) {
-        if (np == 4) hipLaunchKernelGGL((attn_split_kernel<64, G, 4>), grid, dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((attn_split_kernel<64, G, 8>), grid, dim3(256), 0, stream, a);
-    } else {
-        if (np == 2) hipLaunchKernelGGL((attn_split_kernel<128, G, 2>), grid, dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((attn_split_kernel<128, G, 4>), grid, dim3(256), 0, stream, a);
-    }
-}
-
+// P = 64 R positions per workgroup: R in {1, 2, 4} for hd 64, {1, 2} for hd 128.
 template <int HD>
 void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
-    switch (a.gc) {
-        case 1: launch_split_g<HD, 1>(a, grid, stream); break;
-        case 2: launch_split_g<HD, 2>(a, grid, stream); break;
-        case 3: launch_split_g<HD, 3>(a, grid, stream); break;
-        case 4: launch_split_g<HD, 4>(a, grid, stream); break;
-        case 5: launch_split_g<HD, 5>(a, grid, stream); break;
-        case 6: launch_split_g<HD, 6>(a, grid, stream); break;
-        case 7: launch_split_g<HD, 7>(a, grid, stream); break;
-        default: launch_split_g<HD, 8>(a, grid, stream); break;
-    }
+    const int r = a.P / 64;
+    if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1>), grid, dim3(256), 0, stream, a);
+    else if (HD == 128 || r == 2) hipLaunchKernelGGL((attn_split_kernel<HD, 2>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((attn_split_kernel<64, 4>), grid, dim3(256), 0, stream, a);
 }
 
 }  // namespace
@@ -532,20 +536,20 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     a.vbytes = n_positions * vstride * 4;
     a.n_head = n_head;
     a.group = n_head / n_kv_head;
-    int gc = 1;
-    for (int c = 1; c <= 8; c++)
+    int gc = 1;  // query heads per workgroup: the 16 columns of the score product
+    for (int c = 1; c <= 16; c++)
         if (a.group % c == 0) gc = c;
     a.gc = gc;
     const int n_hg = n_head / gc;
     a.L = (int)n_positions;
-    // positions per split, from a short ladder: 16 rows, or the middle rung
-    // when that would give more than about four workgroups per CU, or the
-    // top rung when the merge's split limit needs it
+    // positions per split: the largest rung that still gives a workgroup
+    // per CU, or a larger one when the merge's split limit needs it
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const int ladder[3] = {16, head_dim == 64 ? 64 : 32, head_dim == 64 ? 128 : 64};
-    int step = 0;
-    while (step < 1 && (long long)((n_positions + ladder[step] - 1) / ladder[step]) * n_hg > 4 * cu) step++;
-    while (step < 2 && (n_positions + ladder[step] - 1) / ladder[step] > (size_t)MAX_SPLITS) step++;
+    const int rungs = head_dim == 64 ? 3 : 2;
+    const int ladder[3] = {64, 128, 256};
+    int step = rungs - 1;
+    while (step > 0 && (long long)((n_positions + ladder[step] - 1) / ladder[step]) * n_hg < cu) step--;
+    while (step < rungs - 1 && (n_positions + ladder[step] - 1) / ladder[step] > (size_t)MAX_SPLITS) step++;
     const int P = ladder[step];
     if ((n_positions + P - 1) / P > (size_t)MAX_SPLITS)
         return fail(KH_DECLINED, "attend: sequence longer than the split merge takes");
