@@ -379,9 +379,9 @@ __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.
 // The thread's loads: float4 c = k * T + tid of the f32 input (block c >> 3),
 // or int4 c of the codes and scale and sum c.  One such batch covers the
 // whole activation (the launcher checks it: stage_fits).
-template <int KIND, int SB>
+template <int KIND, int SB, int NWV>
 __device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &st, int nb, int tid) {
-    constexpr int T = WAVE * WPB;
+    constexpr int T = WAVE * NWV;
     // buffer loads: past the input's end they return zeros, with no branch
     if constexpr (KIND == IN_CODES) {
         const rsrc_t Q = rsrc(job.xq, (size_t)nb * BLOCK), S = rsrc(job.xs, (size_t)nb * 4),
@@ -411,10 +411,10 @@ __device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &
 // rms_norm (tensor.rs:329-333) for IN_NORM or swiglu(xf, xf2)
 // (tensor.rs:344-350) for IN_SWIGLU; codes made elsewhere are copied.  `st` holds batch 0,
 // loaded by stage_load.  Every workgroup computes the same values.
-template <int KIND, int SB>
+template <int KIND, int SB, int NWV>
 __device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND, SB> &st, int8_t *sq, float *ssc,
                                                  int *ssum, int PB, int nb, int cols, int tid, int lane, int wv) {
-    constexpr int T = WAVE * WPB;
+    constexpr int T = WAVE * NWV;
     if constexpr (KIND == IN_CODES) {
 #pragma unroll
         for (int k = 0; k < SB; k++) {
@@ -433,7 +433,7 @@ __device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND,
             // Sum of squares over the thread's float4s in index order, then
             // over the wave, then over the waves in order: every workgroup
             // gets the same sum.
-            __shared__ float s_ss[WPB];
+            __shared__ float s_ss[NWV];
             float ss = 0.0f;
 #pragma unroll
             for (int k = 0; k < SB; k++) {
@@ -446,7 +446,7 @@ __device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND,
             __syncthreads();
             float t = 0.0f;
 #pragma unroll
-            for (int w = 0; w < WPB; w++) t = t + s_ss[w];
+            for (int w = 0; w < NWV; w++) t = t + s_ss[w];
             inv = 1.0f / sqrtf(t / (float)cols + job.norm_eps);
         }
 #pragma unroll
@@ -478,8 +478,8 @@ __device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND,
 // A kernel stages 8 loads per thread where its weight registers leave room
 // (CPL >= 4) or where it is built WIDE (rows of several segments), else 4.
 __host__ __device__ constexpr int stage_batch(int cpl, bool wide) { return cpl >= 4 || wide ? 8 : 4; }
-__host__ __device__ inline bool stage_fits(int kind, int PB, int sb) {
-    const int cap = sb * WAVE * WPB;
+__host__ __device__ inline bool stage_fits(int kind, int PB, int sb, int nwv) {
+    const int cap = sb * WAVE * nwv;
     return kind == IN_CODES ? PB * 2 <= cap : PB * 8 <= cap;
 }
 
@@ -493,8 +493,8 @@ __host__ __device__ inline int input_kind(const GemvJob &j) {
 // lw, lw + nw, ... of its job, loading the next group's weights before it
 // computes the current one.  The first group's loads are issued before the
 // activation is staged, so they fly while the workgroup quantises.
-template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false>
-__global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
+template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB>
+__global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
     const int lane = tid & (WAVE - 1);
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     const int PB = padded_blocks(PREC, C, CPL);
     const int ngroups = (rows + R - 1) / R;
     const int nw = job.nwaves;                              // waves on this job
-    const int lw = (blk - job.wave0) * WPB + wv;            // this wave among them
+    const int lw = (blk - job.wave0) * NWV + wv;            // this wave among them
 
     size_t wbytes = PREC == KH_Q8 ? (size_t)rows * cols
                     : PREC == KH_Q4 ? (size_t)rows * cols / 2
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
         __builtin_amdgcn_sched_barrier(0);
     };
     Stage<KIND, stage_batch(CPL, WIDE)> st;
-    stage_load(job, st, nb, tid);
+    stage_load<KIND, stage_batch(CPL, WIDE), NWV>(job, st, nb, tid);
     // The bias and residual values of the wave's rows, lane k * R + i holding
     // those of row (lw + k * nw) * R + i, also ahead of the weights (a load in
     // the epilogue would wait for every weight load in flight).
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_kernel(JobTable tab) {
     int8_t *sq = reinterpret_cast<int8_t *>(lds);
     float *ssc = reinterpret_cast<float *>(lds + (size_t)PB * 32);
     int *ssum = reinterpret_cast<int *>(ssc + PB);
-    stage_activation(job, st, sq, ssc, ssum, PB, nb, cols, tid, lane, wv);
+    stage_activation<KIND, stage_batch(CPL, WIDE), NWV>(job, st, sq, ssc, ssum, PB, nb, cols, tid, lane, wv);
     __syncthreads();
 
     float acc[R];
@@ -844,6 +844,7 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
 
 struct Plan {
     int cpl, r, wg;  // chunks per lane per segment, rows per wave-step, workgroups per CU
+    int nwv;         // waves per workgroup
 };
 
 int env_int(const char *name, int dflt) {
@@ -863,7 +864,7 @@ Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
     int cpl = (maxC + WAVE - 1) / WAVE;
     if (cpl < 1) cpl = 1;
     if (cpl > 8) cpl = 8;  // wider rows take several segments
-    int r, wg;
+    int r, wg, nwv = WPB;
     if (prec == KH_Q4K) {
         cpl = cpl <= 2 ? 1 : 2;
         r = cpl == 1 ? 2 : 1;
@@ -875,7 +876,7 @@ Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
         wg = tall ? 3 : 2;
     }
     // short matrices: fewer rows per wave, more waves
-    while (r > 1 && (rows_total + r - 1) / r < 8 * cu_count) r /= 2;
+    while (r > 1 && (rows_total + r - 1) / r < nwv * cu_count) r /= 2;
     // tuning knobs
     const int fc = env_int("KVAD_GEMV_CPL", 0);  // chunks per lane (more segments when fewer)
     if (fc > 0 && fc <= 8) cpl = fc;
@@ -883,28 +884,33 @@ Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
     if (forced == 1 || (forced == 2 && cpl <= 4) || (forced == 4 && cpl <= 2)) r = forced;
     const int fw = env_int("KVAD_GEMV_WG_PER_CU", 0);
     if (fw > 0) wg = fw;
-    return {cpl, r, wg};
+    // A wide Q4_K activation, staged by every workgroup: one workgroup of 16
+    // waves per CU stages it once, with twice the threads (one staging
+    // batch of four loads per thread covers up to 16384 columns).
+    if (prec == KH_Q4K && cpl == 2 && r == 1 && maxCols >= 8192 && maxCols <= 16384) nwv = 16;
+    if (env_int("KVAD_GEMV_WAVES", 0) == 8) nwv = WPB;
+    return {cpl, r, wg, nwv};
 }
 
-template <int PREC, int CPL, int R, int KIND, bool WIDE>
+template <int PREC, int CPL, int R, int KIND, bool WIDE, int NWV>
 void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds) {
-    hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, KIND, false, WIDE>), dim3(blocks), dim3(WAVE * WPB), lds,
+    hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, KIND, false, WIDE, NWV>), dim3(blocks), dim3(WAVE * NWV), lds,
                        ctx->stream, tab);
 }
 
-template <int PREC, int CPL, int R, bool WIDE>
+template <int PREC, int CPL, int R, bool WIDE, int NWV = WPB>
 void launch_kind(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int kind) {
-    if (kind == IN_F32) launch_one<PREC, CPL, R, IN_F32, WIDE>(ctx, tab, blocks, lds);
-    else if (kind == IN_SWIGLU) launch_one<PREC, CPL, R, IN_SWIGLU, WIDE>(ctx, tab, blocks, lds);
-    else if (kind == IN_NORM) launch_one<PREC, CPL, R, IN_NORM, WIDE>(ctx, tab, blocks, lds);
-    else launch_one<PREC, CPL, R, IN_CODES, WIDE>(ctx, tab, blocks, lds);
+    if (kind == IN_F32) launch_one<PREC, CPL, R, IN_F32, WIDE, NWV>(ctx, tab, blocks, lds);
+    else if (kind == IN_SWIGLU) launch_one<PREC, CPL, R, IN_SWIGLU, WIDE, NWV>(ctx, tab, blocks, lds);
+    else if (kind == IN_NORM) launch_one<PREC, CPL, R, IN_NORM, WIDE, NWV>(ctx, tab, blocks, lds);
+    else launch_one<PREC, CPL, R, IN_CODES, WIDE, NWV>(ctx, tab, blocks, lds);
 }
 
 template <int PREC>
 int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_total, bool dots, int kind) {
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     Plan p = plan_for(PREC, maxC, maxCols, rows_total, cu);
-    if (dots) p = {8, 1, 2};  // block dots (a debugging aid): one kernel shape serves every width
+    if (dots) p = {8, 1, 2, WPB};  // block dots (a debugging aid): one kernel shape serves every width
     for (int i = 0; i < tab.n; i++) {
         size_t wb = (size_t)tab.j[i].rows * tab.j[i].cols;
         if (wb >= 0xfff00000ull) return fail(KH_DECLINED, "matvec: weights of 4 GiB or more are not addressed here");
@@ -914,12 +920,12 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     int blocks = 0;
     for (int i = 0; i < tab.n; i++) {
         const int groups = (tab.j[i].rows + p.r - 1) / p.r;
-        const int want = (groups + WPB - 1) / WPB;
+        const int want = (groups + p.nwv - 1) / p.nwv;
         int share = (int)((long long)cap_wg * tab.j[i].rows / (rows_total > 0 ? rows_total : 1));
         if (share < 1) share = 1;
         const int nwg = want < share ? want : share;
         tab.j[i].wave0 = blocks;  // first workgroup of the job
-        tab.j[i].nwaves = nwg * WPB;
+        tab.j[i].nwaves = nwg * p.nwv;
         blocks += nwg;
     }
     if (blocks == 0) return KH_OK;
@@ -927,8 +933,8 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     const size_t lds = (size_t)pb * 32 + 8 * (size_t)pb;
     if (lds > 64 * 1024) return fail(KH_DECLINED, "matvec: activation too wide for the LDS stage");
     // rows of several segments with R == 1 and CPL < 4 have a WIDE build
-    const bool wide = !stage_fits(kind, pb, stage_batch(p.cpl, false));
-    if (wide && !(p.cpl >= 4 || (p.r == 1 && stage_fits(kind, pb, stage_batch(p.cpl, true)))))
+    const bool wide = !stage_fits(kind, pb, stage_batch(p.cpl, false), p.nwv);
+    if (wide && !(p.cpl >= 4 || (p.r == 1 && stage_fits(kind, pb, stage_batch(p.cpl, true), p.nwv))))
         return fail(KH_DECLINED, "matvec: an f32 activation this wide is quantised in a launch of its own");
     if (dots) {
         dim3 grid(blocks), block(WAVE * WPB);
@@ -952,6 +958,12 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
         launch_kind<PREC, CPL, 1, true>(ctx, tab, blocks, lds, kind);         \
         KH_HIP(hipGetLastError());                                            \
         return KH_OK;                                                         \
+    }
+    if (p.nwv == 16) {
+        if (p.cpl != 2 || p.r != 1 || wide) return fail(KH_EINVAL, "matvec: no 16-wave kernel for this plan");
+        launch_kind<PREC, 2, 1, false, 16>(ctx, tab, blocks, lds, kind);
+        KH_HIP(hipGetLastError());
+        return KH_OK;
     }
     KH_CASE(1, 4) KH_CASE(1, 2) KH_CASE(1, 1)
     KH_CASE(2, 4) KH_CASE(2, 2) KH_CASE(2, 1)
