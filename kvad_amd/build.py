@@ -12,6 +12,10 @@ Flags that matter for parity:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                      no packed-FP32 instructions (they have
                                      given wrong results on these boxes)
+  -mllvm -amdgpu-mfma-vgpr-form      matrix-core results land in VGPRs, where
+                                     the scaling epilogues read them (the
+                                     default parks them in AGPRs and copies
+                                     every value out: one more VALU op each)
 """
 from __future__ import annotations
 
@@ -36,6 +40,7 @@ FLAGS = [
     "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -13,10 +13,15 @@
 // widened unsigned and their sub-block scale/min terms applied as the GEMV
 // does (y += xs * (d*sc*dot - dmin*m*sum), mpp.rs:304-315).
 //
-// The per-block scaling costs three VALU operations per output per block
-// (convert, scale product, fused add) against one MFMA per 32x32 tile per
-// block: with 32-wide scale blocks on both operands this epilogue, not the
-// matrix core, bounds the kernel.
+// The per-block scaling is the bound: with 32-wide scale blocks on both
+// operands every output takes a scaled term per block.  The scale products
+// ws[r] * xs[t] of a tile are an outer product, computed on the matrix core
+// (v_mfma_f32_32x32x2_f32 with one k-slot zero); Q4_K's minimum terms
+// sum_b dmin*m * xs*sum are a true product over the block index and go into
+// the accumulators by MFMA as well.  Two VALU operations per output per
+// block remain (convert the i32 dot, fused multiply-add); matrix-core
+// results are kept in VGPRs (-mllvm -amdgpu-mfma-vgpr-form), where the
+// epilogue reads them without a copy.
 //
 // Tiles.  A workgroup of 4 waves computes a BN x BM (weight rows x tokens)
 // tile; each wave WR/WT-splits it into RT x TT MFMA tiles of 32 x 32.  A
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
     __shared__ __align__(16) float sW[NBS][BN];   // ws (q8/q4) or d*sc (Q4_K)
     __shared__ __align__(16) float sWm[NBS][BN];  // dmin*m (Q4_K)
     __shared__ float sX[NBS][BM];                 // xs
-    __shared__ float sXs[NBS][BM];                // block sums as floats (Q4_K)
+    __shared__ float sXs[NBS][BM];                // xs * block sum (Q4_K)
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             const int c = tid + u * THREADS;
             if (c < BM * NBS) {
                 sX[c % NBS][c / NBS] = rxs[u];
-                if constexpr (PREC == KH_Q4K) sXs[c % NBS][c / NBS] = rxsum[u];
+                if constexpr (PREC == KH_Q4K) sXs[c % NBS][c / NBS] = rxs[u] * rxsum[u];
             }
         }
     };
@@ -315,6 +320,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             for (int v = 0; v < 16; v++) acc[rt][tt][v] = 0.0f;
 
     const v16i zero = {};
+    const v16f fzero = {};
     load_stage(0);
     for (int k0 = 0; k0 < K; k0 += BK) {
         __syncthreads();  // the previous stage's reads of LDS are done
@@ -334,42 +340,42 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             for (int tt = 0; tt < TT; tt++)
                 bf[tt] = *reinterpret_cast<const v4i *>(sB + (wm0 + tt * 32 + (lane & 31)) * ASTR + b * 32 +
                                                         16 * (lane >> 5));
-            float4 wv[RT][4], wm[RT][4];
+            // the block's scale products p[r][t] = ws[r] * xs[t] (quant.rs:903;
+            // Q4_K: d*sc * xs) as an outer product on the matrix core: k-slot 0
+            // holds the 32 rows' (tokens') scales, k-slot 1 zeros
+            const bool lo = lane < 32;
+            float wa[RT], xb[TT];
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++)
+            for (int rt = 0; rt < RT; rt++) wa[rt] = lo ? sW[b][wr0 + rt * 32 + lane] : 0.0f;
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const int r = wr0 + rt * 32 + 8 * g + 4 * (lane >> 5);
-                    wv[rt][g] = *reinterpret_cast<const float4 *>(&sW[b][r]);
-                    if constexpr (PREC == KH_Q4K) wm[rt][g] = *reinterpret_cast<const float4 *>(&sWm[b][r]);
-                }
-            float xv[TT], xsv[TT];
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++) {
-                xv[tt] = sX[b][wm0 + tt * 32 + (lane & 31)];
-                if constexpr (PREC == KH_Q4K) xsv[tt] = sXs[b][wm0 + tt * 32 + (lane & 31)];
-            }
+            for (int tt = 0; tt < TT; tt++) xb[tt] = lo ? sX[b][wm0 + tt * 32 + lane] : 0.0f;
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++) {
                     const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[rt], bf[tt], zero, 0, 0, 0);
+                    const v16f p = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[rt], xb[tt], fzero, 0, 0, 0);
 #pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const float4 w4 = wv[rt][v >> 2];
-                        const float wsc = (v & 3) == 0 ? w4.x : (v & 3) == 1 ? w4.y : (v & 3) == 2 ? w4.z : w4.w;
-                        if constexpr (PREC == KH_Q4K) {
-                            const float4 m4 = wm[rt][v >> 2];
-                            const float mn = (v & 3) == 0 ? m4.x : (v & 3) == 1 ? m4.y : (v & 3) == 2 ? m4.z : m4.w;
-                            const float t2 = mn * xsv[tt];
-                            const float t = __builtin_fmaf(wsc, (float)d[v], -t2);  // d*sc*dot - dmin*m*sum
-                            acc[rt][tt][v] = __builtin_fmaf(xv[tt], t, acc[rt][tt][v]);
-                        } else {
-                            const float p = wsc * xv[tt];  // ws * xs, quant.rs:903
-                            acc[rt][tt][v] = __builtin_fmaf(p, (float)d[v], acc[rt][tt][v]);
-                        }
-                    }
+                    for (int v = 0; v < 16; v++) acc[rt][tt][v] = __builtin_fmaf(p[v], (float)d[v], acc[rt][tt][v]);
                 }
+            if constexpr (PREC == KH_Q4K) {
+                // the minimum terms, sum_b dmin*m[r,b] * xs[t,b]*sum[t,b], are a
+                // product over blocks: two blocks per 32x32x2 product, straight
+                // into the accumulators (mpp.rs:304-315: w = d*sc*q - dmin*m)
+                if (b & 1) {
+                    const int bb = b - 1 + (lane >> 5);
+                    float ma[RT], sb[TT];
+#pragma unroll
+                    for (int rt = 0; rt < RT; rt++) ma[rt] = -sWm[bb][wr0 + rt * 32 + (lane & 31)];
+#pragma unroll
+                    for (int tt = 0; tt < TT; tt++) sb[tt] = sXs[bb][wm0 + tt * 32 + (lane & 31)];
+#pragma unroll
+                    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                        for (int tt = 0; tt < TT; tt++)
+                            acc[rt][tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(ma[rt], sb[tt], acc[rt][tt], 0, 0, 0);
+                }
+            }
         }
     }
     store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane);
