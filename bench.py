@@ -290,7 +290,7 @@ def measured_traffic():
         return None
 
 
-SECTIONS = ("q8", "prefill", "moe", "decode", "attend")
+SECTIONS = ("q8", "prefill", "moe", "decode", "attend", "qcache")
 
 
 def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
@@ -309,7 +309,50 @@ def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
         out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args)
     if want("attend"):
         out["attend_qwen05b"] = attend(torch, K, ctx, stream, dev, gen, args)
+    if want("qcache"):
+        out["qcache_upload"] = qcache_upload(K, ctx)
     return out
+
+
+def qcache_upload(K, ctx, n_mats=16, rows=14336, cols=4096):
+    """The load path of crates/llm/src/qcache.rs onto the device: a cache file
+    of n_mats q8 matrices (Llama-3-8B gate shape, 0.99 GB) written once, then
+    every matrix uploaded from the mapped file (page cache, as on any load
+    after the first) through pinned staging; beside it the same arrays
+    uploaded from ordinary host memory by kh_weight_q8."""
+    import tempfile
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from nanoq import Writer
+
+    rng = np.random.default_rng(0)
+    qs = rng.integers(-127, 128, rows * cols, dtype=np.int8)
+    sc = rng.random(rows * cols // 32, dtype=np.float32) * 1e-3
+    nbytes = n_mats * (qs.nbytes + sc.nbytes)
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "bench.nanoq"
+        w = Writer(path)
+        for i in range(n_mats):
+            w.q8(f"m{i}", rows, cols, sc, qs)
+        w.finish()
+        del w
+        qc = K.QCache(path)
+        for i in range(2):  # warm: page cache and allocator
+            qc.weight(ctx, f"m{i}")
+        t = time.perf_counter()
+        ws = [qc.weight(ctx, f"m{i}") for i in range(n_mats)]
+        t_qc = time.perf_counter() - t
+        del ws
+        t = time.perf_counter()
+        ws = [K.Weight.from_q8(ctx, rows, cols, sc, qs) for _ in range(n_mats)]
+        t_host = time.perf_counter() - t
+        del ws
+        qc.close()
+    res = {"bytes": nbytes, "qcache_GBps": round(nbytes / t_qc / 1e9, 2),
+           "pageable_host_GBps": round(nbytes / t_host / 1e9, 2), "matrices": n_mats,
+           "shape": f"{rows}x{cols} q8"}
+    log(f"qcache upload: {res}")
+    return res
 
 
 def q8_qwen(torch, K, ctx, stream, dev, gen, args):

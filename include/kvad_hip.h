@@ -231,6 +231,35 @@ int kh_moe_run_dev(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *o
 int kh_moe_route(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
                  int32_t *count);
 
+/* ---- the quantised-weight cache file ("NANOQ"), read into device weights */
+
+/* The container of crates/llm/src/qcache.rs:30-40 (magic, 64-byte aligned
+ * arrays, JSON header at the end, trailing u64 header offset).  The file is
+ * mapped and checked as Container::open does (qcache.rs:863-883), every
+ * tensor entry parsed as parse_entry does (qcache.rs:817-834) with spans
+ * bounds-checked against the file (Container::slice, qcache.rs:906-911).
+ * Entries are the CPU engine's q8/q4 (scales + qs spans) and f32 (data), and
+ * the GPU backend's GGML q4k, q8 and q4 blocks (crates/gpu/src/qcache.rs:278-296);
+ * a kind with no device kernel (q6k) is left out of the table.  Needs no
+ * device: provenance checks on the header (Mapped::open, qcache.rs:620-668)
+ * are the caller's. */
+typedef struct kh_qcache kh_qcache;
+int kh_qcache_open(const char *path, kh_qcache **out);
+int kh_qcache_free(kh_qcache *qc);
+/* The JSON header text (library-owned, valid while the handle lives). */
+const char *kh_qcache_header(const kh_qcache *qc);
+/* The tensor table in header order. */
+int kh_qcache_count(const kh_qcache *qc, size_t *n);
+const char *kh_qcache_name(const kh_qcache *qc, size_t i);
+/* Precision of the device weight the entry becomes (GGML q8/q4 become KH_Q8/KH_Q4). */
+int kh_qcache_info(const kh_qcache *qc, const char *name, int *precision, size_t *rows, size_t *cols);
+/* Mapped::vector (qcache.rs:781-790): a [1, n] f32 entry copied to host `out`. */
+int kh_qcache_vector(const kh_qcache *qc, const char *name, float *out, size_t n);
+/* Mapped::build (qcache.rs:689-713), onto the device: the entry's arrays are
+ * copied from the mapping through pinned staging buffers (GGML Q8_0/Q4_0
+ * blocks repacked to kvad's q8/q4 layout with f32 scales, exactly). */
+int kh_qcache_weight(kh_ctx *ctx, const kh_qcache *qc, const char *name, kh_weight **out);
+
 /* ---- a device-resident decoder (Llama family) ------------------------- */
 
 /* Spec (model/mod.rs:286-330) of a Llama-family decoder: Qwen2/2.5, Llama,

@@ -24,7 +24,7 @@ import numpy as np
 
 __all__ = [
     "F32", "Q8", "Q4", "Q4K", "KvadError", "Declined", "lib", "Context", "Weight", "matvec_many",
-    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "Llm", "LlmSpec", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
+    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "QCache", "Llm", "LlmSpec", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
 ]
 
 F32, Q8, Q4, Q4K = 0, 1, 2, 3
@@ -128,6 +128,14 @@ _SIGS = {
     "kh_moe_run": (C.c_int, [_p, _p, _p, _sz, _p]),
     "kh_moe_run_dev": (C.c_int, [_p, _p, _p, _sz, _p]),
     "kh_moe_route": (C.c_int, [_p, _p, _p, _sz, _p, _p, _p]),
+    "kh_qcache_open": (C.c_int, [C.c_char_p, C.POINTER(_p)]),
+    "kh_qcache_free": (C.c_int, [_p]),
+    "kh_qcache_header": (C.c_char_p, [_p]),
+    "kh_qcache_count": (C.c_int, [_p, C.POINTER(_sz)]),
+    "kh_qcache_name": (C.c_char_p, [_p, _sz]),
+    "kh_qcache_info": (C.c_int, [_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(_sz), C.POINTER(_sz)]),
+    "kh_qcache_vector": (C.c_int, [_p, C.c_char_p, _p, _sz]),
+    "kh_qcache_weight": (C.c_int, [_p, _p, C.c_char_p, C.POINTER(_p)]),
 }
 
 
@@ -342,6 +350,55 @@ def qact(ctx: Context, x):
     su = np.empty(n // 32, np.int32)
     _check(lib.kh_debug_qact(ctx.h, _ptr(x), n, _ptr(qs), _ptr(sc), _ptr(su)))
     return qs, sc, su
+
+
+class QCache:
+    """The quantised-weight cache file (crates/llm/src/qcache.rs): the
+    container mapped and its tensor table parsed (Container::open,
+    parse_entry); `weight` uploads an entry as a device Weight
+    (Mapped::build), `vector` copies an f32 vector to the host
+    (Mapped::vector).  Opening needs no device."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        _check(lib.kh_qcache_open(str(path).encode(), C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            lib.kh_qcache_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def header(self) -> str:
+        return lib.kh_qcache_header(self.h).decode()
+
+    def names(self) -> list[str]:
+        n = C.c_size_t()
+        _check(lib.kh_qcache_count(self.h, C.byref(n)))
+        return [lib.kh_qcache_name(self.h, i).decode() for i in range(n.value)]
+
+    def info(self, name: str) -> tuple[int, int, int]:
+        """(precision, rows, cols) of the device weight the entry becomes."""
+        prec, rows, cols = C.c_int(), C.c_size_t(), C.c_size_t()
+        _check(lib.kh_qcache_info(self.h, name.encode(), C.byref(prec), C.byref(rows), C.byref(cols)))
+        return prec.value, rows.value, cols.value
+
+    def vector(self, name: str) -> np.ndarray:
+        _, rows, cols = self.info(name)
+        out = np.empty(cols, np.float32)
+        _check(lib.kh_qcache_vector(self.h, name.encode(), _ptr(out), cols))
+        return out
+
+    def weight(self, ctx: "Context", name: str) -> "Weight":
+        h = C.c_void_p()
+        _check(lib.kh_qcache_weight(ctx.h, self.h, name.encode(), C.byref(h)))
+        return Weight(ctx, h)
 
 
 @dataclass(frozen=True)
