@@ -290,7 +290,7 @@ def measured_traffic():
         return None
 
 
-SECTIONS = ("q8", "prefill", "moe", "decode", "attend", "qcache")
+SECTIONS = ("q8", "prefill", "moe", "decode", "attend", "mla", "qcache")
 
 
 def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
@@ -309,9 +309,40 @@ def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
         out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args)
     if want("attend"):
         out["attend_qwen05b"] = attend(torch, K, ctx, stream, dev, gen, args)
+    if want("mla"):
+        out["mla_deepseek_v2_lite"] = mla(torch, K, ctx, stream, dev, gen, args)
     if want("qcache"):
         out["qcache_upload"] = qcache_upload(K, ctx)
     return out
+
+
+def mla(torch, K, ctx, stream, dev, gen, args, nl=8):
+    """Absorbed latent attention (model/deepseek.rs:553-591) at DeepSeek-V2-Lite
+    geometry: 16 heads, latent 512, rope 64, over nl layers of distinct caches
+    ~ N(0, 1); bytes = every cached row (576 floats) read once, plus the
+    queries and the output; flops 4 * 16 * (576 + 512) / 2 * L per layer."""
+    H = 16
+    res = {}
+    for L in (1024, 8192, 32768):
+        c = torch.randn(nl, L, 512, device=dev, generator=gen)
+        pe = torch.randn(nl, L, 64, device=dev, generator=gen)
+        ql = torch.randn(H * 512, device=dev, generator=gen)
+        qp = torch.randn(H * 64, device=dev, generator=gen)
+        o = torch.empty(H * 512, device=dev)
+
+        def run():
+            for l in range(nl):
+                K.mla_attend_dev(ctx, H, ql.data_ptr(), qp.data_ptr(), c[l].data_ptr(), pe[l].data_ptr(), L,
+                                 1.0 / 192 ** 0.5, o.data_ptr())
+
+        g = Graph(torch, ctx, stream, run)
+        s = g.time(max(5, args.steps // 5), 2) / nl
+        b = 4 * L * 576 + 4 * H * (512 + 64 + 512)
+        res[str(L)] = {"us_per_layer": round(s * 1e6, 2), "GBps": round(b / s / 1e9, 1),
+                       "TFLOPS": round(2 * H * (576 + 512) * L / s / 1e12, 2)}
+        del g, c, pe
+    log(f"mla: {res}")
+    return res
 
 
 def qcache_upload(K, ctx, n_mats=16, rows=14336, cols=4096):

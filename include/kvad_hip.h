@@ -178,6 +178,20 @@ int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t 
 int kh_attend_dev(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
                   const float *k, const float *v, size_t n_positions, float *out);
 
+/* Latent attention, absorbed (model/deepseek.rs:553-591), one token: head h
+ * scores cached position t as (q_lat_h . c_t + q_pe_h . pe_t) * scale,
+ * softmax over the positions, and returns the attended latent
+ * out[h] = sum_t w_t c_t (512 wide; weights below 1e-8 dropped, mod.rs:807's
+ * rule as deepseek.rs:576-579 applies it).  The uk / uv projections around
+ * it are matvecs.  The cache is the reference's: keys are the rotated pe rows
+ * (64 wide), values the normed latents c (512 wide), KvCache::push(layer,
+ * k_pe, c) at deepseek.rs:540-547.  q_lat [n_head*512], q_pe [n_head*64]. */
+int kh_mla_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, const float *q_lat, const float *q_pe,
+                  size_t n_positions, float scale, float *out);
+/* The same over raw device arrays: c rows 512 wide, pe rows 64 wide. */
+int kh_mla_attend_dev(kh_ctx *ctx, size_t n_head, const float *q_lat, const float *q_pe, const float *c,
+                      const float *pe, size_t n_positions, float scale, float *out);
+
 /* ---- decode glue (device pointers, asynchronous on the context's stream) */
 
 /* tensor::rms_norm (tensor.rs:329-333) over m rows of n:

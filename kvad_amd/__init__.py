@@ -24,7 +24,7 @@ import numpy as np
 
 __all__ = [
     "F32", "Q8", "Q4", "Q4K", "KvadError", "Declined", "lib", "Context", "Weight", "matvec_many",
-    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "QCache", "Llm", "LlmSpec", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
+    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "QCache", "mla_attend", "mla_attend_dev", "Llm", "LlmSpec", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
 ]
 
 F32, Q8, Q4, Q4K = 0, 1, 2, 3
@@ -128,6 +128,8 @@ _SIGS = {
     "kh_moe_run": (C.c_int, [_p, _p, _p, _sz, _p]),
     "kh_moe_run_dev": (C.c_int, [_p, _p, _p, _sz, _p]),
     "kh_moe_route": (C.c_int, [_p, _p, _p, _sz, _p, _p, _p]),
+    "kh_mla_attend": (C.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, C.c_float, _p]),
+    "kh_mla_attend_dev": (C.c_int, [_p, _sz, _p, _p, _p, _p, _sz, C.c_float, _p]),
     "kh_qcache_open": (C.c_int, [C.c_char_p, C.POINTER(_p)]),
     "kh_qcache_free": (C.c_int, [_p]),
     "kh_qcache_header": (C.c_char_p, [_p]),
@@ -491,6 +493,22 @@ def attend(ctx: Context, spec: Spec, q, cache: KvCache, layer: int, n_positions:
     _check(lib.kh_attend(ctx.h, cache.h, layer, spec.n_head, spec.n_kv_head, spec.head_dim, _ptr(q),
                          n_positions, _ptr(out)))
     return out
+
+
+def mla_attend(ctx: Context, cache: "KvCache", layer: int, n_head: int, q_lat, q_pe, n_positions: int,
+               scale: float) -> np.ndarray:
+    """The latent-attention core of DeepSeek's Model::attend (model/deepseek.rs:553-591)
+    over a cache whose keys are the rope rows (64) and values the latents (512)."""
+    ql, qp = _f32(q_lat), _f32(q_pe)
+    assert ql.size == n_head * 512 and qp.size == n_head * 64
+    out = np.empty(n_head * 512, np.float32)
+    _check(lib.kh_mla_attend(ctx.h, cache.h, layer, n_head, _ptr(ql), _ptr(qp), n_positions, scale, _ptr(out)))
+    return out
+
+
+def mla_attend_dev(ctx: Context, n_head: int, q_lat_ptr: int, q_pe_ptr: int, c_ptr: int, pe_ptr: int,
+                   n_positions: int, scale: float, out_ptr: int) -> None:
+    _check(lib.kh_mla_attend_dev(ctx.h, n_head, q_lat_ptr, q_pe_ptr, c_ptr, pe_ptr, n_positions, scale, out_ptr))
 
 
 def attend_dev(ctx: Context, spec: Spec, q_ptr: int, k_ptr: int, v_ptr: int, n_positions: int,

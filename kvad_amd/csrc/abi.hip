@@ -714,6 +714,41 @@ int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t 
     return KH_OK;
 }
 
+// ---- latent attention (DeepSeek) ---------------------------------------------
+
+int kh_mla_attend_dev(kh_ctx *ctx, size_t n_head, const float *q_lat, const float *q_pe, const float *c,
+                      const float *pe, size_t n_positions, float scale, float *out) {
+    if (!ctx || !q_lat || !q_pe || !out || (n_positions && (!c || !pe)))
+        return fail(KH_EINVAL, "kh_mla_attend_dev: null argument");
+    Guard g(ctx);
+    return launch_mla(ctx, (int)n_head, q_lat, q_pe, c, pe, 512, 64, n_positions, scale, out);
+}
+
+int kh_mla_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, const float *q_lat, const float *q_pe,
+                  size_t n_positions, float scale, float *out) {
+    if (!ctx || !kv || !q_lat || !q_pe || !out) return fail(KH_EINVAL, "kh_mla_attend: null argument");
+    if (layer >= kv->n_layer) return fail(KH_EINVAL, "kh_mla_attend: no such layer");
+    if (kv->k_dim != 64 || kv->v_dim != 512)
+        return fail(KH_DECLINED, "kh_mla_attend: the cache must hold rope keys of 64 and latents of 512");
+    if (n_positions > kv->rows[layer]) return fail(KH_EINVAL, "kh_mla_attend: more positions than the cache holds");
+    if (n_head == 0 || n_head > 4096) return fail(KH_EINVAL, "kh_mla_attend: bad head count");
+    Guard g(ctx);
+    const size_t nl = n_head * 512, np = n_head * 64;
+    int rc = ensure(ctx, ctx->io, up(4 * nl) + up(4 * np) + up(4 * nl));
+    if (rc) return rc;
+    char *base = static_cast<char *>(ctx->io.ptr);
+    float *dql = reinterpret_cast<float *>(base), *dqp = reinterpret_cast<float *>(base + up(4 * nl));
+    float *dout = reinterpret_cast<float *>(base + up(4 * nl) + up(4 * np));
+    KH_HIP(hipMemcpyAsync(dql, q_lat, 4 * nl, hipMemcpyHostToDevice, ctx->stream));
+    KH_HIP(hipMemcpyAsync(dqp, q_pe, 4 * np, hipMemcpyHostToDevice, ctx->stream));
+    rc = launch_mla(ctx, (int)n_head, dql, dqp, kv->v[layer], kv->k[layer], kv->v_dim, kv->k_dim, n_positions, scale,
+                    dout);
+    if (rc) return rc;
+    KH_HIP(hipMemcpyAsync(out, dout, 4 * nl, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
 // ---- mixture of experts ------------------------------------------------------
 
 int kh_moe_new(kh_ctx *ctx, size_t n_experts, size_t top_k, size_t hidden, size_t inter, int scoring, int select,

@@ -94,8 +94,9 @@ struct AttnArgs {
     const int32_t *len_dev;
     int plus_one;
     float scale;
-    // per split, [nsplit][n_head]: local max, sum, smallest score; and acc
-    float *pm, *pl, *pmin, *pacc;
+    // per split, [nsplit][n_head]: local max, sum, smallest score; acc
+    // [nsplit][n_head][hd]; scores [nsplit][n_head][P]
+    float *pm, *pl, *pmin, *pacc, *psc;
     float *out;               // [n_head][hd]
 };
 
@@ -329,6 +330,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
             a.pl[o] = Ls;
             a.pmin[o] = fminf(fminf(s_st[2][0][h], s_st[2][1][h]), fminf(s_st[2][2][h], s_st[2][3][h]));
         }
+        // the scores, for the merge's decision on the reference's 1e-8 skip
+        // (stored last: a store ahead of a load would hold up its wait)
+        if (hv) {
+            float *ps = a.psc + ((size_t)split * a.n_head + h0 + j16) * P + pw + 4 * c4;
+#pragma unroll
+            for (int u = 0; u < R; u++)
+                *reinterpret_cast<float4 *>(ps + 16 * u) = make_float4(s[u][0], s[u][1], s[u][2], s[u][3]);
+        }
         return;
     }
 
@@ -385,54 +394,92 @@ __device__ __forceinline__ float block_reduce(float v, float *s_red, F op) {
 
 constexpr int MAX_SPLITS = 4096;
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
-    constexpr int DPL = HD / 16;
-    constexpr int NQ = HD / 4, NSG = 256 / NQ;  // float4 slices of a row; split groups
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
-    const int ns = (L + a.P - 1) / a.P, n_head = a.n_head;
-    if (ns <= 1) return;  // the split kernel finished a single split itself
-    __shared__ float s_red[256];
-    __shared__ float s_c[MAX_SPLITS];           // exp(m_j - M)
-    __shared__ __align__(16) float s_acc[NSG][HD];
-    __shared__ float s_fix[16][HD];
-    __shared__ int s_need;
-
-    // the splits' statistics, all loads in flight together
-    float mx = -INFINITY, lo = INFINITY;
-    for (int i = tid; i < ns; i += 256) {
-        mx = fmaxf(mx, a.pm[(size_t)i * n_head + h]);
-        lo = fminf(lo, a.pmin[(size_t)i * n_head + h]);
+// Exclusive prefix sum of one int per thread over the workgroup (256
+// threads); *total gets the sum.  Fixed order.
+__device__ __forceinline__ int block_excl_scan(int v, int *s, int *total) {
+    const int tid = threadIdx.x;
+    s[tid] = v;
+    __syncthreads();
+    for (int d = 1; d < 256; d <<= 1) {
+        const int x = tid >= d ? s[tid - d] : 0;
+        __syncthreads();
+        s[tid] += x;
+        __syncthreads();
     }
-    const float M = block_reduce(mx, s_red, [](float x, float y) { return fmaxf(x, y); });
-    lo = block_reduce(lo, s_red, [](float x, float y) { return fminf(x, y); });
+    *total = s[255];
+    const int incl = s[tid];
+    __syncthreads();
+    return incl - v;
+}
 
-    // c_j = exp(m_j - M);  S = sum l_j c_j
+// The merge of one head's splits (one workgroup of 256 threads), over the
+// head's dims [d0, d0 + D):
+//   M = max m_j,  S = sum_j l_j e^{m_j - M},  out = sum_j e^{m_j - M} acc_j / S,
+// less the terms the reference skips, w_t = e^{s_t - M} * (1/S) < 1e-8
+// (mod.rs:807).  Decided per split from its extremes: a split whose largest
+// weight is under 1e-8 is left out whole; one whose smallest is not is taken
+// whole; the straddling ones have their stored scores read, a batch of
+// candidates at a time, and the value rows of just the skipped positions are
+// gathered, all loads in flight together, and taken back out.  vrow(t, q) is
+// float4 q of position t's value row for this head.  Every list is compacted
+// in index order and every sum has a fixed order.
+template <int HD, int D, typename VRow>
+__device__ __forceinline__ void merge_head(const float *pm, const float *pl, const float *pmin, const float *pacc,
+                                           const float *psc, int ns, int n_head, int h, int d0, int P, int L,
+                                           VRow vrow, float *out) {
+    constexpr int NQ = D / 4, NSG = 256 / NQ;  // float4 slices of the dims; split (or position) groups
+    constexpr int CAP = 1024;                  // skipped positions gathered per flush
+    const int tid = threadIdx.x;
+    __shared__ float s_red[256];
+    __shared__ int s_scan[256];
+    __shared__ float s_c[MAX_SPLITS];           // e^{m_j - M}, or 0 for a split left out
+    __shared__ int s_list[MAX_SPLITS];          // straddling splits, in index order
+    __shared__ __align__(16) float s_acc[NSG][D];
+    __shared__ __align__(16) float s_fix[NSG][D];
+    __shared__ int s_kpos[CAP];
+    __shared__ float s_kw[CAP];
+
+    float mx = -INFINITY;
+    for (int i = tid; i < ns; i += 256) mx = fmaxf(mx, pm[(size_t)i * n_head + h]);
+    const float M = block_reduce(mx, s_red, [](float x, float y) { return fmaxf(x, y); });
     float s = 0.0f;
     for (int i = tid; i < ns; i += 256) {
         const size_t o = (size_t)i * n_head + h;
-        const float c = expf(a.pm[o] - M);
-        s_c[i] = c;
-        s = fmaf(a.pl[o], c, s);
+        s = fmaf(pl[o], expf(pm[o] - M), s);
     }
-    const float S = block_reduce(s, s_red, [](float x, float y) { return x + y; });  // syncs s_c too
+    const float S = block_reduce(s, s_red, [](float x, float y) { return x + y; });
     const float inv = 1.0f / S;  // inv = 1 / sum, tensor.rs:304
+
+    // each thread a run of splits: their weights and straddle flags
+    const int per = (ns + 255) / 256, i0 = tid * per, i1 = min(ns, i0 + per);
+    unsigned mask = 0;  // per <= MAX_SPLITS / 256 = 16
+    for (int i = i0; i < i1; i++) {
+        const size_t o = (size_t)i * n_head + h;
+        const float c = expf(pm[o] - M);
+        const bool out_whole = c * inv < 1e-8f;  // every weight of the split is skipped
+        s_c[i] = out_whole ? 0.0f : c;
+        if (!out_whole && expf(pmin[o] - M) * inv < 1e-8f) mask |= 1u << (i - i0);
+    }
+    int nstr;
+    int at = block_excl_scan(__builtin_popcount(mask), s_scan, &nstr);
+    for (int i = i0; i < i1; i++)
+        if (mask >> (i - i0) & 1u) s_list[at++] = i;
+    __syncthreads();
 
     // acc[d] = sum_j c_j acc_j[d]: thread (split group sg, float4 slice dq)
     // walks splits sg, sg + NSG, ... eight loads at a time
+    const int sg = tid / NQ, dq = tid % NQ;
     {
-        const int sg = tid / NQ, dq = tid % NQ;
-        const rsrc_t PA = rsrc(a.pacc, (size_t)ns * n_head * HD * 4);
+        const rsrc_t PA = rsrc(pacc, (size_t)ns * n_head * HD * 4);
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int i0 = sg; i0 < ns; i0 += 8 * NSG) {
+        for (int j0 = sg; j0 < ns; j0 += 8 * NSG) {
             float4 v[8];
             float c[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const int i = i0 + u * NSG;
+                const int i = j0 + u * NSG;
                 v[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      PA, (unsigned)((((size_t)i * n_head + h) * HD + 4 * dq) * 4), 0, 0));
+                                                      PA, (unsigned)((((size_t)i * n_head + h) * HD + d0 + 4 * dq) * 4), 0, 0));
                 c[u] = i < ns ? s_c[i] : 0.0f;
             }
 #pragma unroll
@@ -445,61 +492,87 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
         }
         *reinterpret_cast<float4 *>(&s_acc[sg][4 * dq]) = x;
     }
-    __syncthreads();
 
-    // ---- skip correction: w = exp(s - M) * (1/S) < 1e-8 ---------------------
-    // possible only where a score is below M + ln S + ln 1e-8 (with a margin)
-    const float thr = M + logf(S) - 18.420681f + 1.0f;
-    if (lo < thr) {
-        const int group16 = tid >> 4, sub = tid & 15, kvh = h / a.group;
-        const rsrc_t K = rsrc(a.k, (size_t)L * a.kstride * 4), V = rsrc(a.v, (size_t)L * a.vstride * 4);
-        float qr[1][DPL];
-#pragma unroll
-        for (int d = 0; d < DPL; d++) qr[0][d] = a.q[(size_t)h * HD + sub * DPL + d];
-        float fix[DPL];
-#pragma unroll
-        for (int d = 0; d < DPL; d++) fix[d] = 0.0f;
-        for (int j = 0; j < ns; j++) {
-            if (tid == 0) s_need = a.pmin[(size_t)j * n_head + h] < thr;
-            __syncthreads();
-            const int need = s_need;
-            __syncthreads();
-            if (!need) continue;
-            const int tj = j * a.P, nj = min(L - tj, a.P);
-            for (int base = 0; base < nj; base += 16) {
-                const int t = tj + base + group16;
-                if (base + group16 >= nj) continue;  // whole 16-lane rows drop out together
-                float kv[DPL], vv[DPL];
-                load_row<DPL>(K, (unsigned)(((size_t)t * a.kstride + (size_t)kvh * HD + sub * DPL) * 4), kv);
-                load_row<DPL>(V, (unsigned)(((size_t)t * a.vstride + (size_t)kvh * HD + sub * DPL) * 4), vv);
-                float sc[1];
-                score_row<1, DPL>(qr, kv, a.scale, 1, sc);
-                float w = expf(sc[0] - M);
+    // the skipped terms of the straddling splits
+    float4 fix = make_float4(0.f, 0.f, 0.f, 0.f);
+    int nk = 0;  // listed skipped positions (the same in every thread)
+    const int B = 256 / P;  // straddling splits per batch of candidates
+    for (int q0 = 0; q0 < nstr; q0 += B) {
+        const int q = q0 + tid / P, k = tid % P;
+        float w = 0.0f;
+        int t = 0;
+        if (q < nstr) {
+            const int j = s_list[q];
+            t = j * P + k;
+            const float sc = psc[((size_t)j * n_head + h) * P + k];
+            if (t < L && sc != -INFINITY) {
+                w = expf(sc - M);
                 w = w * inv;
-                if (w < 1e-8f) {
-#pragma unroll
-                    for (int d = 0; d < DPL; d++) fix[d] = fmaf(w, vv[d], fix[d]);
-                }
+                if (!(w < 1e-8f)) w = 0.0f;  // kept (a weight that underflows to 0 adds nothing either)
             }
         }
-#pragma unroll
-        for (int d = 0; d < DPL; d++) s_fix[group16][sub * DPL + d] = fix[d];
-        __syncthreads();
-        if (tid < HD) {
-            float f = 0.0f;
-            for (int g = 0; g < 16; g++) f += s_fix[g][tid];
-            s_fix[0][tid] = f;
+        int added;
+        const int o = block_excl_scan(w > 0.0f, s_scan, &added);
+        if (w > 0.0f) {
+            s_kpos[nk + o] = t;
+            s_kw[nk + o] = w;
         }
+        nk += added;
         __syncthreads();
-    }
-    if (tid < HD) {
-        float x = s_acc[0][tid];
+        if (nk > CAP - 256 || q0 + B >= nstr) {
+            // gather: thread (group sg, slice dq) takes listed positions sg, sg + NSG, ...
+            for (int k0 = sg; k0 < nk; k0 += 4 * NSG) {
+                float4 v[4];
+                float ww[4];
 #pragma unroll
-        for (int g = 1; g < NSG; g++) x += s_acc[g][tid];
-        x = x * inv;
-        if (lo < thr) x -= s_fix[0][tid];
-        a.out[(size_t)h * HD + tid] = x;
+                for (int u = 0; u < 4; u++) {
+                    const int kk = k0 + u * NSG;
+                    const bool ok = kk < nk;
+                    v[u] = vrow(s_kpos[ok ? kk : 0], d0 / 4 + dq);
+                    ww[u] = ok ? s_kw[kk] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    fix.x = fmaf(ww[u], v[u].x, fix.x);
+                    fix.y = fmaf(ww[u], v[u].y, fix.y);
+                    fix.z = fmaf(ww[u], v[u].z, fix.z);
+                    fix.w = fmaf(ww[u], v[u].w, fix.w);
+                }
+            }
+            nk = 0;
+            __syncthreads();
+        }
     }
+    *reinterpret_cast<float4 *>(&s_fix[sg][4 * dq]) = fix;
+    __syncthreads();
+    if (tid < NQ) {
+        float4 x = *reinterpret_cast<const float4 *>(&s_acc[0][4 * tid]);
+        float4 f = *reinterpret_cast<const float4 *>(&s_fix[0][4 * tid]);
+#pragma unroll
+        for (int g = 1; g < NSG; g++) {
+            const float4 y = *reinterpret_cast<const float4 *>(&s_acc[g][4 * tid]);
+            const float4 z = *reinterpret_cast<const float4 *>(&s_fix[g][4 * tid]);
+            x = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+            f = make_float4(f.x + z.x, f.y + z.y, f.z + z.z, f.w + z.w);
+        }
+        x = make_float4(x.x * inv - f.x, x.y * inv - f.y, x.z * inv - f.z, x.w * inv - f.w);
+        *reinterpret_cast<float4 *>(out + (size_t)h * HD + d0 + 4 * tid) = x;
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+    const int h = blockIdx.x;
+    const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
+    const int ns = (L + a.P - 1) / a.P;
+    if (ns <= 1) return;  // the split kernel finished a single split itself
+    const rsrc_t V = rsrc(a.v, (size_t)L * a.vstride * 4);
+    const size_t voff = (size_t)(h / a.group) * HD;
+    auto vrow = [&](int t, int d4) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              V, (unsigned)(((size_t)t * a.vstride + voff + 4 * d4) * 4), 0, 0));
+    };
+    merge_head<HD, HD>(a.pm, a.pl, a.pmin, a.pacc, a.psc, ns, a.n_head, h, 0, a.P, L, vrow, a.out);
 }
 
 // P = 64 R positions per workgroup: R in {1, 2, 4} for hd 64, {1, 2} for hd 128.
@@ -560,14 +633,20 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     return KH_OK;
 }
 
+// Partials of nsplit splits: pm, pl, pmin [ns], acc [ns][hd], scores [ns][P].
+size_t partial_floats(size_t nsplit, int n_head, int head_dim, int P) {
+    const size_t ns = nsplit * (size_t)n_head;
+    return 3 * ns + ns * (size_t)head_dim + ns * (size_t)P;
+}
+
 void carve(AttnArgs &a, void *ws, int head_dim) {
     const size_t ns = (size_t)a.nsplit * a.n_head;
     float *p = static_cast<float *>(ws);
     a.pm = p, p += ns;
     a.pl = p, p += ns;
     a.pmin = p, p += ns;
-    a.pacc = p;
-    (void)head_dim;
+    a.pacc = p, p += ns * head_dim;
+    a.psc = p;
 }
 
 int run(kh_ctx *ctx, const AttnArgs &a, int head_dim) {
@@ -589,8 +668,9 @@ int run(kh_ctx *ctx, const AttnArgs &a, int head_dim) {
 
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions) {
     (void)n_kv_head;
-    const size_t ns = (max_positions + 15) / 16 * (size_t)n_head;  // the smallest split size bounds the count
-    return 4 * (3 * ns + ns * head_dim) + 1024;
+    // the smallest split size (64) bounds the count; scores take P per split
+    const size_t nsplit = (max_positions + 63) / 64;
+    return 4 * partial_floats(nsplit, n_head, head_dim, 64) + 4 * (max_positions + 256) * (size_t)n_head + 1024;
 }
 
 int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
@@ -604,8 +684,7 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, k, v, kstride, vstride, n_positions, out);
     if (rc) return rc;
     if (a.nsplit > 1) {
-        const size_t ns = (size_t)a.nsplit * n_head;
-        if ((rc = ensure(ctx, ctx->ws, 4 * (3 * ns + ns * head_dim) + 1024))) return rc;
+        if ((rc = ensure(ctx, ctx->ws, 4 * partial_floats(a.nsplit, n_head, head_dim, a.P) + 1024))) return rc;
         carve(a, ctx->ws.ptr, head_dim);
     }
     return run(ctx, a, head_dim);
@@ -622,6 +701,236 @@ int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, c
     a.plus_one = plus_one;
     carve(a, ws, head_dim);
     return run(ctx, a, head_dim);
+}
+
+
+// ---------------------------------------------------------------------------
+// Latent attention, absorbed (model/deepseek.rs:553-591): every query head
+// scores the same cached row [c_t (512) | pe_t (64)] with [q_lat_h | q_pe_h]
+// and averages the compressed rows c_t -- GQA with one shared "KV head" of
+// key width 576 and value width 512, so a workgroup takes up to 16 heads, the
+// 16 columns of the score product, with no padding at DeepSeek's 16.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int MLA_LAT = 512, MLA_ROPE = 64, MLA_K = MLA_LAT + MLA_ROPE;
+constexpr int MLA_QSTR = MLA_K + 4;  // LDS row stride (floats) of the staged queries
+constexpr int MLA_P = 64;            // positions per workgroup: one tile of 16 per wave
+constexpr int MLA_MERGE_D = 128;     // dims per merge workgroup (four per head)
+
+struct MlaArgs {
+    const float *q_lat, *q_pe;  // [n_head][512], [n_head][64]
+    const float *c, *pe;        // cached rows: c [L][cstride], pe [L][pestride]
+    size_t cstride, pestride;
+    int n_head, L, nsplit;
+    float scale;
+    float *pm, *pl, *pmin, *pacc, *psc;  // per split: [nsplit][n_head]; acc [..][512]; scores [..][64]
+    float *out;                    // [n_head][512]
+};
+
+// Split kernel.  Wave w scores positions t0 + 16w .. +15 for the 16 heads:
+// S = K' Q'^T on v_mfma_f32_16x16x4_f32, the 576 key dims dealt to the four
+// k-slots in chunks of 16 (chunk 4k + c of k-step k to slot c: chunks 0-31
+// are c, 32-35 are pe, so each k-step reads one array).  Lane (c, i) holds
+// 144 dims of its row, all loads in flight at once; the queries sit in LDS.
+// The workgroup takes one maximum per head, so every wave's exponentials
+// share it; the probabilities go to LDS and wave w then forms
+// O[heads][dims 128w .. 128w + 127] = P V over all 64 positions.
+__global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
+    const int split = blockIdx.x, h0 = blockIdx.y * 16;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j16 = lane & 15, c4 = lane >> 4;
+    const int L = a.L;
+    const int t0 = split * MLA_P, n = min(L - t0, MLA_P);
+    const bool whole = a.nsplit == 1;
+    const int H = min(a.n_head - h0, 16);
+    __shared__ __align__(16) float sQ[16 * MLA_QSTR];
+    __shared__ float sP[16][MLA_P + 4];
+    __shared__ float s_st[3][4][16];
+    const rsrc_t C = rsrc(a.c, (size_t)L * a.cstride * 4), PE = rsrc(a.pe, (size_t)L * a.pestride * 4);
+
+    // the tile's key rows (the long-latency loads) first
+    f4v kq[9][4];
+    {
+        const size_t pos = (size_t)(t0 + 16 * wave + j16);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const unsigned off = (unsigned)((pos * a.cstride + 16 * (4 * k + c4)) * 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                kq[k][i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 16 * i, 0));
+        }
+        const unsigned off = (unsigned)((pos * a.pestride + 16 * c4) * 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            kq[8][i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(PE, off, 16 * i, 0));
+    }
+    // the queries [q_lat | q_pe] of the group's heads, zero rows past H
+    for (int i = tid; i < 16 * (MLA_K / 4); i += 256) {
+        const int h = i / (MLA_K / 4), d4 = i % (MLA_K / 4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (h < H)
+            v = d4 < MLA_LAT / 4
+                    ? *reinterpret_cast<const float4 *>(a.q_lat + (size_t)(h0 + h) * MLA_LAT + 4 * d4)
+                    : *reinterpret_cast<const float4 *>(a.q_pe + (size_t)(h0 + h) * MLA_ROPE + 4 * (d4 - MLA_LAT / 4));
+        *reinterpret_cast<float4 *>(&sQ[h * MLA_QSTR + 4 * d4]) = v;
+    }
+    __syncthreads();
+
+    // scores: lane (c4, j16) ends with positions 4 c4 .. 4 c4 + 3 of the tile, head j16
+    f4v d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 9; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f4v q4 = *reinterpret_cast<const f4v *>(&sQ[j16 * MLA_QSTR + 16 * (4 * k + c4) + 4 * i]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(kq[k][i][e], q4[e], d, 0, 0, 0);
+        }
+    float s[4], mx = -INFINITY, mn = INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const bool ok = j16 < H && 16 * wave + 4 * c4 + r < n;
+        const float sc = d[r] * a.scale;  // (dot(q_lat, c) + dot(q_pe, pe)) * scale, deepseek.rs:567-570
+        s[r] = ok ? sc : -INFINITY;
+        mx = fmaxf(mx, s[r]);
+        mn = ok ? fminf(mn, sc) : mn;
+    }
+    mx = rows_max(mx);
+    mn = rows_min(mn);
+    if (c4 == 0) {
+        s_st[0][wave][j16] = mx;
+        s_st[2][wave][j16] = mn;
+    }
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_st[0][0][j16], s_st[0][1][j16]), fmaxf(s_st[0][2][j16], s_st[0][3][j16]));
+    float e[4], l = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        e[r] = s[r] == -INFINITY ? 0.0f : expf(s[r] - M);
+        l += e[r];
+    }
+    l = rows_sum(l);
+    if (c4 == 0) s_st[1][wave][j16] = l;
+    __syncthreads();
+    const float S = ((s_st[1][0][j16] + s_st[1][1][j16]) + s_st[1][2][j16]) + s_st[1][3][j16];
+    if (whole) {
+        // the reference's own weights: w = exp(s - M) * (1/S), dropping w < 1e-8
+        // (softmax_inplace, tensor.rs:297-308; deepseek.rs:576-579)
+        const float inv = 1.0f / S;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float w = e[r] * inv;
+            e[r] = w < 1e-8f ? 0.0f : w;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) sP[j16][16 * wave + 4 * c4 + r] = e[r];
+    __syncthreads();
+
+    // values: wave w forms dims 128 w .. 128 w + 127 for every position of the split
+    const int D0 = 128 * wave;
+    f4v vv[4][4][2];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const size_t p = (size_t)(t0 + 16 * u + 4 * c4 + r);
+            const unsigned off = (unsigned)((p * a.cstride + D0 + 4 * j16) * 4);
+            vv[u][r][0] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 0, 0));
+            vv[u][r][1] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 256, 0));
+        }
+    f4v acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) acc[q] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float pa = sP[j16][16 * u + 4 * c4 + r];  // head j16, position 4 c4 + r of tile u
+#pragma unroll
+            for (int v = 0; v < 2; v++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    acc[4 * v + q] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vv[u][r][v][q], acc[4 * v + q], 0, 0, 0);
+        }
+    // acc[4 v + q][i]: head 4 c4 + i, dim D0 + 64 v + 4 j16 + q
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int h = 4 * c4 + i;
+        if (h >= H) continue;
+        float *dst = whole ? a.out + (size_t)(h0 + h) * MLA_LAT
+                           : a.pacc + ((size_t)split * a.n_head + h0 + h) * MLA_LAT;
+#pragma unroll
+        for (int v = 0; v < 2; v++)
+            *reinterpret_cast<float4 *>(dst + D0 + 64 * v + 4 * j16) =
+                make_float4(acc[4 * v][i], acc[4 * v + 1][i], acc[4 * v + 2][i], acc[4 * v + 3][i]);
+    }
+    if (!whole && tid < H) {
+        const int h = tid;
+        const size_t o = (size_t)split * a.n_head + h0 + h;
+        a.pm[o] = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
+        a.pl[o] = ((s_st[1][0][h] + s_st[1][1][h]) + s_st[1][2][h]) + s_st[1][3][h];
+        a.pmin[o] = fminf(fminf(s_st[2][0][h], s_st[2][1][h]), fminf(s_st[2][2][h], s_st[2][3][h]));
+    }
+    if (!whole && j16 < H)  // the scores, for the merge's decision on the 1e-8 skip (stored last)
+        *reinterpret_cast<float4 *>(a.psc + ((size_t)split * a.n_head + h0 + j16) * MLA_P + 16 * wave + 4 * c4) =
+            make_float4(s[0], s[1], s[2], s[3]);
+}
+
+// Merge, one workgroup per head and 128 dims (merge_head): the value row of position t is c_t.
+__global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
+    const int h = blockIdx.x;
+    const rsrc_t C = rsrc(a.c, (size_t)a.L * a.cstride * 4);
+    auto vrow = [&](int t, int d4) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              C, (unsigned)(((size_t)t * a.cstride + 4 * d4) * 4), 0, 0));
+    };
+    merge_head<MLA_LAT, MLA_MERGE_D>(a.pm, a.pl, a.pmin, a.pacc, a.psc, a.nsplit, a.n_head, h,
+                                     MLA_MERGE_D * blockIdx.y, MLA_P, a.L, vrow, a.out);
+}
+
+}  // namespace
+
+size_t mla_ws_bytes(int n_head, size_t max_positions) {
+    return 4 * partial_floats((max_positions + MLA_P - 1) / MLA_P, n_head, MLA_LAT, MLA_P) + 1024;
+}
+
+int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, const float *c, const float *pe,
+               size_t cstride, size_t pestride, size_t n_positions, float scale, float *out) {
+    if (n_head <= 0) return fail(KH_EINVAL, "mla_attend: n_head must be positive");
+    if (n_positions == 0) return launch_fill(ctx, out, (size_t)n_head * MLA_LAT, 0.0f);
+    if (cstride < MLA_LAT || pestride < MLA_ROPE || cstride % 4 || pestride % 4)
+        return fail(KH_EINVAL, "mla_attend: row strides must hold a row and be multiples of 4 floats");
+    if ((n_positions + MLA_P) * cstride * 4 >= 0xffffffffull || (n_positions + MLA_P) * pestride * 4 >= 0xffffffffull)
+        return fail(KH_DECLINED, "mla_attend: caches of 4 GiB or more per layer are not addressed here");
+    MlaArgs a{};
+    a.q_lat = q_lat, a.q_pe = q_pe, a.c = c, a.pe = pe, a.cstride = cstride, a.pestride = pestride;
+    a.n_head = n_head;
+    a.L = (int)n_positions;
+    a.nsplit = (int)((n_positions + MLA_P - 1) / MLA_P);
+    if (a.nsplit > MAX_SPLITS) return fail(KH_DECLINED, "mla_attend: sequence longer than the split merge takes");
+    a.scale = scale;
+    a.out = out;
+    if (a.nsplit > 1) {
+        const size_t ns = (size_t)a.nsplit * n_head;
+        int rc = ensure(ctx, ctx->ws, 4 * partial_floats(a.nsplit, n_head, MLA_LAT, MLA_P) + 1024);
+        if (rc) return rc;
+        float *p = static_cast<float *>(ctx->ws.ptr);
+        a.pm = p, p += ns;
+        a.pl = p, p += ns;
+        a.pmin = p, p += ns;
+        a.pacc = p, p += ns * MLA_LAT;
+        a.psc = p;
+    }
+    hipLaunchKernelGGL(mla_split_kernel, dim3(a.nsplit, (n_head + 15) / 16), dim3(256), 0, ctx->stream, a);
+    KH_HIP(hipGetLastError());
+    if (a.nsplit > 1) {
+        hipLaunchKernelGGL(mla_merge_kernel, dim3(n_head, MLA_LAT / MLA_MERGE_D), dim3(256), 0, ctx->stream, a);
+        KH_HIP(hipGetLastError());
+    }
+    return KH_OK;
 }
 
 }  // namespace kh

@@ -259,4 +259,10 @@ int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, c
                          size_t max_positions, float *out, void *ws);
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions);
 
+// Absorbed latent attention (model/deepseek.rs:553-591): out[n_head][512] =
+// softmax over positions of (q_lat . c_t + q_pe . pe_t) * scale, times c_t.
+int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, const float *c, const float *pe,
+               size_t cstride, size_t pestride, size_t n_positions, float scale, float *out);
+size_t mla_ws_bytes(int n_head, size_t max_positions);
+
 }  // namespace kh

@@ -73,6 +73,7 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         "kvo_rope_apply": (None, [_p, _p, _sz, _p, _sz]),
         "kvo_rope_apply_interleaved": (None, [_p, _p, _sz, _p, _sz]),
         "kvo_attend": (None, [_sz, _sz, _sz, _p, _p, _p, _sz, _p]),
+        "kvo_mla_attend": (None, [_sz, _sz, _sz, _p, _p, _p, _p, _sz, C.c_float, _p]),
         "kvo_route": (C.c_int, [_p, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, _f, _p, _p, _p]),
         "kvo_moe_run_q8": (None, [_p, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, _f, _p]
                            + [_p] * 8 + [_sz] + [_p] * 7),
@@ -333,6 +334,14 @@ def attend(n_head, n_kv_head, head_dim, q, k_cache, v_cache, n_positions, L=None
     out = np.empty(n_head * head_dim, np.float32)
     L.kvo_attend(n_head, n_kv_head, head_dim, P(_c(q, np.float32)), P(_c(k_cache, np.float32)),
                  P(_c(v_cache, np.float32)), n_positions, P(out))
+    return out
+
+
+def mla_attend(n_head, lat, rope, q_lat, q_pe, c_cache, pe_cache, n_positions, scale, L=None) -> np.ndarray:
+    L = L or lib
+    out = np.empty(n_head * lat, np.float32)
+    L.kvo_mla_attend(n_head, lat, rope, P(_c(q_lat, np.float32)), P(_c(q_pe, np.float32)),
+                     P(_c(c_cache, np.float32)), P(_c(pe_cache, np.float32)), n_positions, scale, P(out))
     return out
 
 

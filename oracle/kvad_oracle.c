@@ -865,6 +865,41 @@ void kvo_attend(size_t n_head, size_t n_kv_head, size_t hd, const float *q, cons
     }
 }
 
+/* Latent attention, absorbed (model/deepseek.rs:553-591): head h scores
+ * position t as (dot(q_lat_h, c_t) + dot(q_pe_h, pe_t)) * scale, softmax
+ * over the positions, then averages the compressed rows c_t, skipping
+ * weights below 1e-8.  The uk / uv projections around it are matvecs. */
+void kvo_mla_attend(size_t n_head, size_t lat, size_t rope, const float *q_lat, const float *q_pe,
+                    const float *c_cache, const float *pe_cache, size_t n_positions, float scale, float *out) {
+    memset(out, 0, sizeof(float) * n_head * lat);
+#pragma omp parallel num_threads(kvo_get_threads())
+    {
+        float *scores = (float *)malloc(sizeof(float) * (n_positions ? n_positions : 1));
+#pragma omp for schedule(static)
+        for (size_t h = 0; h < n_head; h++) {
+            const float *ql = q_lat + h * lat, *qp = q_pe + h * rope;
+            for (size_t t = 0; t < n_positions; t++) {
+                float a = kvo_dot(ql, c_cache + t * lat, lat);
+                float b = kvo_dot(qp, pe_cache + t * rope, rope);
+                float d = a + b;
+                scores[t] = d * scale;
+            }
+            kvo_softmax(scores, n_positions);
+            float *acc = out + h * lat;
+            for (size_t t = 0; t < n_positions; t++) {
+                float w = scores[t];
+                if (w < 1e-8f) continue;
+                const float *c = c_cache + t * lat;
+                for (size_t j = 0; j < lat; j++) {
+                    float p = w * c[j];
+                    acc[j] = acc[j] + p;
+                }
+            }
+        }
+        free(scores);
+    }
+}
+
 /* ------------------------------------------------------------------------- */
 /* router                                                                     */
 /* ------------------------------------------------------------------------- */

@@ -104,6 +104,12 @@ void kvo_rope_apply_interleaved(const float *cos_t, const float *sin_t, size_t h
 void kvo_attend(size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
                 const float *k_cache, const float *v_cache, size_t n_positions, float *out);
 
+/* ---- latent attention, absorbed: model/deepseek.rs:553-591 ---- */
+/* c_cache rows are lat wide, pe_cache rows rope wide; out is n_head*lat (the
+ * attended latent of each head, before uv). */
+void kvo_mla_attend(size_t n_head, size_t lat, size_t rope, const float *q_lat, const float *q_pe,
+                    const float *c_cache, const float *pe_cache, size_t n_positions, float scale, float *out);
+
 /* ---- MoE router: Router::route (model/ffn.rs:256-309) ---- */
 /* scoring 0 = softmax, 1 = sigmoid; select 0 greedy, 1 group-limited, 2 noaux_tc.
  * Writes up to top_k (expert, weight) pairs in pick order; returns how many. */

@@ -137,3 +137,24 @@ def test_attend_rejects_more_positions_than_cached(ctx):
         K.attend(ctx, QWEN, O.normal(1, 14 * 64), cache, 0, 11)
     with pytest.raises(K.KvadError):
         K.attend(ctx, K.Spec(14, 3, 64), O.normal(1, 14 * 64), cache, 0, 5)
+
+
+@pytest.mark.parametrize("L", [3000, 20000])
+def test_attend_skip_across_many_splits(ctx, L):
+    # A few dominant positions; the rest spread across the 1e-8 line, so some
+    # splits are left out whole, some kept whole and most straddle it.  Values
+    # are large, so a skipped term wrongly kept (or a kept one dropped) shows.
+    say("attend skip, many splits", L)
+    spec = K.Spec(4, 1, 64)
+    rng = np.random.default_rng(L)
+    q = np.zeros((4, 64), np.float32)
+    q[:, 0] = 8.0  # score_t = q . k_t / 8 = k_t[0]
+    k = np.zeros((L, 64), np.float32)
+    k[:, 0] = rng.uniform(-4.0, 10.0, L)
+    k[rng.choice(L, 3, replace=False), 0] = 24.0
+    v = (rng.standard_normal((L, 64)) * 100.0).astype(np.float32)
+    cache = K.KvCache(ctx, 1, 64, 64)
+    cache.push(0, k.ravel(), v.ravel())
+    got = K.attend(ctx, spec, q.ravel(), cache, 0, L)
+    want = O.attend(4, 1, 64, q.ravel(), k.ravel(), v.ravel(), L)
+    close(got, want)

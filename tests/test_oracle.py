@@ -655,3 +655,42 @@ def test_interleaved_rope_is_the_half_split_rope_a_permutation_apart():
         inter = O.rope_apply_interleaved(c, s, hd // 2, x, pos)
         split = O.rope_apply(c, s, hd // 2, x[perm], pos)
         np.testing.assert_array_equal(inter[perm], split)
+
+
+# ---- latent attention (model/deepseek.rs:553-591) --------------------------
+
+def _mla_f64(ql, qp, c, pe, scale):
+    """Textbook softmax attention in float64 with the reference's skip of weights below 1e-8."""
+    s = (ql.astype(np.float64) @ c.T.astype(np.float64) + qp.astype(np.float64) @ pe.T.astype(np.float64)) * scale
+    w = np.exp(s - s.max(1, keepdims=True))
+    w /= w.sum(1, keepdims=True)
+    w[w < 1e-8] = 0.0
+    return w @ c.astype(np.float64)
+
+
+@pytest.mark.parametrize("H, L", [(16, 1), (16, 9), (5, 300)])
+def test_mla_oracle_is_softmax_attention_over_the_latent(H, L):
+    rng = np.random.default_rng(H * 1000 + L)
+    ql, qp = rng.standard_normal((H, 512)).astype(np.float32), rng.standard_normal((H, 64)).astype(np.float32)
+    c, pe = rng.standard_normal((L, 512)).astype(np.float32), rng.standard_normal((L, 64)).astype(np.float32)
+    scale = 1.0 / np.sqrt(192.0)
+    got = O.mla_attend(H, 512, 64, ql, qp, c, pe, L, scale).reshape(H, 512)
+    want = _mla_f64(ql, qp, c, pe, scale)
+    assert np.max(np.abs(got - want)) <= 2e-6 * np.max(np.abs(want))
+    if L == 1:  # one position: every head's weight is 1, the latent comes back as it is
+        assert np.array_equal(got, np.broadcast_to(c[0], (H, 512)))
+
+
+def test_mla_oracle_drops_weights_below_1e_8():
+    rng = np.random.default_rng(5)
+    H, L = 2, 40
+    ql, qp = rng.standard_normal((H, 512)).astype(np.float32), np.zeros((H, 64), np.float32)
+    c, pe = rng.standard_normal((L, 512)).astype(np.float32), np.zeros((L, 64), np.float32)
+    c[7] = -ql[0] * 3.0  # head 0 scores position 7 far below the rest
+    scale = 1.0 / np.sqrt(192.0)
+    got = O.mla_attend(H, 512, 64, ql, qp, c, pe, L, scale).reshape(H, 512)
+    want = _mla_f64(ql, qp, c, pe, scale)
+    assert np.max(np.abs(got - want)) <= 2e-6 * np.max(np.abs(want))
+    s = (ql[0].astype(np.float64) @ c.T.astype(np.float64)) * scale
+    w = np.exp(s - s.max()) / np.exp(s - s.max()).sum()
+    assert w[7] < 1e-8 < w.max()  # the skip does apply here
