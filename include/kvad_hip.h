@@ -316,6 +316,30 @@ int kh_llm_generate_launch(kh_ctx *ctx, kh_llm *m, size_t n);
 int kh_llm_len(const kh_llm *m, size_t *len);
 int kh_llm_truncate(kh_llm *m, size_t len);
 
+/* A conversation set aside (the Session trait's Parked, model/mod.rs:837). */
+typedef struct kh_llm_parked kh_llm_parked;
+/* Session::park (model/mod.rs:883-893, CpuSession :1204-1207): takes the
+ * session's cache out, leaving an empty one in its place; pointers move,
+ * nothing is copied. */
+int kh_llm_park(kh_llm *m, kh_llm_parked **out);
+/* Session::resume (model/mod.rs:895-897, :1209-1212): puts a parked cache back
+ * in place of the one held, which is dropped.  Consumes `p` (even on error,
+ * except KH_EINVAL for a null argument); a cache another session parked is
+ * refused ("that cache was not this backend's"). */
+int kh_llm_resume(kh_llm *m, kh_llm_parked *p);
+/* Drops a parked cache (the Box<dyn Any> going out of scope). */
+int kh_llm_parked_free(kh_llm_parked *p);
+int kh_llm_parked_len(const kh_llm_parked *p, size_t *len);
+/* Session::forward_each (model/mod.rs:899-930, CpuSession :1190-1202;
+ * Transformer::forward_each, llama.rs:418-434): tokens[i] onto the end of
+ * caches[i], all n in one pass -- one matmul per projection over the n rows,
+ * each row attending over its own cache -- and a row of logits for each
+ * (logits [n][vocab], host, may be NULL) and its greedy next token (next[n],
+ * may be NULL).  The session's own conversation is left as it was.  n == 0
+ * does nothing; the caches must be distinct and this session's. */
+int kh_llm_forward_each(kh_ctx *ctx, kh_llm *m, size_t n, const int32_t *tokens, kh_llm_parked *const *caches,
+                        float *logits, int32_t *next);
+
 #ifdef __cplusplus
 }
 #endif

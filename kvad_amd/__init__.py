@@ -24,7 +24,7 @@ import numpy as np
 
 __all__ = [
     "F32", "Q8", "Q4", "Q4K", "KvadError", "Declined", "lib", "Context", "Weight", "matvec_many",
-    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "QCache", "mla_attend", "mla_attend_dev", "Llm", "LlmSpec", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
+    "KvCache", "Spec", "attend", "LIB_PATH", "Moe", "QCache", "mla_attend", "mla_attend_dev", "Llm", "LlmSpec", "Parked", "SOFTMAX", "SIGMOID", "GREEDY", "GROUP_LIMITED", "NOAUX_TC",
 ]
 
 F32, Q8, Q4, Q4K = 0, 1, 2, 3
@@ -119,6 +119,11 @@ _SIGS = {
     "kh_llm_generate_launch": (C.c_int, [_p, _p, _sz]),
     "kh_llm_len": (C.c_int, [_p, C.POINTER(_sz)]),
     "kh_llm_truncate": (C.c_int, [_p, _sz]),
+    "kh_llm_park": (C.c_int, [_p, C.POINTER(_p)]),
+    "kh_llm_resume": (C.c_int, [_p, _p]),
+    "kh_llm_parked_free": (C.c_int, [_p]),
+    "kh_llm_parked_len": (C.c_int, [_p, C.POINTER(_sz)]),
+    "kh_llm_forward_each": (C.c_int, [_p, _p, _sz, _p, _p, _p, _p]),
     "kh_moe_new": (C.c_int, [_p, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _sz, _sz, C.c_int, C.c_float, _p,
                              C.POINTER(_p)]),
     "kh_moe_free": (C.c_int, [_p]),
@@ -651,9 +656,61 @@ class Llm:
     def truncate(self, n: int) -> None:
         _check(lib.kh_llm_truncate(self.h, n))
 
+    def park(self) -> "Parked":
+        """Session::park (model/mod.rs:883-893): the conversation held so
+        far, set aside; the session is left with an empty one."""
+        h = C.c_void_p()
+        _check(lib.kh_llm_park(self.h, C.byref(h)))
+        return Parked(h)
+
+    def resume(self, parked: "Parked") -> None:
+        """Session::resume (model/mod.rs:895-897): `parked` back in place of
+        the conversation held, which is dropped.  Consumes `parked`."""
+        h, parked.h = parked.h, None
+        _check(lib.kh_llm_resume(self.h, h))
+
+    def forward_each(self, tokens, caches, want_logits: bool = True):
+        """Session::forward_each (model/mod.rs:899-930, llama.rs:418-434):
+        tokens[i] onto caches[i], all in one pass; (logits [n, vocab] or
+        None, next tokens [n])."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = toks.size
+        if n != len(caches):
+            raise KvadError("a token for each conversation, and a conversation for each token")
+        arr = (C.c_void_p * max(n, 1))(*[c.h for c in caches])
+        logits = np.empty((n, self.spec.vocab), np.float32) if want_logits else None
+        nxt = np.empty(n, np.int32)
+        _check(lib.kh_llm_forward_each(self.ctx.h, self.h, n, _ptr(toks), C.cast(arr, C.c_void_p), _ptr(logits),
+                                       _ptr(nxt)))
+        return logits, nxt
+
     def free(self) -> None:
         if self.h:
             lib.kh_llm_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Parked:
+    """A conversation set aside by Llm.park (the Session trait's Parked,
+    model/mod.rs:837): its device cache and length."""
+
+    def __init__(self, h):
+        self.h = h
+
+    def __len__(self) -> int:
+        n = _sz()
+        _check(lib.kh_llm_parked_len(self.h, C.byref(n)))
+        return n.value
+
+    def free(self) -> None:
+        if self.h:
+            lib.kh_llm_parked_free(self.h)
             self.h = None
 
     def __del__(self):

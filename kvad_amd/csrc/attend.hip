@@ -86,7 +86,6 @@ struct AttnArgs {
     const float *k;
     const float *v;
     size_t kstride, vstride;  // floats between consecutive positions
-    size_t kbytes, vbytes;    // readable bytes of the k and v arrays
     int n_head, group, gc;    // group = n_head / n_kv_head; gc = heads per workgroup
     int L, P, nsplit;
     // when set, the length is read here (+ plus_one) and L/nsplit above are
@@ -98,7 +97,26 @@ struct AttnArgs {
     // [nsplit][n_head][hd]; scores [nsplit][n_head][P]
     float *pm, *pl, *pmin, *pacc, *psc;
     float *out;               // [n_head][hd]
+    // batched rows (Transformer::forward_each, llama.rs:418-434): when set,
+    // workgroup row z = blockIdx.z attends with rows[z] (its own cache and
+    // length), its q and out rows z, and partials offset by z * row_floats
+    const AttnRow *rows;
+    size_t row_floats;
 };
+
+// The row of a batched launch: its cache, its length and its slices.
+__device__ __forceinline__ void at_row(AttnArgs &a, int hd) {
+    if (!a.rows) return;
+    const int z = blockIdx.z;
+    const AttnRow r = a.rows[z];
+    a.k = r.k;
+    a.v = r.v;
+    a.L = r.L;
+    a.q += (size_t)z * a.n_head * hd;
+    a.out += (size_t)z * a.n_head * hd;
+    const size_t o = (size_t)z * a.row_floats;
+    a.pm += o, a.pl += o, a.pmin += o, a.pacc += o, a.psc += o;
+}
 
 // One position's scores for the G heads from the 16-lane row's slices: the
 // same arithmetic wherever a score is needed.
@@ -179,6 +197,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 template <int HD, int R>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+    at_row(a, HD);
     constexpr int HQ = HD / 4;   // dims per k-slot of the score product
     constexpr int NQ4 = HQ / 4;  // float4s per lane of a key row
     constexpr int VT = HD / 64;  // float4s per lane of a value row
@@ -377,39 +396,41 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     }
 }
 
-// Fixed-order tree over the 256 threads' values; every thread gets the result.
+// Fixed-order butterfly within each wave, then the four wave results in wave
+// order; every thread gets the result.  s_w holds four floats.
 template <typename F>
-__device__ __forceinline__ float block_reduce(float v, float *s_red, F op) {
-    const int tid = threadIdx.x;
-    s_red[tid] = v;
+__device__ __forceinline__ float block_reduce(float v, float *s_w, F op) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o));
+    if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = v;
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) s_red[tid] = op(s_red[tid], s_red[tid + w]);
-        __syncthreads();
-    }
-    const float r = s_red[0];
-    __syncthreads();
-    return r;
+    return op(op(s_w[0], s_w[1]), op(s_w[2], s_w[3]));
 }
 
 constexpr int MAX_SPLITS = 4096;
 
 // Exclusive prefix sum of one int per thread over the workgroup (256
-// threads); *total gets the sum.  Fixed order.
+// threads); *total gets the sum.  s holds four ints and is free again on return.
 __device__ __forceinline__ int block_excl_scan(int v, int *s, int *total) {
-    const int tid = threadIdx.x;
-    s[tid] = v;
-    __syncthreads();
-    for (int d = 1; d < 256; d <<= 1) {
-        const int x = tid >= d ? s[tid - d] : 0;
-        __syncthreads();
-        s[tid] += x;
-        __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
     }
-    *total = s[255];
-    const int incl = s[tid];
+    if (lane == 63) s[wv] = x;
     __syncthreads();
-    return incl - v;
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const int t = s[w];
+        off += w < wv ? t : 0;
+        tot += t;
+    }
+    *total = tot;
+    __syncthreads();
+    return off + x - v;
 }
 
 // The merge of one head's splits (one workgroup of 256 threads), over the
@@ -418,20 +439,24 @@ __device__ __forceinline__ int block_excl_scan(int v, int *s, int *total) {
 // less the terms the reference skips, w_t = e^{s_t - M} * (1/S) < 1e-8
 // (mod.rs:807).  Decided per split from its extremes: a split whose largest
 // weight is under 1e-8 is left out whole; one whose smallest is not is taken
-// whole; the straddling ones have their stored scores read, a batch of
-// candidates at a time, and the value rows of just the skipped positions are
-// gathered, all loads in flight together, and taken back out.  vrow(t, q) is
-// float4 q of position t's value row for this head.  Every list is compacted
-// in index order and every sum has a fixed order.
+// whole; the straddling ones have their stored scores read, 1024 candidates
+// at a time, and the value rows of just the skipped positions are gathered,
+// all loads in flight together, and taken back out.  The first splits'
+// partial values are loaded before M is known, so their latency overlaps the
+// reductions.  vrow(t, q) is float4 q of position t's value row for this
+// head.  Every list is compacted in index order and every sum has a fixed
+// order.
 template <int HD, int D, typename VRow>
 __device__ __forceinline__ void merge_head(const float *pm, const float *pl, const float *pmin, const float *pacc,
                                            const float *psc, int ns, int n_head, int h, int d0, int P, int L,
                                            VRow vrow, float *out) {
     constexpr int NQ = D / 4, NSG = 256 / NQ;  // float4 slices of the dims; split (or position) groups
-    constexpr int CAP = 1024;                  // skipped positions gathered per flush
+    constexpr int PER = MAX_SPLITS / 256;      // splits per thread at most
+    constexpr int CAP = 2048;                  // skipped positions gathered per flush
+    constexpr int NB = 8;                      // partial values in flight per thread
     const int tid = threadIdx.x;
-    __shared__ float s_red[256];
-    __shared__ int s_scan[256];
+    __shared__ float s_w[2][4];
+    __shared__ int s_scan[4];
     __shared__ float s_c[MAX_SPLITS];           // e^{m_j - M}, or 0 for a split left out
     __shared__ int s_list[MAX_SPLITS];          // straddling splits, in index order
     __shared__ __align__(16) float s_acc[NSG][D];
@@ -439,129 +464,168 @@ __device__ __forceinline__ void merge_head(const float *pm, const float *pl, con
     __shared__ int s_kpos[CAP];
     __shared__ float s_kw[CAP];
 
+    const int sg = tid / NQ, dq = tid % NQ;
+    const rsrc_t PA = rsrc(pacc, (size_t)ns * n_head * HD * 4);
+    auto pa_load = [&](int i) {  // zeros past the last split (buffer range)
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              PA, (unsigned)((((size_t)i * n_head + h) * HD + d0 + 4 * dq) * 4), 0, 0));
+    };
+    float4 v[NB];
+#pragma unroll
+    for (int u = 0; u < NB; u++) v[u] = pa_load(sg + u * NSG);
+
+    // each thread a run of splits, held in registers
+    const int per = (ns + 255) / 256, i0 = tid * per, n = min(ns - i0, per);
+    float m[PER], l[PER], mn[PER];
     float mx = -INFINITY;
-    for (int i = tid; i < ns; i += 256) mx = fmaxf(mx, pm[(size_t)i * n_head + h]);
-    const float M = block_reduce(mx, s_red, [](float x, float y) { return fmaxf(x, y); });
-    float s = 0.0f;
-    for (int i = tid; i < ns; i += 256) {
-        const size_t o = (size_t)i * n_head + h;
-        s = fmaf(pl[o], expf(pm[o] - M), s);
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        if (u < n) {
+            const size_t o = (size_t)(i0 + u) * n_head + h;
+            m[u] = pm[o], l[u] = pl[o], mn[u] = pmin[o];
+            mx = fmaxf(mx, m[u]);
+        }
     }
-    const float S = block_reduce(s, s_red, [](float x, float y) { return x + y; });
+    const float M = block_reduce(mx, s_w[0], [](float x, float y) { return fmaxf(x, y); });
+    float s = 0.0f;
+    float c[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        if (u < n) {
+            c[u] = expf(m[u] - M);
+            s = fmaf(l[u], c[u], s);
+        }
+    }
+    const float S = block_reduce(s, s_w[1], [](float x, float y) { return x + y; });
     const float inv = 1.0f / S;  // inv = 1 / sum, tensor.rs:304
 
-    // each thread a run of splits: their weights and straddle flags
-    const int per = (ns + 255) / 256, i0 = tid * per, i1 = min(ns, i0 + per);
-    unsigned mask = 0;  // per <= MAX_SPLITS / 256 = 16
-    for (int i = i0; i < i1; i++) {
-        const size_t o = (size_t)i * n_head + h;
-        const float c = expf(pm[o] - M);
-        const bool out_whole = c * inv < 1e-8f;  // every weight of the split is skipped
-        s_c[i] = out_whole ? 0.0f : c;
-        if (!out_whole && expf(pmin[o] - M) * inv < 1e-8f) mask |= 1u << (i - i0);
+    unsigned mask = 0;  // straddling splits of this thread's run
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        if (u < n) {
+            const bool out_whole = c[u] * inv < 1e-8f;  // every weight of the split is skipped
+            s_c[i0 + u] = out_whole ? 0.0f : c[u];
+            if (!out_whole && expf(mn[u] - M) * inv < 1e-8f) mask |= 1u << u;
+        }
     }
     int nstr;
-    int at = block_excl_scan(__builtin_popcount(mask), s_scan, &nstr);
-    for (int i = i0; i < i1; i++)
-        if (mask >> (i - i0) & 1u) s_list[at++] = i;
-    __syncthreads();
+    int at = block_excl_scan(__builtin_popcount(mask), s_scan, &nstr);  // its barrier publishes s_c
+    if (nstr) {
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+            if (mask >> u & 1u) s_list[at++] = i0 + u;
+    }
 
     // acc[d] = sum_j c_j acc_j[d]: thread (split group sg, float4 slice dq)
-    // walks splits sg, sg + NSG, ... eight loads at a time
-    const int sg = tid / NQ, dq = tid % NQ;
-    {
-        const rsrc_t PA = rsrc(pacc, (size_t)ns * n_head * HD * 4);
-        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int j0 = sg; j0 < ns; j0 += 8 * NSG) {
-            float4 v[8];
-            float c[8];
+    // walks splits sg, sg + NSG, ..., NB loads at a time
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j0 = sg;; ) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int i = j0 + u * NSG;
-                v[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      PA, (unsigned)((((size_t)i * n_head + h) * HD + d0 + 4 * dq) * 4), 0, 0));
-                c[u] = i < ns ? s_c[i] : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                x.x = fmaf(c[u], v[u].x, x.x);
-                x.y = fmaf(c[u], v[u].y, x.y);
-                x.z = fmaf(c[u], v[u].z, x.z);
-                x.w = fmaf(c[u], v[u].w, x.w);
-            }
+        for (int u = 0; u < NB; u++) {
+            const int i = j0 + u * NSG;
+            const float cu = i < ns ? s_c[i] : 0.0f;
+            x.x = fmaf(cu, v[u].x, x.x);
+            x.y = fmaf(cu, v[u].y, x.y);
+            x.z = fmaf(cu, v[u].z, x.z);
+            x.w = fmaf(cu, v[u].w, x.w);
         }
-        *reinterpret_cast<float4 *>(&s_acc[sg][4 * dq]) = x;
+        j0 += NB * NSG;
+        if (j0 >= ns) break;
+#pragma unroll
+        for (int u = 0; u < NB; u++) v[u] = pa_load(j0 + u * NSG);
     }
+    *reinterpret_cast<float4 *>(&s_acc[sg][4 * dq]) = x;
 
-    // the skipped terms of the straddling splits
+    // the skipped terms of the straddling splits: 1024 candidates a batch,
+    // four consecutive positions of one split per thread
     float4 fix = make_float4(0.f, 0.f, 0.f, 0.f);
-    int nk = 0;  // listed skipped positions (the same in every thread)
-    const int B = 256 / P;  // straddling splits per batch of candidates
-    for (int q0 = 0; q0 < nstr; q0 += B) {
-        const int q = q0 + tid / P, k = tid % P;
-        float w = 0.0f;
-        int t = 0;
-        if (q < nstr) {
-            const int j = s_list[q];
-            t = j * P + k;
-            const float sc = psc[((size_t)j * n_head + h) * P + k];
-            if (t < L && sc != -INFINITY) {
-                w = expf(sc - M);
-                w = w * inv;
-                if (!(w < 1e-8f)) w = 0.0f;  // kept (a weight that underflows to 0 adds nothing either)
-            }
-        }
-        int added;
-        const int o = block_excl_scan(w > 0.0f, s_scan, &added);
-        if (w > 0.0f) {
-            s_kpos[nk + o] = t;
-            s_kw[nk + o] = w;
-        }
-        nk += added;
-        __syncthreads();
-        if (nk > CAP - 256 || q0 + B >= nstr) {
-            // gather: thread (group sg, slice dq) takes listed positions sg, sg + NSG, ...
-            for (int k0 = sg; k0 < nk; k0 += 4 * NSG) {
-                float4 v[4];
-                float ww[4];
+    if (nstr) {
+        __syncthreads();  // s_list
+        int nk = 0;       // listed skipped positions (the same in every thread)
+        const int ncand = nstr * P;
+        for (int c0 = 0; c0 < ncand; c0 += 1024) {
+            const int cand = c0 + 4 * tid;
+            float w4[4] = {0.f, 0.f, 0.f, 0.f};
+            int t0 = 0, cnt = 0;
+            if (cand < ncand) {
+                const int j = s_list[cand / P], k = cand % P;
+                t0 = j * P + k;
+                const float4 sc4 = *reinterpret_cast<const float4 *>(psc + ((size_t)j * n_head + h) * P + k);
+                const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    const int kk = k0 + u * NSG;
-                    const bool ok = kk < nk;
-                    v[u] = vrow(s_kpos[ok ? kk : 0], d0 / 4 + dq);
-                    ww[u] = ok ? s_kw[kk] : 0.0f;
-                }
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    fix.x = fmaf(ww[u], v[u].x, fix.x);
-                    fix.y = fmaf(ww[u], v[u].y, fix.y);
-                    fix.z = fmaf(ww[u], v[u].z, fix.z);
-                    fix.w = fmaf(ww[u], v[u].w, fix.w);
+                    if (t0 + u < L && sc[u] != -INFINITY) {
+                        float w = expf(sc[u] - M);
+                        w = w * inv;
+                        // kept (a weight that underflows to 0 adds nothing either)
+                        w4[u] = w < 1e-8f ? w : 0.0f;
+                        cnt += w4[u] > 0.0f;
+                    }
                 }
             }
-            nk = 0;
+            int added;
+            int o = nk + block_excl_scan(cnt, s_scan, &added);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (w4[u] > 0.0f) {
+                    s_kpos[o] = t0 + u;
+                    s_kw[o] = w4[u];
+                    o++;
+                }
+            }
+            nk += added;
             __syncthreads();
+            if (nk > CAP - 1024 || c0 + 1024 >= ncand) {
+                // gather: thread (group sg, slice dq) takes listed positions sg, sg + NSG, ...
+                for (int k0 = sg; k0 < nk; k0 += 4 * NSG) {
+                    float4 vv[4];
+                    float ww[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int kk = k0 + u * NSG;
+                        const bool ok = kk < nk;
+                        vv[u] = vrow(s_kpos[ok ? kk : 0], d0 / 4 + dq);
+                        ww[u] = ok ? s_kw[kk] : 0.0f;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        fix.x = fmaf(ww[u], vv[u].x, fix.x);
+                        fix.y = fmaf(ww[u], vv[u].y, fix.y);
+                        fix.z = fmaf(ww[u], vv[u].z, fix.z);
+                        fix.w = fmaf(ww[u], vv[u].w, fix.w);
+                    }
+                }
+                nk = 0;
+                __syncthreads();
+            }
         }
+        *reinterpret_cast<float4 *>(&s_fix[sg][4 * dq]) = fix;
     }
-    *reinterpret_cast<float4 *>(&s_fix[sg][4 * dq]) = fix;
     __syncthreads();
     if (tid < NQ) {
         float4 x = *reinterpret_cast<const float4 *>(&s_acc[0][4 * tid]);
-        float4 f = *reinterpret_cast<const float4 *>(&s_fix[0][4 * tid]);
 #pragma unroll
         for (int g = 1; g < NSG; g++) {
             const float4 y = *reinterpret_cast<const float4 *>(&s_acc[g][4 * tid]);
-            const float4 z = *reinterpret_cast<const float4 *>(&s_fix[g][4 * tid]);
             x = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
-            f = make_float4(f.x + z.x, f.y + z.y, f.z + z.z, f.w + z.w);
         }
-        x = make_float4(x.x * inv - f.x, x.y * inv - f.y, x.z * inv - f.z, x.w * inv - f.w);
+        x = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
+        if (nstr) {
+            float4 f = *reinterpret_cast<const float4 *>(&s_fix[0][4 * tid]);
+#pragma unroll
+            for (int g = 1; g < NSG; g++) {
+                const float4 z = *reinterpret_cast<const float4 *>(&s_fix[g][4 * tid]);
+                f = make_float4(f.x + z.x, f.y + z.y, f.z + z.z, f.w + z.w);
+            }
+            x = make_float4(x.x - f.x, x.y - f.y, x.z - f.z, x.w - f.w);
+        }
         *reinterpret_cast<float4 *>(out + (size_t)h * HD + d0 + 4 * tid) = x;
     }
 }
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+    at_row(a, HD);
     const int h = blockIdx.x;
     const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
     const int ns = (L + a.P - 1) / a.P;
@@ -591,7 +655,7 @@ namespace {
 // The launch for n_positions (or, with a device length, for at most that
 // many): split size, partial buffers carved from ws.
 int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
-          const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out) {
+          const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out, int nb = 1) {
     if (n_kv_head <= 0 || n_head <= 0 || n_head % n_kv_head != 0)
         return fail(KH_EINVAL, "attend: n_head must be a positive multiple of n_kv_head");
     if (head_dim != 64 && head_dim != 128)
@@ -605,8 +669,6 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     a.v = v;
     a.kstride = kstride;
     a.vstride = vstride;
-    a.kbytes = n_positions * kstride * 4;
-    a.vbytes = n_positions * vstride * 4;
     a.n_head = n_head;
     a.group = n_head / n_kv_head;
     int gc = 1;  // query heads per workgroup: the 16 columns of the score product
@@ -621,7 +683,7 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     const int rungs = head_dim == 64 ? 3 : 2;
     const int ladder[3] = {64, 128, 256};
     int step = rungs - 1;
-    while (step > 0 && (long long)((n_positions + ladder[step] - 1) / ladder[step]) * n_hg < cu) step--;
+    while (step > 0 && (long long)((n_positions + ladder[step] - 1) / ladder[step]) * n_hg * nb < cu) step--;
     while (step < rungs - 1 && (n_positions + ladder[step] - 1) / ladder[step] > (size_t)MAX_SPLITS) step++;
     const int P = ladder[step];
     if ((n_positions + P - 1) / P > (size_t)MAX_SPLITS)
@@ -633,32 +695,34 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     return KH_OK;
 }
 
-// Partials of nsplit splits: pm, pl, pmin [ns], acc [ns][hd], scores [ns][P].
+// Partials of nsplit splits: pm, pl, pmin [ns], acc [ns][hd], scores [ns][P],
+// each array on a 64-byte boundary (hd and P are multiples of 16).
 size_t partial_floats(size_t nsplit, int n_head, int head_dim, int P) {
-    const size_t ns = nsplit * (size_t)n_head;
-    return 3 * ns + ns * (size_t)head_dim + ns * (size_t)P;
+    const size_t ns = nsplit * (size_t)n_head, ns16 = (ns + 15) & ~(size_t)15;
+    return 3 * ns16 + ns * (size_t)head_dim + ns * (size_t)P;
 }
 
-void carve(AttnArgs &a, void *ws, int head_dim) {
-    const size_t ns = (size_t)a.nsplit * a.n_head;
+template <typename Args>
+void carve_partials(Args &a, void *ws, int head_dim) {
+    const size_t ns = (size_t)a.nsplit * a.n_head, ns16 = (ns + 15) & ~(size_t)15;
     float *p = static_cast<float *>(ws);
-    a.pm = p, p += ns;
-    a.pl = p, p += ns;
-    a.pmin = p, p += ns;
+    a.pm = p, p += ns16;
+    a.pl = p, p += ns16;
+    a.pmin = p, p += ns16;
     a.pacc = p, p += ns * head_dim;
     a.psc = p;
 }
 
-int run(kh_ctx *ctx, const AttnArgs &a, int head_dim) {
-    dim3 grid(a.nsplit, a.n_head / a.gc);
+int run(kh_ctx *ctx, const AttnArgs &a, int head_dim, int nb = 1) {
+    dim3 grid(a.nsplit, a.n_head / a.gc, nb);
     if (head_dim == 64) launch_split<64>(a, grid, ctx->stream);
     else launch_split<128>(a, grid, ctx->stream);
     KH_HIP(hipGetLastError());
     if (a.nsplit > 1) {
         if (head_dim == 64)
-            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(a.n_head), dim3(256), 0, ctx->stream, a);
+            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a);
         else
-            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(a.n_head), dim3(256), 0, ctx->stream, a);
+            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a);
         KH_HIP(hipGetLastError());
     }
     return KH_OK;
@@ -673,6 +737,26 @@ size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_posit
     return 4 * partial_floats(nsplit, n_head, head_dim, 64) + 4 * (max_positions + 256) * (size_t)n_head + 1024;
 }
 
+size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size_t nb) {
+    // per row as attend_ws_bytes: any split size the launch picks fits
+    const size_t nsplit = (max_positions + 63) / 64;
+    return 4 * nb * (partial_floats(nsplit, n_head, head_dim, 64) + (max_positions + 256) * (size_t)n_head) + 1024;
+}
+
+int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,
+                       int nb, size_t kstride, size_t vstride, size_t max_positions, float *out, void *ws,
+                       size_t ws_bytes) {
+    if (nb <= 0 || nb > 65535 || max_positions == 0) return fail(KH_EINVAL, "attend: no rows or no positions");
+    AttnArgs a;
+    int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, nullptr, nullptr, kstride, vstride, max_positions, out, nb);
+    if (rc) return rc;
+    a.rows = rows;
+    a.row_floats = partial_floats(a.nsplit, n_head, head_dim, a.P);
+    if (4 * a.row_floats * nb > ws_bytes) return fail(KH_EINVAL, "attend: workspace too small for the rows");
+    carve_partials(a, ws, head_dim);
+    return run(ctx, a, head_dim, nb);
+}
+
 int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
                   const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out) {
     if (n_positions == 0) {
@@ -685,7 +769,7 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     if (rc) return rc;
     if (a.nsplit > 1) {
         if ((rc = ensure(ctx, ctx->ws, 4 * partial_floats(a.nsplit, n_head, head_dim, a.P) + 1024))) return rc;
-        carve(a, ctx->ws.ptr, head_dim);
+        carve_partials(a, ctx->ws.ptr, head_dim);
     }
     return run(ctx, a, head_dim);
 }
@@ -699,7 +783,7 @@ int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, c
     if (rc) return rc;
     a.len_dev = len_dev;
     a.plus_one = plus_one;
-    carve(a, ws, head_dim);
+    carve_partials(a, ws, head_dim);
     return run(ctx, a, head_dim);
 }
 
@@ -914,15 +998,9 @@ int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, c
     a.scale = scale;
     a.out = out;
     if (a.nsplit > 1) {
-        const size_t ns = (size_t)a.nsplit * n_head;
         int rc = ensure(ctx, ctx->ws, 4 * partial_floats(a.nsplit, n_head, MLA_LAT, MLA_P) + 1024);
         if (rc) return rc;
-        float *p = static_cast<float *>(ctx->ws.ptr);
-        a.pm = p, p += ns;
-        a.pl = p, p += ns;
-        a.pmin = p, p += ns;
-        a.pacc = p, p += ns * MLA_LAT;
-        a.psc = p;
+        carve_partials(a, ctx->ws.ptr, MLA_LAT);
     }
     hipLaunchKernelGGL(mla_split_kernel, dim3(a.nsplit, (n_head + 15) / 16), dim3(256), 0, ctx->stream, a);
     KH_HIP(hipGetLastError());

@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -116,6 +117,24 @@ struct kh_llm {
     size_t attn_ws_bytes = 0;
     size_t len = 0;                                          // positions in the cache
     hipGraphExec_t graph = nullptr;                          // one captured step
+    // Session::park / resume (model/mod.rs:889-897): caches handed out and
+    // not yet taken back or freed, and freed ones kept for the next park
+    std::set<kh_llm_parked *> parked;
+    std::vector<std::pair<std::vector<float *>, std::vector<float *>>> spare;
+    // forward_each's buffers for rows_cap rows, one allocation laid out by
+    // session.hip, and the host copy of the table it uploads per call
+    void *rows_buf = nullptr;
+    size_t rows_cap = 0;
+    std::vector<char> rows_host;
+};
+
+// A conversation's cache set aside (Session::park, model/mod.rs:889-893): per
+// layer [n_ctx, kv_dim] keys and values, and the positions held.
+struct kh_llm_parked {
+    kh_llm *owner = nullptr;  // null once the session is freed
+    int device = 0;
+    std::vector<float *> k, v;
+    size_t len = 0;
 };
 
 struct kh_kv {
@@ -177,6 +196,8 @@ int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, 
 
 // Batched prefill y[m, rows] = xs[m, cols] W^T (+bias), m > 1 (device pointers).
 int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
+// The same over rows already quantised (QActBatch form), quantised weights only.
+int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, const float *bias, float *y);
 
 // GEMM over activations already quantised (QActBatch form), optionally
 // grouped by expert: with `tiles` set, workgroup row y of the grid takes tile
@@ -252,12 +273,28 @@ int launch_dequant_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out);
 int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out);
 // tensor::rms_norm over m rows of n (glue.hip).
 int launch_rms_norm(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out);
+// x += y over n floats; gate = silu(gate) * up over n floats (glue.hip).
+int launch_add(kh_ctx *ctx, float *x, const float *y, size_t n);
+int launch_swiglu(kh_ctx *ctx, float *gate, const float *up, size_t n);
 // Attention whose length is read from device memory: n_positions = *len_dev
 // (+1 when plus_one), at most max_positions; partials in `ws` (attend_ws_bytes).
 int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
                          const float *v, size_t kv_stride_k, size_t kv_stride_v, const int32_t *len_dev, int plus_one,
                          size_t max_positions, float *out, void *ws);
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions);
+// Attention of nb rows at once, each over its own cache (forward_each,
+// llama.rs:258-271): row z's query is q + z * n_head * head_dim, its output
+// out + z * n_head * head_dim, its keys and values rows[z].k / .v (strides
+// kstride / vstride) over rows[z].L <= max_positions positions.  `rows` is in
+// device memory; partials in `ws` (attend_rows_ws_bytes).
+struct AttnRow {
+    float *k, *v;
+    int L;
+};
+int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,
+                       int nb, size_t kstride, size_t vstride, size_t max_positions, float *out, void *ws,
+                       size_t ws_bytes);
+size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size_t nb);
 
 // Absorbed latent attention (model/deepseek.rs:553-591): out[n_head][512] =
 // softmax over positions of (q_lat . c_t + q_pe . pe_t) * scale, times c_t.

@@ -583,8 +583,25 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     char *p = static_cast<char *>(ctx->ws.ptr);
     QAct q{reinterpret_cast<int8_t *>(p), reinterpret_cast<float *>(p + qb), reinterpret_cast<int32_t *>(p + qb + sb)};
     if ((rc = launch_qact(ctx, xs, m, cols, q))) return rc;
+    return launch_matmul_q(ctx, w, q, m, bias, y);
+}
+
+int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, const float *bias, float *y) {
+    const size_t rows = w->rows, cols = w->cols;
+    if (w->precision == KH_F32) return fail(KH_EINVAL, "matmul: f32 weights take f32 rows");
+    if (rows * cols + 4 * 128 * cols >= 0xffffffffull || m * cols + 4 * 128 * cols >= 0xffffffffull ||
+        rows > 0x7fffffff || m > 0x7fffffff)
+        return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
     // a few tokens: stream the weights once through the multi-token GEMV
     if (m <= (size_t)MULTI_TOKENS && !matmul_force_gemm()) return launch_gemv_multi(ctx, w, q, m, bias, y);
+    GemmArgs a{};
+    a.w = w->qs;
+    a.ws = w->scales;
+    a.bias = bias;
+    a.y = y;
+    a.M = (int)m;
+    a.N = (int)rows;
+    a.K = (int)cols;
     a.xq = q.qs;
     a.xs = q.scales;
     a.xsum = q.sums;

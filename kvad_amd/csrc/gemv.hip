@@ -1104,8 +1104,11 @@ int launch_multi_p(kh_ctx *ctx, MultiArgs a) {
 
 int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
     // one launch per input kind present (a kernel stages one kind), in table order
-    for (int i = 0; i < njobs; i++)
+    for (int i = 0; i < njobs; i++) {
         if (jobs[i].xf2 && jobs[i].norm_w) return fail(KH_EINVAL, "matvec: rms_norm and swiglu inputs do not combine");
+        if (precision == KH_F32 && (jobs[i].xf2 || jobs[i].norm_w || !jobs[i].xf))
+            return fail(KH_EINVAL, "matvec: the f32 GEMV takes its f32 input as it is");
+    }
     for (int kind : {IN_F32, IN_NORM, IN_SWIGLU, IN_CODES}) {
         std::vector<GemvJob> js;
         for (int i = 0; i < njobs; i++)

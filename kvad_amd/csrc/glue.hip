@@ -86,6 +86,12 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float *gate, const float *u
     gate[i] = silu * up[i];
 }
 
+// The residual add, x[i] = x[i] + y[i] (llama.rs:273-275, :283-285).
+__global__ __launch_bounds__(256) void add_kernel(float *x, const float *y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = x[i] + y[i];
+}
+
 // One row per workgroup: max, exp(x - max), sum, times 1/sum.
 __global__ __launch_bounds__(256) void softmax_kernel(float *x, int n) {
     __shared__ float s_red[256];
@@ -104,6 +110,20 @@ __global__ __launch_bounds__(256) void softmax_kernel(float *x, int n) {
 }
 
 }  // namespace
+
+int launch_add(kh_ctx *ctx, float *x, const float *y, size_t n) {
+    if (n == 0) return KH_OK;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, x, y, n);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+int launch_swiglu(kh_ctx *ctx, float *gate, const float *up, size_t n) {
+    if (n == 0) return KH_OK;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, gate, up, n);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
 
 int launch_rms_norm(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out) {
     if (m == 0 || n == 0) return KH_OK;
@@ -150,9 +170,7 @@ int kh_swiglu_dev(kh_ctx *ctx, float *gate, const float *up, size_t n) {
     if (n == 0) return KH_OK;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
-    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, gate, up, n);
-    KH_HIP(hipGetLastError());
-    return KH_OK;
+    return launch_swiglu(ctx, gate, up, n);
 }
 
 int kh_softmax_dev(kh_ctx *ctx, float *x, size_t m, size_t n) {

@@ -12,6 +12,8 @@
 // launch; attention over the cache, its length read from the device; o as a
 // GEMV that adds into the residual; RMSNorm; gate and up as one launch; down
 // with swiglu(gate, up) staged by the GEMV and added into the residual.
+#include <algorithm>
+#include <initializer_list>
 #include <memory>
 
 #include "common.hpp"
@@ -19,28 +21,18 @@
 namespace kh {
 namespace {
 
-// One workgroup per head of q or k (then the v copy): optional per-head
-// RMSNorm (norm_heads, llama.rs:122-127), RoPE at the device position,
-// and k and v into the cache row.
-__global__ __launch_bounds__(128) void rope_push_kernel(float *qkv, int n_head, int n_kv, int hd,
-                                                       const float *cos_t, const float *sin_t, int interleaved,
-                                                       const float *q_norm, const float *k_norm, float eps,
-                                                       float *kc, float *vc, const int32_t *pos_dev) {
-    const int h = blockIdx.x, t = threadIdx.x, half = hd / 2;
-    const int pos = *pos_dev;
-    const int kv_dim = n_kv * hd;
+// One head (128 threads): optional per-head RMSNorm (norm_heads,
+// llama.rs:122-127; rms_norm, tensor.rs:329-333, tree sum), then RoPE at
+// `pos` (Rope::apply / apply_interleaved, tensor.rs:437-472) into dst, which
+// may be src.
+__device__ void rope_head(const float *src, float *dst, int hd, int pos, const float *cos_t, const float *sin_t,
+                          int interleaved, const float *nw, float eps) {
+    const int t = threadIdx.x, half = hd / 2;
     __shared__ float s_x[256];
     __shared__ float s_red[128];
-    if (h == n_head + n_kv) {  // the values: straight into the cache
-        for (int i = t; i < kv_dim; i += 128) vc[(size_t)pos * kv_dim + i] = qkv[(size_t)(n_head + n_kv) * hd + i];
-        return;
-    }
-    const bool is_q = h < n_head;
-    float *x = qkv + (size_t)h * hd;
-    for (int i = t; i < hd; i += 128) s_x[i] = x[i];
+    for (int i = t; i < hd; i += 128) s_x[i] = src[i];
     __syncthreads();
-    const float *nw = is_q ? q_norm : k_norm;
-    if (nw) {  // rms_norm of the head (tensor.rs:329-333), tree sum
+    if (nw) {
         float s = 0.0f;
         for (int i = t; i < hd; i += 128) {
             const float sq = s_x[i] * s_x[i];
@@ -60,8 +52,6 @@ __global__ __launch_bounds__(128) void rope_push_kernel(float *qkv, int n_head, 
         }
         __syncthreads();
     }
-    // Rope::apply / apply_interleaved (tensor.rs:437-472)
-    float *dst = is_q ? x : kc + (size_t)pos * kv_dim + (size_t)(h - n_head) * hd;
     for (int i = t; i < half; i += 128) {
         const float c = cos_t[(size_t)pos * half + i], s = sin_t[(size_t)pos * half + i];
         const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + half;
@@ -69,6 +59,50 @@ __global__ __launch_bounds__(128) void rope_push_kernel(float *qkv, int n_head, 
         const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
         dst[ia] = ac - bs;
         dst[ib] = bc + as;
+    }
+}
+
+// One workgroup per head of q or k (then the v copy): q rotated in place,
+// k rotated into the cache row at the device position, v copied there.
+__global__ __launch_bounds__(128) void rope_push_kernel(float *qkv, int n_head, int n_kv, int hd,
+                                                       const float *cos_t, const float *sin_t, int interleaved,
+                                                       const float *q_norm, const float *k_norm, float eps,
+                                                       float *kc, float *vc, const int32_t *pos_dev) {
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int pos = *pos_dev;
+    const int kv_dim = n_kv * hd;
+    if (h == n_head + n_kv) {  // the values: straight into the cache
+        for (int i = t; i < kv_dim; i += 128) vc[(size_t)pos * kv_dim + i] = qkv[(size_t)(n_head + n_kv) * hd + i];
+        return;
+    }
+    const bool is_q = h < n_head;
+    float *x = qkv + (size_t)h * hd;
+    float *dst = is_q ? x : kc + (size_t)pos * kv_dim + (size_t)(h - n_head) * hd;
+    rope_head(x, dst, hd, pos, cos_t, sin_t, interleaved, is_q ? q_norm : k_norm, eps);
+}
+
+// The same for n rows (grid y), each at its own position in its own cache
+// (rows[i]: position L - 1; run_rows, llama.rs:249-256): q [n][n_head*hd],
+// k and v [n][n_kv*hd].
+__global__ __launch_bounds__(128) void rope_push_rows_kernel(float *q, const float *k, const float *v, int n_head,
+                                                            int n_kv, int hd, const float *cos_t, const float *sin_t,
+                                                            int interleaved, const float *q_norm,
+                                                            const float *k_norm, float eps, const AttnRow *rows) {
+    const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
+    const int kv_dim = n_kv * hd;
+    const AttnRow r = rows[i];
+    const int pos = r.L - 1;
+    if (h == n_head + n_kv) {
+        for (int j = t; j < kv_dim; j += 128) r.v[(size_t)pos * kv_dim + j] = v[(size_t)i * kv_dim + j];
+        return;
+    }
+    if (h < n_head) {
+        float *x = q + ((size_t)i * n_head + h) * hd;
+        rope_head(x, x, hd, pos, cos_t, sin_t, interleaved, q_norm, eps);
+    } else {
+        const int kh = h - n_head;
+        rope_head(k + (size_t)i * kv_dim + (size_t)kh * hd, r.k + (size_t)pos * kv_dim + (size_t)kh * hd, hd, pos,
+                  cos_t, sin_t, interleaved, k_norm, eps);
     }
 }
 
@@ -100,9 +134,13 @@ __device__ void block_best(float &bv, int &bi, float *s_v, int *s_i) {
     bv = s_v[0], bi = s_i[0];
 }
 
+// Row blockIdx.y of v [rows][n]: partials [rows][ARGMAX_BLOCKS].
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int n, float *pv, int *pi) {
     __shared__ float s_v[256];
     __shared__ int s_i[256];
+    v += (size_t)blockIdx.y * n;
+    pv += (size_t)blockIdx.y * ARGMAX_BLOCKS;
+    pi += (size_t)blockIdx.y * ARGMAX_BLOCKS;
     const int per = (n - 1 + ARGMAX_BLOCKS - 1) / ARGMAX_BLOCKS;
     const int lo = 1 + blockIdx.x * per, hi = min(n, lo + per);
     float bv = -INFINITY;
@@ -115,6 +153,24 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int
     if (threadIdx.x == 0) pv[blockIdx.x] = bv, pi[blockIdx.x] = bi;
 }
 
+// Entry 0 against the best of entries 1..: the first of equal maxima wins.
+__device__ __forceinline__ int pick(const float *v, int n, float bv, int bi) {
+    const float first = n > 0 ? v[0] : 0.0f;
+    return n > 1 && first == first && bi >= 0 && bv > first ? bi : 0;
+}
+
+// One workgroup per row of v [rows][n]: next[row].
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const float *v, int n, const float *pv, const int *pi,
+                                                         int32_t *next) {
+    __shared__ float s_v[256];
+    __shared__ int s_i[256];
+    const int row = blockIdx.x;
+    float bv = pv[(size_t)row * ARGMAX_BLOCKS + threadIdx.x];
+    int bi = pi[(size_t)row * ARGMAX_BLOCKS + threadIdx.x];
+    block_best(bv, bi, s_v, s_i);
+    if (threadIdx.x == 0) next[row] = pick(v + (size_t)row * n, n, bv, bi);
+}
+
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float *v, int n, const float *pv, const int *pi,
                                                           int32_t *token, int32_t *pos, int32_t *step, int32_t *out,
                                                           int out_cap) {
@@ -124,9 +180,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *v, int n
     int bi = pi[threadIdx.x];
     block_best(bv, bi, s_v, s_i);
     if (threadIdx.x == 0) {
-        const float first = n > 0 ? v[0] : 0.0f;
-        int best = 0;
-        if (n > 1 && first == first && bi >= 0 && bv > first) best = bi;
+        const int best = pick(v, n, bv, bi);
         *token = best;
         *pos = *pos + 1;
         const int k = *step;
@@ -180,7 +234,9 @@ int run_jobs(kh_ctx *ctx, const std::vector<std::pair<const kh_weight *, GemvJob
     return KH_OK;
 }
 
-bool fusable(const kh_weight *w) { return w->precision == KH_F32 || w->cols <= fuse_max_cols(w->precision); }
+// The quantised GEMV can take swiglu(gate, up) as its input when it stages
+// the activation itself; the f32 GEMV reads its input as it is.
+bool fusable(const kh_weight *w) { return w->precision != KH_F32 && w->cols <= fuse_max_cols(w->precision); }
 
 // The GEMV can take rms_norm(x) as its input when it stages x itself.
 bool norm_fusable(const kh_weight *w) { return w->precision != KH_F32 && w->cols <= fuse_max_cols(w->precision); }
@@ -227,7 +283,10 @@ int step(kh_ctx *ctx, kh_llm *m) {
         jobs.push_back({L.up, normed(gemv_job(L.up, min_, nullptr, nullptr, m->u, 0), fm, L.mlp_norm, s.eps)});
         if ((rc = run_jobs(ctx, jobs))) return rc;
         jobs.clear();
-        if (fusable(L.down)) {
+        if (L.down->precision == KH_F32) {  // swiglu_inplace (ffn.rs:386), then the f32 GEMV
+            if ((rc = launch_swiglu(ctx, m->g, m->u, s.n_ff))) return rc;
+            jobs.push_back({L.down, gemv_job(L.down, m->g, nullptr, nullptr, m->x, 1)});
+        } else if (fusable(L.down)) {
             jobs.push_back({L.down, gemv_job(L.down, m->g, m->u, nullptr, m->x, 1)});
         } else {  // too wide to stage in LDS: quantise swiglu(gate, up) first
             if ((rc = launch_swiglu_qact(ctx, m->g, m->u, 1, s.n_ff, m->hq))) return rc;
@@ -266,6 +325,180 @@ int check_weight_shape(const kh_weight *w, size_t rows, size_t cols, const char 
         return fail(KH_EINVAL, std::string("kh_llm_set_layer: ") + what + " has the wrong shape");
     if (w->precision != KH_F32 && w->cols > 0x7fffffff) return fail(KH_EINVAL, "too wide");
     return KH_OK;
+}
+
+// ---- forward_each: n rows through the layers at once --------------------
+
+// The rows' buffers, carved from one allocation for `cap` rows (base null:
+// sizes only).  QActBatch codes take the widest activation of a block.
+struct RowsBuf {
+    float *x, *h, *q, *k, *v, *att, *tmp, *g, *u, *logits, *pv;
+    int *pi;
+    int32_t *tok, *next;
+    AttnRow *tab;  // [n_layer][n]: each row's cache and length
+    QAct qa;
+    void *ws;
+    size_t ws_bytes, bytes;
+};
+
+RowsBuf rows_layout(const kh_llm_spec &s, size_t cap, char *base) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        char *p = base ? base + off : nullptr;
+        off += (bytes + 255) / 256 * 256;
+        return p;
+    };
+    const size_t e = s.n_embd, qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
+    const size_t wide = std::max(e, std::max(qd, s.n_ff)), nb = (cap * wide + BLOCK - 1) / BLOCK;
+    RowsBuf b{};
+    b.x = reinterpret_cast<float *>(take(4 * cap * e));
+    b.h = reinterpret_cast<float *>(take(4 * cap * e));
+    b.tmp = reinterpret_cast<float *>(take(4 * cap * e));
+    b.q = reinterpret_cast<float *>(take(4 * cap * qd));
+    b.att = reinterpret_cast<float *>(take(4 * cap * qd));
+    b.k = reinterpret_cast<float *>(take(4 * cap * kvd));
+    b.v = reinterpret_cast<float *>(take(4 * cap * kvd));
+    b.g = reinterpret_cast<float *>(take(4 * cap * s.n_ff));
+    b.u = reinterpret_cast<float *>(take(4 * cap * s.n_ff));
+    b.logits = reinterpret_cast<float *>(take(4 * cap * s.vocab));
+    b.pv = reinterpret_cast<float *>(take(4 * cap * ARGMAX_BLOCKS));
+    b.pi = reinterpret_cast<int *>(take(4 * cap * ARGMAX_BLOCKS));
+    b.tok = reinterpret_cast<int32_t *>(take(4 * cap));
+    b.next = reinterpret_cast<int32_t *>(take(4 * cap));
+    b.tab = reinterpret_cast<AttnRow *>(take(sizeof(AttnRow) * cap * s.n_layer));
+    b.qa.qs = reinterpret_cast<int8_t *>(take(cap * wide));
+    b.qa.scales = reinterpret_cast<float *>(take(4 * nb));
+    b.qa.sums = reinterpret_cast<int32_t *>(take(4 * nb));
+    b.ws_bytes = attend_rows_ws_bytes((int)s.n_head, (int)s.head_dim, s.n_ctx, cap);
+    b.ws = take(b.ws_bytes);
+    b.bytes = off;
+    return b;
+}
+
+int ensure_rows(kh_llm *m, size_t n) {
+    if (n <= m->rows_cap) return KH_OK;
+    const size_t cap = (n + 7) / 8 * 8;
+    KH_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (m->rows_buf) (void)hipFree(m->rows_buf);
+    m->rows_buf = nullptr;
+    m->rows_cap = 0;
+    KH_HIP(hipMalloc(&m->rows_buf, rows_layout(m->spec, cap, nullptr).bytes));
+    m->rows_cap = cap;
+    return KH_OK;
+}
+
+// y[n][rows] = xs W^T (+bias): f32 weights on the f32 GEMM, quantised ones
+// from the rows' codes in qa (matmul_bt, quant.rs:751; tensor.rs:102).
+int project(kh_ctx *ctx, const kh_weight *w, const float *xs, const QAct &qa, size_t n, const float *bias, float *y) {
+    if (w->precision == KH_F32) return launch_matmul(ctx, w, xs, n, bias, y);
+    return launch_matmul_q(ctx, w, qa, n, bias, y);
+}
+
+bool any_quantised(std::initializer_list<const kh_weight *> ws) {
+    for (auto w : ws)
+        if (w->precision != KH_F32) return true;
+    return false;
+}
+
+// run_rows (llama.rs:224-289) with Rows::Each, then the head over every row
+// (llama.rs:404-416) and each row's greedy token.  The table (tokens, and per
+// layer each row's cache and length) is already on the device.
+int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
+    const kh_llm_spec &s = m->spec;
+    const size_t e = s.n_embd, qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
+    int rc;
+    for (size_t i = 0; i < n; i++)  // embed (llama.rs:384-391)
+        if ((rc = launch_dequant_row_dev(ctx, m->embed, b.tok + i, b.x + i * e))) return rc;
+    for (size_t l = 0; l < s.n_layer; l++) {
+        const kh_llm::Layer &L = m->layers[l];
+        // ---- attention sub-block (llama.rs:241-275)
+        if ((rc = launch_rms_norm(ctx, b.x, L.attn_norm, n, e, s.eps, b.h))) return rc;
+        if (any_quantised({L.q, L.k, L.v}) && (rc = launch_qact(ctx, b.h, n, e, b.qa))) return rc;
+        if ((rc = project(ctx, L.q, b.h, b.qa, n, L.q_b, b.q)) || (rc = project(ctx, L.k, b.h, b.qa, n, L.k_b, b.k)) ||
+            (rc = project(ctx, L.v, b.h, b.qa, n, L.v_b, b.v)))
+            return rc;
+        const AttnRow *tab = b.tab + l * n;
+        hipLaunchKernelGGL(rope_push_rows_kernel, dim3((unsigned)(s.n_head + s.n_kv_head + 1), (unsigned)n), dim3(128),
+                           0, ctx->stream, b.q, b.k, b.v, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim,
+                           m->rope_cos, m->rope_sin, s.rope_interleaved, L.q_norm, L.k_norm, s.eps, tab);
+        KH_HIP(hipGetLastError());
+        if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
+                                     kvd, s.n_ctx, b.att, b.ws, b.ws_bytes)))
+            return rc;
+        if (L.o->precision != KH_F32 && (rc = launch_qact(ctx, b.att, n, qd, b.qa))) return rc;
+        if ((rc = project(ctx, L.o, b.att, b.qa, n, nullptr, b.tmp)) || (rc = launch_add(ctx, b.x, b.tmp, n * e)))
+            return rc;
+        // ---- MLP sub-block (llama.rs:277-285, Ffn::run ffn.rs:370-375)
+        if ((rc = launch_rms_norm(ctx, b.x, L.mlp_norm, n, e, s.eps, b.h))) return rc;
+        if (any_quantised({L.gate, L.up}) && (rc = launch_qact(ctx, b.h, n, e, b.qa))) return rc;
+        if ((rc = project(ctx, L.gate, b.h, b.qa, n, nullptr, b.g)) ||
+            (rc = project(ctx, L.up, b.h, b.qa, n, nullptr, b.u)))
+            return rc;
+        if (L.down->precision != KH_F32) {  // QActBatch::new of swiglu(gate, up), then down
+            if ((rc = launch_swiglu_qact(ctx, b.g, b.u, n, s.n_ff, b.qa))) return rc;
+        } else if ((rc = launch_swiglu(ctx, b.g, b.u, n * s.n_ff))) {
+            return rc;
+        }
+        if ((rc = project(ctx, L.down, b.g, b.qa, n, nullptr, b.tmp)) || (rc = launch_add(ctx, b.x, b.tmp, n * e)))
+            return rc;
+    }
+    // ---- head over every row (llama.rs:412-415), then each row's argmax
+    const kh_weight *head = m->head ? m->head : m->embed;
+    if ((rc = launch_rms_norm(ctx, b.x, m->final_norm, n, e, s.eps, b.h))) return rc;
+    if (head->precision != KH_F32 && (rc = launch_qact(ctx, b.h, n, e, b.qa))) return rc;
+    if ((rc = project(ctx, head, b.h, b.qa, n, nullptr, b.logits))) return rc;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(ARGMAX_BLOCKS, (unsigned)n), dim3(256), 0, ctx->stream, b.logits,
+                       (int)s.vocab, b.pv, b.pi);
+    KH_HIP(hipGetLastError());
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)n), dim3(256), 0, ctx->stream, b.logits, (int)s.vocab,
+                       b.pv, b.pi, b.next);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+// A cache of n_ctx positions per layer: a spare one if the session has it.
+int take_cache(kh_llm *m, std::vector<float *> &k, std::vector<float *> &v) {
+    if (!m->spare.empty()) {
+        k = std::move(m->spare.back().first);
+        v = std::move(m->spare.back().second);
+        m->spare.pop_back();
+        return KH_OK;
+    }
+    const size_t n = m->spec.n_ctx * m->spec.n_kv_head * m->spec.head_dim;
+    k.assign(m->spec.n_layer, nullptr);
+    v.assign(m->spec.n_layer, nullptr);
+    int rc = KH_OK;
+    for (size_t l = 0; l < m->spec.n_layer && !rc; l++)
+        if ((rc = dev_alloc(&k[l], n)) == KH_OK) rc = dev_alloc(&v[l], n);
+    if (rc) {
+        for (float *p : k)
+            if (p) (void)hipFree(p);
+        for (float *p : v)
+            if (p) (void)hipFree(p);
+        k.clear();
+        v.clear();
+    }
+    return rc;
+}
+
+// A cache no longer held: kept for the next park (a few), else freed.
+void drop_cache(kh_llm *m, std::vector<float *> &k, std::vector<float *> &v) {
+    if (m->spare.size() < 4) {
+        m->spare.emplace_back(std::move(k), std::move(v));
+    } else {
+        (void)hipStreamSynchronize(m->ctx->stream);
+        for (float *p : k) (void)hipFree(p);
+        for (float *p : v) (void)hipFree(p);
+    }
+    k.clear();
+    v.clear();
+}
+
+void drop_graph(kh_llm *m) {  // the captured step names the held cache
+    if (m->graph) {
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
 }
 
 }  // namespace
@@ -322,6 +555,12 @@ int kh_llm_free(kh_llm *m) {
         if (m->graph) (void)hipGraphExecDestroy(m->graph);
         for (auto p : m->kc) (void)hipFree(p);
         for (auto p : m->vc) (void)hipFree(p);
+        for (auto &c : m->spare) {
+            for (auto p : c.first) (void)hipFree(p);
+            for (auto p : c.second) (void)hipFree(p);
+        }
+        for (kh_llm_parked *p : m->parked) p->owner = nullptr;  // theirs now, freed with the handle
+        if (m->rows_buf) (void)hipFree(m->rows_buf);
         for (auto &L : m->layers)
             for (float *p : {L.attn_norm, L.mlp_norm, L.q_b, L.k_b, L.v_b, L.q_norm, L.k_norm})
                 if (p) (void)hipFree(p);
@@ -498,6 +737,122 @@ int kh_llm_generate_launch(kh_ctx *ctx, kh_llm *m, size_t n) {
     if (m->len + n > m->spec.n_ctx) return fail(KH_EINVAL, "kh_llm_generate_launch: the steps would overrun the context");
     for (size_t i = 0; i < n; i++) KH_HIP(hipGraphLaunch(m->graph, ctx->stream));
     m->len += n;
+    return KH_OK;
+}
+
+int kh_llm_park(kh_llm *m, kh_llm_parked **out) {
+    if (!m || !out) return fail(KH_EINVAL, "kh_llm_park: null argument");
+    *out = nullptr;
+    std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+    (void)hipSetDevice(m->ctx->device);
+    std::vector<float *> k, v;
+    int rc = take_cache(m, k, v);  // the empty one left in its place
+    if (rc) return rc;
+    std::unique_ptr<kh_llm_parked> p(new kh_llm_parked());
+    p->owner = m;
+    p->device = m->ctx->device;
+    p->k = std::move(m->kc);
+    p->v = std::move(m->vc);
+    p->len = m->len;
+    m->kc = std::move(k);
+    m->vc = std::move(v);
+    m->len = 0;
+    drop_graph(m);
+    const int32_t st[3] = {0, 0, 0};
+    KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, m->ctx->stream));
+    KH_HIP(hipStreamSynchronize(m->ctx->stream));
+    m->parked.insert(p.get());
+    *out = p.release();
+    return KH_OK;
+}
+
+int kh_llm_parked_free(kh_llm_parked *p) {
+    if (!p) return KH_OK;
+    if (kh_llm *m = p->owner) {
+        std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+        (void)hipSetDevice(m->ctx->device);
+        m->parked.erase(p);
+        drop_cache(m, p->k, p->v);
+    } else {  // the session is gone: the cache is this handle's alone
+        (void)hipSetDevice(p->device);
+        (void)hipDeviceSynchronize();
+        for (float *q : p->k) (void)hipFree(q);
+        for (float *q : p->v) (void)hipFree(q);
+    }
+    delete p;
+    return KH_OK;
+}
+
+int kh_llm_resume(kh_llm *m, kh_llm_parked *p) {
+    if (!m || !p) return fail(KH_EINVAL, "kh_llm_resume: null argument");
+    if (p->owner != m) {
+        kh_llm_parked_free(p);
+        return fail(KH_EINVAL, "kh_llm_resume: that cache was not this backend's");
+    }
+    std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+    (void)hipSetDevice(m->ctx->device);
+    KH_HIP(hipStreamSynchronize(m->ctx->stream));
+    m->parked.erase(p);
+    drop_cache(m, m->kc, m->vc);  // the conversation held until now is dropped
+    m->kc = std::move(p->k);
+    m->vc = std::move(p->v);
+    m->len = p->len;
+    delete p;
+    drop_graph(m);
+    const int32_t st[3] = {0, (int32_t)m->len, 0};
+    KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, m->ctx->stream));
+    KH_HIP(hipStreamSynchronize(m->ctx->stream));
+    return KH_OK;
+}
+
+int kh_llm_parked_len(const kh_llm_parked *p, size_t *len) {
+    if (!p || !len) return fail(KH_EINVAL, "kh_llm_parked_len: null argument");
+    *len = p->len;
+    return KH_OK;
+}
+
+int kh_llm_forward_each(kh_ctx *ctx, kh_llm *m, size_t n, const int32_t *tokens, kh_llm_parked *const *caches,
+                        float *logits, int32_t *next) {
+    if (!ctx || !m || m->ctx != ctx) return fail(KH_EINVAL, "kh_llm_forward_each: null argument or foreign context");
+    if (n == 0) return KH_OK;
+    if (!tokens || !caches) return fail(KH_EINVAL, "kh_llm_forward_each: null argument");
+    const kh_llm_spec &s = m->spec;
+    if (n > 65535) return fail(KH_EINVAL, "kh_llm_forward_each: at most 65535 conversations at once");
+    std::set<const kh_llm_parked *> seen;
+    for (size_t i = 0; i < n; i++) {
+        const kh_llm_parked *p = caches[i];
+        if (!p) return fail(KH_EINVAL, "kh_llm_forward_each: null cache");
+        if (p->owner != m) return fail(KH_EINVAL, "kh_llm_forward_each: that cache was not this backend's");
+        if (!seen.insert(p).second) return fail(KH_EINVAL, "kh_llm_forward_each: a conversation given twice");
+        if (tokens[i] < 0 || (size_t)tokens[i] >= s.vocab)
+            return fail(KH_EINVAL, "kh_llm_forward_each: token out of range");
+        if (p->len >= s.n_ctx) return fail(KH_EINVAL, "kh_llm_forward_each: a context window is full");
+    }
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = ready(m);
+    if (rc) return rc;
+    if ((rc = ensure_rows(m, n))) return rc;
+    const RowsBuf b = rows_layout(s, m->rows_cap, static_cast<char *>(m->rows_buf));
+    // the table: tokens, then per layer each row's cache and its length
+    // after this token (positions are fixed before anything is pushed,
+    // llama.rs:229-236)
+    const size_t tok_bytes = 4 * n, tab_bytes = sizeof(AttnRow) * n * s.n_layer;
+    m->rows_host.resize(tok_bytes + tab_bytes);
+    std::copy(tokens, tokens + n, reinterpret_cast<int32_t *>(m->rows_host.data()));
+    AttnRow *tab = reinterpret_cast<AttnRow *>(m->rows_host.data() + tok_bytes);
+    for (size_t l = 0; l < s.n_layer; l++)
+        for (size_t i = 0; i < n; i++) tab[l * n + i] = AttnRow{caches[i]->k[l], caches[i]->v[l], (int)caches[i]->len + 1};
+    KH_HIP(hipMemcpyAsync(b.tok, m->rows_host.data(), tok_bytes, hipMemcpyHostToDevice, ctx->stream));
+    KH_HIP(hipMemcpyAsync(b.tab, tab, tab_bytes, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = step_rows(ctx, m, n, b))) {
+        (void)hipStreamSynchronize(ctx->stream);
+        return rc;
+    }
+    if (logits) KH_HIP(hipMemcpyAsync(logits, b.logits, 4 * n * s.vocab, hipMemcpyDeviceToHost, ctx->stream));
+    if (next) KH_HIP(hipMemcpyAsync(next, b.next, 4 * n, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    for (size_t i = 0; i < n; i++) caches[i]->len += 1;  // Rows::advance (llama.rs:322-326)
     return KH_OK;
 }
 

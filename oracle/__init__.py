@@ -386,7 +386,8 @@ class Llm:
     """A Llama-family decoder on the CPU for one token at a time: the forward
     of crates/llm/src/model/llama.rs:224-289 (run_rows, m = 1) between the
     embedding and the head (llama.rs:384-415), every operator the oracle's.
-    Weights are q8 (scales, qs) pairs; norms and biases f32 arrays."""
+    Weights are q8 (scales, qs) pairs or 1-tuples (f32 data,) -- Precision::F32,
+    tensor::matvec_bt (tensor.rs:56-79); norms and biases f32 arrays."""
 
     def __init__(self, spec: dict, layers: list, embed, final_norm, lm_head=None, cos_t=None, sin_t=None):
         self.s, self.layers, self.embed, self.final_norm = spec, layers, embed, final_norm
@@ -402,13 +403,22 @@ class Llm:
         e, hd, nh, nkv, eps = s["n_embd"], s["head_dim"], s["n_head"], s["n_kv_head"], s["eps"]
         qd, kvd, half = nh * hd, nkv * hd, hd // 2
         pos = self.len
-        x = row_q8(*self.embed, e, token)                       # Weight::row, llama.rs:384-391
+
+        def mv(w, rows, cols, x, bias=None):
+            if len(w) == 1:
+                return matvec_f32(w[0], rows, cols, x, bias)
+            return matvec_q8(*w, rows, cols, x, bias)
+
+        if len(self.embed) == 1:                                # Weight::row, llama.rs:384-391
+            x = np.asarray(self.embed[0], np.float32).reshape(-1, e)[token].copy()
+        else:
+            x = row_q8(*self.embed, e, token)
         rope = rope_apply_interleaved if s.get("rope_interleaved") else rope_apply
         for l, L in enumerate(self.layers):
             h = rms_norm(x, L["attn_norm"], eps)
-            q = matvec_q8(*L["q"], qd, e, h, L.get("q_b"))
-            k = matvec_q8(*L["k"], kvd, e, h, L.get("k_b"))
-            v = matvec_q8(*L["v"], kvd, e, h, L.get("v_b"))
+            q = mv(L["q"], qd, e, h, L.get("q_b"))
+            k = mv(L["k"], kvd, e, h, L.get("k_b"))
+            v = mv(L["v"], kvd, e, h, L.get("v_b"))
             for head in range(nh):
                 seg = q[head * hd:(head + 1) * hd]
                 if L.get("q_norm") is not None:
@@ -421,13 +431,13 @@ class Llm:
                 k[head * hd:(head + 1) * hd] = rope(self.cos, self.sin, half, seg, pos)
             self.kc[l][pos], self.vc[l][pos] = k, v             # KvCache::push
             a = attend(nh, nkv, hd, q, self.kc[l][:pos + 1].ravel(), self.vc[l][:pos + 1].ravel(), pos + 1)
-            x = (x + matvec_q8(*L["o"], e, qd, a)).astype(np.float32)
+            x = (x + mv(L["o"], e, qd, a)).astype(np.float32)
             h = rms_norm(x, L["mlp_norm"], eps)
-            g = matvec_q8(*L["gate"], s["n_ff"], e, h)
-            u = matvec_q8(*L["up"], s["n_ff"], e, h)
-            x = (x + matvec_q8(*L["down"], e, s["n_ff"], swiglu(g, u))).astype(np.float32)
+            g = mv(L["gate"], s["n_ff"], e, h)
+            u = mv(L["up"], s["n_ff"], e, h)
+            x = (x + mv(L["down"], e, s["n_ff"], swiglu(g, u))).astype(np.float32)
         self.len += 1
-        return matvec_q8(*self.head, s["vocab"], e, rms_norm(x, self.final_norm, eps))
+        return mv(self.head, s["vocab"], e, rms_norm(x, self.final_norm, eps))
 
 
 def argmax(v) -> int:

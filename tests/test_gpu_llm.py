@@ -28,14 +28,17 @@ LOGIT_RTOL = 2e-3
 
 
 def build(ctx, seed, n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=64, n_ff=256, vocab=512, n_ctx=64,
-          bias=True, qk_norm=False, tied=True, interleaved=False, sd=0.02):
+          bias=True, qk_norm=False, tied=True, interleaved=False, sd=0.02, prec="q8"):
     spec = dict(n_layer=n_layer, n_embd=n_embd, n_head=n_head, n_kv_head=n_kv_head, head_dim=head_dim, n_ff=n_ff,
                 vocab=vocab, n_ctx=n_ctx, eps=1e-6, rope_interleaved=int(interleaved))
     rng = iter(range(seed, seed + 10000))
     qd, kvd = n_head * head_dim, n_kv_head * head_dim
 
-    def q8(rows, cols, scale=sd):
-        s, q = O.quantize_q8(O.normal(next(rng), rows * cols, scale), rows, cols)
+    def q8(rows, cols, scale=sd):  # f32 weights (Precision::F32) when prec == "f32"
+        data = O.normal(next(rng), rows * cols, scale)
+        if prec == "f32":
+            return (data,), K.Weight.from_f32(ctx, data.reshape(rows, cols))
+        s, q = O.quantize_q8(data, rows, cols)
         return (s, q), K.Weight.from_q8(ctx, rows, cols, s, q)
 
     def vec(n, base=1.0, scale=0.1):
@@ -81,11 +84,12 @@ def run_both(m, ref, tokens):
     return worst
 
 
-@pytest.mark.parametrize("variant", ["qwen2", "qwen3", "llama_interleaved"])
+@pytest.mark.parametrize("variant", ["qwen2", "qwen3", "llama_interleaved", "qwen2_f32"])
 def test_forward_matches_the_oracle(ctx, variant):
     kw = {"qwen2": dict(bias=True), "qwen3": dict(bias=False, qk_norm=True, tied=False),
           "llama_interleaved": dict(bias=False, interleaved=True, n_head=8, n_kv_head=2, head_dim=128,
-                                    n_embd=256)}[variant]
+                                    n_embd=256),
+          "qwen2_f32": dict(bias=True, tied=False, prec="f32")}[variant]
     say("llm forward", variant)
     m, mk = build(ctx, 100, **kw)
     ref = mk()
