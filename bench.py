@@ -612,8 +612,34 @@ def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256
            "launches_per_token": 24 * 7 + 4, "vs_reference_cpu_q8_112tps": round(tps / 112.0, 2),
            "vs_reference_metal_q8_191tps": round(tps / 191.0, 2), "first_tokens": [int(t) for t in first[:4]]}
     log(f"qwen0.5b q8 decode: {res}")
+    res["batched"] = decode_batched(torch, m, warm)
     m.free()
     return res
+
+
+def decode_batched(torch, m, warm, steps=20):
+    """Batched decode (Session::forward_each, mod.rs:1190-1202; llama.rs:418-434)
+    on the same session: B conversations of `warm` + b tokens each, parked,
+    then advanced together one token per call, greedy (each row's next token
+    fed back).  Each call is host to host: the tables up, one captured pass
+    for B rows, the next tokens back.  Timed over `steps` calls after one
+    untimed call (the capture) with the host clock."""
+    out = {}
+    for B in (2, 4, 8, 16, 32):
+        parked = []
+        for b in range(B):
+            m.generate(1 + b, warm + b)
+            parked.append(m.park())
+        _, toks = m.forward_each(np.arange(B, dtype=np.int32), parked, want_logits=False)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            _, toks = m.forward_each(toks, parked, want_logits=False)
+        s = (time.perf_counter() - t0) / steps
+        out[str(B)] = {"ms_per_step": round(s * 1e3, 4), "tok_per_s": round(B / s, 1)}
+        for p in parked:
+            p.free()
+    log(f"qwen0.5b q8 batched decode: {out}")
+    return out
 
 
 def cpu_baseline(layers, budget_s: float):

@@ -7,6 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdlib>
+#include <map>
 #include <mutex>
 #include <set>
 #include <string>
@@ -126,6 +127,7 @@ struct kh_llm {
     void *rows_buf = nullptr;
     size_t rows_cap = 0;
     std::vector<char> rows_host;
+    std::map<size_t, hipGraphExec_t> rows_graphs;            // the pass for n rows, captured once per n
 };
 
 // A conversation's cache set aside (Session::park, model/mod.rs:889-893): per

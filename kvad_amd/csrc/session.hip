@@ -375,10 +375,18 @@ RowsBuf rows_layout(const kh_llm_spec &s, size_t cap, char *base) {
     return b;
 }
 
+// The captured passes name the weights, the tables and the rows' buffers:
+// any change to those drops them.
+void drop_rows_graphs(kh_llm *m) {
+    for (auto &g : m->rows_graphs) (void)hipGraphExecDestroy(g.second);
+    m->rows_graphs.clear();
+}
+
 int ensure_rows(kh_llm *m, size_t n) {
     if (n <= m->rows_cap) return KH_OK;
     const size_t cap = (n + 7) / 8 * 8;
     KH_HIP(hipStreamSynchronize(m->ctx->stream));
+    drop_rows_graphs(m);
     if (m->rows_buf) (void)hipFree(m->rows_buf);
     m->rows_buf = nullptr;
     m->rows_cap = 0;
@@ -553,6 +561,7 @@ int kh_llm_free(kh_llm *m) {
         (void)hipSetDevice(m->ctx->device);
         (void)hipStreamSynchronize(m->ctx->stream);
         if (m->graph) (void)hipGraphExecDestroy(m->graph);
+        drop_rows_graphs(m);
         for (auto p : m->kc) (void)hipFree(p);
         for (auto p : m->vc) (void)hipFree(p);
         for (auto &c : m->spare) {
@@ -601,10 +610,8 @@ int kh_llm_set_layer(kh_llm *m, size_t l, const kh_weight *q, const kh_weight *k
         (rc = dev_vector(&L.v_b, v_b, kvd)) || (rc = dev_vector(&L.q_norm, q_norm, s.head_dim)) ||
         (rc = dev_vector(&L.k_norm, k_norm, s.head_dim)))
         return rc;
-    if (m->graph) {
-        (void)hipGraphExecDestroy(m->graph);
-        m->graph = nullptr;
-    }
+    drop_graph(m);
+    drop_rows_graphs(m);
     return KH_OK;
 }
 
@@ -622,10 +629,8 @@ int kh_llm_set_ends(kh_llm *m, const kh_weight *embed, const float *final_norm, 
     if (rc) return rc;
     m->embed = embed;
     m->head = lm_head;
-    if (m->graph) {
-        (void)hipGraphExecDestroy(m->graph);
-        m->graph = nullptr;
-    }
+    drop_graph(m);
+    drop_rows_graphs(m);
     return KH_OK;
 }
 
@@ -638,6 +643,8 @@ int kh_llm_set_rope(kh_llm *m, const float *cos_t, const float *sin_t, size_t ma
     if (m->rope_cos) (void)hipFree(m->rope_cos);
     if (m->rope_sin) (void)hipFree(m->rope_sin);
     m->rope_cos = m->rope_sin = nullptr;
+    drop_graph(m);  // the captured passes name the old tables
+    drop_rows_graphs(m);
     int rc;
     if ((rc = dev_vector(&m->rope_cos, cos_t, n)) || (rc = dev_vector(&m->rope_sin, sin_t, n))) return rc;
     return KH_OK;
@@ -843,12 +850,29 @@ int kh_llm_forward_each(kh_ctx *ctx, kh_llm *m, size_t n, const int32_t *tokens,
     AttnRow *tab = reinterpret_cast<AttnRow *>(m->rows_host.data() + tok_bytes);
     for (size_t l = 0; l < s.n_layer; l++)
         for (size_t i = 0; i < n; i++) tab[l * n + i] = AttnRow{caches[i]->k[l], caches[i]->v[l], (int)caches[i]->len + 1};
+    // the pass for n rows reads everything it varies on from the table, so
+    // it is captured once per n and replayed
+    auto it = m->rows_graphs.find(n);
+    if (it == m->rows_graphs.end()) {
+        KH_HIP(hipStreamSynchronize(ctx->stream));
+        hipGraph_t g = nullptr;
+        KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        rc = step_rows(ctx, m, n, b);
+        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+        hipGraphExec_t x = nullptr;
+        e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+        it = m->rows_graphs.emplace(n, x).first;
+    }
     KH_HIP(hipMemcpyAsync(b.tok, m->rows_host.data(), tok_bytes, hipMemcpyHostToDevice, ctx->stream));
     KH_HIP(hipMemcpyAsync(b.tab, tab, tab_bytes, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = step_rows(ctx, m, n, b))) {
-        (void)hipStreamSynchronize(ctx->stream);
-        return rc;
-    }
+    KH_HIP(hipGraphLaunch(it->second, ctx->stream));
     if (logits) KH_HIP(hipMemcpyAsync(logits, b.logits, 4 * n * s.vocab, hipMemcpyDeviceToHost, ctx->stream));
     if (next) KH_HIP(hipMemcpyAsync(next, b.next, 4 * n, hipMemcpyDeviceToHost, ctx->stream));
     KH_HIP(hipStreamSynchronize(ctx->stream));

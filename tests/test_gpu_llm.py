@@ -140,3 +140,16 @@ def test_a_full_context_is_an_error(ctx):
         m.forward(1)
     with pytest.raises(K.KvadError):
         m.generate(1, 1)
+
+
+def test_new_rope_tables_reach_the_captured_step(ctx):
+    # the captured step names the tables; replacing them drops it
+    say("llm set_rope after capture")
+    m1, _ = build(ctx, 600)
+    m1.generate(5, 3)
+    m1.truncate(0)
+    cos_t, sin_t = O.rope_tables(64, 64, 1e4)
+    m1.set_rope(cos_t, sin_t, 64)
+    m2, _ = build(ctx, 600)
+    m2.set_rope(cos_t, sin_t, 64)
+    np.testing.assert_array_equal(m1.generate(5, 6), m2.generate(5, 6))
