@@ -684,6 +684,9 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     const int ladder[3] = {64, 128, 256};
     int step = rungs - 1;
     while (step > 0 && (long long)((n_positions + ladder[step] - 1) / ladder[step]) * n_hg * nb < cu) step--;
+    const int forced = env_int("KVAD_ATTN_SPLIT", 0);  // tuning knob: positions per split
+    for (int i = 0; i < rungs; i++)
+        if (ladder[i] == forced) step = i;
     while (step < rungs - 1 && (n_positions + ladder[step] - 1) / ladder[step] > (size_t)MAX_SPLITS) step++;
     const int P = ladder[step];
     if ((n_positions + P - 1) / P > (size_t)MAX_SPLITS)

@@ -32,6 +32,12 @@ int hip_fail(hipError_t e, const char *what);
         if (e_ != hipSuccess) return ::kh::hip_fail(e_, #call); \
     } while (0)
 
+// A launch-shape tuning knob from the environment (dflt when unset).
+inline int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
 // ---- device workspace ---------------------------------------------------
 // One growable device buffer per context, carved into named regions per
 // call.  All work of a context runs on one stream, so reusing the same bytes

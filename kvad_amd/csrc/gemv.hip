@@ -847,11 +847,6 @@ struct Plan {
     int nwv;         // waves per workgroup
 };
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 // Launch shape from sweeps over Llama-3-8B and Qwen2.5-0.5B shapes with
 // weights far larger than the cache.  Q4_K: short steps pipeline best -- one
 // chunk per lane (two segments per 4096-wide row) and two rows per step, or
