@@ -321,6 +321,17 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
 
     const v16i zero = {};
     const v16f fzero = {};
+    // One tile pair's products are held while the next pair's are issued:
+    // the matrix core works on tile i while the VALU scales tile i - 1
+    // (otherwise every convert waits out its own MFMA).  The pair still
+    // pending at any block's end is (RT - 1, TT - 1).
+    v16i dq = {};
+    v16f pq = {};
+    bool pending = false;
+    auto scale_into = [&](v16f &c, const v16f &p, const v16i &d) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) c[v] = __builtin_fmaf(p[v], (float)d[v], c[v]);
+    };
     load_stage(0);
     for (int k0 = 0; k0 < K; k0 += BK) {
         __syncthreads();  // the previous stage's reads of LDS are done
@@ -328,35 +339,49 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
         __syncthreads();
         if (k0 + BK < K) load_stage(k0 + BK);  // in flight during this stage's MFMAs
         const int nblk = min(NBS, (K - k0) / BLOCK);
-#pragma unroll
-        for (int b = 0; b < NBS; b++) {
-            if (b >= nblk) break;
-            v4i af[RT], bf[TT];
+        // block b's fragments (and its scale columns) from LDS; the next
+        // block's are read while this one's products are scaled
+        v4i af[2][RT], bf[2][TT];
+        float wa[2][RT], xb[2][TT];
+        const bool lo = lane < 32;
+        auto frags = [&](int b, int f) {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
-                af[rt] = *reinterpret_cast<const v4i *>(sA + (wr0 + rt * 32 + (lane & 31)) * ASTR + b * 32 +
-                                                        16 * (lane >> 5));
+                af[f][rt] = *reinterpret_cast<const v4i *>(sA + (wr0 + rt * 32 + (lane & 31)) * ASTR + b * 32 +
+                                                           16 * (lane >> 5));
 #pragma unroll
             for (int tt = 0; tt < TT; tt++)
-                bf[tt] = *reinterpret_cast<const v4i *>(sB + (wm0 + tt * 32 + (lane & 31)) * ASTR + b * 32 +
-                                                        16 * (lane >> 5));
+                bf[f][tt] = *reinterpret_cast<const v4i *>(sB + (wm0 + tt * 32 + (lane & 31)) * ASTR + b * 32 +
+                                                           16 * (lane >> 5));
             // the block's scale products p[r][t] = ws[r] * xs[t] (quant.rs:903;
             // Q4_K: d*sc * xs) as an outer product on the matrix core: k-slot 0
             // holds the 32 rows' (tokens') scales, k-slot 1 zeros
-            const bool lo = lane < 32;
-            float wa[RT], xb[TT];
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) wa[rt] = lo ? sW[b][wr0 + rt * 32 + lane] : 0.0f;
+            for (int rt = 0; rt < RT; rt++) wa[f][rt] = lo ? sW[b][wr0 + rt * 32 + lane] : 0.0f;
 #pragma unroll
-            for (int tt = 0; tt < TT; tt++) xb[tt] = lo ? sX[b][wm0 + tt * 32 + lane] : 0.0f;
+            for (int tt = 0; tt < TT; tt++) xb[f][tt] = lo ? sX[b][wm0 + tt * 32 + lane] : 0.0f;
+        };
+        frags(0, 0);
+#pragma unroll
+        for (int b = 0; b < NBS; b++) {
+            if (b >= nblk) break;
+            const int f = b & 1;
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++) {
-                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[rt], bf[tt], zero, 0, 0, 0);
-                    const v16f p = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[rt], xb[tt], fzero, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 16; v++) acc[rt][tt][v] = __builtin_fmaf(p[v], (float)d[v], acc[rt][tt][v]);
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[f][rt], bf[f][tt], zero, 0, 0, 0);
+                    const v16f p = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[f][rt], xb[f][tt], fzero, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (rt == 0 && tt == 0 && b + 1 < NBS && b + 1 < nblk) frags(b + 1, f ^ 1);
+                    // the previous pair: (rt, tt - 1), (rt - 1, TT - 1), or the last block's last
+                    if (tt > 0) scale_into(acc[rt][tt - 1], pq, dq);
+                    else if (rt > 0) scale_into(acc[rt - 1][TT - 1], pq, dq);
+                    else if (pending) scale_into(acc[RT - 1][TT - 1], pq, dq);
+                    __builtin_amdgcn_sched_barrier(0);
+                    dq = d;
+                    pq = p;
+                    pending = true;
                 }
             if constexpr (PREC == KH_Q4K) {
                 // the minimum terms, sum_b dmin*m[r,b] * xs[t,b]*sum[t,b], are a
@@ -378,6 +403,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             }
         }
     }
+    if (pending) scale_into(acc[RT - 1][TT - 1], pq, dq);
     store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane);
 }
 
@@ -477,6 +503,8 @@ __global__ __launch_bounds__(THREADS) void gemm_f32_kernel(GemmArgs a) {
 enum Shape { T128x128, T128x64, T128x32 };
 
 Shape pick_shape(int M, int N, int cu) {
+    const int forced = env_int("KVAD_GEMM_TILE_M", 0);  // tuning knob: tokens per tile
+    if (forced == 128 || forced == 64 || forced == 32) return forced == 128 ? T128x128 : forced == 64 ? T128x64 : T128x32;
     const long long nt = (N + 127) / 128;
     if (nt * ((M + 127) / 128) >= cu) return T128x128;
     if (nt * ((M + 63) / 64) >= cu) return T128x64;
@@ -503,10 +531,20 @@ int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m) {
     return KH_OK;
 }
 
+// The f32 GEMM runs best on shorter token tiles than the int8 one (swept at
+// both prefill shapes): 64 tokens while that still gives two workgroups per
+// CU, else 32.
+Shape pick_shape_f32(int M, int N, int cu) {
+    const int forced = env_int("KVAD_GEMM_TILE_M", 0);
+    if (forced == 128 || forced == 64 || forced == 32) return forced == 128 ? T128x128 : forced == 64 ? T128x64 : T128x32;
+    const long long nt = (N + 127) / 128;
+    return nt * ((M + 63) / 64) >= 2LL * cu ? T128x64 : T128x32;
+}
+
 int launch_f32gemm(kh_ctx *ctx, const GemmArgs &a) {
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const unsigned gx = (unsigned)((a.N + 127) / 128);
-    switch (pick_shape(a.M, a.N, cu)) {
+    switch (pick_shape_f32(a.M, a.N, cu)) {
         case T128x128:
             hipLaunchKernelGGL((gemm_f32_kernel<2, 2, 2, 2>), dim3(gx, (a.M + 127) / 128), dim3(THREADS), 0,
                                ctx->stream, a);
