@@ -5,25 +5,23 @@
 // Reference: model::attend (crates/llm/src/model/mod.rs:769-819) with
 // tensor::dot (tensor.rs:220-235) and softmax_inplace (tensor.rs:297-308).
 // The reference walks every cached key once per query head; here a workgroup
-// owns one KV head's query heads (up to 8 of them) and a run of P positions,
+// owns one KV head's query heads (up to 16 of them) and a run of P positions,
 // and reads each key and value row once for the whole group -- the
 // restructuring the reference's notes ask for (docs/engine.md:783-791).
 //
 // Split kernel, workgroup (split j, head group): all its K and V rows are
-// loaded up front (16 lanes per row, 16 rows per pass); scores s = dot(q, k)
-// * scale; local max m_j, l_j = sum exp(s - m_j), acc_j = sum exp(s - m_j) v,
-// and the smallest score.  When one split covers the whole sequence it
+// loaded up front; scores s = dot(q, k) * scale; local max m_j,
+// l_j = sum exp(s - m_j), acc_j = sum exp(s - m_j) v, the smallest score,
+// and the scores themselves.  When one split covers the whole sequence it
 // finishes the job itself with the reference's exact weights
 // w = exp(s - M) * (1/S), dropping w < 1e-8 (mod.rs:807).
 //
 // Merge kernel, one workgroup per query head:
 //   M = max m_j,  S = sum l_j exp(m_j - M),  acc = sum exp(m_j - M) acc_j,
-// and out = acc * (1/S).  The reference's skip of weights below 1e-8 can
-// only bite in a split whose smallest score is below M + ln S + ln 1e-8
-// (checked with a margin); such a split's positions are scored again,
-// identically, and each skipped term w * v is taken back out.  Real scores
-// never qualify (it takes a gap of about 18 + ln S), so the fast path is the
-// whole cost; the slow path keeps the reference's weights when it does occur.
+// and out = acc * (1/S), less the terms the reference skips: splits whose
+// largest weight is under 1e-8 are left out, and in the splits that straddle
+// the threshold the stored scores name the skipped positions, whose
+// w * v are taken back out (merge_head).
 //
 // The two launches share nothing but the partials in device memory, so no
 // workgroup waits on another and no cross-XCD fence is needed.  Every sum has
@@ -39,46 +37,6 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
                                              (int)(bytes > 0xffffffffu ? 0xffffffffu : bytes), RSRC_WORD3);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dppf(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
-
-// Sum over each row of 16 lanes; all 16 get it, in a fixed order.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dppf<DPP_XOR1>(v);
-    v += dppf<DPP_XOR2>(v);
-    v += dppf<DPP_HALF_MIRROR>(v);
-    v += dppf<DPP_MIRROR>(v);
-    return v;
-}
-
-__device__ __forceinline__ float lane_read(float v, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dppf<DPP_XOR1>(v));
-    v = fmaxf(v, dppf<DPP_XOR2>(v));
-    v = fmaxf(v, dppf<DPP_HALF_MIRROR>(v));
-    v = fmaxf(v, dppf<DPP_MIRROR>(v));
-    return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
-}
-
-__device__ __forceinline__ float wave_min(float v) {
-    v = fminf(v, dppf<DPP_XOR1>(v));
-    v = fminf(v, dppf<DPP_XOR2>(v));
-    v = fminf(v, dppf<DPP_HALF_MIRROR>(v));
-    v = fminf(v, dppf<DPP_MIRROR>(v));
-    return fminf(fminf(lane_read(v, 0), lane_read(v, 16)), fminf(lane_read(v, 32), lane_read(v, 48)));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-    v = row16_sum(v);
-    return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
 }
 
 struct AttnArgs {
@@ -118,32 +76,6 @@ __device__ __forceinline__ void at_row(AttnArgs &a, int hd) {
     a.pm += o, a.pl += o, a.pmin += o, a.pacc += o, a.psc += o;
 }
 
-// One position's scores for the G heads from the 16-lane row's slices: the
-// same arithmetic wherever a score is needed.
-template <int GM, int DPL>
-__device__ __forceinline__ void score_row(const float (&qr)[GM][DPL], const float (&kv)[DPL], float scale, int G,
-                                          float (&s)[GM]) {
-#pragma unroll
-    for (int h = 0; h < GM; h++) {
-        float a = 0.0f;
-        if (h < G) {
-#pragma unroll
-            for (int d = 0; d < DPL; d++) a = fmaf(qr[h][d], kv[d], a);
-        }
-        a = row16_sum(a);
-        s[h] = a * scale;  // dot(q, k) * scale, mod.rs:802
-    }
-}
-
-template <int DPL>
-__device__ __forceinline__ void load_row(const rsrc_t &R, unsigned off, float (&r)[DPL]) {
-#pragma unroll
-    for (int d = 0; d < DPL; d += 4) {
-        const float4 f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(R, off, d * 4, 0));
-        r[d] = f.x, r[d + 1] = f.y, r[d + 2] = f.z, r[d + 3] = f.w;
-    }
-}
-
 // Sums (or maxima) over the wave's four rows of 16 lanes, by swapping
 // rows (v_permlane16_swap) and then halves (v_permlane32_swap) between two
 // copies of a value; every lane gets the total, in a fixed order.  Written
@@ -178,10 +110,11 @@ __device__ __forceinline__ float rows_min(float x) {
 // four waves owns one KV head's G <= 16 query heads and P = 64 R positions;
 // wave w takes R tiles of 16 consecutive positions.  Per tile:
 //   scores  S = K Q^T: A = 16 positions x 4 k-slots, B = 4 k-slots x 16
-//           heads; k-slot c of lane (c, i) covers the head dims
-//           [c HD/4, (c+1) HD/4), one product per dim, so lane (c, i) reads
-//           HD bytes of key row i contiguously; the 16 columns are the G
-//           query heads (the rest zero).
+//           heads; in product m (of HD/16) k-slot c of lane (c, i) takes
+//           the head dims 16m + 4c .. 16m + 4c + 3 (q dealt the same way),
+//           so one load instruction reads 64 contiguous bytes of each of
+//           the 16 key rows; the 16 columns are the G query heads (the rest
+//           zero).
 //   S lands as lane (c, j) holding positions 4c .. 4c+3 of head j: after
 //   exp, exactly the A operand of the value product for the four position
 //   groups r = 0..3 (position 4c + r in k-slot c).
@@ -198,8 +131,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 template <int HD, int R>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     at_row(a, HD);
-    constexpr int HQ = HD / 4;   // dims per k-slot of the score product
-    constexpr int NQ4 = HQ / 4;  // float4s per lane of a key row
+    constexpr int NQ4 = HD / 16;  // float4s per lane of a key row: products of 16 dims
     constexpr int VT = HD / 64;  // float4s per lane of a value row
     constexpr int NT = HD / 16;  // 16-column tiles of the output
     constexpr int P = 64 * R;
@@ -226,10 +158,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     const bool hv = j16 < G;
     f4v qb4[NQ4];
     {
-        const float *qh = a.q + (size_t)(h0 + (hv ? j16 : 0)) * HD + HQ * c4;
+        const float *qh = a.q + (size_t)(h0 + (hv ? j16 : 0)) * HD + 4 * c4;
 #pragma unroll
         for (int m = 0; m < NQ4; m++) {
-            const float4 f = *reinterpret_cast<const float4 *>(qh + 4 * m);
+            const float4 f = *reinterpret_cast<const float4 *>(qh + 16 * m);
             qb4[m] = hv ? f4v{f.x, f.y, f.z, f.w} : f4v{0.f, 0.f, 0.f, 0.f};
         }
     }
@@ -238,10 +170,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < R; u++) {
         const size_t t = (size_t)(t0 + pw + 16 * u + j16);
-        const unsigned off = (unsigned)((t * a.kstride + (size_t)kvh * HD + HQ * c4) * 4);
+        const unsigned off = (unsigned)((t * a.kstride + (size_t)kvh * HD + 4 * c4) * 4);
 #pragma unroll
         for (int m = 0; m < NQ4; m++)
-            kq[u][m] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(K, off, 16 * m, 0));
+            kq[u][m] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(K, off, 64 * m, 0));
     }
 #pragma unroll
     for (int u = 0; u < R; u++)
@@ -816,10 +748,11 @@ struct MlaArgs {
 };
 
 // Split kernel.  Wave w scores positions t0 + 16w .. +15 for the 16 heads:
-// S = K' Q'^T on v_mfma_f32_16x16x4_f32, the 576 key dims dealt to the four
-// k-slots in chunks of 16 (chunk 4k + c of k-step k to slot c: chunks 0-31
-// are c, 32-35 are pe, so each k-step reads one array).  Lane (c, i) holds
-// 144 dims of its row, all loads in flight at once; the queries sit in LDS.
+// S = K' Q'^T on v_mfma_f32_16x16x4_f32 over 36 products of 16 dims (32 of
+// c, 4 of pe, so each reads one array); in product 4k + i k-slot c takes
+// dims 64k + 16i + 4c .. + 3, so one load instruction reads 64 contiguous
+// bytes of each row.  Lane (c, j) holds 144 dims of its row, all loads in
+// flight at once; the queries sit in LDS, dealt the same way.
 // The workgroup takes one maximum per head, so every wave's exponentials
 // share it; the probabilities go to LDS and wave w then forms
 // O[heads][dims 128w .. 128w + 127] = P V over all 64 positions.
@@ -841,17 +774,18 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
     f4v kq[9][4];
     {
         const size_t pos = (size_t)(t0 + 16 * wave + j16);
+        // lane (c4, j16), load (k, i): dims 64 k + 16 i + 4 c4 .. + 3, so each
+        // load instruction reads 64 contiguous bytes of every row
+        const unsigned off = (unsigned)((pos * a.cstride + 4 * c4) * 4);
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const unsigned off = (unsigned)((pos * a.cstride + 16 * (4 * k + c4)) * 4);
+        for (int k = 0; k < 8; k++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                kq[k][i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 16 * i, 0));
-        }
-        const unsigned off = (unsigned)((pos * a.pestride + 16 * c4) * 4);
+                kq[k][i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 256 * k + 64 * i, 0));
+        const unsigned poff = (unsigned)((pos * a.pestride + 4 * c4) * 4);
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            kq[8][i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(PE, off, 16 * i, 0));
+            kq[8][i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(PE, poff, 64 * i, 0));
     }
     // the queries [q_lat | q_pe] of the group's heads, zero rows past H
     for (int i = tid; i < 16 * (MLA_K / 4); i += 256) {
@@ -871,7 +805,7 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
     for (int k = 0; k < 9; k++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const f4v q4 = *reinterpret_cast<const f4v *>(&sQ[j16 * MLA_QSTR + 16 * (4 * k + c4) + 4 * i]);
+            const f4v q4 = *reinterpret_cast<const f4v *>(&sQ[j16 * MLA_QSTR + 64 * k + 16 * i + 4 * c4]);
 #pragma unroll
             for (int e = 0; e < 4; e++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(kq[k][i][e], q4[e], d, 0, 0, 0);
         }
