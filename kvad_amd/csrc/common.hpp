@@ -201,11 +201,20 @@ int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs);
 // weights stream once for all of them.  x holds the rows' codes.
 constexpr int MULTI_TOKENS = 8;  // launch_matmul takes this path up to here
 int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, const float *bias, float *y);
+// The same for up to MULTI_JOBS weights of one precision and width over the
+// same rows of codes, in one launch: y[i] (+)= x W_i^T (+ bias[i]), adding
+// into y[i] where accumulate[i] is set (accumulate and bias may be null).
+constexpr int MULTI_JOBS = 3;
+int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,
+                           float *const *y, const int *accumulate, const QAct &x, size_t m);
 
 // Batched prefill y[m, rows] = xs[m, cols] W^T (+bias), m > 1 (device pointers).
-int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
-// The same over rows already quantised (QActBatch form), quantised weights only.
-int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, const float *bias, float *y);
+int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y,
+                  int accumulate = 0);
+// The same over rows already quantised (QActBatch form), quantised weights
+// only; with accumulate, y += the product.
+int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, const float *bias, float *y,
+                    int accumulate = 0);
 
 // GEMM over activations already quantised (QActBatch form), optionally
 // grouped by expert: with `tiles` set, workgroup row y of the grid takes tile
@@ -221,6 +230,7 @@ struct GemmArgs {
     const float *xf;        // f32 activations [M, K] (f32 GEMM)
     const float *bias;      // [N] or null
     float *y;               // [M, N]
+    int accumulate;         // y += x W^T (+ bias): the residual add
     int M, N, K;
     const int32_t *tiles;
     const int32_t *gather;
@@ -233,6 +243,10 @@ int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, 
 int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots);
 int matvec_many_device(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *const *x, float *const *y);
 int matmul_device(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y);
+// QActBatch::new of rms_norm(x) * w (gemv.hip): m rows of n values (n % 32 ==
+// 0), the normed rows also into h when h is set.
+int launch_norm_qact(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *h,
+                     const QAct &out);
 // QActBatch::new of swiglu(g, u) (gemv.hip): m rows of k values.
 int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, size_t k, const QAct &out);
 // Moe::run on device pointers, and Router::route alone (moe.hip).
@@ -281,8 +295,7 @@ int launch_dequant_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out);
 int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out);
 // tensor::rms_norm over m rows of n (glue.hip).
 int launch_rms_norm(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out);
-// x += y over n floats; gate = silu(gate) * up over n floats (glue.hip).
-int launch_add(kh_ctx *ctx, float *x, const float *y, size_t n);
+// gate = silu(gate) * up over n floats (glue.hip).
 int launch_swiglu(kh_ctx *ctx, float *gate, const float *up, size_t n);
 // Attention whose length is read from device memory: n_positions = *len_dev
 // (+1 when plus_one), at most max_positions; partials in `ws` (attend_ws_bytes).

@@ -97,11 +97,15 @@ __device__ __forceinline__ void store_tiles(const GemmArgs &a, const v16f (&acc)
                 }
                 float *dst = a.y + (size_t)tok * a.N + r;
                 if (vec && r + 3 < a.N) {
+                    if (a.accumulate) {  // x += proj (llama.rs:273-276)
+                        const float4 o = *reinterpret_cast<const float4 *>(dst);
+                        v[0] = o.x + v[0], v[1] = o.y + v[1], v[2] = o.z + v[2], v[3] = o.w + v[3];
+                    }
                     *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        if (r + e < a.N) dst[e] = v[e];
+                        if (r + e < a.N) dst[e] = a.accumulate ? dst[e] + v[e] : v[e];
                 }
             }
         }
@@ -564,7 +568,8 @@ int launch_f32gemm(kh_ctx *ctx, const GemmArgs &a) {
 
 // Row-at-a-time path for shapes the tiled kernels do not take (f32 weights
 // whose width is not a multiple of 4): one GEMV job per activation row.
-int matmul_rows(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
+int matmul_rows(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y,
+                int accumulate) {
     std::vector<GemvJob> jobs(m);
     for (size_t i = 0; i < m; i++) {
         GemvJob &j = jobs[i];
@@ -575,6 +580,7 @@ int matmul_rows(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, cons
         j.y = y + i * w->rows;
         j.rows = (int)w->rows;
         j.cols = (int)w->cols;
+        j.accumulate = accumulate;
     }
     return launch_gemv(ctx, w->precision, jobs.data(), (int)m);
 }
@@ -592,7 +598,8 @@ bool matmul_force_gemm() {
 }
 }  // namespace
 
-int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y) {
+int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y,
+                  int accumulate) {
     const size_t rows = w->rows, cols = w->cols;
     // 32-bit buffer offsets: the weights and activations (plus one tile of
     // overhang) must stay below 4 GiB
@@ -606,11 +613,12 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     a.ws = w->scales;
     a.bias = bias;
     a.y = y;
+    a.accumulate = accumulate;
     a.M = (int)m;
     a.N = (int)rows;
     a.K = (int)cols;
     if (w->precision == KH_F32) {
-        if (cols % 4) return matmul_rows(ctx, w, xs, m, bias, y);
+        if (cols % 4) return matmul_rows(ctx, w, xs, m, bias, y, accumulate);
         a.xf = xs;
         return launch_f32gemm(ctx, a);
     }
@@ -621,22 +629,25 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     char *p = static_cast<char *>(ctx->ws.ptr);
     QAct q{reinterpret_cast<int8_t *>(p), reinterpret_cast<float *>(p + qb), reinterpret_cast<int32_t *>(p + qb + sb)};
     if ((rc = launch_qact(ctx, xs, m, cols, q))) return rc;
-    return launch_matmul_q(ctx, w, q, m, bias, y);
+    return launch_matmul_q(ctx, w, q, m, bias, y, accumulate);
 }
 
-int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, const float *bias, float *y) {
+int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, const float *bias, float *y,
+                    int accumulate) {
     const size_t rows = w->rows, cols = w->cols;
     if (w->precision == KH_F32) return fail(KH_EINVAL, "matmul: f32 weights take f32 rows");
     if (rows * cols + 4 * 128 * cols >= 0xffffffffull || m * cols + 4 * 128 * cols >= 0xffffffffull ||
         rows > 0x7fffffff || m > 0x7fffffff)
         return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
     // a few tokens: stream the weights once through the multi-token GEMV
-    if (m <= (size_t)MULTI_TOKENS && !matmul_force_gemm()) return launch_gemv_multi(ctx, w, q, m, bias, y);
+    if (m <= (size_t)MULTI_TOKENS && !matmul_force_gemm())
+        return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, q, m);
     GemmArgs a{};
     a.w = w->qs;
     a.ws = w->scales;
     a.bias = bias;
     a.y = y;
+    a.accumulate = accumulate;
     a.M = (int)m;
     a.N = (int)rows;
     a.K = (int)cols;

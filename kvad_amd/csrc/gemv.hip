@@ -202,6 +202,54 @@ __global__ __launch_bounds__(256) void swiglu_qact_kernel(const float *__restric
     }
 }
 
+// QActBatch::new of rms_norm(x) * w (tensor.rs:329-333, quant.rs:693-714),
+// one workgroup per row of n floats (n % 32 == 0): the sum of squares over
+// the thread's float4s in index order, then over the wave, then over the
+// waves in order (as the GEMV's own staging of a normed input); h, when set,
+// receives the normed row in f32.
+__global__ __launch_bounds__(256) void norm_qact_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                       int n, float eps, float *__restrict__ h,
+                                                       int8_t *__restrict__ qs, float *__restrict__ scales,
+                                                       int32_t *__restrict__ sums) {
+    __shared__ float s_ss[4];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid >> 6;
+    const int n4 = n / 4, nb = n / BLOCK;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)row * n);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float ss = 0.0f;
+    for (int i = tid; i < n4; i += 256) {
+        const float4 v = xr[i];
+        const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+        ss = ss + ((a + b) + (c + d));
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) s_ss[wv] = ss;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) t = t + s_ss[i];
+    const float inv = 1.0f / sqrtf(t / (float)n + eps);
+    // eight lanes per 32-block; every lane runs quantize4 (it swaps across lanes)
+    for (int base = 0; base < n4; base += 256) {
+        const int i = base + tid;
+        const bool ok = i < n4;  // whole 8-lane groups: n4 % 8 == 0
+        float4 v = ok ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 g = ok ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v = make_float4((v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z, (v.w * inv) * g.w);
+        float scale;
+        int s;
+        const int packed = quantize4(v, &scale, &s);
+        if (ok) {
+            if (h) reinterpret_cast<float4 *>(h + (size_t)row * n)[i] = v;
+            reinterpret_cast<int *>(qs + (size_t)row * n)[i] = packed;
+            if ((tid & 7) == 0) {
+                scales[(size_t)row * nb + (i >> 3)] = scale;
+                sums[(size_t)row * nb + (i >> 3)] = s;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // the quantised GEMV kernel family
 // ---------------------------------------------------------------------------
@@ -655,15 +703,24 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(JobTable tab) {
 // ---------------------------------------------------------------------------
 
 
-struct MultiArgs {
+// Weights that read the same rows of codes (q/k/v, gate/up) in one launch:
+// the workgroups are dealt to the jobs in proportion to their rows.
+struct MultiJob {
     const void *w;
     const float *ws;
+    const float *bias;    // [rows] or null
+    float *y;             // [m][rows]
+    int rows;
+    int accumulate;       // y += x W^T (+ bias): the residual add
+    int wg0, nwaves;      // set by the launcher: the job's first workgroup, its waves
+};
+
+struct MultiArgs {
     const int8_t *xq;     // [m][cols] codes
     const float *xs;      // [m][cols / 32]
     const int32_t *xsum;  // [m][cols / 32]
-    const float *bias;    // [rows] or null
-    float *y;             // [m][rows]
-    int rows, cols, m, nwaves;
+    int cols, m, njobs;
+    MultiJob j[MULTI_JOBS];
 };
 
 // The chunks' contribution to each token's accumulator (one row per step).
@@ -774,11 +831,15 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rows = a.rows, cols = a.cols, nb = cols / BLOCK;
+    int ji = 0;
+    for (int i = 1; i < a.njobs; i++)
+        if ((int)blockIdx.x >= a.j[i].wg0) ji = i;
+    const MultiJob &job = a.j[ji];
+    const int rows = job.rows, cols = a.cols, nb = cols / BLOCK;
     const int C = chunks_per_row(PREC, cols);
     const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
     const int PB = padded_blocks(PREC, C, CPL);
-    const int nw = a.nwaves, lw = blockIdx.x * WPB + wv;
+    const int nw = job.nwaves, lw = ((int)blockIdx.x - job.wg0) * WPB + wv;
     const int my_rows = lw < rows ? (rows - lw + nw - 1) / nw : 0;
     const int steps = my_rows * nseg;
 
@@ -806,8 +867,8 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
     const size_t wbytes = PREC == KH_Q8 ? (size_t)rows * cols
                           : PREC == KH_Q4 ? (size_t)rows * cols / 2
                                           : (size_t)rows * (cols / QK_K) * Q4K_BYTES;
-    const rsrc_t W = rsrc(a.w, wbytes);
-    const rsrc_t WS = rsrc(a.ws, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
+    const rsrc_t W = rsrc(job.w, wbytes);
+    const rsrc_t WS = rsrc(job.ws, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
     auto load_step = [&](Chunks<PREC, CPL, 1> &c, int s) {
         __builtin_amdgcn_sched_barrier(0);
         load_chunks<PREC, CPL, 1>(c, W, WS, lw + (s / nseg) * nw, cols, nb, s % nseg, lane);
@@ -824,11 +885,15 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
         const int r = lw + (step / nseg) * nw, seg = step % nseg;
         compute_multi<PREC, CPL, T>(c, acc, sq, ssc, ssum, PB, seg, lane);
         if (seg == nseg - 1) {
-            const float b = a.bias && r < rows ? ((const_f32 *)a.bias)[r] : 0.0f;
+            const float b = job.bias && r < rows ? ((const_f32 *)job.bias)[r] : 0.0f;
 #pragma unroll
             for (int k = 0; k < T; k++) {
                 const float v = wave_sum(acc[k]);
-                if (lane == 0 && r < rows && k < a.m) a.y[(size_t)k * rows + r] = a.bias ? v + b : v;
+                if (lane == 0 && r < rows && k < a.m) {
+                    float *dst = job.y + (size_t)k * rows + r;
+                    const float o = job.bias ? v + b : v;
+                    *dst = job.accumulate ? *dst + o : o;  // x += proj (llama.rs:273-276)
+                }
                 acc[k] = 0.0f;
             }
         }
@@ -1045,6 +1110,16 @@ int launch_qact(kh_ctx *ctx, const float *x, size_t m, size_t k, const QAct &out
     return KH_OK;
 }
 
+int launch_norm_qact(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *h,
+                     const QAct &out) {
+    if (m == 0 || n == 0) return KH_OK;
+    if (n % BLOCK || n > 0x7fffffff || m > 0x7fffffff) return fail(KH_EINVAL, "norm_qact: n must be a multiple of 32");
+    hipLaunchKernelGGL(norm_qact_kernel, dim3((unsigned)m), dim3(256), 0, ctx->stream, x, w, (int)n, eps, h, out.qs,
+                       out.scales, out.sums);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
 int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, size_t k, const QAct &out) {
     size_t nblocks = m * k / BLOCK;
     if (nblocks == 0) return KH_OK;
@@ -1072,9 +1147,19 @@ int launch_multi_p(kh_ctx *ctx, MultiArgs a) {
     const int C = chunks_per_row(PREC, a.cols);
     const int cpl = C <= 2 * WAVE ? 1 : 2;  // short steps: a row in segments of one or two chunks per lane
     const int PB = padded_blocks(PREC, C, cpl);
-    int nwg = (a.rows + WPB - 1) / WPB;
-    if (nwg > 2 * cu) nwg = 2 * cu;
-    a.nwaves = nwg * WPB;
+    long long rows_total = 0;
+    for (int i = 0; i < a.njobs; i++) rows_total += a.j[i].rows;
+    int want = (int)((rows_total + WPB - 1) / WPB);
+    if (want > 2 * cu) want = 2 * cu;
+    // each job at least one workgroup, the rest in proportion to its rows
+    int nwg = 0;
+    for (int i = 0; i < a.njobs; i++) {
+        int g = (int)((long long)want * a.j[i].rows / rows_total);
+        if (g < 1) g = 1;
+        a.j[i].wg0 = nwg;
+        a.j[i].nwaves = g * WPB;
+        nwg += g;
+    }
     // token slots: the smallest of 2, 4, 8 that holds m, in as many launches
     // as the LDS stage needs (each launch streams the weights once)
     for (int t0 = 0; t0 < a.m;) {
@@ -1086,7 +1171,7 @@ int launch_multi_p(kh_ctx *ctx, MultiArgs a) {
         b.xq = a.xq + (size_t)t0 * a.cols;
         b.xs = a.xs + (size_t)t0 * (a.cols / BLOCK);
         b.xsum = a.xsum + (size_t)t0 * (a.cols / BLOCK);
-        b.y = a.y + (size_t)t0 * a.rows;
+        for (int i = 0; i < a.njobs; i++) b.j[i].y = a.j[i].y + (size_t)t0 * a.j[i].rows;
         const size_t lds = (size_t)T * PB * 40;
         int rc = T == 2 ? launch_multi_t<PREC, 2>(ctx, b, cpl, nwg, lds)
                  : T == 4 ? launch_multi_t<PREC, 4>(ctx, b, cpl, nwg, lds)
@@ -1136,27 +1221,39 @@ int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
     return KH_OK;
 }
 
-int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, const float *bias, float *y) {
+int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,
+                           float *const *y, const int *accumulate, const QAct &x, size_t m) {
     if (m == 0) return KH_OK;
-    if ((size_t)w->rows * w->cols >= 0xfff00000ull || m * w->cols >= 0xfff00000ull)
-        return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
+    if (njobs < 1 || njobs > MULTI_JOBS) return fail(KH_EINVAL, "matmul: one to three weights per launch");
     MultiArgs a{};
-    a.w = w->qs;
-    a.ws = w->scales;
     a.xq = x.qs;
     a.xs = x.scales;
     a.xsum = x.sums;
-    a.bias = bias;
-    a.y = y;
-    a.rows = (int)w->rows;
-    a.cols = (int)w->cols;
+    a.cols = (int)w[0]->cols;
     a.m = (int)m;
-    switch (w->precision) {
+    a.njobs = njobs;
+    for (int i = 0; i < njobs; i++) {
+        if (w[i]->precision != w[0]->precision || w[i]->cols != w[0]->cols)
+            return fail(KH_EINVAL, "matmul: weights of one launch share precision and width");
+        if ((size_t)w[i]->rows * w[i]->cols >= 0xfff00000ull || m * w[i]->cols >= 0xfff00000ull)
+            return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
+        a.j[i].w = w[i]->qs;
+        a.j[i].ws = w[i]->scales;
+        a.j[i].bias = bias ? bias[i] : nullptr;
+        a.j[i].y = y[i];
+        a.j[i].rows = (int)w[i]->rows;
+        a.j[i].accumulate = accumulate ? accumulate[i] : 0;
+    }
+    switch (w[0]->precision) {
         case KH_Q8: return launch_multi_p<KH_Q8>(ctx, a);
         case KH_Q4: return launch_multi_p<KH_Q4>(ctx, a);
         case KH_Q4K: return launch_multi_p<KH_Q4K>(ctx, a);
         default: return fail(KH_EINVAL, "matmul: the multi-token GEMV takes quantised weights");
     }
+}
+
+int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, const float *bias, float *y) {
+    return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, nullptr, x, m);
 }
 
 size_t fuse_max_cols(int precision) {

@@ -86,12 +86,6 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float *gate, const float *u
     gate[i] = silu * up[i];
 }
 
-// The residual add, x[i] = x[i] + y[i] (llama.rs:273-275, :283-285).
-__global__ __launch_bounds__(256) void add_kernel(float *x, const float *y, size_t n) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) x[i] = x[i] + y[i];
-}
-
 // One row per workgroup: max, exp(x - max), sum, times 1/sum.
 __global__ __launch_bounds__(256) void softmax_kernel(float *x, int n) {
     __shared__ float s_red[256];
@@ -110,13 +104,6 @@ __global__ __launch_bounds__(256) void softmax_kernel(float *x, int n) {
 }
 
 }  // namespace
-
-int launch_add(kh_ctx *ctx, float *x, const float *y, size_t n) {
-    if (n == 0) return KH_OK;
-    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, x, y, n);
-    KH_HIP(hipGetLastError());
-    return KH_OK;
-}
 
 int launch_swiglu(kh_ctx *ctx, float *gate, const float *up, size_t n) {
     if (n == 0) return KH_OK;

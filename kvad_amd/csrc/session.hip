@@ -332,7 +332,7 @@ int check_weight_shape(const kh_weight *w, size_t rows, size_t cols, const char 
 // The rows' buffers, carved from one allocation for `cap` rows (base null:
 // sizes only).  QActBatch codes take the widest activation of a block.
 struct RowsBuf {
-    float *x, *h, *q, *k, *v, *att, *tmp, *g, *u, *logits, *pv;
+    float *x, *h, *q, *k, *v, *att, *g, *u, *logits, *pv;
     int *pi;
     int32_t *tok, *next;
     AttnRow *tab;  // [n_layer][n]: each row's cache and length
@@ -353,7 +353,6 @@ RowsBuf rows_layout(const kh_llm_spec &s, size_t cap, char *base) {
     RowsBuf b{};
     b.x = reinterpret_cast<float *>(take(4 * cap * e));
     b.h = reinterpret_cast<float *>(take(4 * cap * e));
-    b.tmp = reinterpret_cast<float *>(take(4 * cap * e));
     b.q = reinterpret_cast<float *>(take(4 * cap * qd));
     b.att = reinterpret_cast<float *>(take(4 * cap * qd));
     b.k = reinterpret_cast<float *>(take(4 * cap * kvd));
@@ -395,17 +394,51 @@ int ensure_rows(kh_llm *m, size_t n) {
     return KH_OK;
 }
 
-// y[n][rows] = xs W^T (+bias): f32 weights on the f32 GEMM, quantised ones
-// from the rows' codes in qa (matmul_bt, quant.rs:751; tensor.rs:102).
-int project(kh_ctx *ctx, const kh_weight *w, const float *xs, const QAct &qa, size_t n, const float *bias, float *y) {
-    if (w->precision == KH_F32) return launch_matmul(ctx, w, xs, n, bias, y);
-    return launch_matmul_q(ctx, w, qa, n, bias, y);
+// y[n][rows] (+)= xs W^T (+bias): f32 weights on the f32 GEMM, quantised
+// ones from the rows' codes in qa (matmul_bt, quant.rs:751; tensor.rs:102);
+// with accumulate the product is added into y (the residual add).
+// Rows up to this many take the multi-token GEMV, eight rows a launch (the
+// weights stream once per launch): at decode's small matrices that beats a
+// GEMM whose 128-row tiles leave most CUs idle.
+size_t rows_multi_max() {
+    static const size_t v = (size_t)env_int("KVAD_ROWS_MULTI", 32);  // tuning knob
+    return v;
 }
 
-bool any_quantised(std::initializer_list<const kh_weight *> ws) {
+int project(kh_ctx *ctx, const kh_weight *w, const float *xs, const QAct &qa, size_t n, const float *bias, float *y,
+            int accumulate = 0) {
+    if (w->precision == KH_F32) return launch_matmul(ctx, w, xs, n, bias, y, accumulate);
+    if (n <= rows_multi_max()) return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, qa, n);
+    return launch_matmul_q(ctx, w, qa, n, bias, y, accumulate);
+}
+
+bool any_f32(std::initializer_list<const kh_weight *> ws) {
     for (auto w : ws)
-        if (w->precision != KH_F32) return true;
+        if (w->precision == KH_F32) return true;
     return false;
+}
+
+// Projections of the same input: one multi-token launch when they are all
+// quantised alike and the rows are few, else one projection at a time.
+int project_all(kh_ctx *ctx, int k, const kh_weight *const *w, const float *xs, const QAct &qa, size_t n,
+                const float *const *bias, float *const *y) {
+    bool one = n <= rows_multi_max();
+    for (int i = 0; i < k; i++)
+        one = one && w[i]->precision != KH_F32 && w[i]->precision == w[0]->precision && w[i]->cols == w[0]->cols;
+    if (one) return launch_gemv_multi_jobs(ctx, k, w, bias, y, nullptr, qa, n);
+    for (int i = 0; i < k; i++) {
+        int rc = project(ctx, w[i], xs, qa, n, bias[i], y[i]);
+        if (rc) return rc;
+    }
+    return KH_OK;
+}
+
+// rms_norm of the n rows, quantised for the projections that read it (and in
+// f32 into h for the f32 ones).
+int norm_rows(kh_ctx *ctx, const float *x, const float *w, size_t n, size_t e, float eps, bool need_f32, float *h,
+              const QAct &qa) {
+    if (e % BLOCK) return launch_rms_norm(ctx, x, w, n, e, eps, h);  // only f32 weights take such rows
+    return launch_norm_qact(ctx, x, w, n, e, eps, need_f32 ? h : nullptr, qa);
 }
 
 // run_rows (llama.rs:224-289) with Rows::Each, then the head over every row
@@ -420,11 +453,13 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
     for (size_t l = 0; l < s.n_layer; l++) {
         const kh_llm::Layer &L = m->layers[l];
         // ---- attention sub-block (llama.rs:241-275)
-        if ((rc = launch_rms_norm(ctx, b.x, L.attn_norm, n, e, s.eps, b.h))) return rc;
-        if (any_quantised({L.q, L.k, L.v}) && (rc = launch_qact(ctx, b.h, n, e, b.qa))) return rc;
-        if ((rc = project(ctx, L.q, b.h, b.qa, n, L.q_b, b.q)) || (rc = project(ctx, L.k, b.h, b.qa, n, L.k_b, b.k)) ||
-            (rc = project(ctx, L.v, b.h, b.qa, n, L.v_b, b.v)))
-            return rc;
+        if ((rc = norm_rows(ctx, b.x, L.attn_norm, n, e, s.eps, any_f32({L.q, L.k, L.v}), b.h, b.qa))) return rc;
+        {
+            const kh_weight *w[3] = {L.q, L.k, L.v};
+            const float *bias[3] = {L.q_b, L.k_b, L.v_b};
+            float *y[3] = {b.q, b.k, b.v};
+            if ((rc = project_all(ctx, 3, w, b.h, b.qa, n, bias, y))) return rc;
+        }
         const AttnRow *tab = b.tab + l * n;
         hipLaunchKernelGGL(rope_push_rows_kernel, dim3((unsigned)(s.n_head + s.n_kv_head + 1), (unsigned)n), dim3(128),
                            0, ctx->stream, b.q, b.k, b.v, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim,
@@ -434,26 +469,25 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
                                      kvd, s.n_ctx, b.att, b.ws, b.ws_bytes)))
             return rc;
         if (L.o->precision != KH_F32 && (rc = launch_qact(ctx, b.att, n, qd, b.qa))) return rc;
-        if ((rc = project(ctx, L.o, b.att, b.qa, n, nullptr, b.tmp)) || (rc = launch_add(ctx, b.x, b.tmp, n * e)))
-            return rc;
+        if ((rc = project(ctx, L.o, b.att, b.qa, n, nullptr, b.x, 1))) return rc;  // x += o(attn)
         // ---- MLP sub-block (llama.rs:277-285, Ffn::run ffn.rs:370-375)
-        if ((rc = launch_rms_norm(ctx, b.x, L.mlp_norm, n, e, s.eps, b.h))) return rc;
-        if (any_quantised({L.gate, L.up}) && (rc = launch_qact(ctx, b.h, n, e, b.qa))) return rc;
-        if ((rc = project(ctx, L.gate, b.h, b.qa, n, nullptr, b.g)) ||
-            (rc = project(ctx, L.up, b.h, b.qa, n, nullptr, b.u)))
-            return rc;
+        if ((rc = norm_rows(ctx, b.x, L.mlp_norm, n, e, s.eps, any_f32({L.gate, L.up}), b.h, b.qa))) return rc;
+        {
+            const kh_weight *w[2] = {L.gate, L.up};
+            const float *bias[2] = {nullptr, nullptr};
+            float *y[2] = {b.g, b.u};
+            if ((rc = project_all(ctx, 2, w, b.h, b.qa, n, bias, y))) return rc;
+        }
         if (L.down->precision != KH_F32) {  // QActBatch::new of swiglu(gate, up), then down
             if ((rc = launch_swiglu_qact(ctx, b.g, b.u, n, s.n_ff, b.qa))) return rc;
         } else if ((rc = launch_swiglu(ctx, b.g, b.u, n * s.n_ff))) {
             return rc;
         }
-        if ((rc = project(ctx, L.down, b.g, b.qa, n, nullptr, b.tmp)) || (rc = launch_add(ctx, b.x, b.tmp, n * e)))
-            return rc;
+        if ((rc = project(ctx, L.down, b.g, b.qa, n, nullptr, b.x, 1))) return rc;  // x += mlp
     }
     // ---- head over every row (llama.rs:412-415), then each row's argmax
     const kh_weight *head = m->head ? m->head : m->embed;
-    if ((rc = launch_rms_norm(ctx, b.x, m->final_norm, n, e, s.eps, b.h))) return rc;
-    if (head->precision != KH_F32 && (rc = launch_qact(ctx, b.h, n, e, b.qa))) return rc;
+    if ((rc = norm_rows(ctx, b.x, m->final_norm, n, e, s.eps, head->precision == KH_F32, b.h, b.qa))) return rc;
     if ((rc = project(ctx, head, b.h, b.qa, n, nullptr, b.logits))) return rc;
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(ARGMAX_BLOCKS, (unsigned)n), dim3(256), 0, ctx->stream, b.logits,
                        (int)s.vocab, b.pv, b.pi);

@@ -137,9 +137,10 @@ def test_a_batch_of_one_is_a_token_and_a_batch_of_none_is_nothing(ctx):
     assert got.shape == (0, m.spec.vocab) and nxt.size == 0
 
 
-@pytest.mark.parametrize("n", [8, 13])
+@pytest.mark.parametrize("n", [8, 13, 40])
 def test_many_rows_on_the_multi_token_gemv_and_the_gemm(ctx, n):
-    # 8 rows: one multi-token GEMV launch per projection; 13: the int8 GEMM
+    # 8 rows: one multi-token GEMV launch per projection group; 13: two
+    # launches of up to eight rows; 40: the int8 GEMM, residual added in its epilogue
     say("forward_each rows", n)
     m, mk = build(ctx, 740 + n)
     prompts = [[(7 * i + j) % 500 for j in range(1 + (5 * i) % 11)] for i in range(n)]
