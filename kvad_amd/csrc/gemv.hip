@@ -124,6 +124,19 @@ __device__ __forceinline__ float swiglu1(float g, float u) {
     return silu * u;
 }
 
+// The 6-bit scale and minimum of Q4_K sub-block j (mpp.rs:276-282) from
+// bytes 4..15 of the block header (h.y, h.z, h.w), without a branch: j is
+// fixed per lane, so sh = 8 (j & 3) and hij = (j >= 4 ? ~0 : 0) are lane
+// constants.  For j < 4 this is A & 63 and B & 63; for j >= 4, the low four
+// bits from byte 8 + j and the top two from bytes j and 4 + j.
+__device__ __forceinline__ void q4k_scale_min(const int4 &h, int sh, unsigned hij, unsigned &sc, unsigned &mn) {
+    const unsigned A = (unsigned)h.y >> sh, B = (unsigned)h.z >> sh, Cw = (unsigned)h.w >> sh;
+    const unsigned s2 = hij & 2u;
+    const unsigned X = A ^ ((A ^ Cw) & hij), Y = B ^ ((B ^ (Cw >> 4)) & hij);
+    sc = (X & 0xfu) | ((A >> s2) & 0x30u);
+    mn = (Y & 0xfu) | ((B >> s2) & 0x30u);
+}
+
 // ---------------------------------------------------------------------------
 // activation quantisation: 8 lanes per 32-block, 4 values each
 // ---------------------------------------------------------------------------
@@ -364,6 +377,7 @@ __device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, fl
         // Q4_K: the sub-block a lane finishes is fixed by the lane (64 % 8 == 0)
         const int half = lane & 1, cc = (lane & 7) >> 1, j = 2 * cc + half;
         const int sh = 8 * (j & 3);
+        const unsigned hij = j >= 4 ? ~0u : 0u;
 #pragma unroll
         for (int t = 0; t < CPL; t++) {
             const int g = gl + t * WAVE;
@@ -386,12 +400,10 @@ __device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, fl
                 lo += dpp<DPP_XOR1>(lo);
                 hi += dpp<DPP_XOR1>(hi);
                 const int d = half ? hi : lo;
-                // 6-bit scale and minimum of sub-block j (mpp.rs:276-282);
-                // bytes 4..15 of the block are h.y, h.z, h.w
+                // 6-bit scale and minimum of sub-block j (mpp.rs:276-282)
                 const int4 h = c.h[i][t];
-                const unsigned A = (unsigned)h.y >> sh, B = (unsigned)h.z >> sh, Cw = (unsigned)h.w >> sh;
-                const unsigned sc = j < 4 ? (A & 63) : ((Cw & 0xf) | ((A >> 2) & 0x30));
-                const unsigned mn = j < 4 ? (B & 63) : (((Cw >> 4) & 0xf) | ((B >> 2) & 0x30));
+                unsigned sc, mn;
+                q4k_scale_min(h, sh, hij, sc, mn);
                 const float dl = half_bits_to_float((unsigned)h.x) * (float)sc;
                 const float ml = half_bits_to_float((unsigned)h.x >> 16) * (float)mn;
                 float t1 = dl * (float)d;
@@ -779,6 +791,7 @@ __device__ __forceinline__ void compute_multi(const Chunks<PREC, CPL, 1> &c, flo
     } else {
         const int half = lane & 1, cc = (lane & 7) >> 1, j = 2 * cc + half;
         const int sh = 8 * (j & 3);
+        const unsigned hij = j >= 4 ? ~0u : 0u;
 #pragma unroll
         for (int t = 0; t < CPL; t++) {
             const int g = gl + t * WAVE;
@@ -788,9 +801,8 @@ __device__ __forceinline__ void compute_multi(const Chunks<PREC, CPL, 1> &c, flo
             const int4 hi4 = {(q.x >> 4) & 0x0f0f0f0f, (q.y >> 4) & 0x0f0f0f0f, (q.z >> 4) & 0x0f0f0f0f,
                               (q.w >> 4) & 0x0f0f0f0f};
             const int4 h = c.h[0][t];
-            const unsigned A = (unsigned)h.y >> sh, B = (unsigned)h.z >> sh, Cw = (unsigned)h.w >> sh;
-            const unsigned scb = j < 4 ? (A & 63) : ((Cw & 0xf) | ((A >> 2) & 0x30));
-            const unsigned mnb = j < 4 ? (B & 63) : (((Cw >> 4) & 0xf) | ((B >> 2) & 0x30));
+            unsigned scb, mnb;
+            q4k_scale_min(h, sh, hij, scb, mnb);
             const float dl = half_bits_to_float((unsigned)h.x) * (float)scb;
             const float ml = half_bits_to_float((unsigned)h.x >> 16) * (float)mnb;
 #pragma unroll

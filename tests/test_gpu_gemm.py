@@ -158,3 +158,27 @@ def test_llama_prefill_shape_on_a_sampled_grid(ctx, prec):
         sub = oracle_matmul("f32", (wf.reshape(rows, cols)[r_idx].ravel(),), nr, cols, sub_x, len(t_idx))
     close(got[np.ix_(t_idx, r_idx)], sub.reshape(len(t_idx), nr))
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("m", [2, 16])
+def test_two_by_two_known_answer(ctx, m):
+    # The reference's SMMLA known answer (simd.rs:236-261): A0 = 1..8,
+    # A1 = ones, B0 = ones, B1 = 0,...,0,10 gives [A0.B0, A0.B1, A1.B0, A1.B1]
+    # = [36, 80, 8, 10].  Here through matmul_bt: weight codes as given with
+    # scale 1, activations whose block maximum is 127 (column 31, where the
+    # weights are 0) so their codes are the values themselves and their scale
+    # is 1.  m = 2 runs the multi-token GEMV, m = 16 the MFMA GEMM (rows
+    # repeated); the products sit in y[token][row].
+    say("matmul 2x2 known answer", m)
+    a = np.zeros((2, 32), np.int8)
+    a[0, :8] = np.arange(1, 9)
+    a[1, :8] = 1
+    w = K.Weight.from_q8(ctx, 2, 32, np.ones(2, np.float32), a.ravel())
+    x = np.zeros((2, 32), np.float32)
+    x[0, :8] = 1.0
+    x[1, 7] = 10.0
+    x[:, 31] = 127.0
+    xs = np.tile(x, (m // 2, 1))
+    y = w.matmul_bt(xs.ravel(), m).reshape(m, 2)
+    want = np.tile(np.array([[36.0, 8.0], [80.0, 10.0]], np.float32), (m // 2, 1))
+    np.testing.assert_array_equal(y, want)
