@@ -36,7 +36,7 @@ __device__ __forceinline__ int total_key(float f) {
 // sums them; the top-k picks the largest choice, the lowest index on ties.
 __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
     const int tok = blockIdx.x, lane = threadIdx.x, n = r.n;
-    __shared__ float s_score[MAX_EXPERTS], s_choice[MAX_EXPERTS];
+    __shared__ __align__(16) float s_score[MAX_EXPERTS], s_choice[MAX_EXPERTS];  // padded to n16
     __shared__ float s_inv;
     __shared__ int s_order[MAX_GROUPS];
     __shared__ float s_str[MAX_GROUPS];
@@ -44,16 +44,33 @@ __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
     __shared__ float s_pick_w[MAX_TOPK];
     __shared__ int s_best;
     const float *lg = r.logits + (size_t)tok * n;
+    // Serial loops over the experts read 16 values at a time (four 16-byte
+    // LDS reads in flight) and then use them in index order: one LDS round
+    // trip per 16 experts rather than per expert.  Padding past n reads as
+    // 0 (adding 0.0f to a positive sum is exact) or -inf (never a choice).
+    const int n16 = (n + 15) & ~15;
+    auto batch = [&](const float *a, int i0, float (&v)[16]) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = reinterpret_cast<const float4 *>(a + i0)[q];
+            v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+        }
+    };
 
     if (r.scoring == 0) {  // softmax_inplace (tensor.rs:297-308)
         float mx = -INFINITY;
         for (int i = lane; i < n; i += 64) mx = fmaxf(mx, lg[i]);
         for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        for (int i = lane; i < n; i += 64) s_score[i] = expf(lg[i] - mx);
+        for (int i = lane; i < n16; i += 64) s_score[i] = i < n ? expf(lg[i] - mx) : 0.0f;
         __syncthreads();
-        if (lane == 0) {
+        if (lane == 0) {  // summed in index order, as the reference does
             float sum = 0.0f;
-            for (int i = 0; i < n; i++) sum += s_score[i];
+            for (int i0 = 0; i0 < n16; i0 += 16) {
+                float v[16];
+                batch(s_score, i0, v);
+#pragma unroll
+                for (int t = 0; t < 16; t++) sum += v[t];
+            }
             s_inv = 1.0f / sum;
         }
         __syncthreads();
@@ -62,7 +79,8 @@ __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
         for (int i = lane; i < n; i += 64) s_score[i] = 1.0f / (1.0f + expf(-lg[i]));
     }
     __syncthreads();
-    for (int i = lane; i < n; i += 64) s_choice[i] = r.bias ? s_score[i] + r.bias[i] : s_score[i];
+    for (int i = lane; i < n16; i += 64)
+        s_choice[i] = i >= n ? -INFINITY : r.bias ? s_score[i] + r.bias[i] : s_score[i];
     __syncthreads();
 
     // mask_to_best_groups (ffn.rs:312-349)
@@ -119,9 +137,11 @@ __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
         const float v = s_choice[i];
         if (!(v > -INFINITY)) continue;
         int rank = 0;
-        for (int j = 0; j < n; j++) {
-            const float u = s_choice[j];
-            rank += u > -INFINITY && (u > v || (u == v && j < i));
+        for (int j0 = 0; j0 < n16; j0 += 16) {
+            float u[16];
+            batch(s_choice, j0, u);
+#pragma unroll
+            for (int t = 0; t < 16; t++) rank += u[t] > -INFINITY && (u[t] > v || (u[t] == v && j0 + t < i));
         }
         if (rank < k) {
             s_pick_e[rank] = i;
