@@ -1159,10 +1159,22 @@ int launch_multi_p(kh_ctx *ctx, MultiArgs a) {
     const int C = chunks_per_row(PREC, a.cols);
     const int cpl = C <= 2 * WAVE ? 1 : 2;  // short steps: a row in segments of one or two chunks per lane
     const int PB = padded_blocks(PREC, C, cpl);
+    // token slots: the smallest of 2, 4, 8 that holds m, in as many launches
+    // as the LDS stage needs (each launch streams the weights once).  A
+    // workgroup may hold up to 160 KB of LDS on gfx950; a stage past half of
+    // that leaves one workgroup per CU, and the grid is sized for that.
+    constexpr size_t LDS_MAX = 160 * 1024;
+    auto slots = [&](int left) {
+        int T = left <= 2 ? 2 : left <= 4 ? 4 : 8;
+        while (T > 2 && (size_t)T * PB * 40 > LDS_MAX) T /= 2;
+        return T;
+    };
+    if ((size_t)slots(a.m) * PB * 40 > LDS_MAX) return fail(KH_DECLINED, "matmul: activation too wide for the LDS stage");
+    const int per_cu = (size_t)slots(a.m) * PB * 40 > LDS_MAX / 2 ? 1 : 2;
     long long rows_total = 0;
     for (int i = 0; i < a.njobs; i++) rows_total += a.j[i].rows;
     int want = (int)((rows_total + WPB - 1) / WPB);
-    if (want > 2 * cu) want = 2 * cu;
+    if (want > per_cu * cu) want = per_cu * cu;
     // each job at least one workgroup, the rest in proportion to its rows
     int nwg = 0;
     for (int i = 0; i < a.njobs; i++) {
@@ -1172,12 +1184,8 @@ int launch_multi_p(kh_ctx *ctx, MultiArgs a) {
         a.j[i].nwaves = g * WPB;
         nwg += g;
     }
-    // token slots: the smallest of 2, 4, 8 that holds m, in as many launches
-    // as the LDS stage needs (each launch streams the weights once)
     for (int t0 = 0; t0 < a.m;) {
-        int T = a.m - t0 <= 2 ? 2 : a.m - t0 <= 4 ? 4 : 8;
-        while (T > 2 && (size_t)T * PB * 40 > 64 * 1024) T /= 2;
-        if ((size_t)T * PB * 40 > 64 * 1024) return fail(KH_DECLINED, "matmul: activation too wide for the LDS stage");
+        const int T = slots(a.m - t0);
         MultiArgs b = a;
         b.m = a.m - t0 < T ? a.m - t0 : T;
         b.xq = a.xq + (size_t)t0 * a.cols;

@@ -182,3 +182,15 @@ def test_two_by_two_known_answer(ctx, m):
     y = w.matmul_bt(xs.ravel(), m).reshape(m, 2)
     want = np.tile(np.array([[36.0, 8.0], [80.0, 10.0]], np.float32), (m // 2, 1))
     np.testing.assert_array_equal(y, want)
+
+
+@pytest.mark.parametrize("prec", ["q8", "q4k"])
+@pytest.mark.parametrize("m", [3, 8])
+def test_few_tokens_over_a_wide_activation(ctx, prec, m):
+    # the multi-token GEMV with Llama-3-8B's 14336-wide down-projection input:
+    # eight token slots of it need a stage past 64 KB of LDS (up to 160 KB)
+    rows, cols = 64, 14336
+    say("matmul wide", prec, m)
+    w, parts = make(ctx, prec, rows, cols, seed=rows + m)
+    xs = O.normal(m + 99, m * cols)
+    close(w.matmul_bt(xs, m), oracle_matmul(prec, parts, rows, cols, xs, m))
