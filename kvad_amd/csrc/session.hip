@@ -832,7 +832,8 @@ int kh_llm_resume(kh_llm *m, kh_llm_parked *p) {
     }
     std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
     (void)hipSetDevice(m->ctx->device);
-    KH_HIP(hipStreamSynchronize(m->ctx->stream));
+    // the swap is host-side, so the handle is consumed whatever follows; a
+    // dropped cache is reused only by later work on the same stream
     m->parked.erase(p);
     drop_cache(m, m->kc, m->vc);  // the conversation held until now is dropped
     m->kc = std::move(p->k);
@@ -878,7 +879,7 @@ int kh_llm_forward_each(kh_ctx *ctx, kh_llm *m, size_t n, const int32_t *tokens,
     // the table: tokens, then per layer each row's cache and its length
     // after this token (positions are fixed before anything is pushed,
     // llama.rs:229-236)
-    const size_t tok_bytes = 4 * n, tab_bytes = sizeof(AttnRow) * n * s.n_layer;
+    const size_t tok_bytes = (4 * n + 15) & ~(size_t)15, tab_bytes = sizeof(AttnRow) * n * s.n_layer;
     m->rows_host.resize(tok_bytes + tab_bytes);
     std::copy(tokens, tokens + n, reinterpret_cast<int32_t *>(m->rows_host.data()));
     AttnRow *tab = reinterpret_cast<AttnRow *>(m->rows_host.data() + tok_bytes);
