@@ -720,6 +720,7 @@ int kh_mla_attend_dev(kh_ctx *ctx, size_t n_head, const float *q_lat, const floa
                       const float *pe, size_t n_positions, float scale, float *out) {
     if (!ctx || !q_lat || !q_pe || !out || (n_positions && (!c || !pe)))
         return fail(KH_EINVAL, "kh_mla_attend_dev: null argument");
+    if (n_head == 0 || n_head > 4096) return fail(KH_EINVAL, "kh_mla_attend_dev: bad head count");
     Guard g(ctx);
     return launch_mla(ctx, (int)n_head, q_lat, q_pe, c, pe, 512, 64, n_positions, scale, out);
 }
