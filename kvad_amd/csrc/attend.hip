@@ -46,6 +46,7 @@ struct AttnArgs {
     size_t kstride, vstride;  // floats between consecutive positions
     int n_head, group, gc;    // group = n_head / n_kv_head; gc = heads per workgroup
     int L, P, nsplit;
+    int nw;                   // waves per split workgroup: P = 16 R nw
     // when set, the length is read here (+ plus_one) and L/nsplit above are
     // the launch's maxima; splits past the length return at once
     const int32_t *len_dev;
@@ -128,13 +129,14 @@ __device__ __forceinline__ float rows_min(float x) {
 // w = exp(s - M) * (1/S) with w < 1e-8 dropped (mod.rs:805-812).
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-template <int HD, int R>
-__global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+template <int HD, int R, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
     at_row(a, HD);
     constexpr int NQ4 = HD / 16;  // float4s per lane of a key row: products of 16 dims
     constexpr int VT = HD / 64;  // float4s per lane of a value row
     constexpr int NT = HD / 16;  // 16-column tiles of the output
-    constexpr int P = 64 * R;
+    constexpr int P = 16 * R * NW;
+    constexpr int NTH = 64 * NW;
     const int split = blockIdx.x, hg = blockIdx.y;
     const int G = a.gc;
     const int h0 = hg * G, kvh = h0 / a.group;
@@ -150,8 +152,21 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     const rsrc_t K = rsrc(a.k, (size_t)L * a.kstride * 4), V = rsrc(a.v, (size_t)L * a.vstride * 4);
     const int pw = wave * 16 * R;  // the wave's first position in the split
 
-    __shared__ __align__(16) float s_acc[4][16][HD];  // per-wave totals
-    __shared__ float s_st[3][4][16];                  // per-wave max, sum, smallest score
+    __shared__ __align__(16) float s_acc[NW][16][HD];  // per-wave totals
+    __shared__ float s_st[3][NW][16];                  // per-wave max, sum, smallest score
+    // over the waves in wave order: the largest of row st, the total of row st
+    auto wmax = [&](int st, int h) {
+        float x = s_st[st][0][h];
+#pragma unroll
+        for (int w = 1; w < NW; w++) x = fmaxf(x, s_st[st][w][h]);
+        return x;
+    };
+    auto wmin = [&](int st, int h) {
+        float x = s_st[st][0][h];
+#pragma unroll
+        for (int w = 1; w < NW; w++) x = fminf(x, s_st[st][w][h]);
+        return x;
+    };
 
     // q first (the score products wait on it before any key), then keys,
     // then values: loads complete in issue order
@@ -256,12 +271,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         }
         __syncthreads();
         // the split's statistics: M over the waves, each wave rescaled to it
-        for (int i = tid; i < G * HD; i += 256) {
+        for (int i = tid; i < G * HD; i += NTH) {
             const int h = i / HD, d = i % HD;
-            const float M = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
+            const float M = wmax(0, h);
             float x = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
+            for (int w = 0; w < NW; w++) {
                 const float c = s_st[0][w][h] == -INFINITY ? 0.0f : expf(s_st[0][w][h] - M);
                 x = fmaf(c, s_acc[w][h][d], x);
             }
@@ -269,17 +284,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         }
         if (tid < G) {
             const int h = tid;
-            const float M = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
+            const float M = wmax(0, h);
             float Ls = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
+            for (int w = 0; w < NW; w++) {
                 const float c = s_st[0][w][h] == -INFINITY ? 0.0f : expf(s_st[0][w][h] - M);
                 Ls = fmaf(c, s_st[1][w][h], Ls);
             }
             const size_t o = (size_t)split * a.n_head + h0 + h;
             a.pm[o] = M;
             a.pl[o] = Ls;
-            a.pmin[o] = fminf(fminf(s_st[2][0][h], s_st[2][1][h]), fminf(s_st[2][2][h], s_st[2][3][h]));
+            a.pmin[o] = wmin(2, h);
         }
         // the scores, for the merge's decision on the reference's 1e-8 skip
         // (stored last: a store ahead of a load would hold up its wait)
@@ -298,7 +313,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     if (c4 == 0 && hv) s_st[0][wave][j16] = mx;
     __syncthreads();
     const int hj = hv ? j16 : 0;
-    const float M = fmaxf(fmaxf(s_st[0][0][hj], s_st[0][1][hj]), fmaxf(s_st[0][2][hj], s_st[0][3][hj]));
+    const float M = wmax(0, hj);
     l = 0.0f;
 #pragma unroll
     for (int u = 0; u < R; u++)
@@ -310,7 +325,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     l = rows_sum(l);
     if (c4 == 0 && hv) s_st[1][wave][j16] = l;
     __syncthreads();
-    const float inv = 1.0f / (((s_st[1][0][hj] + s_st[1][1][hj]) + s_st[1][2][hj]) + s_st[1][3][hj]);
+    float S = s_st[1][0][hj];
+#pragma unroll
+    for (int w = 1; w < NW; w++) S = S + s_st[1][w][hj];
+    const float inv = 1.0f / S;
 #pragma unroll
     for (int u = 0; u < R; u++)
 #pragma unroll
@@ -322,9 +340,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     values(e, acc);
     store_acc(acc);
     __syncthreads();
-    for (int i = tid; i < G * HD; i += 256) {
+    for (int i = tid; i < G * HD; i += NTH) {
         const int h = i / HD, d = i % HD;
-        a.out[(size_t)(h0 + h) * HD + d] = ((s_acc[0][h][d] + s_acc[1][h][d]) + s_acc[2][h][d]) + s_acc[3][h][d];
+        float x = s_acc[0][h][d];
+#pragma unroll
+        for (int w = 1; w < NW; w++) x = x + s_acc[w][h][d];
+        a.out[(size_t)(h0 + h) * HD + d] = x;
     }
 }
 
@@ -571,13 +592,23 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     merge_head<HD, HD>(a.pm, a.pl, a.pmin, a.pacc, a.psc, ns, a.n_head, h, 0, a.P, L, vrow, a.out);
 }
 
-// P = 64 R positions per workgroup: R in {1, 2, 4} for hd 64, {1, 2} for hd 128.
+// P = 16 R nw positions per workgroup of nw waves: four waves with R in
+// {1, 2, 4} (hd 64) or {1, 2} (hd 128), or eight waves with R in {1, 2} (hd 64)
+// or 1 (hd 128) for P >= 128.
 template <int HD>
 void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
-    const int r = a.P / 64;
-    if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1>), grid, dim3(256), 0, stream, a);
-    else if (HD == 128 || r == 2) hipLaunchKernelGGL((attn_split_kernel<HD, 2>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((attn_split_kernel<64, 4>), grid, dim3(256), 0, stream, a);
+    const int r = a.P / (16 * a.nw);
+    const dim3 block(64 * a.nw);
+    if (a.nw == 8) {
+        if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1, 8>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((attn_split_kernel<64, 2, 8>), grid, block, 0, stream, a);
+    } else if (r == 1) {
+        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 4>), grid, block, 0, stream, a);
+    } else if (HD == 128 || r == 2) {
+        hipLaunchKernelGGL((attn_split_kernel<HD, 2, 4>), grid, block, 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((attn_split_kernel<64, 4, 4>), grid, block, 0, stream, a);
+    }
 }
 
 }  // namespace
@@ -624,6 +655,10 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     if ((n_positions + P - 1) / P > (size_t)MAX_SPLITS)
         return fail(KH_DECLINED, "attend: sequence longer than the split merge takes");
     a.P = P;
+    // waves per workgroup: eight at 256 positions (measured faster at long
+    // context), else four; KVAD_ATTN_WAVES = 4 or 8 forces it where P >= 128
+    const int fw = env_int("KVAD_ATTN_WAVES", 0);
+    a.nw = P >= 128 && (fw == 8 || (fw != 4 && P == 256)) ? 8 : 4;
     a.nsplit = (int)((n_positions + P - 1) / P);
     a.scale = 1.0f / sqrtf((float)head_dim);  // mod.rs:777
     a.out = out;

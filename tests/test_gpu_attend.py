@@ -139,22 +139,25 @@ def test_attend_rejects_more_positions_than_cached(ctx):
         K.attend(ctx, K.Spec(14, 3, 64), O.normal(1, 14 * 64), cache, 0, 5)
 
 
-@pytest.mark.parametrize("L", [3000, 20000])
-def test_attend_skip_across_many_splits(ctx, L):
+@pytest.mark.parametrize("n_head,n_kv,L", [(4, 1, 3000), (4, 1, 20000), (14, 2, 32768)])
+def test_attend_skip_across_many_splits(ctx, n_head, n_kv, L):
     # A few dominant positions; the rest spread across the 1e-8 line, so some
     # splits are left out whole, some kept whole and most straddle it.  Values
     # are large, so a skipped term wrongly kept (or a kept one dropped) shows.
-    say("attend skip, many splits", L)
-    spec = K.Spec(4, 1, 64)
+    # Qwen's geometry at 32768 positions runs the 256-position splits.
+    say("attend skip, many splits", n_head, n_kv, L)
+    spec = K.Spec(n_head, n_kv, 64)
+    kvd = n_kv * 64
     rng = np.random.default_rng(L)
-    q = np.zeros((4, 64), np.float32)
-    q[:, 0] = 8.0  # score_t = q . k_t / 8 = k_t[0]
-    k = np.zeros((L, 64), np.float32)
-    k[:, 0] = rng.uniform(-4.0, 10.0, L)
-    k[rng.choice(L, 3, replace=False), 0] = 24.0
-    v = (rng.standard_normal((L, 64)) * 100.0).astype(np.float32)
-    cache = K.KvCache(ctx, 1, 64, 64)
+    q = np.zeros((n_head, 64), np.float32)
+    q[:, 0] = 8.0  # score_t = q . k_t / 8 = k_t[0] of the head's KV head
+    k = np.zeros((L, kvd), np.float32)
+    for h in range(n_kv):
+        k[:, 64 * h] = rng.uniform(-4.0, 10.0, L)
+        k[rng.choice(L, 3, replace=False), 64 * h] = 24.0
+    v = (rng.standard_normal((L, kvd)) * 100.0).astype(np.float32)
+    cache = K.KvCache(ctx, 1, kvd, kvd)
     cache.push(0, k.ravel(), v.ravel())
     got = K.attend(ctx, spec, q.ravel(), cache, 0, L)
-    want = O.attend(4, 1, 64, q.ravel(), k.ravel(), v.ravel(), L)
+    want = O.attend(n_head, n_kv, 64, q.ravel(), k.ravel(), v.ravel(), L)
     close(got, want)
