@@ -61,6 +61,12 @@ struct AttnArgs {
     // length), its q and out rows z, and partials offset by z * row_floats
     const AttnRow *rows;
     size_t row_floats;
+    // the session's step with RoPE and the cache push fused (when kraw is
+    // set): q holds the new position's query unrotated; position L - 1's key
+    // is RoPE(k_norm(kraw)) and its value vraw, both written into the caches
+    // (kw, vw) at L - 1 by the split that holds it
+    AttnRope rope;
+    float *kw, *vw;
 };
 
 // The row of a batched launch: its cache, its length and its slices.
@@ -75,6 +81,12 @@ __device__ __forceinline__ void at_row(AttnArgs &a, int hd) {
     a.out += (size_t)z * a.n_head * hd;
     const size_t o = (size_t)z * a.row_floats;
     a.pm += o, a.pl += o, a.pmin += o, a.pacc += o, a.psc += o;
+    a.kw = r.k;
+    a.vw = r.v;
+    if (a.rope.kraw) {
+        a.rope.kraw += (size_t)z * a.rope.raw_stride;
+        a.rope.vraw += (size_t)z * a.rope.raw_stride;
+    }
 }
 
 // Sums (or maxima) over the wave's four rows of 16 lanes, by swapping
@@ -129,7 +141,7 @@ __device__ __forceinline__ float rows_min(float x) {
 // w = exp(s - M) * (1/S) with w < 1e-8 dropped (mod.rs:805-812).
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-template <int HD, int R, int NW>
+template <int HD, int R, int NW, bool ROPE>
 __global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
     at_row(a, HD);
     constexpr int NQ4 = HD / 16;  // float4s per lane of a key row: products of 16 dims
@@ -172,7 +184,29 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
     // then values: loads complete in issue order
     const bool hv = j16 < G;
     f4v qb4[NQ4];
-    {
+    // Fused RoPE: wave w takes heads w, w + NW, ...: the G query heads, then
+    // (in the split holding the new position) the KV head's new key as head
+    // G; lane l holds dims l (+ 64) of the head, loaded now and rotated once
+    // the K and V loads are in flight.
+    constexpr bool rope = ROPE;  // launched with the rope argument set
+    const int pos = L - 1;
+    const bool holds = rope && pos >= t0 && pos < t0 + P;
+    constexpr int RH = (16 + NW) / NW;  // heads per wave (at most G + 1 <= 17 heads)
+    constexpr int HE = HD / 64;         // dims per lane
+    float xr[RH][HE];
+    if (rope) {
+#pragma unroll
+        for (int i = 0; i < RH; i++) {
+            const int h = wave + i * NW;
+#pragma unroll
+            for (int e = 0; e < HE; e++) xr[i][e] = 0.0f;
+            if (h < G || (h == G && holds)) {  // uniform per wave
+                const float *src = h < G ? a.q + (size_t)(h0 + h) * HD : a.rope.kraw + (size_t)kvh * HD;
+#pragma unroll
+                for (int e = 0; e < HE; e++) xr[i][e] = src[lane + 64 * e];
+            }
+        }
+    } else {
         const float *qh = a.q + (size_t)(h0 + (hv ? j16 : 0)) * HD + 4 * c4;
 #pragma unroll
         for (int m = 0; m < NQ4; m++) {
@@ -200,6 +234,100 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
             for (int v = 0; v < VT; v++)
                 vv[u][r][v] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(V, off, 256 * v, 0));
         }
+
+    if (rope) {
+        // per head: rms_norm with q_norm / k_norm (norm_heads, llama.rs:122-127),
+        // then RoPE at the new position (Rope::apply / apply_interleaved,
+        // tensor.rs:437-472), into LDS; the new key and value also into the
+        // caches and into this workgroup's own registers for that position
+        __shared__ __align__(16) float s_rot[17][HD];
+        __shared__ __align__(16) float s_vnew[HD];
+        const int half = HD / 2;
+#pragma unroll
+        for (int i = 0; i < RH; i++) {
+            const int h = wave + i * NW;
+            if (!(h < G || (h == G && holds))) continue;  // uniform per wave
+            float x[HE];
+#pragma unroll
+            for (int e = 0; e < HE; e++) x[e] = xr[i][e];
+            const float *nw = h < G ? a.rope.q_norm : a.rope.k_norm;
+            if (nw) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < HE; e++) {
+                    const float sq = x[e] * x[e];
+                    ss = ss + sq;
+                }
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+                const float inv = 1.0f / sqrtf(ss / (float)HD + a.rope.eps);
+#pragma unroll
+                for (int e = 0; e < HE; e++) {
+                    const float u = x[e] * inv;
+                    x[e] = u * nw[lane + 64 * e];
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < HE; e++) {
+                const int d = lane + 64 * e;
+                // the pair partner: dim d +- half (half split) or d ^ 1 (interleaved)
+                float pv;
+                if (a.rope.interleaved) {
+                    pv = __shfl_xor(x[e], 1);
+                } else {
+                    if constexpr (HD == 128) pv = x[e ^ 1];  // d and d + 64 sit in one lane
+                    else pv = __shfl_xor(x[e], 32);
+                }
+                const int ip = a.rope.interleaved ? d >> 1 : d % half;
+                const bool first = a.rope.interleaved ? (d & 1) == 0 : d < half;
+                const float c = a.rope.cos_t[(size_t)pos * half + ip], sn = a.rope.sin_t[(size_t)pos * half + ip];
+                float out;
+                if (first) {  // a = x, b = partner: a c - b s
+                    const float ac = x[e] * c, bs = pv * sn;
+                    out = ac - bs;
+                } else {      // b = x, a = partner: b c + a s
+                    const float bc = x[e] * c, as = pv * sn;
+                    out = bc + as;
+                }
+                s_rot[h][d] = out;
+                if (h == G) a.kw[(size_t)pos * a.kstride + (size_t)kvh * HD + d] = out;
+            }
+        }
+        if (holds) {
+            for (int d = tid; d < HD; d += NTH) {
+                const float v = a.rope.vraw[(size_t)kvh * HD + d];
+                s_vnew[d] = v;
+                a.vw[(size_t)pos * a.vstride + (size_t)kvh * HD + d] = v;
+            }
+        }
+        __syncthreads();
+        const float *qh = &s_rot[hv ? j16 : 0][4 * c4];
+#pragma unroll
+        for (int m = 0; m < NQ4; m++) {
+            const float4 f = *reinterpret_cast<const float4 *>(qh + 16 * m);
+            qb4[m] = hv ? f4v{f.x, f.y, f.z, f.w} : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+        if (holds) {  // the new position's key and value, in place of the cache's old row
+#pragma unroll
+            for (int u = 0; u < R; u++) {
+                const bool mine = t0 + pw + 16 * u + j16 == pos;
+#pragma unroll
+                for (int m = 0; m < NQ4; m++) {
+                    const float4 f = *reinterpret_cast<const float4 *>(&s_rot[G][16 * m + 4 * c4]);
+                    if (mine) kq[u][m] = f4v{f.x, f.y, f.z, f.w};
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const bool vmine = t0 + pw + 16 * u + 4 * c4 + r == pos;
+#pragma unroll
+                    for (int v = 0; v < VT; v++) {
+                        const float4 f = *reinterpret_cast<const float4 *>(&s_vnew[64 * v + 4 * j16]);
+                        if (vmine) vv[u][r][v] = f4v{f.x, f.y, f.z, f.w};
+                    }
+                }
+            }
+        }
+    }
 
     // scores: lane (c4, j16) holds positions pw + 16u + 4c4 + r of head j16
     f4v s[R];
@@ -594,21 +722,27 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
 
 // P = 16 R nw positions per workgroup of nw waves: four waves with R in
 // {1, 2, 4} (hd 64) or {1, 2} (hd 128), or eight waves with R in {1, 2} (hd 64)
-// or 1 (hd 128) for P >= 128.
-template <int HD>
-void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
+// or 1 (hd 128) for P >= 128; the fused-RoPE form when the rope argument is set.
+template <int HD, bool ROPE>
+void launch_split_r(const AttnArgs &a, dim3 grid, hipStream_t stream) {
     const int r = a.P / (16 * a.nw);
     const dim3 block(64 * a.nw);
     if (a.nw == 8) {
-        if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1, 8>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((attn_split_kernel<64, 2, 8>), grid, block, 0, stream, a);
+        if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1, 8, ROPE>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((attn_split_kernel<64, 2, 8, ROPE>), grid, block, 0, stream, a);
     } else if (r == 1) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 4>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 4, ROPE>), grid, block, 0, stream, a);
     } else if (HD == 128 || r == 2) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 2, 4>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn_split_kernel<HD, 2, 4, ROPE>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL((attn_split_kernel<64, 4, 4>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn_split_kernel<64, 4, 4, ROPE>), grid, block, 0, stream, a);
     }
+}
+
+template <int HD>
+void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
+    if (a.rope.kraw) launch_split_r<HD, true>(a, grid, stream);
+    else launch_split_r<HD, false>(a, grid, stream);
 }
 
 }  // namespace
@@ -715,12 +849,13 @@ size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size
 
 int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,
                        int nb, size_t kstride, size_t vstride, size_t max_positions, float *out, void *ws,
-                       size_t ws_bytes) {
+                       size_t ws_bytes, const AttnRope *rope) {
     if (nb <= 0 || nb > 65535 || max_positions == 0) return fail(KH_EINVAL, "attend: no rows or no positions");
     AttnArgs a;
     int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, nullptr, nullptr, kstride, vstride, max_positions, out, nb);
     if (rc) return rc;
     a.rows = rows;
+    if (rope) a.rope = *rope;
     a.row_floats = partial_floats(a.nsplit, n_head, head_dim, a.P);
     if (4 * a.row_floats * nb > ws_bytes) return fail(KH_EINVAL, "attend: workspace too small for the rows");
     carve_partials(a, ws, head_dim);
@@ -746,13 +881,18 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
 
 int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
                          const float *v, size_t kstride, size_t vstride, const int32_t *len_dev, int plus_one,
-                         size_t max_positions, float *out, void *ws) {
+                         size_t max_positions, float *out, void *ws, const AttnRope *rope) {
     if (max_positions == 0) return fail(KH_EINVAL, "attend: no positions");
     AttnArgs a;
     int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, k, v, kstride, vstride, max_positions, out);
     if (rc) return rc;
     a.len_dev = len_dev;
     a.plus_one = plus_one;
+    if (rope) {  // the caches are written at the new position
+        a.rope = *rope;
+        a.kw = const_cast<float *>(k);
+        a.vw = const_cast<float *>(v);
+    }
     carve_partials(a, ws, head_dim);
     return run(ctx, a, head_dim);
 }

@@ -297,24 +297,38 @@ int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, fl
 int launch_rms_norm(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out);
 // gate = silu(gate) * up over n floats (glue.hip).
 int launch_swiglu(kh_ctx *ctx, float *gate, const float *up, size_t n);
+// A row of a batched attention launch: its caches and its length.
+struct AttnRow {
+    float *k, *v;
+    int L;
+};
+// RoPE and the cache push of the new position fused into the attention
+// (the session's step): the new token's key and value unrotated (kraw, vraw;
+// raw_stride floats apart per batched row), the tables [max_pos][hd/2],
+// optional per-head norms (Qwen3) and the pairing.  The query passed to the
+// launch is unrotated too.
+struct AttnRope {
+    const float *kraw, *vraw;
+    const float *cos_t, *sin_t, *q_norm, *k_norm;
+    float eps;
+    int interleaved;
+    size_t raw_stride;
+};
+
 // Attention whose length is read from device memory: n_positions = *len_dev
 // (+1 when plus_one), at most max_positions; partials in `ws` (attend_ws_bytes).
 int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
                          const float *v, size_t kv_stride_k, size_t kv_stride_v, const int32_t *len_dev, int plus_one,
-                         size_t max_positions, float *out, void *ws);
+                         size_t max_positions, float *out, void *ws, const AttnRope *rope = nullptr);
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions);
 // Attention of nb rows at once, each over its own cache (forward_each,
 // llama.rs:258-271): row z's query is q + z * n_head * head_dim, its output
 // out + z * n_head * head_dim, its keys and values rows[z].k / .v (strides
 // kstride / vstride) over rows[z].L <= max_positions positions.  `rows` is in
 // device memory; partials in `ws` (attend_rows_ws_bytes).
-struct AttnRow {
-    float *k, *v;
-    int L;
-};
 int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,
                        int nb, size_t kstride, size_t vstride, size_t max_positions, float *out, void *ws,
-                       size_t ws_bytes);
+                       size_t ws_bytes, const AttnRope *rope = nullptr);
 size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size_t nb);
 
 // Absorbed latent attention (model/deepseek.rs:553-591): out[n_head][512] =

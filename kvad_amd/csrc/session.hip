@@ -6,12 +6,13 @@
 //
 // The position and the token live in device memory, so one token's launches
 // are the same every step: `kh_llm_generate` captures them once as a HIP
-// graph and replays it per token.  Per layer: RMSNorm; q/k/v (+bias) as one
-// GEMV launch; RoPE of q and k (per-head RMSNorm first where the model has
-// q/k norms) with k and v written into the cache row at the position, one
-// launch; attention over the cache, its length read from the device; o as a
-// GEMV that adds into the residual; RMSNorm; gate and up as one launch; down
-// with swiglu(gate, up) staged by the GEMV and added into the residual.
+// graph and replays it per token.  Per layer: q/k/v (+bias) as one GEMV
+// launch with the RMSNorm staged by the GEMV; attention over the cache, its
+// length read from the device, with RoPE of q and k (per-head RMSNorm first
+// where the model has q/k norms) and the push of k and v into the cache row
+// done by the attention's own split kernel; o as a GEMV that adds into the
+// residual; gate and up as one launch, RMSNorm staged; down with
+// swiglu(gate, up) staged by the GEMV and added into the residual.
 #include <algorithm>
 #include <initializer_list>
 #include <memory>
@@ -20,91 +21,6 @@
 
 namespace kh {
 namespace {
-
-// One head (128 threads): optional per-head RMSNorm (norm_heads,
-// llama.rs:122-127; rms_norm, tensor.rs:329-333, tree sum), then RoPE at
-// `pos` (Rope::apply / apply_interleaved, tensor.rs:437-472) into dst, which
-// may be src.
-__device__ void rope_head(const float *src, float *dst, int hd, int pos, const float *cos_t, const float *sin_t,
-                          int interleaved, const float *nw, float eps) {
-    const int t = threadIdx.x, half = hd / 2;
-    __shared__ float s_x[256];
-    __shared__ float s_red[128];
-    for (int i = t; i < hd; i += 128) s_x[i] = src[i];
-    __syncthreads();
-    if (nw) {
-        float s = 0.0f;
-        for (int i = t; i < hd; i += 128) {
-            const float sq = s_x[i] * s_x[i];
-            s = s + sq;
-        }
-        s_red[t] = s;
-        __syncthreads();
-        for (int w = 64; w > 0; w >>= 1) {
-            if (t < w) s_red[t] = s_red[t] + s_red[t + w];
-            __syncthreads();
-        }
-        const float inv = 1.0f / sqrtf(s_red[0] / (float)hd + eps);
-        __syncthreads();
-        for (int i = t; i < hd; i += 128) {
-            const float u = s_x[i] * inv;
-            s_x[i] = u * nw[i];
-        }
-        __syncthreads();
-    }
-    for (int i = t; i < half; i += 128) {
-        const float c = cos_t[(size_t)pos * half + i], s = sin_t[(size_t)pos * half + i];
-        const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + half;
-        const float a = s_x[ia], b = s_x[ib];
-        const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
-        dst[ia] = ac - bs;
-        dst[ib] = bc + as;
-    }
-}
-
-// One workgroup per head of q or k (then the v copy): q rotated in place,
-// k rotated into the cache row at the device position, v copied there.
-__global__ __launch_bounds__(128) void rope_push_kernel(float *qkv, int n_head, int n_kv, int hd,
-                                                       const float *cos_t, const float *sin_t, int interleaved,
-                                                       const float *q_norm, const float *k_norm, float eps,
-                                                       float *kc, float *vc, const int32_t *pos_dev) {
-    const int h = blockIdx.x, t = threadIdx.x;
-    const int pos = *pos_dev;
-    const int kv_dim = n_kv * hd;
-    if (h == n_head + n_kv) {  // the values: straight into the cache
-        for (int i = t; i < kv_dim; i += 128) vc[(size_t)pos * kv_dim + i] = qkv[(size_t)(n_head + n_kv) * hd + i];
-        return;
-    }
-    const bool is_q = h < n_head;
-    float *x = qkv + (size_t)h * hd;
-    float *dst = is_q ? x : kc + (size_t)pos * kv_dim + (size_t)(h - n_head) * hd;
-    rope_head(x, dst, hd, pos, cos_t, sin_t, interleaved, is_q ? q_norm : k_norm, eps);
-}
-
-// The same for n rows (grid y), each at its own position in its own cache
-// (rows[i]: position L - 1; run_rows, llama.rs:249-256): q [n][n_head*hd],
-// k and v [n][n_kv*hd].
-__global__ __launch_bounds__(128) void rope_push_rows_kernel(float *q, const float *k, const float *v, int n_head,
-                                                            int n_kv, int hd, const float *cos_t, const float *sin_t,
-                                                            int interleaved, const float *q_norm,
-                                                            const float *k_norm, float eps, const AttnRow *rows) {
-    const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
-    const int kv_dim = n_kv * hd;
-    const AttnRow r = rows[i];
-    const int pos = r.L - 1;
-    if (h == n_head + n_kv) {
-        for (int j = t; j < kv_dim; j += 128) r.v[(size_t)pos * kv_dim + j] = v[(size_t)i * kv_dim + j];
-        return;
-    }
-    if (h < n_head) {
-        float *x = q + ((size_t)i * n_head + h) * hd;
-        rope_head(x, x, hd, pos, cos_t, sin_t, interleaved, q_norm, eps);
-    } else {
-        const int kh = h - n_head;
-        rope_head(k + (size_t)i * kv_dim + (size_t)kh * hd, r.k + (size_t)pos * kv_dim + (size_t)kh * hd, hd, pos,
-                  cos_t, sin_t, interleaved, k_norm, eps);
-    }
-}
 
 // sampler::argmax (sampler.rs:217-226): the first of equal maxima; a NaN
 // never wins, and a NaN first entry keeps index 0.  Two launches: each
@@ -264,12 +180,12 @@ int step(kh_ctx *ctx, kh_llm *m) {
         jobs.push_back(
             {L.v, normed(gemv_job(L.v, qin, nullptr, L.v_b, m->qkv + qd + kvd, 0), fq, L.attn_norm, s.eps)});
         if ((rc = run_jobs(ctx, jobs))) return rc;
-        hipLaunchKernelGGL(rope_push_kernel, dim3((unsigned)(s.n_head + s.n_kv_head + 1)), dim3(128), 0,
-                           ctx->stream, m->qkv, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, m->rope_cos,
-                           m->rope_sin, s.rope_interleaved, L.q_norm, L.k_norm, s.eps, m->kc[l], m->vc[l], m->pos);
-        KH_HIP(hipGetLastError());
+        // attention over the cache, its length read from the device, with the
+        // per-head norms, RoPE and the push of k and v fused in
+        const AttnRope rp{m->qkv + qd, m->qkv + qd + kvd, m->rope_cos, m->rope_sin, L.q_norm, L.k_norm,
+                          s.eps, s.rope_interleaved, 0};
         if ((rc = launch_attend_devlen(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, m->qkv, m->kc[l],
-                                       m->vc[l], kvd, kvd, m->pos, 1, s.n_ctx, m->att, m->attn_ws)))
+                                       m->vc[l], kvd, kvd, m->pos, 1, s.n_ctx, m->att, m->attn_ws, &rp)))
             return rc;
         jobs.clear();
         jobs.push_back({L.o, gemv_job(L.o, m->att, nullptr, nullptr, m->x, 1)});
@@ -460,13 +376,12 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
             float *y[3] = {b.q, b.k, b.v};
             if ((rc = project_all(ctx, 3, w, b.h, b.qa, n, bias, y))) return rc;
         }
+        // each row at its own position over its own cache (run_rows,
+        // llama.rs:249-271), RoPE and the cache push fused in
         const AttnRow *tab = b.tab + l * n;
-        hipLaunchKernelGGL(rope_push_rows_kernel, dim3((unsigned)(s.n_head + s.n_kv_head + 1), (unsigned)n), dim3(128),
-                           0, ctx->stream, b.q, b.k, b.v, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim,
-                           m->rope_cos, m->rope_sin, s.rope_interleaved, L.q_norm, L.k_norm, s.eps, tab);
-        KH_HIP(hipGetLastError());
+        const AttnRope rp{b.k, b.v, m->rope_cos, m->rope_sin, L.q_norm, L.k_norm, s.eps, s.rope_interleaved, kvd};
         if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
-                                     kvd, s.n_ctx, b.att, b.ws, b.ws_bytes)))
+                                     kvd, s.n_ctx, b.att, b.ws, b.ws_bytes, &rp)))
             return rc;
         if (L.o->precision != KH_F32 && (rc = launch_qact(ctx, b.att, n, qd, b.qa))) return rc;
         if ((rc = project(ctx, L.o, b.att, b.qa, n, nullptr, b.x, 1))) return rc;  // x += o(attn)
