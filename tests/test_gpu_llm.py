@@ -34,10 +34,15 @@ def build(ctx, seed, n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=64, 
     rng = iter(range(seed, seed + 10000))
     qd, kvd = n_head * head_dim, n_kv_head * head_dim
 
-    def q8(rows, cols, scale=sd):  # f32 weights (Precision::F32) when prec == "f32"
+    def q8(rows, cols, scale=sd, layer=False):
+        # f32 weights (Precision::F32) when prec == "f32"; Q4_K layer
+        # weights (the embedding and head stay q8) when prec == "q4k"
         data = O.normal(next(rng), rows * cols, scale)
         if prec == "f32":
             return (data,), K.Weight.from_f32(ctx, data.reshape(rows, cols))
+        if prec == "q4k" and layer:
+            b = O.quantize_q4k(data, rows, cols)
+            return ("q4k", b), K.Weight.from_q4k(ctx, rows, cols, b)
         s, q = O.quantize_q8(data, rows, cols)
         return (s, q), K.Weight.from_q8(ctx, rows, cols, s, q)
 
@@ -51,7 +56,7 @@ def build(ctx, seed, n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=64, 
         handles = {}
         for name, (r, c) in dict(q=(qd, n_embd), k=(kvd, n_embd), v=(kvd, n_embd), o=(n_embd, qd),
                                  gate=(n_ff, n_embd), up=(n_ff, n_embd), down=(n_embd, n_ff)).items():
-            parts[name], handles[name] = q8(r, c)
+            parts[name], handles[name] = q8(r, c, layer=True)
         parts["attn_norm"], parts["mlp_norm"] = vec(n_embd), vec(n_embd)
         if bias:
             parts["q_b"], parts["k_b"], parts["v_b"] = vec(qd, 0.0), vec(kvd, 0.0), vec(kvd, 0.0)
@@ -84,12 +89,16 @@ def run_both(m, ref, tokens):
     return worst
 
 
-@pytest.mark.parametrize("variant", ["qwen2", "qwen3", "llama_interleaved", "qwen2_f32"])
+@pytest.mark.parametrize("variant", ["qwen2", "qwen3", "llama_interleaved", "qwen2_f32", "llama_q4k"])
 def test_forward_matches_the_oracle(ctx, variant):
     kw = {"qwen2": dict(bias=True), "qwen3": dict(bias=False, qk_norm=True, tied=False),
           "llama_interleaved": dict(bias=False, interleaved=True, n_head=8, n_kv_head=2, head_dim=128,
                                     n_embd=256),
-          "qwen2_f32": dict(bias=True, tied=False, prec="f32")}[variant]
+          "qwen2_f32": dict(bias=True, tied=False, prec="f32"),
+          # Q4_K layer weights (GGUF-style): q/k/v take the fused rms_norm
+          # input, down swiglu(gate, up), o and down add the residual
+          "llama_q4k": dict(bias=False, interleaved=True, n_head=16, n_kv_head=4, head_dim=128, n_embd=2048,
+                            n_ff=2048, prec="q4k")}[variant]
     say("llm forward", variant)
     m, mk = build(ctx, 100, **kw)
     ref = mk()
