@@ -204,9 +204,12 @@ int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, 
 // The same for up to MULTI_JOBS weights of one precision and width over the
 // same rows of codes, in one launch: y[i] (+)= x W_i^T (+ bias[i]), adding
 // into y[i] where accumulate[i] is set (accumulate and bias may be null).
+// With xf set, the rows are f32 ([m][cols]) and every workgroup quantises
+// them as it stages them (the same codes as launch_qact); x is then unused.
 constexpr int MULTI_JOBS = 3;
 int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,
-                           float *const *y, const int *accumulate, const QAct &x, size_t m);
+                           float *const *y, const int *accumulate, const QAct &x, size_t m,
+                           const float *xf = nullptr);
 
 // Batched prefill y[m, rows] = xs[m, cols] W^T (+bias), m > 1 (device pointers).
 int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y,

@@ -731,6 +731,7 @@ struct MultiArgs {
     const int8_t *xq;     // [m][cols] codes
     const float *xs;      // [m][cols / 32]
     const int32_t *xsum;  // [m][cols / 32]
+    const float *xf;      // or, when set: [m][cols] f32 rows each workgroup quantises itself
     int cols, m, njobs;
     MultiJob j[MULTI_JOBS];
 };
@@ -858,7 +859,26 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
     int8_t *sq = reinterpret_cast<int8_t *>(lds);
     float *ssc = reinterpret_cast<float *>(lds + (size_t)T * PB * 32);
     int *ssum = reinterpret_cast<int *>(ssc + (size_t)T * PB);
-    {
+    if (a.xf) {
+        // f32 rows quantised here as QActBatch::new does (quant.rs:682-738),
+        // 8 lanes per 32-block as qact_kernel: the same codes, scales and
+        // sums.  float4 i: token i / (8 PB), float4 i % (8 PB) of its padded
+        // row; a group of 8 lanes is always whole (the stride is a multiple
+        // of 8), and padding quantises to zeros.
+        const rsrc_t X = rsrc(a.xf, (size_t)a.m * cols * 4);
+        for (int i = tid; i < T * PB * 8; i += WAVE * WPB) {
+            const int k = i / (PB * 8), c = i % (PB * 8);
+            const bool ok = k < a.m && c < nb * 8;
+            const float4 v = __builtin_bit_cast(float4, bld16(X, ok ? (unsigned)((k * cols + c * 4) * 4) : 0xffffffffu));
+            float scale;
+            int sum;
+            reinterpret_cast<int *>(sq)[i] = quantize4(v, &scale, &sum);
+            if ((tid & 7) == 0) {
+                ssc[i >> 3] = scale;
+                ssum[i >> 3] = sum;
+            }
+        }
+    } else {
         const rsrc_t Q = rsrc(a.xq, (size_t)a.m * cols), S = rsrc(a.xs, (size_t)a.m * nb * 4),
                      M = rsrc(a.xsum, (size_t)a.m * nb * 4);
         for (int i = tid; i < T * PB * 2; i += WAVE * WPB) {  // int4 i: token i / (2 PB), 16 bytes
@@ -1188,9 +1208,13 @@ int launch_multi_p(kh_ctx *ctx, MultiArgs a) {
         const int T = slots(a.m - t0);
         MultiArgs b = a;
         b.m = a.m - t0 < T ? a.m - t0 : T;
-        b.xq = a.xq + (size_t)t0 * a.cols;
-        b.xs = a.xs + (size_t)t0 * (a.cols / BLOCK);
-        b.xsum = a.xsum + (size_t)t0 * (a.cols / BLOCK);
+        if (a.xf) {
+            b.xf = a.xf + (size_t)t0 * a.cols;
+        } else {
+            b.xq = a.xq + (size_t)t0 * a.cols;
+            b.xs = a.xs + (size_t)t0 * (a.cols / BLOCK);
+            b.xsum = a.xsum + (size_t)t0 * (a.cols / BLOCK);
+        }
         for (int i = 0; i < a.njobs; i++) b.j[i].y = a.j[i].y + (size_t)t0 * a.j[i].rows;
         const size_t lds = (size_t)T * PB * 40;
         int rc = T == 2 ? launch_multi_t<PREC, 2>(ctx, b, cpl, nwg, lds)
@@ -1242,20 +1266,21 @@ int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
 }
 
 int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,
-                           float *const *y, const int *accumulate, const QAct &x, size_t m) {
+                           float *const *y, const int *accumulate, const QAct &x, size_t m, const float *xf) {
     if (m == 0) return KH_OK;
     if (njobs < 1 || njobs > MULTI_JOBS) return fail(KH_EINVAL, "matmul: one to three weights per launch");
     MultiArgs a{};
     a.xq = x.qs;
     a.xs = x.scales;
     a.xsum = x.sums;
+    a.xf = xf;
     a.cols = (int)w[0]->cols;
     a.m = (int)m;
     a.njobs = njobs;
     for (int i = 0; i < njobs; i++) {
         if (w[i]->precision != w[0]->precision || w[i]->cols != w[0]->cols)
             return fail(KH_EINVAL, "matmul: weights of one launch share precision and width");
-        if ((size_t)w[i]->rows * w[i]->cols >= 0xfff00000ull || m * w[i]->cols >= 0xfff00000ull)
+        if ((size_t)w[i]->rows * w[i]->cols >= 0xfff00000ull || m * w[i]->cols * (xf ? 4 : 1) >= 0xfff00000ull)
             return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
         a.j[i].w = w[i]->qs;
         a.j[i].ws = w[i]->scales;

@@ -383,8 +383,18 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
         if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
                                      kvd, s.n_ctx, b.att, b.ws, b.ws_bytes, &rp)))
             return rc;
-        if (L.o->precision != KH_F32 && (rc = launch_qact(ctx, b.att, n, qd, b.qa))) return rc;
-        if ((rc = project(ctx, L.o, b.att, b.qa, n, nullptr, b.x, 1))) return rc;  // x += o(attn)
+        if (L.o->precision != KH_F32 && n <= 8 && n <= rows_multi_max()) {
+            // x += o(attn): the multi-token GEMV quantises the attention rows
+            // itself, in its one launch (past eight rows it takes several, each
+            // quantising its rows in every workgroup: measured slower than one
+            // quantisation launch at 32 rows)
+            const float *no_bias = nullptr;
+            const int acc = 1;
+            if ((rc = launch_gemv_multi_jobs(ctx, 1, &L.o, &no_bias, &b.x, &acc, b.qa, n, b.att))) return rc;
+        } else {
+            if (L.o->precision != KH_F32 && (rc = launch_qact(ctx, b.att, n, qd, b.qa))) return rc;
+            if ((rc = project(ctx, L.o, b.att, b.qa, n, nullptr, b.x, 1))) return rc;  // x += o(attn)
+        }
         // ---- MLP sub-block (llama.rs:277-285, Ffn::run ffn.rs:370-375)
         if ((rc = norm_rows(ctx, b.x, L.mlp_norm, n, e, s.eps, any_f32({L.gate, L.up}), b.h, b.qa))) return rc;
         {
