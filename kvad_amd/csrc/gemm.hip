@@ -622,6 +622,10 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
         a.xf = xs;
         return launch_f32gemm(ctx, a);
     }
+    // up to eight rows: the multi-token GEMV quantises them as it stages them
+    // (QActBatch::new's codes, one launch fewer)
+    if (m <= (size_t)MULTI_TOKENS && !matmul_force_gemm())
+        return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, QAct{}, m, xs);
     // QActBatch::new (quant.rs:693-714): the activation rows quantised per block
     const size_t qb = (m * cols + 255) / 256 * 256, sb = (4 * m * cols / BLOCK + 255) / 256 * 256;
     int rc = ensure(ctx, ctx->ws, qb + 2 * sb);

@@ -383,7 +383,7 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
         if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
                                      kvd, s.n_ctx, b.att, b.ws, b.ws_bytes, &rp)))
             return rc;
-        if (L.o->precision != KH_F32 && n <= 8 && n <= rows_multi_max()) {
+        if (L.o->precision != KH_F32 && n <= (size_t)MULTI_TOKENS && n <= rows_multi_max()) {
             // x += o(attn): the multi-token GEMV quantises the attention rows
             // itself, in its one launch (past eight rows it takes several, each
             // quantising its rows in every workgroup: measured slower than one
