@@ -113,6 +113,16 @@ int kh_weight_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out);
 int kh_matvec(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y);
 int kh_matvec_dev(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y);
 
+/* Weight::matvec_bt_dequant (quant.rs:522-589): the same product with each
+ * weight unpacked to f32 and x used as it is, unquantised -- the baseline the
+ * reference keeps beside its integer path and selects with KVAD_DEQUANT=1
+ * (quant.rs:592-610).  With KVAD_DEQUANT set to "1" or "true", kh_matvec and
+ * kh_matvec_dev (and kh_matmul at m == 1) run this kernel too, and
+ * kh_matvec_many declines, as matvec_many returns None.  q8, q4 and Q4_K
+ * weights (Q4_K as mpp.rs:304-315 decodes it); f32 weights are KH_EINVAL. */
+int kh_matvec_dequant(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y);
+int kh_matvec_dequant_dev(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y);
+
 /* quant::matvec_many (quant.rs:628-671): n GEMVs in one launch, each result
  * bit-identical to kh_matvec on the same job.  Returns KH_DECLINED when a
  * weight is f32 or x's length does not match, as the reference returns None. */

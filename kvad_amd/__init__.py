@@ -84,6 +84,8 @@ _SIGS = {
     "kh_weight_row": (C.c_int, [_p, _p, _sz, _p]),
     "kh_matvec": (C.c_int, [_p, _p, _p, _p, _p]),
     "kh_matvec_dev": (C.c_int, [_p, _p, _p, _p, _p]),
+    "kh_matvec_dequant": (C.c_int, [_p, _p, _p, _p, _p]),
+    "kh_matvec_dequant_dev": (C.c_int, [_p, _p, _p, _p, _p]),
     "kh_matvec_many": (C.c_int, [_p, _sz, _p, _p, _p]),
     "kh_matvec_many_dev": (C.c_int, [_p, _sz, _p, _p, _p]),
     "kh_matmul": (C.c_int, [_p, _p, _p, _sz, _p, _p]),
@@ -296,6 +298,19 @@ class Weight:
 
     def matvec_bt_dev(self, x_ptr: int, y_ptr: int, bias_ptr: int | None = None) -> None:
         _check(lib.kh_matvec_dev(self.ctx.h, self.h, x_ptr, bias_ptr, y_ptr))
+
+    def matvec_bt_dequant(self, x, bias=None) -> np.ndarray:
+        """Weight::matvec_bt_dequant (quant.rs:522-589): weights unpacked to
+        f32, x unquantised."""
+        x = _f32(x)
+        assert x.size == self.cols, "matvec_bt_dequant shape mismatch"
+        b = None if bias is None else _f32(bias)
+        y = np.empty(self.rows, np.float32)
+        _check(lib.kh_matvec_dequant(self.ctx.h, self.h, _ptr(x), _ptr(b), _ptr(y)))
+        return y
+
+    def matvec_bt_dequant_dev(self, x_ptr: int, y_ptr: int, bias_ptr: int | None = None) -> None:
+        _check(lib.kh_matvec_dequant_dev(self.ctx.h, self.h, x_ptr, bias_ptr, y_ptr))
 
     def matvec_q_dev(self, qs_ptr: int, scales_ptr: int, sums_ptr: int, y_ptr: int,
                      bias_ptr: int | None = None) -> None:

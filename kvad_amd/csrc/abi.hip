@@ -119,6 +119,9 @@ int make_jobs(kh_ctx *ctx, size_t n, const kh_weight *const *w, const float *con
 
 // matvec on device pointers.
 int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots) {
+    // KVAD_DEQUANT=1 selects the dequantising kernel (quant.rs:485-486); the
+    // block-dot hook always reads the integer path
+    if (!dots && w->precision != KH_F32 && dequant_selected()) return launch_gemv_dequant(ctx, w, x, bias, y);
     std::vector<GemvJob> jobs;
     int rc = make_jobs(ctx, 1, &w, &x, &bias, &y, dots, jobs);
     if (rc) return rc;
@@ -132,6 +135,8 @@ int matvec_many_device(kh_ctx *ctx, size_t n, const kh_weight *const *w, const f
         if (check_weight(w[i])) return KH_EINVAL;
         if (w[i]->precision == KH_F32) return fail(KH_DECLINED, "matvec_many: an f32 weight is not this call's to run");
     }
+    // quant.rs:629-633: None when the dequantising kernel was asked for
+    if (dequant_selected()) return fail(KH_DECLINED, "matvec_many: KVAD_DEQUANT asks for one matvec at a time");
     std::vector<GemvJob> all;
     int rc = make_jobs(ctx, n, w, x, nullptr, y, nullptr, all);
     if (rc) return rc;
@@ -428,6 +433,31 @@ static int matvec_host(kh_ctx *ctx, const kh_weight *w, const float *x, const fl
 int kh_matvec(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y) {
     if (!ctx || check_weight(w) || !x || !y) return fail(KH_EINVAL, "kh_matvec: null argument");
     return matvec_host(ctx, w, x, bias, y, nullptr);
+}
+
+int kh_matvec_dequant_dev(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y) {
+    if (!ctx || check_weight(w) || !x || !y) return fail(KH_EINVAL, "kh_matvec_dequant_dev: null argument");
+    Guard g(ctx);
+    return launch_gemv_dequant(ctx, w, x, bias, y);
+}
+
+int kh_matvec_dequant(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y) {
+    if (!ctx || check_weight(w) || !x || !y) return fail(KH_EINVAL, "kh_matvec_dequant: null argument");
+    if (w->precision == KH_F32) return fail(KH_EINVAL, "kh_matvec_dequant: f32 weights have nothing to dequantise");
+    Guard g(ctx);
+    const size_t rows = w->rows, cols = w->cols;
+    int rc = ensure(ctx, ctx->io, up(4 * cols) + 2 * up(4 * rows));
+    if (rc) return rc;
+    char *p = static_cast<char *>(ctx->io.ptr);
+    float *dx = reinterpret_cast<float *>(p);
+    float *dy = reinterpret_cast<float *>(p + up(4 * cols));
+    float *db = reinterpret_cast<float *>(p + up(4 * cols) + up(4 * rows));
+    KH_HIP(hipMemcpyAsync(dx, x, 4 * cols, hipMemcpyHostToDevice, ctx->stream));
+    if (bias) KH_HIP(hipMemcpyAsync(db, bias, 4 * rows, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = launch_gemv_dequant(ctx, w, dx, bias ? db : nullptr, dy))) return rc;
+    KH_HIP(hipMemcpyAsync(y, dy, 4 * rows, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
 }
 
 int kh_debug_block_dots(kh_ctx *ctx, const kh_weight *w, const float *x, int32_t *dots) {

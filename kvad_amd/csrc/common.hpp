@@ -190,6 +190,13 @@ struct GemvJob {
     int nwaves;             // set by the launcher: waves working on the job
 };
 
+// Weight::matvec_bt_dequant (quant.rs:522-589, dequant.hip): y = x W^T
+// (+ bias) with the weights unpacked to f32 and x used as it is, for q8, q4
+// and Q4_K weights; one launch.
+int launch_gemv_dequant(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y);
+// Whether KVAD_DEQUANT asks for it (quant.rs:608-610: "1" or "true").
+bool dequant_selected();
+
 // Widest rows whose GEMV quantises its f32 input itself (each workgroup
 // stages it in LDS); wider inputs are quantised once in a launch of their own.
 size_t fuse_max_cols(int precision);

@@ -1,0 +1,73 @@
+// Device helpers shared by the GEMV kernels (gemv.hip, dequant.hip): buffer
+// loads, DPP lane moves, the wave sum and the Q4_K header decode.
+#pragma once
+
+#include "common.hpp"
+
+namespace kh {
+namespace dev {
+
+constexpr int WAVE = 64;
+constexpr unsigned RSRC_WORD3 = 0x00020000;  // raw buffer, gfx9 family
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// A buffer descriptor over `bytes` bytes at p: loads past the end return 0.
+__device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes > 0xffffffffu ? 0xffffffffu : bytes), RSRC_WORD3);
+}
+__device__ __forceinline__ int4 bld16(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float4 bld16f(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float bldf(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// DPP lane movement (gfx9 encodings): quad_perm [1,0,3,2] = xor 1,
+// quad_perm [2,3,0,1] = xor 2, row_half_mirror, row_mirror.
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(int, v)));
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+// Sum over the wave; every lane gets the same value, in a fixed order.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dppf<DPP_XOR1>(v);
+    v += dppf<DPP_XOR2>(v);
+    v += dppf<DPP_HALF_MIRROR>(v);
+    v += dppf<DPP_MIRROR>(v);
+    float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float half_bits_to_float(unsigned h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffff));
+}
+
+// The 6-bit scale and minimum of Q4_K sub-block j (mpp.rs:276-282) from
+// bytes 4..15 of the block header (h.y, h.z, h.w), without a branch: j is
+// fixed per lane, so sh = 8 (j & 3) and hij = (j >= 4 ? ~0 : 0) are lane
+// constants.  For j < 4 this is A & 63 and B & 63; for j >= 4, the low four
+// bits from byte 8 + j and the top two from bytes j and 4 + j.
+__device__ __forceinline__ void q4k_scale_min(const int4 &h, int sh, unsigned hij, unsigned &sc, unsigned &mn) {
+    const unsigned A = (unsigned)h.y >> sh, B = (unsigned)h.z >> sh, Cw = (unsigned)h.w >> sh;
+    const unsigned s2 = hij & 2u;
+    const unsigned X = A ^ ((A ^ Cw) & hij), Y = B ^ ((B ^ (Cw >> 4)) & hij);
+    sc = (X & 0xfu) | ((A >> s2) & 0x30u);
+    mn = (Y & 0xfu) | ((B >> s2) & 0x30u);
+}
+
+}  // namespace dev
+}  // namespace kh
