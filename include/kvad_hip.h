@@ -188,6 +188,21 @@ int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t 
 int kh_attend_dev(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
                   const float *k, const float *v, size_t n_positions, float *out);
 
+/* kh_attend_dev without allocating: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): the same kernels,
+ * with the split partials in a static device array of
+ * kh_noalloc_scratch_bytes() bytes (8 MiB) that each GPU holds from library
+ * load until the process ends; kh_init looks up its address once per device.
+ * A call whose partials need more (long contexts at many heads: about 2.3 MB
+ * at Qwen2.5-0.5B geometry and 32768 positions) is KH_EINVAL with the size in
+ * kh_last_error().  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams or threads) race; calls on one stream
+ * are ordered. */
+int kh_attend_dev_noalloc(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
+                          const float *k, const float *v, size_t n_positions, float *out);
+size_t kh_noalloc_scratch_bytes(void);
+
 /* Latent attention, absorbed (model/deepseek.rs:553-591), one token: head h
  * scores cached position t as (q_lat_h . c_t + q_pe_h . pe_t) * scale,
  * softmax over the positions, and returns the attended latent

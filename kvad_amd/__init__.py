@@ -107,6 +107,8 @@ _SIGS = {
     "kh_kv_layer_ptrs": (C.c_int, [_p, _sz, C.POINTER(_p), C.POINTER(_p)]),
     "kh_attend": (C.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "kh_attend_dev": (C.c_int, [_p, _sz, _sz, _sz, _p, _p, _p, _sz, _p]),
+    "kh_attend_dev_noalloc": (C.c_int, [_p, _sz, _sz, _sz, _p, _p, _p, _sz, _p]),
+    "kh_noalloc_scratch_bytes": (_sz, []),
     "kh_rms_norm_dev": (C.c_int, [_p, _p, _p, _sz, _sz, C.c_float, _p]),
     "kh_rope_dev": (C.c_int, [_p, _p, _p, _sz, _p, _sz, _sz, _sz, C.c_int]),
     "kh_swiglu_dev": (C.c_int, [_p, _p, _p, _sz]),

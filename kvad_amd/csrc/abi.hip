@@ -179,6 +179,8 @@ int kh_init(int device, kh_ctx **out) {
     KH_HIP(hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device));
     KH_HIP(hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking));
     ctx->stream = ctx->own;
+    int rc = scratch_init(device);  // once per device: the no-allocation entry points' array
+    if (rc) return rc;
     KH_HIP(hipDeviceSynchronize());
     *out = ctx.release();
     return KH_OK;
@@ -721,6 +723,17 @@ int kh_attend_dev(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim,
     size_t kv_dim = n_kv_head * head_dim;
     return launch_attend(ctx, (int)n_head, (int)n_kv_head, (int)head_dim, q, k, v, kv_dim, kv_dim, n_positions, out);
 }
+
+int kh_attend_dev_noalloc(kh_ctx *ctx, size_t n_head, size_t n_kv_head, size_t head_dim, const float *q,
+                          const float *k, const float *v, size_t n_positions, float *out) {
+    if (!ctx || !q || !out || (n_positions && (!k || !v))) return fail(KH_EINVAL, "kh_attend_dev_noalloc: null argument");
+    Guard g(ctx);
+    size_t kv_dim = n_kv_head * head_dim;
+    return launch_attend_noalloc(ctx, (int)n_head, (int)n_kv_head, (int)head_dim, q, k, v, kv_dim, kv_dim,
+                                 n_positions, out);
+}
+
+size_t kh_noalloc_scratch_bytes(void) { return scratch_bytes(); }
 
 int kh_attend(kh_ctx *ctx, const kh_kv *kv, size_t layer, size_t n_head, size_t n_kv_head, size_t head_dim,
               const float *q, size_t n_positions, float *out) {

@@ -879,6 +879,68 @@ int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const fl
     return run(ctx, a, head_dim);
 }
 
+// ---------------------------------------------------------------------------
+// Attention for callers that cannot allocate (graph capture, tight serving
+// loops): the split partials live in `scratch`, a static device array of
+// SCRATCH_BYTES per GPU, held from library load until the process ends.
+// Host code never uses the array's name as an address: scratch_init looks up
+// the device address once per device, with that device current, and the
+// launches take that pointer.  Every call on a device shares its array, so
+// calls that overlap on one GPU (two streams, two threads) race; calls on one
+// stream are ordered.  Nothing in it has to start at zero: the split kernel
+// writes every partial the merge reads.
+// ---------------------------------------------------------------------------
+constexpr size_t SCRATCH_BYTES = 8u << 20;
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+namespace {
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[SCRATCH_DEVICES];  // per device: the array's device address
+}  // namespace
+
+int scratch_init(int device) {
+    if (device < 0 || device >= SCRATCH_DEVICES) return fail(KH_EINVAL, "scratch: device index out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[device]) return KH_OK;
+    int cur = -1;
+    KH_HIP(hipGetDevice(&cur));
+    if (cur != device) return fail(KH_EINVAL, "scratch: set up with another device current");
+    void *p = nullptr;
+    KH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(KH_EHIP, "scratch: no device address for the scratch array");
+    g_scratch[device] = p;
+    return KH_OK;
+}
+
+size_t scratch_bytes() { return SCRATCH_BYTES; }
+
+int launch_attend_noalloc(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
+                          const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out) {
+    void *ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (ctx->device >= 0 && ctx->device < SCRATCH_DEVICES) ws = g_scratch[ctx->device];
+    }
+    if (!ws) return fail(KH_EINVAL, "attend_noalloc: this device's scratch array was not set up by kh_init");
+    if (n_positions == 0) {
+        if (n_kv_head <= 0 || n_head <= 0 || n_head % n_kv_head != 0)
+            return fail(KH_EINVAL, "attend: n_head must be a positive multiple of n_kv_head");
+        return launch_fill(ctx, out, (size_t)n_head * head_dim, 0.0f);
+    }
+    AttnArgs a;
+    int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, k, v, kstride, vstride, n_positions, out);
+    if (rc) return rc;
+    if (a.nsplit > 1) {
+        const size_t need = 4 * partial_floats(a.nsplit, n_head, head_dim, a.P) + 1024;
+        if (need > SCRATCH_BYTES)
+            return fail(KH_EINVAL, "attend_noalloc: this call needs " + std::to_string(need) +
+                                       " bytes of scratch, more than the " + std::to_string(SCRATCH_BYTES) +
+                                       " the library holds per device");
+        carve_partials(a, ws, head_dim);
+    }
+    return run(ctx, a, head_dim);
+}
+
 int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
                          const float *v, size_t kstride, size_t vstride, const int32_t *len_dev, int plus_one,
                          size_t max_positions, float *out, void *ws, const AttnRope *rope) {

@@ -331,6 +331,14 @@ int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, c
                          const float *v, size_t kv_stride_k, size_t kv_stride_v, const int32_t *len_dev, int plus_one,
                          size_t max_positions, float *out, void *ws, const AttnRope *rope = nullptr);
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions);
+// Attention with its partials in the library's static per-device scratch
+// array (attend.hip): no allocation.  scratch_init(device), with that device
+// current, looks up the array's device address once per device (kh_init
+// calls it); scratch_bytes() is the array's size.
+int scratch_init(int device);
+size_t scratch_bytes();
+int launch_attend_noalloc(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
+                          const float *v, size_t kstride, size_t vstride, size_t n_positions, float *out);
 // Attention of nb rows at once, each over its own cache (forward_each,
 // llama.rs:258-271): row z's query is q + z * n_head * head_dim, its output
 // out + z * n_head * head_dim, its keys and values rows[z].k / .v (strides
