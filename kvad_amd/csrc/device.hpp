@@ -26,6 +26,25 @@ __device__ __forceinline__ float4 bld16f(rsrc_t r, unsigned off) {
 __device__ __forceinline__ float bldf(rsrc_t r, unsigned off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
+__device__ __forceinline__ int bldi(rsrc_t r, unsigned off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// f32 read through the scalar cache (constant address space): for values a
+// kernel only reads, at wave-uniform addresses.  Such loads are counted apart
+// from vector loads, so they never wait for weight loads in flight.
+typedef const __attribute__((address_space(4))) float const_f32;
+
+// A pointer every lane holds alike, moved to scalar registers.
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+    const unsigned long long v = reinterpret_cast<unsigned long long>(p);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return reinterpret_cast<T *>(((unsigned long long)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // DPP lane movement (gfx9 encodings): quad_perm [1,0,3,2] = xor 1,
 // quad_perm [2,3,0,1] = xor 2, row_half_mirror, row_mirror.

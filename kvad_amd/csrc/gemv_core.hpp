@@ -1,0 +1,361 @@
+// The building blocks of the quantised GEMV kernels (gemv.hip):
+// job tables, the 16-byte weight chunks a lane loads and their block dots
+// (Weight::qrow, crates/llm/src/quant.rs:410-452; q4_row_dots, quant.rs:168-189;
+// Q4_K, crates/gpu/src/mpp.rs:241-315), and the staging of the activation in
+// LDS with its quantisation (QActivation::new, quant.rs:1044-1066).
+#pragma once
+
+#include "common.hpp"
+#include "device.hpp"
+
+namespace kh {
+namespace {
+
+using namespace dev;
+
+constexpr int WAVES_PER_BLOCK = 4;
+constexpr int MAX_JOBS = 24;
+
+struct JobTable {
+    GemvJob j[MAX_JOBS];
+    int n;
+};
+
+// Chunks of 16 bytes per weight row.
+__host__ __device__ inline int chunks_per_row(int prec, int cols) {
+    switch (prec) {
+        case KH_Q8: return cols / 16;
+        case KH_Q4: return cols / 32;
+        case KH_Q4K: return (cols / QK_K) * 8;
+        default: return (cols + 3) / 4;
+    }
+}
+
+__host__ __device__ inline int align16(int n) { return (n + 15) & ~15; }
+
+// silu(g) * u with silu(g) = g / (1 + exp(-g)), as swiglu_inplace computes
+// it (tensor.rs:344-350): one divide, one product.
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    const float silu = g / (1.0f + expf(-g));
+    return silu * u;
+}
+
+// ---------------------------------------------------------------------------
+// activation quantisation: 8 lanes per 32-block, 4 values each
+// ---------------------------------------------------------------------------
+
+// One lane's share of QActivation::new (quant.rs:1051-1064): returns the four
+// codes packed; *scale and *sum are the block's (same in all 8 lanes).
+__device__ __forceinline__ int quantize4(float4 v, float *scale_out, int *sum_out) {
+    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    a = fmaxf(a, dppf<DPP_XOR1>(a));
+    a = fmaxf(a, dppf<DPP_XOR2>(a));
+    a = fmaxf(a, dppf<DPP_HALF_MIRROR>(a));
+    float scale = a / 127.0f;
+    float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    float e[4] = {v.x, v.y, v.z, v.w};
+    int packed = 0, s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float t = e[k] * inv;
+        t = roundf(t);
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        int q = (int)t;
+        s += q;
+        packed |= (q & 0xff) << (8 * k);
+    }
+    s += dpp<DPP_XOR1>(s);
+    s += dpp<DPP_XOR2>(s);
+    s += dpp<DPP_HALF_MIRROR>(s);
+    *scale_out = scale;
+    *sum_out = s;
+    return packed;
+}
+
+// ---------------------------------------------------------------------------
+// the quantised GEMV kernel family
+// ---------------------------------------------------------------------------
+
+constexpr int WPB = 8;  // waves per workgroup (512 threads)
+
+// Activation blocks the LDS stage holds for a launch whose widest row has
+// `C` chunks at `cpl` chunks per lane per segment: the row's blocks, padded
+// with zero blocks up to what the last segment's lanes index.
+__host__ __device__ inline int padded_blocks(int prec, int C, int cpl) {
+    const int nseg = (C + WAVE * cpl - 1) / (WAVE * cpl);
+    const int cp = nseg * WAVE * cpl;
+    return prec == KH_Q8 ? cp / 2 : cp;
+}
+
+// A row group's weight chunks in registers.
+template <int PREC, int CPL, int R>
+struct Chunks {
+    int4 w[R][CPL];
+    int4 h[R][CPL];      // Q4_K block headers
+    float s[R][CPL];     // q8/q4 block scales
+};
+
+template <int PREC, int CPL, int R>
+__device__ __forceinline__ void load_chunks(Chunks<PREC, CPL, R> &c, const rsrc_t &W, const rsrc_t &WS, int r0,
+                                            int cols, int nb, int seg, int lane) {
+    const int gl = seg * WAVE * CPL + lane;  // chunk of t = 0
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const unsigned r = (unsigned)(r0 + i);
+        if constexpr (PREC == KH_Q8) {
+            const unsigned wo = r * (unsigned)cols + (unsigned)gl * 16;
+            const unsigned so = (r * (unsigned)nb + (unsigned)(gl >> 1)) * 4;
+#pragma unroll
+            for (int t = 0; t < CPL; t++) {
+                c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1024, 0));
+                c.s[i][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(WS, so, t * 128, 0));
+            }
+        } else if constexpr (PREC == KH_Q4) {
+            const unsigned wo = r * (unsigned)(cols / 2) + (unsigned)gl * 16;
+            const unsigned so = (r * (unsigned)nb + (unsigned)gl) * 4;
+#pragma unroll
+            for (int t = 0; t < CPL; t++) {
+                c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1024, 0));
+                c.s[i][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(WS, so, t * 256, 0));
+            }
+        } else {
+            const unsigned row_bytes = (unsigned)(cols / QK_K) * Q4K_BYTES;
+            const unsigned bo = r * row_bytes + (unsigned)(gl >> 3) * Q4K_BYTES;
+            const unsigned wo = bo + 16 + 16 * (unsigned)(gl & 7);
+#pragma unroll
+            for (int t = 0; t < CPL; t++) {  // 64 chunks = 8 blocks = 1152 bytes per step
+                c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1152, 0));
+                c.h[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, bo, t * 1152, 0));
+            }
+        }
+    }
+}
+
+// The chunks' contribution to each row's accumulator, in chunk order.
+template <int PREC, int CPL, int R, bool DOTS>
+__device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, float (&acc)[R], const int8_t *sq,
+                                               const float *ssc, const int *ssum, int seg, int lane, int r0,
+                                               int rows, int nb, int C, int32_t *dots) {
+    const int gl = seg * WAVE * CPL + lane;
+    if constexpr (PREC == KH_Q8) {
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int4 a = *reinterpret_cast<const int4 *>(sq + g * 16);
+            const float as = ssc[g >> 1];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                int d = dot4(c.w[i][t].x, a.x, 0);
+                d = dot4(c.w[i][t].y, a.y, d);
+                d = dot4(c.w[i][t].z, a.z, d);
+                d = dot4(c.w[i][t].w, a.w, d);
+                d += dpp<DPP_XOR1>(d);  // the other half of the 32-block
+                float s = c.s[i][t] * as;
+                s = s * (float)d;
+                acc[i] += (lane & 1) ? 0.0f : s;
+                if (DOTS && !(lane & 1) && g < C && r0 + i < rows) dots[(size_t)(r0 + i) * nb + (g >> 1)] = d;
+            }
+        }
+    } else if constexpr (PREC == KH_Q4) {
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int4 alo = *reinterpret_cast<const int4 *>(sq + g * 32);
+            const int4 ahi = *reinterpret_cast<const int4 *>(sq + g * 32 + 16);
+            const float as = ssc[g];
+            const int asum = ssum[g];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int4 q = c.w[i][t];
+                int lo = dot4(q.x & 0x0f0f0f0f, alo.x, 0);
+                lo = dot4(q.y & 0x0f0f0f0f, alo.y, lo);
+                lo = dot4(q.z & 0x0f0f0f0f, alo.z, lo);
+                lo = dot4(q.w & 0x0f0f0f0f, alo.w, lo);
+                int hi = dot4((q.x >> 4) & 0x0f0f0f0f, ahi.x, 0);
+                hi = dot4((q.y >> 4) & 0x0f0f0f0f, ahi.y, hi);
+                hi = dot4((q.z >> 4) & 0x0f0f0f0f, ahi.z, hi);
+                hi = dot4((q.w >> 4) & 0x0f0f0f0f, ahi.w, hi);
+                const int d = lo + hi - 8 * asum;  // quant.rs:187
+                float s = c.s[i][t] * as;
+                s = s * (float)d;
+                acc[i] += s;
+                if (DOTS && g < C && r0 + i < rows) dots[(size_t)(r0 + i) * nb + g] = d;
+            }
+        }
+    } else {
+        // Q4_K: the sub-block a lane finishes is fixed by the lane (64 % 8 == 0)
+        const int half = lane & 1, cc = (lane & 7) >> 1, j = 2 * cc + half;
+        const int sh = 8 * (j & 3);
+        const unsigned hij = j >= 4 ? ~0u : 0u;
+#pragma unroll
+        for (int t = 0; t < CPL; t++) {
+            const int g = gl + t * WAVE;
+            const int b0 = (g >> 3) * 8 + 2 * cc;  // sub-blocks b0 (low nibbles), b0 + 1 (high)
+            const int4 alo = *reinterpret_cast<const int4 *>(sq + b0 * 32 + 16 * half);
+            const int4 ahi = *reinterpret_cast<const int4 *>(sq + (b0 + 1) * 32 + 16 * half);
+            const float as = ssc[b0 + half];
+            const int asum = ssum[b0 + half];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int4 q = c.w[i][t];
+                int lo = dot4(q.x & 0x0f0f0f0f, alo.x, 0);
+                lo = dot4(q.y & 0x0f0f0f0f, alo.y, lo);
+                lo = dot4(q.z & 0x0f0f0f0f, alo.z, lo);
+                lo = dot4(q.w & 0x0f0f0f0f, alo.w, lo);
+                int hi = dot4((q.x >> 4) & 0x0f0f0f0f, ahi.x, 0);
+                hi = dot4((q.y >> 4) & 0x0f0f0f0f, ahi.y, hi);
+                hi = dot4((q.z >> 4) & 0x0f0f0f0f, ahi.z, hi);
+                hi = dot4((q.w >> 4) & 0x0f0f0f0f, ahi.w, hi);
+                lo += dpp<DPP_XOR1>(lo);
+                hi += dpp<DPP_XOR1>(hi);
+                const int d = half ? hi : lo;
+                // 6-bit scale and minimum of sub-block j (mpp.rs:276-282)
+                const int4 h = c.h[i][t];
+                unsigned sc, mn;
+                q4k_scale_min(h, sh, hij, sc, mn);
+                const float dl = half_bits_to_float((unsigned)h.x) * (float)sc;
+                const float ml = half_bits_to_float((unsigned)h.x >> 16) * (float)mn;
+                float t1 = dl * (float)d;
+                float t2 = ml * (float)asum;
+                float s = t1 - t2;
+                s = as * s;
+                acc[i] += s;
+                if (DOTS && g < C && r0 + i < rows) dots[(size_t)(r0 + i) * nb + (g >> 3) * 8 + j] = d;
+            }
+        }
+    }
+}
+
+// Activation staging.  A thread's activation loads are issued before the
+// workgroup's first weight loads: vector loads complete in order, so an
+// activation load issued after them would wait for HBM.  The input kind is a
+// template parameter so that a launch holds registers only for what it loads.
+constexpr int IN_F32 = 0;       // f32 x
+constexpr int IN_SWIGLU = 1;    // swiglu(xf, xf2)
+constexpr int IN_CODES = 2;     // int8 codes, scales and sums made elsewhere
+constexpr int IN_NORM = 3;      // rms_norm(xf) * norm_w
+
+// SB float4s (or code int4s) per thread per batch: 4, or 8 where the
+// kernel's weight registers leave room (one batch then covers 16384 columns).
+template <int KIND, int SB>
+struct Stage {
+    float4 v[SB];                    // f32 input, or int4 codes
+    float4 u[KIND == IN_F32 ? 1 : SB];  // swiglu's second input, norm weights, or (scale, sum)
+};
+
+__device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// The thread's loads: float4 c = k * T + tid of the f32 input (block c >> 3),
+// or int4 c of the codes and scale and sum c.  One such batch covers the
+// whole activation (the launcher checks it: stage_fits).
+template <int KIND, int SB, int NWV>
+__device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &st, int nb, int tid) {
+    constexpr int T = WAVE * NWV;
+    // buffer loads: past the input's end they return zeros, with no branch
+    if constexpr (KIND == IN_CODES) {
+        const rsrc_t Q = rsrc(job.xq, (size_t)nb * BLOCK), S = rsrc(job.xs, (size_t)nb * 4),
+                     M = rsrc(job.xsum, (size_t)nb * 4);
+#pragma unroll
+        for (int k = 0; k < SB; k++) {
+            const unsigned c = (unsigned)(k * T + tid);
+            st.v[k] = __builtin_bit_cast(float4, bld16(Q, c * 16));
+            st.u[k] = make_float4(bldf(S, c * 4), __builtin_bit_cast(float, bldi(M, c * 4)), 0.f, 0.f);
+        }
+    } else {
+        const rsrc_t X = rsrc(job.xf, (size_t)nb * BLOCK * 4);
+        const void *x2 = KIND == IN_SWIGLU ? (const void *)job.xf2 : KIND == IN_NORM ? (const void *)job.norm_w : job.xf;
+        const rsrc_t X2 = rsrc(x2, (size_t)nb * BLOCK * 4);
+#pragma unroll
+        for (int k = 0; k < SB; k++) {
+            const unsigned c = (unsigned)(k * T + tid);
+            st.v[k] = __builtin_bit_cast(float4, bld16(X, c * 16));
+            if constexpr (KIND != IN_F32) st.u[k] = __builtin_bit_cast(float4, bld16(X2, c * 16));
+        }
+    }
+}
+
+// Stages the activation of `job` in LDS for a workgroup: int8 codes, scales
+// and code sums of PB blocks (blocks past nb are zero).  From f32 input it
+// quantises as QActivation::new (quant.rs:1044-1066), first applying
+// rms_norm (tensor.rs:329-333) for IN_NORM or swiglu(xf, xf2)
+// (tensor.rs:344-350) for IN_SWIGLU; codes made elsewhere are copied.  `st` holds batch 0,
+// loaded by stage_load.  Every workgroup computes the same values.
+template <int KIND, int SB, int NWV>
+__device__ __forceinline__ void stage_activation(const GemvJob &job, Stage<KIND, SB> &st, int8_t *sq, float *ssc,
+                                                 int *ssum, int PB, int nb, int cols, int tid, int lane, int wv) {
+    constexpr int T = WAVE * NWV;
+    if constexpr (KIND == IN_CODES) {
+#pragma unroll
+        for (int k = 0; k < SB; k++) {
+            const int c = k * T + tid;
+            if (c < PB * 2) reinterpret_cast<int4 *>(sq)[c] = __builtin_bit_cast(int4, st.v[k]);
+            if (c < PB) {
+                ssc[c] = st.u[k].x;
+                ssum[c] = __builtin_bit_cast(int, st.u[k].y);
+            }
+        }
+        return;
+    } else {
+        constexpr bool nw = KIND == IN_NORM;
+        float inv = 1.0f;
+        if constexpr (nw) {
+            // Sum of squares over the thread's float4s in index order, then
+            // over the wave, then over the waves in order: every workgroup
+            // gets the same sum.
+            __shared__ float s_ss[NWV];
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < SB; k++) {
+                const float4 v = st.v[k];
+                const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+                ss = ss + ((a + b) + (c + d));
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) s_ss[wv] = ss;
+            __syncthreads();
+            float t = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NWV; w++) t = t + s_ss[w];
+            inv = 1.0f / sqrtf(t / (float)cols + job.norm_eps);
+        }
+#pragma unroll
+        for (int k = 0; k < SB; k++) {
+            const int i = k * T + tid, b = i >> 3;
+            if (b >= PB) break;  // uniform per 8-lane block group, and past every later k
+            float4 x = st.v[k];
+            if constexpr (nw) {
+                const float4 w = st.u[k];  // zeros past the end, like x
+                x = make_float4((x.x * inv) * w.x, (x.y * inv) * w.y, (x.z * inv) * w.z, (x.w * inv) * w.w);
+            }
+            if constexpr (KIND == IN_SWIGLU) {
+                const float4 u = st.u[k];
+                x = make_float4(swiglu1(x.x, u.x), swiglu1(x.y, u.y), swiglu1(x.z, u.z), swiglu1(x.w, u.w));
+            }
+            float scale;
+            int s;
+            const int packed = quantize4(x, &scale, &s);
+            reinterpret_cast<int *>(sq)[i] = packed;
+            if ((tid & 7) == 0) {
+                ssc[b] = scale;
+                ssum[b] = s;
+            }
+        }
+    }
+}
+
+// Whether one staging batch (SB loads per thread) covers PB blocks.
+// A kernel stages 8 loads per thread where its weight registers leave room
+// (CPL >= 4) or where it is built WIDE (rows of several segments), else 4.
+__host__ __device__ constexpr int stage_batch(int cpl, bool wide) { return cpl >= 4 || wide ? 8 : 4; }
+__host__ __device__ inline bool stage_fits(int kind, int PB, int sb, int nwv) {
+    const int cap = sb * WAVE * nwv;
+    return kind == IN_CODES ? PB * 2 <= cap : PB * 8 <= cap;
+}
+
+// The input kind of a job.
+__host__ __device__ inline int input_kind(const GemvJob &j) {
+    return j.xf ? (j.xf2 ? IN_SWIGLU : j.norm_w ? IN_NORM : IN_F32) : IN_CODES;
+}
+
+}  // namespace
+}  // namespace kh
