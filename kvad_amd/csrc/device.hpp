@@ -46,6 +46,15 @@ __device__ __forceinline__ T *uniform_ptr(T *p) {
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// a * b for operands the caller knows to fit in 24 signed bits: one
+// full-rate v_mul_i32_i24 (the compiler would otherwise mask the operands or
+// use the quarter-rate 32-bit multiply).
+__device__ __forceinline__ int mul24(int a, int b) {
+    int r;
+    asm("v_mul_i32_i24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // DPP lane movement (gfx9 encodings): quad_perm [1,0,3,2] = xor 1,
 // quad_perm [2,3,0,1] = xor 2, row_half_mirror, row_mirror.
 template <int CTRL>

@@ -373,8 +373,7 @@ __device__ __forceinline__ void compute_multi(const Chunks<PREC, CPL, 1> &c, flo
         }
     } else {
         const int half = lane & 1, cc = (lane & 7) >> 1, j = 2 * cc + half;
-        const int sh = 8 * (j & 3);
-        const unsigned hij = j >= 4 ? ~0u : 0u;
+        const Q4kLane L = q4k_lane(j);
 #pragma unroll
         for (int t = 0; t < CPL; t++) {
             const int g = gl + t * WAVE;
@@ -385,7 +384,7 @@ __device__ __forceinline__ void compute_multi(const Chunks<PREC, CPL, 1> &c, flo
                               (q.w >> 4) & 0x0f0f0f0f};
             const int4 h = c.h[0][t];
             unsigned scb, mnb;
-            q4k_scale_min(h, sh, hij, scb, mnb);
+            q4k_scale_min_bfe(h, L, scb, mnb);
             const float dl = half_bits_to_float((unsigned)h.x) * (float)scb;
             const float ml = half_bits_to_float((unsigned)h.x >> 16) * (float)mnb;
 #pragma unroll

@@ -98,37 +98,69 @@ struct Chunks {
 template <int PREC, int CPL, int R>
 __device__ __forceinline__ void load_chunks(Chunks<PREC, CPL, R> &c, const rsrc_t &W, const rsrc_t &WS, int r0,
                                             int cols, int nb, int seg, int lane) {
-    const int gl = seg * WAVE * CPL + lane;  // chunk of t = 0
+    // Offsets are a row's part, the same in every lane (made scalar with
+    // readfirstlane, so the compiler cannot fold it into a per-lane multiply),
+    // plus the lane's part, the same at every step.  The whole offset stays
+    // in the vector operand, which the buffer's range check covers.
 #pragma unroll
     for (int i = 0; i < R; i++) {
         const unsigned r = (unsigned)(r0 + i);
         if constexpr (PREC == KH_Q8) {
-            const unsigned wo = r * (unsigned)cols + (unsigned)gl * 16;
-            const unsigned so = (r * (unsigned)nb + (unsigned)(gl >> 1)) * 4;
+            // chunk gl = seg * 64 * CPL + lane: weights 16 gl.., block gl / 2
+            const unsigned uw = __builtin_amdgcn_readfirstlane(r * (unsigned)cols + (unsigned)(seg * CPL) * 1024u);
+            const unsigned us = __builtin_amdgcn_readfirstlane(r * (unsigned)nb * 4u + (unsigned)(seg * CPL) * 128u);
+            const unsigned wo = uw + (unsigned)lane * 16u, so = us + (unsigned)(lane >> 1) * 4u;
 #pragma unroll
             for (int t = 0; t < CPL; t++) {
                 c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1024, 0));
                 c.s[i][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(WS, so, t * 128, 0));
             }
         } else if constexpr (PREC == KH_Q4) {
-            const unsigned wo = r * (unsigned)(cols / 2) + (unsigned)gl * 16;
-            const unsigned so = (r * (unsigned)nb + (unsigned)gl) * 4;
+            const unsigned uw = __builtin_amdgcn_readfirstlane(r * (unsigned)(cols / 2) + (unsigned)(seg * CPL) * 1024u);
+            const unsigned us = __builtin_amdgcn_readfirstlane(r * (unsigned)nb * 4u + (unsigned)(seg * CPL) * 256u);
+            const unsigned wo = uw + (unsigned)lane * 16u, so = us + (unsigned)lane * 4u;
 #pragma unroll
             for (int t = 0; t < CPL; t++) {
                 c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1024, 0));
                 c.s[i][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(WS, so, t * 256, 0));
             }
         } else {
+            // chunk gl: block gl / 8 (= seg * 8 * CPL + lane / 8), 16 bytes at
+            // 16 + 16 (lane & 7) of it; 64 chunks = 8 blocks = 1152 bytes per t
             const unsigned row_bytes = (unsigned)(cols / QK_K) * Q4K_BYTES;
-            const unsigned bo = r * row_bytes + (unsigned)(gl >> 3) * Q4K_BYTES;
-            const unsigned wo = bo + 16 + 16 * (unsigned)(gl & 7);
+            const unsigned ub = __builtin_amdgcn_readfirstlane(r * row_bytes + (unsigned)(seg * CPL) * 8u * Q4K_BYTES);
+            const unsigned bo = ub + (unsigned)(lane >> 3) * Q4K_BYTES;
+            const unsigned wo = bo + 16u + 16u * (unsigned)(lane & 7);
 #pragma unroll
-            for (int t = 0; t < CPL; t++) {  // 64 chunks = 8 blocks = 1152 bytes per step
+            for (int t = 0; t < CPL; t++) {
                 c.w[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, wo, t * 1152, 0));
                 c.h[i][t] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(W, bo, t * 1152, 0));
             }
         }
     }
+}
+
+// The 6-bit scale and minimum of Q4_K sub-block j (mpp.rs:276-282) from
+// bytes 4..15 of the block header (h.y = bytes 4..7, h.z = 8..11, h.w =
+// 12..15, i.e. s[0..3], s[4..7], s[8..11]), with lane constants: j < 4 reads
+// s[j] & 63 and s[j+4] & 63; j >= 4 reads the low four bits from s[j+4] and
+// the top two from s[j-4] and s[j].  Two selects, four bit-field extracts and
+// two shift-ors.
+struct Q4kLane {
+    bool hi4;           // j >= 4
+    unsigned o1, w1;    // scale's low bits: offset and width in hi4 ? h.w : h.y
+    unsigned o3;        // minimum's low bits: offset (same width) in hi4 ? h.w : h.z
+    unsigned o2, w2;    // top two bits (j >= 4; width 0 otherwise) in h.y / h.z
+};
+__device__ __forceinline__ Q4kLane q4k_lane(int j) {
+    const unsigned jj = (unsigned)(j & 3);
+    const bool hi4 = j >= 4;
+    return {hi4, 8 * jj, hi4 ? 4u : 6u, hi4 ? 8 * jj + 4 : 8 * jj, 8 * jj + 6, hi4 ? 2u : 0u};
+}
+__device__ __forceinline__ void q4k_scale_min_bfe(const int4 &h, const Q4kLane &L, unsigned &sc, unsigned &mn) {
+    const unsigned y = (unsigned)h.y, z = (unsigned)h.z, w = (unsigned)h.w;
+    sc = __builtin_amdgcn_ubfe(L.hi4 ? w : y, L.o1, L.w1) | (__builtin_amdgcn_ubfe(y, L.o2, L.w2) << 4);
+    mn = __builtin_amdgcn_ubfe(L.hi4 ? w : z, L.o3, L.w1) | (__builtin_amdgcn_ubfe(z, L.o2, L.w2) << 4);
 }
 
 // The chunks' contribution to each row's accumulator, in chunk order.
@@ -185,8 +217,7 @@ __device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, fl
     } else {
         // Q4_K: the sub-block a lane finishes is fixed by the lane (64 % 8 == 0)
         const int half = lane & 1, cc = (lane & 7) >> 1, j = 2 * cc + half;
-        const int sh = 8 * (j & 3);
-        const unsigned hij = j >= 4 ? ~0u : 0u;
+        const Q4kLane L = q4k_lane(j);
 #pragma unroll
         for (int t = 0; t < CPL; t++) {
             const int g = gl + t * WAVE;
@@ -212,11 +243,14 @@ __device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, fl
                 // 6-bit scale and minimum of sub-block j (mpp.rs:276-282)
                 const int4 h = c.h[i][t];
                 unsigned sc, mn;
-                q4k_scale_min(h, sh, hij, sc, mn);
-                const float dl = half_bits_to_float((unsigned)h.x) * (float)sc;
-                const float ml = half_bits_to_float((unsigned)h.x >> 16) * (float)mn;
-                float t1 = dl * (float)d;
-                float t2 = ml * (float)asum;
+                q4k_scale_min_bfe(h, L, sc, mn);
+                // (d * sc) * dot rounded once, as f32(d) * sc is exact; sc * dot
+                // (|dot| < 2^16, sc < 64) and mn * asum are exact 24-bit products,
+                // so d * (sc * dot) is the same single rounding
+                const int isc = mul24((int)sc, d);
+                const int imn = mul24((int)mn, asum);
+                float t1 = half_bits_to_float((unsigned)h.x) * (float)isc;
+                float t2 = half_bits_to_float((unsigned)h.x >> 16) * (float)imn;
                 float s = t1 - t2;
                 s = as * s;
                 acc[i] += s;
