@@ -58,6 +58,7 @@ def _declare(lib: C.CDLL) -> C.CDLL:
         "kvo_matvec_q8": (None, [_p, _p, _sz, _sz, _p, _p, _p]),
         "kvo_matvec_q4": (None, [_p, _p, _sz, _sz, _p, _p, _p]),
         "kvo_matvec_q4k": (None, [_p, _sz, _sz, _p, _p, _p]),
+        "kvo_matvec_q4k_fast": (None, [_p, _sz, _sz, _p, _p, _p]),
         "kvo_matvec_f32": (None, [_p, _sz, _sz, _p, _p, _p]),
         "kvo_matvec_dequant": (None, [C.c_int, _p, _p, _sz, _sz, _p, _p]),
         "kvo_matmul_q8": (None, [_p, _p, _sz, _sz, _p, _sz, _p, _p]),
@@ -228,6 +229,15 @@ def matvec_q4k(blocks, rows, cols, x, bias=None, L=None) -> np.ndarray:
     y = np.empty(rows, np.float32)
     b = None if bias is None else _c(bias, np.float32)
     L.kvo_matvec_q4k(P(_c(blocks, np.uint8)), rows, cols, P(_c(x, np.float32)), P(b), P(y))
+    return y
+
+
+def matvec_q4k_fast(blocks, rows, cols, x, bias=None, L=None) -> np.ndarray:
+    """matvec_q4k organised for the CPU baseline (equal to the bit)."""
+    L = L or lib
+    y = np.empty(rows, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    L.kvo_matvec_q4k_fast(P(_c(blocks, np.uint8)), rows, cols, P(_c(x, np.float32)), P(b), P(y))
     return y
 
 

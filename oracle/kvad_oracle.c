@@ -505,6 +505,57 @@ void kvo_matvec_q4k(const uint8_t *blocks, size_t rows, size_t cols, const float
     add_bias(y, bias, rows);
 }
 
+/* The same product as kvo_matvec_q4k, organised for the CPU baseline rather
+ * than for reading against the reference: per super-block the eight (dl, ml)
+ * pairs are decoded once, and each 32-byte group of codes is unpacked once
+ * into its two sub-blocks' dots (contiguous int loops the compiler
+ * vectorises).  The integers and every rounded step of pass 2 are those of
+ * kvo_matvec_q4k, so the outputs are equal to the bit (tests/test_oracle.py). */
+void kvo_matvec_q4k_fast(const uint8_t *blocks, size_t rows, size_t cols, const float *x, const float *bias,
+                         float *y) {
+    size_t nsb = cols / KVO_QK_K;
+    qact_t a = qact_alloc(x, 1, cols);
+#pragma omp parallel for schedule(static) num_threads(kvo_get_threads())
+    for (size_t r = 0; r < rows; r++) {
+        const uint8_t *row = blocks + r * nsb * KVO_Q4K_BYTES;
+        float s[2] = {0.0f, 0.0f};
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t *blk = row + sb * KVO_Q4K_BYTES;
+            const int8_t *xq = a.qs + sb * KVO_QK_K;
+            uint16_t d16, m16;
+            memcpy(&d16, blk, 2);
+            memcpy(&m16, blk + 2, 2);
+            const float d = kvo_f16_to_f32(d16), dmin = kvo_f16_to_f32(m16);
+            int32_t dot[8];
+            for (int c = 0; c < 4; c++) {
+                const uint8_t *q = blk + 16 + 32 * c;
+                const int8_t *xl = xq + 64 * c, *xh = xq + 64 * c + 32;
+                int32_t lo = 0, hi = 0;
+                for (int l = 0; l < 32; l++) {
+                    lo += (int32_t)(q[l] & 0x0f) * (int32_t)xl[l];
+                    hi += (int32_t)(q[l] >> 4) * (int32_t)xh[l];
+                }
+                dot[2 * c] = lo;
+                dot[2 * c + 1] = hi;
+            }
+            for (int j = 0; j < 8; j++) {
+                const size_t b = sb * 8 + j;
+                uint8_t sc, m;
+                kvo_q4k_scale_min(blk + 4, j, &sc, &m);
+                const float dl = d * (float)sc, ml = dmin * (float)m;
+                float t1 = dl * (float)dot[j];
+                float t2 = ml * (float)a.sums[b];
+                float t = t1 - t2;
+                t = a.scales[b] * t;
+                s[b & 1] = s[b & 1] + t;
+            }
+        }
+        y[r] = s[0] + s[1];
+    }
+    qact_free(&a);
+    add_bias(y, bias, rows);
+}
+
 static inline float matvec_f32_row(const float *row, const float *x, size_t cols) {
     /* tensor.rs:62-75: four lanes, pairwise combine, serial tail */
     float acc[4] = {0, 0, 0, 0};

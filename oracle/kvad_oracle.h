@@ -70,6 +70,9 @@ void kvo_matvec_q4(const float *scales, const uint8_t *qs, size_t rows, size_t c
                    const float *x, const float *bias, float *y);
 void kvo_matvec_q4k(const uint8_t *blocks, size_t rows, size_t cols, const float *x,
                     const float *bias, float *y);
+/* kvo_matvec_q4k organised for the CPU baseline; equal outputs to the bit. */
+void kvo_matvec_q4k_fast(const uint8_t *blocks, size_t rows, size_t cols, const float *x, const float *bias,
+                         float *y);
 /* tensor::matvec_bt (tensor.rs:56-79) */
 void kvo_matvec_f32(const float *w, size_t rows, size_t cols, const float *x, const float *bias, float *y);
 /* matvec_bt_dequant (quant.rs:522-589), the KVAD_DEQUANT=1 baseline; precision 1=q8, 2=q4 */

@@ -448,6 +448,24 @@ def test_q4k_block_dots_and_gemv_equal_the_exact_value():
     assert np.max(np.abs(y - ywant)) <= 1e-6 * np.max(np.abs(ywant))
 
 
+def test_q4k_cpu_baseline_loop_equals_the_oracle_to_the_bit():
+    # the CPU baseline's loop (scales decoded once per sub-block) computes the
+    # oracle's integers and pass-2 steps; at several widths and thread counts
+    for rows, cols in [(1, 256), (37, 512), (64, 4096), (5, 14336)]:
+        blocks = O.quantize_q4k(O.normal(30 + rows, rows * cols, 0.02), rows, cols)
+        x = O.normal(31 + cols, cols)
+        x[:32] *= 500.0
+        bias = O.normal(32, rows)
+        want = O.matvec_q4k(blocks, rows, cols, x, bias)
+        np.testing.assert_array_equal(O.matvec_q4k_fast(blocks, rows, cols, x, bias), want)
+        old = O.threads()
+        try:
+            O.set_threads(1)
+            np.testing.assert_array_equal(O.matvec_q4k_fast(blocks, rows, cols, x, bias), want)
+        finally:
+            O.set_threads(old)
+
+
 def test_f16_conversion_round_trips_and_rounds_to_nearest_even():
     for v in [0.0, 1.0, -2.5, 65504.0, 6.1035156e-05, 5.9604645e-08, 1e-3, 0.333]:
         h = O.f32_to_f16(v)
