@@ -194,6 +194,7 @@ int kh_free(kh_ctx *ctx) {
         if (ctx->ws.ptr) (void)hipFree(ctx->ws.ptr);
         if (ctx->io.ptr) (void)hipFree(ctx->io.ptr);
         if (ctx->moe.ptr) (void)hipFree(ctx->moe.ptr);
+        if (ctx->gemm.ptr) (void)hipFree(ctx->gemm.ptr);
         if (ctx->own) (void)hipStreamDestroy(ctx->own);
     }
     delete ctx;

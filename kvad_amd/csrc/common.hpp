@@ -66,6 +66,7 @@ struct kh_ctx {
     kh::Workspace ws;        // per-call scratch (activations, partials)
     kh::Workspace io;        // staging for host-pointer calls
     kh::Workspace moe;       // mixture-of-experts intermediates
+    kh::Workspace gemm;      // split-K partials, after a zeroed block of tile counters
 };
 
 struct kh_weight {
@@ -246,8 +247,17 @@ struct GemmArgs {
     const int32_t *gather;
     const void *const *wtab;
     const float *const *wstab;
+    // split-K (ungrouped launches): ksplit > 1 splits the k-stages over grid
+    // z; split z writes its tile to part[z][M][N], and the last of a tile's
+    // splits to finish (tile_ctr, left at 0 again) adds them in split order
+    int ksplit;
+    float *part;
+    unsigned *tile_ctr;
 };
 int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m);
+// Allocates the split-K workspace now (a GEMM captured into a graph splits
+// only when it was allocated before the capture).
+int gemm_split_reserve(kh_ctx *ctx);
 
 // Operator bodies on device pointers (abi.hip), for the layers built on them.
 int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots);

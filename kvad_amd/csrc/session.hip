@@ -814,6 +814,7 @@ int kh_llm_forward_each(kh_ctx *ctx, kh_llm *m, size_t n, const int32_t *tokens,
     // it is captured once per n and replayed
     auto it = m->rows_graphs.find(n);
     if (it == m->rows_graphs.end()) {
+        if ((rc = gemm_split_reserve(ctx))) return rc;
         KH_HIP(hipStreamSynchronize(ctx->stream));
         hipGraph_t g = nullptr;
         KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));

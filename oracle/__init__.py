@@ -397,8 +397,9 @@ class Llm:
     of crates/llm/src/model/llama.rs:224-289 (run_rows, m = 1) between the
     embedding and the head (llama.rs:384-415), every operator the oracle's.
     Weights are q8 (scales, qs) pairs, 1-tuples (f32 data,) -- Precision::F32,
-    tensor::matvec_bt (tensor.rs:56-79) -- or ("q4k", blocks) for Q4_K layer
-    weights (matvec_q4k); norms and biases f32 arrays."""
+    tensor::matvec_bt (tensor.rs:56-79) -- ("q4k", blocks) for Q4_K layer
+    weights (matvec_q4k) or ("q4", scales, qs) for q4 ones (matvec_q4); norms
+    and biases f32 arrays."""
 
     def __init__(self, spec: dict, layers: list, embed, final_norm, lm_head=None, cos_t=None, sin_t=None):
         self.s, self.layers, self.embed, self.final_norm = spec, layers, embed, final_norm
@@ -420,6 +421,8 @@ class Llm:
                 return matvec_f32(w[0], rows, cols, x, bias)
             if isinstance(w[0], str) and w[0] == "q4k":
                 return matvec_q4k(w[1], rows, cols, x, bias)
+            if isinstance(w[0], str) and w[0] == "q4":
+                return matvec_q4(w[1], w[2], rows, cols, x, bias)
             return matvec_q8(*w, rows, cols, x, bias)
 
         if len(self.embed) == 1:                                # Weight::row, llama.rs:384-391

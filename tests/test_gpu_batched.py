@@ -59,6 +59,10 @@ VARIANTS = {
     "qwen3_q8": dict(bias=False, qk_norm=True, tied=False),
     "llama_hd128_q8": dict(bias=False, interleaved=True, n_head=8, n_kv_head=2, head_dim=128, n_embd=256),
     "qwen2_f32": dict(bias=True, tied=False, prec="f32"),  # every projection on the f32 GEMM / GEMV
+    # Q4_K and q4 layer weights (embedding and head q8), 256-multiple widths
+    "llama_q4k": dict(bias=False, interleaved=True, n_head=4, n_kv_head=2, head_dim=64, n_embd=256, n_ff=512,
+                      prec="q4k"),
+    "qwen2_q4": dict(bias=True, prec="q4"),
 }
 
 
@@ -137,12 +141,24 @@ def test_a_batch_of_one_is_a_token_and_a_batch_of_none_is_nothing(ctx):
     assert got.shape == (0, m.spec.vocab) and nxt.size == 0
 
 
-@pytest.mark.parametrize("n", [8, 13, 40])
-def test_many_rows_on_the_multi_token_gemv_and_the_gemm(ctx, n):
-    # 8 rows: one multi-token GEMV launch per projection group; 13: two
-    # launches of up to eight rows; 40: the int8 GEMM, residual added in its epilogue
-    say("forward_each rows", n)
-    m, mk = build(ctx, 740 + n)
+ROW_CASES = {
+    "q8_8": (8, {}), "q8_13": (13, {}), "q8_40": (40, {}),
+    # the down projection's 1024-wide input is eight k-stages: at 40 rows the
+    # GEMM splits them over the grid and the last split adds the residual
+    "q8_40_split": (40, dict(n_ff=1024)),
+    "q4k_5": (5, dict(prec="q4k", n_embd=256, n_ff=512)), "q4k_40": (40, dict(prec="q4k", n_embd=256, n_ff=1024)),
+    "q4_6": (6, dict(prec="q4")), "q4_40": (40, dict(prec="q4", n_ff=1024)),
+}
+
+
+@pytest.mark.parametrize("case", list(ROW_CASES))
+def test_many_rows_on_the_multi_token_gemv_and_the_gemm(ctx, case):
+    # up to 8 rows: one multi-token GEMV launch per projection group; 13:
+    # two launches of up to eight rows; 40: the int8 GEMM, residual added in
+    # its epilogue (q8, q4 and Q4_K layer weights)
+    n, kw = ROW_CASES[case]
+    say("forward_each rows", case)
+    m, mk = build(ctx, 740 + n, **kw)
     prompts = [[(7 * i + j) % 500 for j in range(1 + (5 * i) % 11)] for i in range(n)]
     parked = set_aside(m, prompts)
     refs = [mk() for _ in prompts]

@@ -61,6 +61,51 @@ def test_qwen_prefill_shape(ctx, prec):
     close(w.matmul_bt(xs, m), oracle_matmul(prec, parts, rows, cols, xs, m))
 
 
+# (m tokens, rows, cols) with fewer tiles than CUs and at least four k-stages
+# of 128: the k-stages split over the grid and the last split of each tile
+# adds the others' partials; rows not a multiple of 4 take the scalar tail
+SPLIT_SHAPES = [(32, 896, 4864), (100, 257, 1024), (9, 130, 2048), (128, 896, 4864)]
+
+
+@pytest.mark.parametrize("prec", ["q8", "q4", "q4k"])
+def test_split_k_matches_the_oracle(ctx, prec, monkeypatch):
+    for m, rows, cols in SPLIT_SHAPES:
+        w, parts = make(ctx, prec, rows, cols, seed=m + rows)
+        xs = O.normal(m + 1, m * cols)
+        bias = O.normal(rows + 2, rows)
+        want = oracle_matmul(prec, parts, rows, cols, xs, m, bias)
+        for ks in ("", "1", "3", "16"):  # automatic, none, forced
+            say("matmul split-k", prec, m, rows, cols, ks or "auto")
+            monkeypatch.setenv("KVAD_GEMM_KSPLIT", ks)
+            got = w.matmul_bt(xs, m, bias)
+            close(got, want)
+            np.testing.assert_array_equal(w.matmul_bt(xs, m, bias), got)  # the same order every call
+
+
+def test_split_k_partials_of_exact_integers_are_exact(ctx, monkeypatch):
+    # scale-1 q8 blocks (the block maximum sits where the other operand is 0)
+    # and small activation codes: every partial and every sum of partials is
+    # an integer below 2^24, so however the k-stages split the result is the
+    # exact integer product
+    rng = np.random.default_rng(5)
+    m, rows, cols = 70, 150, 4096
+    x = rng.integers(-3, 4, size=(m, cols)).astype(np.float32)
+    x[:, ::32] = 127.0
+    wi = rng.integers(-127, 128, size=(rows, cols)).astype(np.float32)
+    wi[:, ::32] = 0.0
+    wi[:, 5::32] = -127.0
+    s, q = O.quantize_q8(wi.ravel(), rows, cols)
+    assert np.all(s == 1.0)
+    w = K.Weight.from_q8(ctx, rows, cols, s, q)
+    want = (x.astype(np.int64) @ q.reshape(rows, cols).astype(np.int64).T).astype(np.float64)
+    assert np.max(np.abs(want)) < 2**24
+    for ks in ("1", "2", "5", "16", "32"):
+        say("split-k exact", ks)
+        monkeypatch.setenv("KVAD_GEMM_KSPLIT", ks)
+        got = w.matmul_bt(x.ravel(), m).reshape(m, rows)
+        np.testing.assert_array_equal(got.astype(np.float64), want)
+
+
 @pytest.mark.parametrize("prec", ["q8", "q4", "q4k"])
 def test_integer_block_dots_are_exact(ctx, prec):
     # Weights and activations whose every block holds its extreme (+-127 for

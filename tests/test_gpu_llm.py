@@ -35,14 +35,17 @@ def build(ctx, seed, n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=64, 
     qd, kvd = n_head * head_dim, n_kv_head * head_dim
 
     def q8(rows, cols, scale=sd, layer=False):
-        # f32 weights (Precision::F32) when prec == "f32"; Q4_K layer
-        # weights (the embedding and head stay q8) when prec == "q4k"
+        # f32 weights (Precision::F32) when prec == "f32"; Q4_K or q4 layer
+        # weights (the embedding and head stay q8) when prec == "q4k" / "q4"
         data = O.normal(next(rng), rows * cols, scale)
         if prec == "f32":
             return (data,), K.Weight.from_f32(ctx, data.reshape(rows, cols))
         if prec == "q4k" and layer:
             b = O.quantize_q4k(data, rows, cols)
             return ("q4k", b), K.Weight.from_q4k(ctx, rows, cols, b)
+        if prec == "q4" and layer:
+            s4, q4 = O.quantize_q4(data, rows, cols)
+            return ("q4", s4, q4), K.Weight.from_q4(ctx, rows, cols, s4, q4)
         s, q = O.quantize_q8(data, rows, cols)
         return (s, q), K.Weight.from_q8(ctx, rows, cols, s, q)
 
