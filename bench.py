@@ -69,6 +69,8 @@ def parse():
                     help="run one secondary workload alone (for per-kernel rocprofv3 summaries) and print its figures")
     ap.add_argument("--counters", type=int, default=0, metavar="MIB",
                     help="only run a MIB-sized copy and two eager steps of the GEMV kernels (for rocprofv3 --pmc)")
+    ap.add_argument("--gemm-counters", action="store_true",
+                    help="only run three eager q8 prefill GEMMs per shape (for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -133,6 +135,24 @@ def main() -> int:
     ctx.reserve(64 << 20)
     gen = torch.Generator(device=dev)
     gen.manual_seed(20251201)
+
+    if args.gemm_counters:
+        # a workload for rocprofv3 --pmc: the q8 prefill GEMM at the two
+        # prefill configurations and at 32 rows of mlp.down (k-stages split)
+        shapes = ((512, 896, 4864), (2048, 4096, 14336), (32, 4864, 896))
+        for (m, k, n) in shapes:
+            f = torch.randn(n, k, device=dev, generator=gen) * 0.02
+            xs = torch.randn(m, k, device=dev, generator=gen)
+            y = torch.empty(m, n, device=dev)
+            with torch.cuda.stream(stream):
+                w = K.Weight.quantize_dev(ctx, n, k, f.data_ptr(), K.Q8)
+                for _ in range(3):
+                    w.matmul_bt_dev(xs.data_ptr(), m, y.data_ptr())
+            torch.cuda.synchronize()
+            del w, f, xs, y
+        print(json.dumps({"gemm_counters_run": {"shapes_mkn": shapes, "calls_each": 3}}), flush=True)
+        ctx.set_stream(None)
+        return 0
 
     if args.only:
         res = secondary(torch, K, ctx, stream, dev, gen, args, only=args.only)

@@ -258,6 +258,9 @@ int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, 
 // Allocates the split-K workspace now (a GEMM captured into a graph splits
 // only when it was allocated before the capture).
 int gemm_split_reserve(kh_ctx *ctx);
+// Sets a's split-K fields for an ungrouped launch of tile_m-token tiles when
+// it has fewer tiles than the chip has CUs (ksplit 0: no split).
+int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m);
 
 // Operator bodies on device pointers (abi.hip), for the layers built on them.
 int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots);

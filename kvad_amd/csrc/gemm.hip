@@ -722,6 +722,43 @@ int gemm_split_reserve(kh_ctx *ctx) {
     return KH_OK;
 }
 
+int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m) {
+    a.ksplit = 0;
+    if (a.tiles) return KH_OK;  // grouped launches are not split
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    // Fewer tiles than CUs: split the k-stages so that the whole chip works,
+    // up to SPLIT_PER_CU workgroups per CU (a CU holds several: one's loads
+    // wait while another's MFMAs run), at least SPLIT_MIN_STAGES stages a
+    // split (fewer leaves the partials' traffic and the last split's sum
+    // longer than the stages saved), at most SPLIT_MAX splits.
+    const long long tiles = (long long)((a.N + 127) / 128) * ((a.M + tile_m - 1) / tile_m);
+    const int S = (a.K + BK - 1) / BK;
+    int ks = 1;
+    if (tiles < cu) {
+        ks = (int)(((long long)SPLIT_PER_CU * cu + tiles - 1) / tiles);
+        if (ks > S / SPLIT_MIN_STAGES) ks = S / SPLIT_MIN_STAGES;
+        if (ks > SPLIT_MAX) ks = SPLIT_MAX;
+        if (ks < 1) ks = 1;
+    }
+    const int forced = env_int("KVAD_GEMM_KSPLIT", 0);  // tuning knob: k splits (1: none)
+    if (forced > 0) ks = forced < S ? forced : S;
+    if (ks > 1 && tiles <= (long long)SPLIT_TILES && SPLIT_TILES * 4 + (size_t)ks * a.M * a.N * 4 <= SPLIT_BYTES) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        KH_HIP(hipStreamIsCapturing(ctx->stream, &cap));
+        if (cap == hipStreamCaptureStatusNone) {  // no allocation under capture
+            const int rc = gemm_split_reserve(ctx);
+            if (rc) return rc;
+        }
+    }
+    if (ks > 1 && ctx->gemm.ptr && tiles <= (long long)SPLIT_TILES &&
+        SPLIT_TILES * 4 + (size_t)ks * a.M * a.N * 4 <= SPLIT_BYTES) {
+        a.ksplit = ks;
+        a.tile_ctr = static_cast<unsigned *>(ctx->gemm.ptr);
+        a.part = reinterpret_cast<float *>(static_cast<char *>(ctx->gemm.ptr) + SPLIT_TILES * 4);
+    }
+    return KH_OK;
+}
+
 int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, const float *bias, float *y,
                   int accumulate) {
     const size_t rows = w->rows, cols = w->cols;
@@ -785,36 +822,8 @@ int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, co
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const Shape sh = pick_shape(a.M, a.N, cu);
     const int tile_m = sh == T128x128 ? 128 : sh == T128x64 ? 64 : 32;
-    // Fewer tiles than CUs: split the k-stages so that the whole chip works,
-    // up to SPLIT_PER_CU workgroups per CU (a CU holds several: one's loads
-    // wait while another's MFMAs run), at least SPLIT_MIN_STAGES stages a
-    // split (fewer leaves the partials' traffic and the last split's sum
-    // longer than the stages saved), at most SPLIT_MAX splits.
-    const long long tiles = (long long)((a.N + 127) / 128) * ((a.M + tile_m - 1) / tile_m);
-    const int S = (a.K + BK - 1) / BK;
-    int ks = 1;
-    if (tiles < cu) {
-        ks = (int)(((long long)SPLIT_PER_CU * cu + tiles - 1) / tiles);
-        if (ks > S / SPLIT_MIN_STAGES) ks = S / SPLIT_MIN_STAGES;
-        if (ks > SPLIT_MAX) ks = SPLIT_MAX;
-        if (ks < 1) ks = 1;
-    }
-    const int forced = env_int("KVAD_GEMM_KSPLIT", 0);  // tuning knob: k splits (1: none)
-    if (forced > 0) ks = forced < S ? forced : S;
-    if (ks > 1 && tiles <= (long long)SPLIT_TILES && SPLIT_TILES * 4 + (size_t)ks * a.M * a.N * 4 <= SPLIT_BYTES) {
-        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-        KH_HIP(hipStreamIsCapturing(ctx->stream, &cap));
-        if (cap == hipStreamCaptureStatusNone) {  // no allocation under capture
-            int rc = gemm_split_reserve(ctx);
-            if (rc) return rc;
-        }
-    }
-    if (ks > 1 && ctx->gemm.ptr && tiles <= (long long)SPLIT_TILES &&
-        SPLIT_TILES * 4 + (size_t)ks * a.M * a.N * 4 <= SPLIT_BYTES) {
-        a.ksplit = ks;
-        a.tile_ctr = static_cast<unsigned *>(ctx->gemm.ptr);
-        a.part = reinterpret_cast<float *>(static_cast<char *>(ctx->gemm.ptr) + SPLIT_TILES * 4);
-    }
+    int rc = plan_split(ctx, a, tile_m);
+    if (rc) return rc;
     return launch_gemm_q(ctx, w->precision, a, 0, tile_m);
 }
 

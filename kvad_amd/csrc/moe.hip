@@ -192,105 +192,116 @@ __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
     }
 }
 
-// by_expert (ffn.rs:627-640): rows in expert order, tokens in order within an
-// expert.  One workgroup of 1024 threads.  The tokens fall into at most 64
-// runs; (1) each run's count per expert (LDS atomics: order
-// free), (2) each (expert, run)'s first row by a prefix over experts then
-// runs, (3) each pick's row = its run's first row for that expert plus the
-// picks of that expert by earlier tokens of the same run.
+// by_expert (ffn.rs:627-640): the picks' rows grouped by expert, experts in
+// order.  Within an expert the rows are placed by LDS atomics, in no fixed
+// order: no output depends on it (each row's products and its mix are its
+// own; pos records where every pick went).  One workgroup of 1024 threads:
+// (1) the picks per expert, (2) exclusive prefixes over experts of rows and
+// of tile_m-row tiles, each expert writing its own tiles, (3) each pick's
+// row.  For the mix, each token's rows and weights are also written in
+// expert order (pos, wpos), the order of ffn.rs:775-805.
 constexpr int GROUP_THREADS = 1024;
-constexpr int GROUP_CELLS = 16384;  // runs x experts counters in LDS
+constexpr int GROUP_PICKS = 8192;  // picks (tokens x top_k) staged in LDS when they fit
+
+// Exclusive prefix of v over the workgroup's threads in thread order; `total`
+// gets the sum.  Every thread calls it.
+__device__ int group_scan(int v, int *s_wave, int &total) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    constexpr int NW = GROUP_THREADS / 64;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) s_wave[w] = x;
+    __syncthreads();
+    if (tid < 64) {
+        int y = tid < NW ? s_wave[tid] : 0;
+#pragma unroll
+        for (int d = 1; d < NW; d <<= 1) {
+            const int z = __shfl_up(y, d, 64);
+            if (lane >= d) y += z;
+        }
+        if (tid < NW) s_wave[tid] = y;
+    }
+    __syncthreads();
+    total = s_wave[NW - 1];
+    const int r = (w ? s_wave[w - 1] : 0) + x - v;
+    __syncthreads();  // s_wave free again
+    return r;
+}
 
 __global__ __launch_bounds__(GROUP_THREADS) void group_kernel(const int32_t *experts, const float *weights,
                                                              const int32_t *count, int m, int top_k, int n_exp,
-                                                             int tile_m, int nrun, int run_len,
-                                                             int32_t *row_token, float *row_weight, int32_t *pos,
-                                                             int32_t *tiles) {
-    __shared__ int s_cnt[GROUP_CELLS];  // [run][expert], then each cell's first row
-    __shared__ int s_tot[MAX_EXPERTS];
+                                                             int tile_m, int32_t *row_token, float *row_weight,
+                                                             int32_t *pos, float *wpos, int32_t *tiles) {
+    __shared__ int s_cnt[MAX_EXPERTS];  // picks per expert, then its next free row
+    __shared__ int s_wave[GROUP_THREADS / 64];
+    __shared__ int s_exp[GROUP_PICKS], s_count[GROUP_PICKS];
     const int tid = threadIdx.x;
-    for (int i = tid; i < nrun * n_exp; i += GROUP_THREADS) s_cnt[i] = 0;
+    const bool staged = m * top_k <= GROUP_PICKS;
+    for (int x = tid; x < n_exp; x += GROUP_THREADS) s_cnt[x] = 0;
+    if (staged) {
+        for (int i = tid; i < m * top_k; i += GROUP_THREADS) s_exp[i] = experts[i];
+        for (int t = tid; t < m; t += GROUP_THREADS) s_count[t] = count[t];
+    }
     __syncthreads();
+    const int *E = staged ? s_exp : experts, *C = staged ? s_count : count;
     for (int i = tid; i < m * top_k; i += GROUP_THREADS) {
         const int t = i / top_k, k = i % top_k;
-        if (k < count[t]) atomicAdd(&s_cnt[(t / run_len) * n_exp + experts[i]], 1);
+        if (k < C[t]) atomicAdd(&s_cnt[E[i]], 1);
     }
     __syncthreads();
-    for (int x = tid; x < n_exp; x += GROUP_THREADS) {
-        int c = 0;
-        for (int r = 0; r < nrun; r++) c += s_cnt[r * n_exp + x];
-        s_tot[x] = c;
-    }
-    __syncthreads();
-    if (tid == 0) {  // expert offsets and the tile table, in expert order
-        int off = 0, nt = 0;
-        for (int x = 0; x < n_exp; x++) {
-            const int c = s_tot[x];
-            for (int r0 = 0; r0 < c; r0 += tile_m) {
-                tiles[1 + 3 * nt] = x;
-                tiles[2 + 3 * nt] = off + r0;
-                tiles[3 + 3 * nt] = c - r0 < tile_m ? c - r0 : tile_m;
-                nt++;
-            }
-            s_tot[x] = off;
-            off += c;
+    // n_exp <= MAX_EXPERTS <= GROUP_THREADS: thread x holds expert x
+    const int c = tid < n_exp ? s_cnt[tid] : 0, nt = (c + tile_m - 1) / tile_m;
+    int rows_total, tiles_total;
+    const int first = group_scan(c, s_wave, rows_total);
+    const int tile0 = group_scan(nt, s_wave, tiles_total);
+    if (tid < n_exp) {
+        for (int j = 0; j < nt; j++) {
+            tiles[1 + 3 * (tile0 + j)] = tid;
+            tiles[2 + 3 * (tile0 + j)] = first + j * tile_m;
+            tiles[3 + 3 * (tile0 + j)] = c - j * tile_m < tile_m ? c - j * tile_m : tile_m;
         }
-        tiles[0] = nt;
+        s_cnt[tid] = first;
     }
+    if (tid == 0) tiles[0] = tiles_total;
     __syncthreads();
-    for (int x = tid; x < n_exp; x += GROUP_THREADS) {  // first row of each (run, expert)
-        int row = s_tot[x];
-        for (int r = 0; r < nrun; r++) {
-            const int c = s_cnt[r * n_exp + x];
-            s_cnt[r * n_exp + x] = row;
-            row += c;
-        }
-    }
-    __syncthreads();
-    for (int t = tid; t < m; t += GROUP_THREADS) {
-        const int run = t / run_len, t0 = run * run_len, n = count[t];
-        for (int k = 0; k < n; k++) {
-            const int x = experts[(size_t)t * top_k + k];
-            int rank = 0;
-            for (int u = t0; u < t; u++)
-                for (int j = 0; j < count[u]; j++) rank += experts[(size_t)u * top_k + j] == x;
-            const int row = s_cnt[run * n_exp + x] + rank;
-            row_token[row] = t;
-            row_weight[row] = weights[(size_t)t * top_k + k];
-            pos[(size_t)t * top_k + k] = row;
-        }
+    for (int i = tid; i < m * top_k; i += GROUP_THREADS) {
+        const int t = i / top_k, k = i % top_k, n = C[t];
+        if (k >= n) continue;
+        const int *pick = E + (size_t)t * top_k;
+        const int x = pick[k];
+        const int row = atomicAdd(&s_cnt[x], 1);
+        const float w = weights[i];
+        row_token[row] = t;
+        row_weight[row] = w;
+        int o = 0;  // the pick's place in expert order (ties: pick order)
+        for (int j = 0; j < n; j++) o += pick[j] < x || (pick[j] == x && j < k);
+        pos[(size_t)t * top_k + o] = row;
+        wpos[(size_t)t * top_k + o] = w;
     }
 }
 
 // out[t] = base[t] (or 0), then + w * y[row] over token t's picks in expert
-// order (the mix order, ffn.rs:775-805).  `pos` null: the picks are already
-// in expert order and pick k's row is t * top_k + k.  Grid: (hidden / 256,
-// tokens); every load of a thread is independent, so they fly together.
-__global__ __launch_bounds__(256) void combine_kernel(const float *base, const float *y, const int32_t *experts,
-                                                     const float *weights, const int32_t *count,
-                                                     const int32_t *pos, int top_k, int hidden, float *out) {
+// order (the mix order, ffn.rs:775-805): pick k's row is pos[t * top_k + k]
+// (in expert order, as group_kernel writes it) or, `pos` null, t * top_k + k
+// (the picks already in expert order); weights in the same order.  Grid:
+// (hidden / 256, tokens); every load of a thread is independent, so they fly
+// together.
+__global__ __launch_bounds__(256) void combine_kernel(const float *base, const float *y, const float *weights,
+                                                     const int32_t *count, const int32_t *pos, int top_k, int hidden,
+                                                     float *out) {
     const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
     const int n = count[t];
-    int pe[MAX_TOPK], pr[MAX_TOPK];
+    int pr[MAX_TOPK];
     float pw[MAX_TOPK];
 #pragma unroll
     for (int k = 0; k < MAX_TOPK; k++) {
         const bool ok = k < n;
-        pe[k] = ok ? experts[(size_t)t * top_k + k] : 0x7fffffff;
         pr[k] = ok ? (pos ? pos[(size_t)t * top_k + k] : t * top_k + k) : 0;
         pw[k] = ok ? weights[(size_t)t * top_k + k] : 0.0f;
-    }
-    if (pos) {  // into expert order: a fixed network, so the arrays stay in registers
-#pragma unroll
-        for (int a = 0; a < MAX_TOPK - 1; a++)
-#pragma unroll
-            for (int b = 0; b < MAX_TOPK - 1 - a; b++) {
-                const bool sw = pe[b] > pe[b + 1];
-                const int e0 = pe[b], r0 = pr[b];
-                const float w0 = pw[b];
-                pe[b] = sw ? pe[b + 1] : e0, pr[b] = sw ? pr[b + 1] : r0, pw[b] = sw ? pw[b + 1] : w0;
-                pe[b + 1] = sw ? e0 : pe[b + 1], pr[b + 1] = sw ? r0 : pr[b + 1], pw[b + 1] = sw ? w0 : pw[b + 1];
-            }
     }
     if (i >= hidden) return;
     float yv[MAX_TOPK];
@@ -445,7 +456,7 @@ int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
     }
     // (5) out = shared, then + w * y in expert order
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((hid + 255) / 256), 1), dim3(256), 0, ctx->stream,
-                       sh ? ys : nullptr, y, se, sw, cnt, nullptr, (int)k, (int)hid, out);
+                       sh ? ys : nullptr, y, sw, cnt, nullptr, (int)k, (int)hid, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -459,14 +470,15 @@ int ffn_rows(kh_ctx *ctx, const kh_weight *gate, const kh_weight *up, const kh_w
     const int tm = m >= 128 ? 128 : m >= 64 ? 64 : 32;
     int rc;
     a.w = gate->qs, a.ws = gate->scales, a.N = (int)gate->rows, a.y = g;
-    if ((rc = launch_gemm_q(ctx, gate->precision, a, 0, tm))) return rc;
+    if ((rc = plan_split(ctx, a, tm)) || (rc = launch_gemm_q(ctx, gate->precision, a, 0, tm))) return rc;
     a.w = up->qs, a.ws = up->scales, a.N = (int)up->rows, a.y = u;
-    if ((rc = launch_gemm_q(ctx, up->precision, a, 0, tm))) return rc;
+    if ((rc = plan_split(ctx, a, tm)) || (rc = launch_gemm_q(ctx, up->precision, a, 0, tm))) return rc;
     if ((rc = launch_swiglu_qact(ctx, g, u, m, gate->rows, hq))) return rc;
     GemmArgs d{};
     d.xq = hq.qs, d.xs = hq.scales, d.xsum = hq.sums;
     d.M = (int)m, d.K = (int)down->cols, d.N = (int)down->rows;
     d.w = down->qs, d.ws = down->scales, d.y = y;
+    if ((rc = plan_split(ctx, d, tm))) return rc;
     return launch_gemm_q(ctx, down->precision, d, 0, tm);
 }
 
@@ -475,12 +487,16 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
     const size_t sh = moe->sgate ? moe->sgate->rows : 0;
     const size_t total = m * k;
-    const int tile_m = total / n >= 64 ? 64 : 32;
+    const int forced = env_int("KVAD_MOE_TILE_M", 0);  // tuning knob: rows per expert tile (32 / 64)
+    // 64-row tiles once experts average 32 rows: an expert's weights are
+    // then read by fewer tiles (measured at DeepSeek-V2-Lite's 48 rows a
+    // expert: 477 against 501 us a layer)
+    const int tile_m = forced == 32 || forced == 64 ? forced : total / n >= 32 ? 64 : 32;
     const size_t max_tiles = (total + tile_m - 1) / tile_m + n;
     Carve c{static_cast<char *>(ctx->moe.ptr)};
     float *logits = c.take<float>(m * n);
     int32_t *pe = c.take<int32_t>(total), *cnt = c.take<int32_t>(m), *pos = c.take<int32_t>(total);
-    float *pw = c.take<float>(total);
+    float *pw = c.take<float>(total), *wpos = c.take<float>(total);
     int32_t *row_token = c.take<int32_t>(total), *tiles = c.take<int32_t>(1 + 3 * max_tiles);
     float *row_weight = c.take<float>(total);
     QAct hq = take_qact(c, m, hid);
@@ -500,11 +516,8 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     if ((rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits))) return rc;
     if ((rc = launch_route(ctx, route_args(moe, logits, pe, pw, cnt), (int)m))) return rc;
     // by_expert, and the tiles of the grouped GEMMs
-    const int nrun_max = (int)(GROUP_CELLS / n) < 64 ? (int)(GROUP_CELLS / n) : 64;
-    const int run_len = (int)((m + nrun_max - 1) / nrun_max);
-    const int nrun = (int)((m + run_len - 1) / run_len);
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), 0, ctx->stream, pe, pw, cnt, (int)m, (int)k,
-                       (int)n, tile_m, nrun, run_len, row_token, row_weight, pos, tiles);
+                       (int)n, tile_m, row_token, row_weight, pos, wpos, tiles);
     KH_HIP(hipGetLastError());
     // the activations, quantised once for every expert and the shared one
     if ((rc = launch_qact(ctx, hs, m, hid, hq))) return rc;
@@ -535,7 +548,7 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     if ((rc = launch_gemm_q(ctx, moe->precision, d, (int)max_tiles, tile_m))) return rc;
     // out = shared, then + w * y per token in expert order
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((hid + 255) / 256), (unsigned)m), dim3(256), 0, ctx->stream,
-                       base, y, pe, pw, cnt, pos, (int)k, (int)hid, out);
+                       base, y, wpos, cnt, pos, (int)k, (int)hid, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -545,7 +558,7 @@ size_t workspace_bytes(const kh_moe *moe, size_t m) {
     const size_t sh = moe->sgate ? moe->sgate->rows : 0;
     const size_t total = m * k, max_tiles = total / 32 + 1 + n;
     auto q = [](size_t a, size_t b) { return up256(a * b) + 2 * up256(4 * a * b / BLOCK); };
-    size_t b = up256(4 * m * n) + 5 * up256(4 * total) + up256(4 * m) + up256(4 * (1 + 3 * max_tiles));
+    size_t b = up256(4 * m * n) + 6 * up256(4 * total) + up256(4 * m) + up256(4 * (1 + 3 * max_tiles));
     b += q(m, hid) + 2 * up256(4 * total * inter) + q(total, inter) + up256(4 * total * hid);
     b += sh ? up256(4 * m * hid) + 2 * up256(4 * m * sh) + q(m, sh) : 0;
     b += up256(4 * hid) + 2 * up256(4 * (sh ? sh : 1)) + 4 * up256(4 * k) + up256(4 * k * hid);  // decode extras

@@ -99,7 +99,7 @@ def build(ctx, hidden, inter, n_exp, top_k, seed, sh_inter=0, **kw):
 SMALL = dict(hidden=256, inter=128, n_exp=16, top_k=4, sh_inter=256)
 
 
-@pytest.mark.parametrize("m", [1, 2, 33, 200])
+@pytest.mark.parametrize("m", [1, 2, 33, 200, 2100])  # 2100 x 4 picks: more than the group kernel stages in LDS
 def test_moe_matches_the_oracle(ctx, m):
     say("moe small", m)
     moe, oracle = build(ctx, seed=100, **SMALL)
