@@ -66,7 +66,7 @@ struct kh_ctx {
     kh::Workspace ws;        // per-call scratch (activations, partials)
     kh::Workspace io;        // staging for host-pointer calls
     kh::Workspace moe;       // mixture-of-experts intermediates
-    kh::Workspace gemm;      // split-K partials, after a zeroed block of tile counters
+    kh::Workspace gemm;      // split-K partials
 };
 
 struct kh_weight {
@@ -248,19 +248,20 @@ struct GemmArgs {
     const void *const *wtab;
     const float *const *wstab;
     // split-K (ungrouped launches): ksplit > 1 splits the k-stages over grid
-    // z; split z writes its tile to part[z][M][N], and the last of a tile's
-    // splits to finish (tile_ctr, left at 0 again) adds them in split order
+    // z; split z writes its tile to part[z][M][N] and a second launch adds
+    // the splits in order, then bias and residual
     int ksplit;
     float *part;
-    unsigned *tile_ctr;
 };
 int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m);
 // Allocates the split-K workspace now (a GEMM captured into a graph splits
 // only when it was allocated before the capture).
 int gemm_split_reserve(kh_ctx *ctx);
 // Sets a's split-K fields for an ungrouped launch of tile_m-token tiles when
-// it has fewer tiles than the chip has CUs (ksplit 0: no split).
+// splitting its k-stages pays (ksplit 0: no split).
 int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m);
+// Tokens per tile for an ungrouped M x N launch of the int8 GEMM.
+int gemm_tile_m(kh_ctx *ctx, int M, int N);
 
 // Operator bodies on device pointers (abi.hip), for the layers built on them.
 int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots);

@@ -34,13 +34,14 @@
 // f32 weights use v_mfma_f32_32x32x2_f32 over 32-wide k stages with the same
 // tile map.  Sums are taken in a different order from the reference's
 // 4-lane register tiles, so results agree to rounding (1e-5 relative).
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace kh {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -59,16 +60,6 @@ __device__ __forceinline__ float ldf(const rsrc_t &r, unsigned off) {
 }
 __device__ __forceinline__ int ldi(const rsrc_t &r, unsigned off) {
     return (int)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-
-// Split-K partials cross XCDs: written through to memory, read past the
-// L2 (sc1), ordered by a relaxed device-scope counter.
-constexpr int CPOL_SC1 = 16;
-__device__ __forceinline__ void st_wt4(const rsrc_t &r, unsigned off, float4 v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, CPOL_SC1);
-}
-__device__ __forceinline__ float4 ld_wt4(const rsrc_t &r, unsigned off) {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_SC1));
 }
 
 __device__ __forceinline__ float half_bits_to_float(unsigned h) {
@@ -122,86 +113,76 @@ __device__ __forceinline__ void store_tiles(const GemmArgs &a, const v16f (&acc)
         }
 }
 
-// Split-K: this split's tile into part[z] (write-through), then the last of
-// the tile's splits to arrive adds the splits in order z = 0, 1, ... and
-// finishes as store_tiles does (bias, residual).  Nobody waits: the others
-// return, so no workgroup depends on another being resident.
+// Split-K: split z writes its tile's sums, unscaled by bias or residual, to
+// part[z][M][N]; split_reduce_kernel, launched next, adds the splits.
 template <int RT, int TT>
-__device__ __forceinline__ void split_tiles(const GemmArgs &a, const v16f (&acc)[RT][TT], int r_base, int t_base,
-                                            int t_end, int lane, int n0, int m0, int BN, int BM) {
-    const int z = blockIdx.z, ks = a.ksplit;
+__device__ __forceinline__ void store_partials(const GemmArgs &a, const v16f (&acc)[RT][TT], int r_base, int t_base,
+                                               int t_end, int lane) {
     const size_t plane = (size_t)a.M * a.N;
-    const rsrc_t PT = rsrc(a.part, (size_t)ks * plane * 4);
+    float *part = a.part + blockIdx.z * plane;
     const bool vec = (a.N & 3) == 0;
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) {
             const int tok = t_base + tt * 32 + (lane & 31);
+            if (tok >= t_end) continue;
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const int r = r_base + rt * 32 + 8 * g + 4 * (lane >> 5);
-                if (vec) {  // rows past N fall outside the buffer and are dropped
-                    const bool ok = tok < t_end && r < a.N;
-                    const unsigned off = ok ? (unsigned)((z * plane + (size_t)tok * a.N + r) * 4) : 0xffffffffu;
-                    st_wt4(PT, off, make_float4(acc[rt][tt][4 * g], acc[rt][tt][4 * g + 1], acc[rt][tt][4 * g + 2],
-                                                acc[rt][tt][4 * g + 3]));
-                } else if (tok < t_end) {
+                float *dst = part + (size_t)tok * a.N + r;
+                if (vec && r + 3 < a.N) {
+                    *reinterpret_cast<float4 *>(dst) = make_float4(acc[rt][tt][4 * g], acc[rt][tt][4 * g + 1],
+                                                                   acc[rt][tt][4 * g + 2], acc[rt][tt][4 * g + 3]);
+                } else {
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        if (r + e < a.N)
-                            __hip_atomic_store(a.part + z * plane + (size_t)tok * a.N + r + e, acc[rt][tt][4 * g + e],
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (r + e < a.N) dst[e] = acc[rt][tt][4 * g + e];
                 }
             }
         }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partials are in memory
-    __syncthreads();
-    __shared__ int s_last;
-    const unsigned tile = blockIdx.y * gridDim.x + blockIdx.x;
-    if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(a.tile_ctr + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = old == (unsigned)ks - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    if (threadIdx.x == 0) __hip_atomic_store(a.tile_ctr + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the tile's outputs, four rows (consecutive in memory) per item
-    const int nq = BN / 4;
-    for (int i = threadIdx.x; i < nq * BM; i += THREADS) {
-        const int tok = m0 + i / nq, r = n0 + 4 * (i % nq);
-        if (tok >= t_end || r >= a.N) continue;
+}
+
+// Split-K's second launch: y = part[0] + part[1] + ... (split order), then
+// bias and residual as store_tiles.  One thread per four outputs.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float *part, int ks, int M, int N,
+                                                           const float *bias, int accumulate, float *y) {
+    const size_t plane = (size_t)M * N, e0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e0 >= plane) return;
+    if ((N & 3) == 0) {  // the four outputs share a token
+        const rsrc_t PT = rsrc(part, (size_t)ks * plane * 4);
+        const unsigned o = (unsigned)(e0 * 4), step = (unsigned)(plane * 4);
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (vec) {  // N % 4 == 0: the four rows are all there
-            // eight splits' loads in flight at a time (those past ks read
-            // outside the buffer, as zeros), added in split order
-            const unsigned o = (unsigned)(((size_t)tok * a.N + r) * 4), step = (unsigned)(plane * 4);
-            for (int z0 = 0; z0 < ks; z0 += 8) {
-                float4 p[8];
+        for (int z0 = 0; z0 < ks; z0 += 8) {
+            float4 p[8];
 #pragma unroll
-                for (int j = 0; j < 8; j++) p[j] = ld_wt4(PT, z0 + j < ks ? o + (z0 + j) * step : 0xffffffffu);
+            for (int j = 0; j < 8; j++)
+                p[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      PT, z0 + j < ks ? o + (z0 + j) * step : 0xffffffffu, 0, 0));
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    if (z0 + j < ks) x = make_float4(x.x + p[j].x, x.y + p[j].y, x.z + p[j].z, x.w + p[j].w);
-            }
-        } else {
-            float xx[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int zz = 0; zz < ks; zz++)
-                for (int e = 0; e < 4; e++)
-                    if (r + e < a.N)
-                        xx[e] = xx[e] + __hip_atomic_load(a.part + zz * plane + (size_t)tok * a.N + r + e,
-                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            x = make_float4(xx[0], xx[1], xx[2], xx[3]);
+            for (int j = 0; j < 8; j++)
+                if (z0 + j < ks) x = make_float4(x.x + p[j].x, x.y + p[j].y, x.z + p[j].z, x.w + p[j].w);
         }
-        const float v[4] = {x.x, x.y, x.z, x.w};
-        float *dst = a.y + (size_t)tok * a.N + r;
+        const int r = (int)(e0 % N);
+        float v[4] = {x.x, x.y, x.z, x.w};
+        if (bias) {  // finish, quant.rs:849-858
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (r + e >= a.N) break;
-            float o = a.bias ? v[e] + a.bias[r + e] : v[e];  // finish, quant.rs:849-858
-            if (a.accumulate) o = dst[e] + o;                 // x += proj (llama.rs:273-276)
-            dst[e] = o;
+            for (int e = 0; e < 4; e++) v[e] = v[e] + bias[r + e];
         }
+        float4 *dst = reinterpret_cast<float4 *>(y + e0);
+        if (accumulate) {  // x += proj (llama.rs:273-276)
+            const float4 o4 = *dst;
+            v[0] = o4.x + v[0], v[1] = o4.y + v[1], v[2] = o4.z + v[2], v[3] = o4.w + v[3];
+        }
+        *dst = make_float4(v[0], v[1], v[2], v[3]);
+        return;
+    }
+    for (int e = 0; e < 4 && e0 + e < plane; e++) {
+        float x = 0.f;
+        for (int z = 0; z < ks; z++) x = x + part[z * plane + e0 + e];
+        const int r = (int)((e0 + e) % N);
+        if (bias) x = x + bias[r];
+        y[e0 + e] = accumulate ? y[e0 + e] + x : x;
     }
 }
 
@@ -509,7 +490,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
         }
     }
     if (pending) scale_into(acc[RT - 1][TT - 1], pq, dq);
-    if (a.ksplit > 1) split_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane, n0, m0, BN, BM);
+    if (a.ksplit > 1) store_partials<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane);
     else store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane);
 }
 
@@ -617,6 +598,15 @@ Shape pick_shape(int M, int N, int cu) {
     return T128x32;
 }
 
+}  // namespace
+
+int gemm_tile_m(kh_ctx *ctx, int M, int N) {
+    const Shape sh = pick_shape(M, N, ctx->cu_count > 0 ? ctx->cu_count : 256);
+    return sh == T128x128 ? 128 : sh == T128x64 ? 64 : 32;
+}
+
+namespace {
+
 template <int PREC>
 int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m) {
     const unsigned gx = (unsigned)((a.N + 127) / 128);
@@ -635,6 +625,12 @@ int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m) {
             break;
     }
     KH_HIP(hipGetLastError());
+    if (a.ksplit > 1) {
+        const size_t quads = ((size_t)a.M * a.N + 3) / 4;
+        hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, ctx->stream,
+                           a.part, a.ksplit, a.M, a.N, a.bias, a.accumulate, a.y);
+        KH_HIP(hipGetLastError());
+    }
     return KH_OK;
 }
 
@@ -702,23 +698,19 @@ bool matmul_force_gemm() {
 }  // namespace
 
 namespace {
-// The split-K workspace: SPLIT_TILES tile counters (zero, and left at zero by
-// every launch) and the partials after them.  One fixed allocation, made on
-// the first split launch and never moved, so graphs captured over later
-// launches stay valid; a split whose partials do not fit is not made.  The
-// automatic choice needs at most (3 CUs + tiles) x 128 x 128 x 4 bytes.
-constexpr size_t SPLIT_TILES = 16384;
+// The split-K workspace: one fixed allocation for the partials, made on the
+// first split launch and never moved, so graphs captured over later launches
+// stay valid; a split whose partials do not fit is cut to what fits.
 constexpr size_t SPLIT_BYTES = 64u << 20;
-const int SPLIT_MIN_STAGES = env_int("KVAD_GEMM_SPLIT_MIN", 4);  // tuning knobs
-const int SPLIT_MAX = env_int("KVAD_GEMM_SPLIT_MAX", 8);
-const int SPLIT_PER_CU = env_int("KVAD_GEMM_SPLIT_PER_CU", 3);
+const int SPLIT_MIN_STAGES = env_int("KVAD_GEMM_SPLIT_MIN", 2);  // tuning knobs
+const int SPLIT_MAX = env_int("KVAD_GEMM_SPLIT_MAX", 32);
+const int SPLIT_PER_CU = env_int("KVAD_GEMM_SPLIT_PER_CU", 2);
 }  // namespace
 
 int gemm_split_reserve(kh_ctx *ctx) {
     if (ctx->gemm.ptr) return KH_OK;
     KH_HIP(hipMalloc(&ctx->gemm.ptr, SPLIT_BYTES));
     ctx->gemm.bytes = SPLIT_BYTES;
-    KH_HIP(hipMemsetAsync(ctx->gemm.ptr, 0, SPLIT_TILES * 4, ctx->stream));
     return KH_OK;
 }
 
@@ -726,36 +718,31 @@ int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m) {
     a.ksplit = 0;
     if (a.tiles) return KH_OK;  // grouped launches are not split
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    // Fewer tiles than CUs: split the k-stages so that the whole chip works,
-    // up to SPLIT_PER_CU workgroups per CU (a CU holds several: one's loads
-    // wait while another's MFMAs run), at least SPLIT_MIN_STAGES stages a
-    // split (fewer leaves the partials' traffic and the last split's sum
-    // longer than the stages saved), at most SPLIT_MAX splits.
+    // Split the k-stages so that the grid comes to about SPLIT_PER_CU
+    // workgroups per CU (a CU holds several: one's loads wait while
+    // another's MFMAs run), with at least SPLIT_MIN_STAGES stages a split,
+    // at most SPLIT_MAX splits, and partials (4 M N bytes a split, written
+    // and read again) of at most the weights' N K bytes.
     const long long tiles = (long long)((a.N + 127) / 128) * ((a.M + tile_m - 1) / tile_m);
     const int S = (a.K + BK - 1) / BK;
-    int ks = 1;
-    if (tiles < cu) {
-        ks = (int)(((long long)SPLIT_PER_CU * cu + tiles - 1) / tiles);
-        if (ks > S / SPLIT_MIN_STAGES) ks = S / SPLIT_MIN_STAGES;
-        if (ks > SPLIT_MAX) ks = SPLIT_MAX;
-        if (ks < 1) ks = 1;
-    }
+    const size_t plane = (size_t)a.M * a.N * 4;
+    long long ks = ((long long)SPLIT_PER_CU * cu + tiles / 2) / tiles;
+    ks = std::min<long long>(ks, S / SPLIT_MIN_STAGES);
+    ks = std::min<long long>(ks, SPLIT_MAX);
+    ks = std::min<long long>(ks, (long long)((size_t)a.K / (4 * (size_t)a.M)));
     const int forced = env_int("KVAD_GEMM_KSPLIT", 0);  // tuning knob: k splits (1: none)
-    if (forced > 0) ks = forced < S ? forced : S;
-    if (ks > 1 && tiles <= (long long)SPLIT_TILES && SPLIT_TILES * 4 + (size_t)ks * a.M * a.N * 4 <= SPLIT_BYTES) {
-        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-        KH_HIP(hipStreamIsCapturing(ctx->stream, &cap));
-        if (cap == hipStreamCaptureStatusNone) {  // no allocation under capture
-            const int rc = gemm_split_reserve(ctx);
-            if (rc) return rc;
-        }
+    if (forced > 0) ks = std::min(forced, S);
+    ks = std::min<long long>(ks, (long long)(SPLIT_BYTES / plane));
+    if (ks < 2) return KH_OK;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    KH_HIP(hipStreamIsCapturing(ctx->stream, &cap));
+    if (cap == hipStreamCaptureStatusNone) {  // no allocation under capture
+        const int rc = gemm_split_reserve(ctx);
+        if (rc) return rc;
     }
-    if (ks > 1 && ctx->gemm.ptr && tiles <= (long long)SPLIT_TILES &&
-        SPLIT_TILES * 4 + (size_t)ks * a.M * a.N * 4 <= SPLIT_BYTES) {
-        a.ksplit = ks;
-        a.tile_ctr = static_cast<unsigned *>(ctx->gemm.ptr);
-        a.part = reinterpret_cast<float *>(static_cast<char *>(ctx->gemm.ptr) + SPLIT_TILES * 4);
-    }
+    if (!ctx->gemm.ptr) return KH_OK;
+    a.ksplit = (int)ks;
+    a.part = static_cast<float *>(ctx->gemm.ptr);
     return KH_OK;
 }
 

@@ -467,7 +467,7 @@ int ffn_rows(kh_ctx *ctx, const kh_weight *gate, const kh_weight *up, const kh_w
     GemmArgs a{};
     a.xq = xq.qs, a.xs = xq.scales, a.xsum = xq.sums;
     a.M = (int)m, a.K = (int)gate->cols;
-    const int tm = m >= 128 ? 128 : m >= 64 ? 64 : 32;
+    const int tm = gemm_tile_m(ctx, (int)m, (int)gate->rows);
     int rc;
     a.w = gate->qs, a.ws = gate->scales, a.N = (int)gate->rows, a.y = g;
     if ((rc = plan_split(ctx, a, tm)) || (rc = launch_gemm_q(ctx, gate->precision, a, 0, tm))) return rc;
@@ -478,8 +478,9 @@ int ffn_rows(kh_ctx *ctx, const kh_weight *gate, const kh_weight *up, const kh_w
     d.xq = hq.qs, d.xs = hq.scales, d.xsum = hq.sums;
     d.M = (int)m, d.K = (int)down->cols, d.N = (int)down->rows;
     d.w = down->qs, d.ws = down->scales, d.y = y;
-    if ((rc = plan_split(ctx, d, tm))) return rc;
-    return launch_gemm_q(ctx, down->precision, d, 0, tm);
+    const int td = gemm_tile_m(ctx, (int)m, (int)down->rows);
+    if ((rc = plan_split(ctx, d, td))) return rc;
+    return launch_gemm_q(ctx, down->precision, d, 0, td);
 }
 
 // A batch: Moe::run for m > 1 (ffn.rs:615-708, mix ffn.rs:788-805).
