@@ -162,6 +162,24 @@ GemvJob normed(GemvJob j, bool fuse, const float *w, float eps) {
     return j;
 }
 
+// Jobs whose shared f32 input x (n wide) is too wide for the quantised
+// GEMV to stage itself: x is quantised first into m->hq
+// (QActivation::new, quant.rs:1037-1067) and those jobs read the codes.
+int wide_input(kh_ctx *ctx, kh_llm *m, std::vector<std::pair<const kh_weight *, GemvJob>> &jobs, const float *x,
+               size_t n) {
+    bool wide = false;
+    for (auto &j : jobs) wide |= j.first->precision != KH_F32 && n > fuse_max_cols(j.first->precision);
+    if (!wide) return KH_OK;
+    const int rc = launch_qact(ctx, x, 1, n, m->hq);
+    if (rc) return rc;
+    for (auto &j : jobs) {
+        if (j.first->precision == KH_F32) continue;
+        j.second.xf = nullptr;
+        j.second.xq = m->hq.qs, j.second.xs = m->hq.scales, j.second.xsum = m->hq.sums;
+    }
+    return KH_OK;
+}
+
 // One token's launches, all on the context's stream.
 int step(kh_ctx *ctx, kh_llm *m) {
     const kh_llm_spec &s = m->spec;
@@ -179,7 +197,7 @@ int step(kh_ctx *ctx, kh_llm *m) {
         jobs.push_back({L.k, normed(gemv_job(L.k, qin, nullptr, L.k_b, m->qkv + qd, 0), fq, L.attn_norm, s.eps)});
         jobs.push_back(
             {L.v, normed(gemv_job(L.v, qin, nullptr, L.v_b, m->qkv + qd + kvd, 0), fq, L.attn_norm, s.eps)});
-        if ((rc = run_jobs(ctx, jobs))) return rc;
+        if ((!fq && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) || (rc = run_jobs(ctx, jobs))) return rc;
         // attention over the cache, its length read from the device, with the
         // per-head norms, RoPE and the push of k and v fused in
         const AttnRope rp{m->qkv + qd, m->qkv + qd + kvd, m->rope_cos, m->rope_sin, L.q_norm, L.k_norm,
@@ -189,7 +207,7 @@ int step(kh_ctx *ctx, kh_llm *m) {
             return rc;
         jobs.clear();
         jobs.push_back({L.o, gemv_job(L.o, m->att, nullptr, nullptr, m->x, 1)});
-        if ((rc = run_jobs(ctx, jobs))) return rc;
+        if ((rc = wide_input(ctx, m, jobs, m->att, qd)) || (rc = run_jobs(ctx, jobs))) return rc;
         // ---- MLP sub-block (llama.rs:278-285, Ffn::run ffn.rs:370-375)
         const bool fm = norm_fusable(L.gate) && norm_fusable(L.up);
         const float *min_ = fm ? m->x : m->h;
@@ -197,7 +215,7 @@ int step(kh_ctx *ctx, kh_llm *m) {
         jobs.clear();
         jobs.push_back({L.gate, normed(gemv_job(L.gate, min_, nullptr, nullptr, m->g, 0), fm, L.mlp_norm, s.eps)});
         jobs.push_back({L.up, normed(gemv_job(L.up, min_, nullptr, nullptr, m->u, 0), fm, L.mlp_norm, s.eps)});
-        if ((rc = run_jobs(ctx, jobs))) return rc;
+        if ((!fm && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) || (rc = run_jobs(ctx, jobs))) return rc;
         jobs.clear();
         if (L.down->precision == KH_F32) {  // swiglu_inplace (ffn.rs:386), then the f32 GEMV
             if ((rc = launch_swiglu(ctx, m->g, m->u, s.n_ff))) return rc;
@@ -218,7 +236,7 @@ int step(kh_ctx *ctx, kh_llm *m) {
     if (!fh && (rc = launch_rms_norm(ctx, m->x, m->final_norm, 1, s.n_embd, s.eps, m->h))) return rc;
     std::vector<std::pair<const kh_weight *, GemvJob>> jobs{
         {head, normed(gemv_job(head, fh ? m->x : m->h, nullptr, nullptr, m->logits, 0), fh, m->final_norm, s.eps)}};
-    if ((rc = run_jobs(ctx, jobs))) return rc;
+    if ((!fh && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) || (rc = run_jobs(ctx, jobs))) return rc;
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(ARGMAX_BLOCKS), dim3(256), 0, ctx->stream, m->logits,
                        (int)s.vocab, m->arg_v, m->arg_i);
     KH_HIP(hipGetLastError());
@@ -498,11 +516,13 @@ int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out) {
     for (size_t l = 0; l < s.n_layer; l++) {
         if ((rc = dev_alloc(&m->kc[l], s.n_ctx * kvd)) || (rc = dev_alloc(&m->vc[l], s.n_ctx * kvd))) return rc;
     }
+    // codes of the widest activation quantised ahead of its GEMV
+    const size_t hq_n = std::max(s.n_ff, std::max(qd, s.n_embd));
     if ((rc = dev_alloc(&m->x, s.n_embd)) || (rc = dev_alloc(&m->h, s.n_embd)) ||
         (rc = dev_alloc(&m->qkv, qd + 2 * kvd)) || (rc = dev_alloc(&m->att, qd)) || (rc = dev_alloc(&m->g, s.n_ff)) ||
         (rc = dev_alloc(&m->u, s.n_ff)) || (rc = dev_alloc(&m->logits, s.vocab)) ||
-        (rc = dev_alloc(&m->hq.qs, s.n_ff)) || (rc = dev_alloc(&m->hq.scales, s.n_ff / BLOCK)) ||
-        (rc = dev_alloc(&m->hq.sums, s.n_ff / BLOCK)) || (rc = dev_alloc(&m->state, 3)) ||
+        (rc = dev_alloc(&m->hq.qs, hq_n)) || (rc = dev_alloc(&m->hq.scales, hq_n / BLOCK)) ||
+        (rc = dev_alloc(&m->hq.sums, hq_n / BLOCK)) || (rc = dev_alloc(&m->state, 3)) ||
         (rc = dev_alloc(&m->arg_v, ARGMAX_BLOCKS)) || (rc = dev_alloc(&m->arg_i, ARGMAX_BLOCKS)))
         return rc;
     m->token = m->state, m->pos = m->state + 1, m->steps = m->state + 2;

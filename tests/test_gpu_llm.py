@@ -111,6 +111,29 @@ def test_forward_matches_the_oracle(ctx, variant):
     assert len(m) == len(tokens)
 
 
+@pytest.mark.parametrize("variant", ["wide_embd", "wide_heads"])
+def test_activations_too_wide_to_stage_are_quantised_first(ctx, variant):
+    # q8 GEMVs stage an f32 input of at most 8192 columns themselves; past
+    # that (n_embd for q/k/v, gate/up and the head once the norm is not
+    # fused, n_head * head_dim for o) the input is quantised by a launch of
+    # its own and the GEMV reads the codes -- one token at a time and in
+    # the captured step alike
+    kw = {"wide_embd": dict(n_embd=8448, n_ff=256, n_layer=1),
+          "wide_heads": dict(n_embd=256, n_head=132, n_kv_head=12, head_dim=64, n_ff=256, n_layer=1)}[variant]
+    say("llm wide activations", variant)
+    m, mk = build(ctx, 130, **kw)
+    run_both(m, mk(), [3, 17, 500, 42])
+    m2, _ = build(ctx, 130, **kw)
+    for t in [3, 17, 500, 42]:
+        m2.forward(t, want_logits=False)
+    got = m2.generate(9, 4)  # the captured step
+    t, want = 9, []
+    for _ in range(4):
+        _, t = m.forward(t)
+        want.append(t)
+    np.testing.assert_array_equal(got, want)
+
+
 def test_generate_equals_forward_one_token_at_a_time(ctx):
     say("llm generate vs forward")
     m1, _ = build(ctx, 300)
