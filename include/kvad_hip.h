@@ -269,6 +269,25 @@ int kh_moe_run_dev(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *o
  * experts/weights [m, top_k] in pick order (unused slots -1 / 0), count [m]. */
 int kh_moe_route(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
                  int32_t *count);
+/* Parity hook (a debugging aid; no counterpart in the reference): after a
+ * kh_moe_run[_dev] of m tokens, the run's intermediates copied to the host,
+ * per token and pick, picks in expert order (mix order, ffn.rs:775-805),
+ * unused picks zero.  Any pointer may be NULL.  hidden_qs / hidden_scales
+ * (the quantised swiglu(gate, up) the down projections read) exist for
+ * m > 1 only: one token's stay inside the down GEMV (KH_DECLINED). */
+typedef struct kh_moe_picks {
+    float *logits;         /* [m][n_experts] router logits */
+    int32_t *count;        /* [m] */
+    int32_t *experts;      /* [m][top_k] */
+    float *weights;        /* [m][top_k] */
+    float *gate, *up;      /* [m][top_k][inter] */
+    int8_t *hidden_qs;     /* [m][top_k][inter] */
+    float *hidden_scales;  /* [m][top_k][inter / 32] */
+    float *out;            /* [m][top_k][hidden]: each expert's down projection */
+    float *shared_gate, *shared_up;  /* [m][shared width] */
+    float *shared_out;     /* [m][hidden] */
+} kh_moe_picks;
+int kh_debug_moe_picks(kh_ctx *ctx, const kh_moe *moe, size_t m, const kh_moe_picks *out);
 
 /* ---- the quantised-weight cache file ("NANOQ"), read into device weights */
 
@@ -331,6 +350,20 @@ int kh_llm_set_rope(kh_llm *m, const float *cos_t, const float *sin_t, size_t ma
 /* Session::forward for one token at the next position: logits [vocab] (host,
  * may be NULL) and the greedy next token (sampler::argmax, sampler.rs:217). */
 int kh_llm_forward(kh_ctx *ctx, kh_llm *m, int32_t token, float *logits, int32_t *next);
+/* Parity hook (a debugging aid; no counterpart in the reference): one
+ * kh_llm_forward step of `token` that copies each sub-block's results to the
+ * host as it ends.  With L = n_layer, n = the positions held after the step
+ * (length before it + 1), qd = n_head * head_dim, kvd = n_kv_head * head_dim:
+ * x_embed [n_embd] (the embedding row); per layer qkv [L][qd + 2 kvd] (the
+ * projections with biases, before the head norms and RoPE), k_cache / v_cache
+ * [L][n][kvd] (the cache after the push), att [L][qd] (attention output),
+ * x_attn [L][n_embd] (the residual after the o projection), gate / up
+ * [L][n_ff] (quantised weights only), x_mlp [L][n_embd] (the residual after
+ * the MLP); logits [vocab].  Any pointer may be NULL. */
+typedef struct kh_llm_trace {
+    float *x_embed, *qkv, *k_cache, *v_cache, *att, *x_attn, *gate, *up, *x_mlp, *logits;
+} kh_llm_trace;
+int kh_debug_llm_trace(kh_ctx *ctx, kh_llm *m, int32_t token, const kh_llm_trace *tr);
 /* n greedy steps from `token`, one captured HIP graph replayed per token;
  * tokens[n] receives the tokens generated. */
 int kh_llm_generate(kh_ctx *ctx, kh_llm *m, int32_t token, size_t n, int32_t *tokens);

@@ -119,6 +119,7 @@ _SIGS = {
     "kh_llm_set_ends": (C.c_int, [_p, _p, _p, _p]),
     "kh_llm_set_rope": (C.c_int, [_p, _p, _p, _sz]),
     "kh_llm_forward": (C.c_int, [_p, _p, C.c_int32, _p, _p]),
+    "kh_debug_llm_trace": (C.c_int, [_p, _p, C.c_int32, _p]),
     "kh_llm_generate": (C.c_int, [_p, _p, C.c_int32, _sz, _p]),
     "kh_llm_generate_launch": (C.c_int, [_p, _p, _sz]),
     "kh_llm_len": (C.c_int, [_p, C.POINTER(_sz)]),
@@ -137,6 +138,7 @@ _SIGS = {
     "kh_moe_run": (C.c_int, [_p, _p, _p, _sz, _p]),
     "kh_moe_run_dev": (C.c_int, [_p, _p, _p, _sz, _p]),
     "kh_moe_route": (C.c_int, [_p, _p, _p, _sz, _p, _p, _p]),
+    "kh_debug_moe_picks": (C.c_int, [_p, _p, _sz, _p]),
     "kh_mla_attend": (C.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, C.c_float, _p]),
     "kh_mla_attend_dev": (C.c_int, [_p, _sz, _p, _p, _p, _p, _sz, C.c_float, _p]),
     "kh_qcache_open": (C.c_int, [C.c_char_p, C.POINTER(_p)]),
@@ -587,6 +589,29 @@ class Moe:
         k = self.top_k
         return [[(int(e[i * k + j]), float(w[i * k + j])) for j in range(int(c[i]))] for i in range(m)]
 
+    def picks(self, m: int, hidden_codes: bool = False) -> dict:
+        """The last run's intermediates (kh_debug_moe_picks) for its m tokens,
+        picks in expert order: logits, count, experts, weights, gate, up,
+        out (each expert's down projection), shared_gate/_up/_out when a
+        shared expert is set, hidden_qs/_scales (m > 1) when asked."""
+        k, inter, hid = self.top_k, self.inter, self.hidden
+        r = {"logits": np.zeros((m, self.n_experts), np.float32), "count": np.zeros(m, np.int32),
+             "experts": np.zeros((m, k), np.int32), "weights": np.zeros((m, k), np.float32),
+             "gate": np.zeros((m, k, inter), np.float32), "up": np.zeros((m, k, inter), np.float32),
+             "out": np.zeros((m, k, hid), np.float32)}
+        if hidden_codes:
+            r["hidden_qs"] = np.zeros((m, k, inter), np.int8)
+            r["hidden_scales"] = np.zeros((m, k, inter // 32), np.float32)
+        if "shared" in self._keep:
+            sh = self._keep["shared"][0].rows
+            r["shared_gate"], r["shared_up"] = np.zeros((m, sh), np.float32), np.zeros((m, sh), np.float32)
+            r["shared_out"] = np.zeros((m, hid), np.float32)
+        names = ["logits", "count", "experts", "weights", "gate", "up", "hidden_qs", "hidden_scales", "out",
+                 "shared_gate", "shared_up", "shared_out"]
+        ptrs = (_p * len(names))(*[r[n].ctypes.data if n in r else None for n in names])
+        _check(lib.kh_debug_moe_picks(self.ctx.h, self.h, m, ptrs))
+        return r
+
     def free(self) -> None:
         if self.h:
             lib.kh_moe_free(self.h)
@@ -656,6 +681,24 @@ class Llm:
         nxt = C.c_int32()
         _check(lib.kh_llm_forward(self.ctx.h, self.h, token, _ptr(logits), C.byref(nxt)))
         return logits, nxt.value
+
+    def trace(self, token: int) -> dict:
+        """forward() of one token with each sub-block's results copied out
+        (kh_debug_llm_trace): x_embed, and per layer qkv, k_cache, v_cache
+        (the positions held after the push), att, x_attn, gate, up, x_mlp;
+        then logits."""
+        s = self.spec
+        L, n = s.n_layer, len(self) + 1
+        qd, kvd = s.n_head * s.head_dim, s.n_kv_head * s.head_dim
+        r = {"x_embed": np.zeros(s.n_embd, np.float32), "qkv": np.zeros((L, qd + 2 * kvd), np.float32),
+             "k_cache": np.zeros((L, n, kvd), np.float32), "v_cache": np.zeros((L, n, kvd), np.float32),
+             "att": np.zeros((L, qd), np.float32), "x_attn": np.zeros((L, s.n_embd), np.float32),
+             "gate": np.zeros((L, s.n_ff), np.float32), "up": np.zeros((L, s.n_ff), np.float32),
+             "x_mlp": np.zeros((L, s.n_embd), np.float32), "logits": np.zeros(s.vocab, np.float32)}
+        names = ["x_embed", "qkv", "k_cache", "v_cache", "att", "x_attn", "gate", "up", "x_mlp", "logits"]
+        ptrs = (_p * len(names))(*[r[k].ctypes.data for k in names])
+        _check(lib.kh_debug_llm_trace(self.ctx.h, self.h, token, ptrs))
+        return r
 
     def generate(self, token: int, n: int) -> np.ndarray:
         out = np.empty(n, np.int32)

@@ -913,6 +913,14 @@ int kh_moe_run(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out) 
     return KH_OK;
 }
 
+int kh_debug_moe_picks(kh_ctx *ctx, const kh_moe *moe, size_t m, const kh_moe_picks *out) {
+    if (!ctx || !moe || !out) return fail(KH_EINVAL, "kh_debug_moe_picks: null argument");
+    Guard g(ctx);
+    MoePicks o{out->logits,  out->count,     out->experts, out->weights,     out->gate,      out->up,
+               out->hidden_qs, out->hidden_scales, out->out, out->shared_gate, out->shared_up, out->shared_out};
+    return moe_picks(ctx, moe, m, o);
+}
+
 int kh_moe_route(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
                  int32_t *count) {
     if (!ctx || !moe || !logits || !experts || !weights || !count) return fail(KH_EINVAL, "kh_moe_route: null argument");

@@ -275,6 +275,22 @@ int launch_norm_qact(kh_ctx *ctx, const float *x, const float *w, size_t m, size
 int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, size_t k, const QAct &out);
 // Moe::run on device pointers, and Router::route alone (moe.hip).
 int moe_run_device(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out);
+// A debugging aid: after a MoE run of m tokens, its intermediates per token
+// and pick (picks in expert order, unused ones zero), copied to the host.
+// Any pointer may be null.
+struct MoePicks {
+    float *logits;                    // [m][n_experts]
+    int32_t *count;                   // [m]
+    int32_t *experts;                 // [m][top_k]
+    float *weights;                   // [m][top_k]
+    float *gate, *up;                 // [m][top_k][inter]
+    int8_t *hidden_qs;                // [m][top_k][inter] (m > 1 only)
+    float *hidden_scales;             // [m][top_k][inter / 32]
+    float *out;                       // [m][top_k][hidden]
+    float *shared_gate, *shared_up;   // [m][shared width]
+    float *shared_out;                // [m][hidden]
+};
+int moe_picks(kh_ctx *ctx, const kh_moe *moe, size_t m, const MoePicks &o);
 int route_device(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
                  int32_t *count);
 

@@ -16,6 +16,10 @@
 // by_expert is filled, ffn.rs:627-640), runs each expert's gate/up and down as
 // one grouped int8 GEMM over tiles of its rows, and combines per token in
 // expert order after the shared expert (which runs on every token).
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
 #include "common.hpp"
 
 namespace kh {
@@ -406,16 +410,35 @@ GemvJob plain_job(const kh_weight *w, const float *xf, const float *xf2, float *
 }
 
 // One token: decode_together (ffn.rs:820-842) after early() (ffn.rs:556-612).
-int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
+// One token's buffers in the MoE workspace.
+struct DecodeBufs {
+    float *logits, *sg, *su;
+    int32_t *pe, *cnt, *se;  // picks by rank, their count, picks in expert order
+    float *pw, *sw;
+    float *g, *u, *y, *ys;   // per pick in expert order; the shared expert's output
+};
+
+DecodeBufs decode_bufs(kh_ctx *ctx, const kh_moe *moe) {
     const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
     const size_t sh = moe->sgate ? moe->sgate->rows : 0;
     Carve c{static_cast<char *>(ctx->moe.ptr)};
-    float *logits = c.take<float>(n);
-    float *sg = c.take<float>(sh ? sh : 1), *su = c.take<float>(sh ? sh : 1);
-    int32_t *pe = c.take<int32_t>(k), *cnt = c.take<int32_t>(1), *se = c.take<int32_t>(k);
-    float *pw = c.take<float>(k), *sw = c.take<float>(k);
-    float *g = c.take<float>(k * inter), *u = c.take<float>(k * inter);
-    float *y = c.take<float>(k * hid), *ys = c.take<float>(hid);
+    DecodeBufs b;
+    b.logits = c.take<float>(n);
+    b.sg = c.take<float>(sh ? sh : 1), b.su = c.take<float>(sh ? sh : 1);
+    b.pe = c.take<int32_t>(k), b.cnt = c.take<int32_t>(1), b.se = c.take<int32_t>(k);
+    b.pw = c.take<float>(k), b.sw = c.take<float>(k);
+    b.g = c.take<float>(k * inter), b.u = c.take<float>(k * inter);
+    b.y = c.take<float>(k * hid), b.ys = c.take<float>(hid);
+    return b;
+}
+
+int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
+    const size_t k = moe->top_k, hid = moe->hidden, inter = moe->inter;
+    const size_t sh = moe->sgate ? moe->sgate->rows : 0;
+    const DecodeBufs b = decode_bufs(ctx, moe);
+    float *logits = b.logits, *sg = b.sg, *su = b.su, *pw = b.pw, *sw = b.sw, *g = b.g, *u = b.u, *y = b.y,
+          *ys = b.ys;
+    int32_t *pe = b.pe, *cnt = b.cnt, *se = b.se;
 
     // (1) the router and the shared expert's gate and up read x together
     std::vector<const kh_weight *> w{moe->router};
@@ -484,6 +507,48 @@ int ffn_rows(kh_ctx *ctx, const kh_weight *gate, const kh_weight *up, const kh_w
 }
 
 // A batch: Moe::run for m > 1 (ffn.rs:615-708, mix ffn.rs:788-805).
+// A batch's buffers in the MoE workspace.  Rows are the picks grouped by
+// expert; pos / wpos give each token's rows and weights in expert order.
+struct PrefillBufs {
+    float *logits;
+    int32_t *pe, *cnt, *pos;
+    float *pw, *wpos;
+    int32_t *row_token, *tiles;
+    float *row_weight;
+    QAct hq;
+    float *g, *u;
+    QAct rq;                     // swiglu(g, u) per row, quantised
+    float *y;
+    float *base, *sg, *su;       // the shared expert (null without one)
+    QAct sq;
+};
+
+size_t prefill_max_tiles(size_t total, size_t n, int tile_m) { return (total + tile_m - 1) / tile_m + n; }
+
+PrefillBufs prefill_bufs(kh_ctx *ctx, const kh_moe *moe, size_t m) {
+    const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
+    const size_t sh = moe->sgate ? moe->sgate->rows : 0;
+    const size_t total = m * k, max_tiles = prefill_max_tiles(total, n, 32);
+    Carve c{static_cast<char *>(ctx->moe.ptr)};
+    PrefillBufs b{};
+    b.logits = c.take<float>(m * n);
+    b.pe = c.take<int32_t>(total), b.cnt = c.take<int32_t>(m), b.pos = c.take<int32_t>(total);
+    b.pw = c.take<float>(total), b.wpos = c.take<float>(total);
+    b.row_token = c.take<int32_t>(total), b.tiles = c.take<int32_t>(1 + 3 * max_tiles);
+    b.row_weight = c.take<float>(total);
+    b.hq = take_qact(c, m, hid);
+    b.g = c.take<float>(total * inter), b.u = c.take<float>(total * inter);
+    b.rq = take_qact(c, total, inter);
+    b.y = c.take<float>(total * hid);
+    if (sh) {
+        b.base = c.take<float>(m * hid);
+        b.sg = c.take<float>(m * sh);
+        b.su = c.take<float>(m * sh);
+        b.sq = take_qact(c, m, sh);
+    }
+    return b;
+}
+
 int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out) {
     const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
     const size_t sh = moe->sgate ? moe->sgate->rows : 0;
@@ -493,25 +558,12 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     // then read by fewer tiles (measured at DeepSeek-V2-Lite's 48 rows a
     // expert: 477 against 501 us a layer)
     const int tile_m = forced == 32 || forced == 64 ? forced : total / n >= 32 ? 64 : 32;
-    const size_t max_tiles = (total + tile_m - 1) / tile_m + n;
-    Carve c{static_cast<char *>(ctx->moe.ptr)};
-    float *logits = c.take<float>(m * n);
-    int32_t *pe = c.take<int32_t>(total), *cnt = c.take<int32_t>(m), *pos = c.take<int32_t>(total);
-    float *pw = c.take<float>(total), *wpos = c.take<float>(total);
-    int32_t *row_token = c.take<int32_t>(total), *tiles = c.take<int32_t>(1 + 3 * max_tiles);
-    float *row_weight = c.take<float>(total);
-    QAct hq = take_qact(c, m, hid);
-    float *g = c.take<float>(total * inter), *u = c.take<float>(total * inter);
-    QAct rq = take_qact(c, total, inter);
-    float *y = c.take<float>(total * hid);
-    float *base = nullptr, *sg = nullptr, *su = nullptr;
-    QAct sq{};
-    if (sh) {
-        base = c.take<float>(m * hid);
-        sg = c.take<float>(m * sh);
-        su = c.take<float>(m * sh);
-        sq = take_qact(c, m, sh);
-    }
+    const size_t max_tiles = prefill_max_tiles(total, n, tile_m);
+    const PrefillBufs b = prefill_bufs(ctx, moe, m);
+    float *logits = b.logits, *pw = b.pw, *wpos = b.wpos, *row_weight = b.row_weight, *g = b.g, *u = b.u,
+          *y = b.y, *base = b.base, *sg = b.sg, *su = b.su;
+    int32_t *pe = b.pe, *cnt = b.cnt, *pos = b.pos, *row_token = b.row_token, *tiles = b.tiles;
+    const QAct hq = b.hq, rq = b.rq, sq = b.sq;
     int rc;
     // router logits (any precision), then the routes
     if ((rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits))) return rc;
@@ -557,7 +609,7 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
 size_t workspace_bytes(const kh_moe *moe, size_t m) {
     const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
     const size_t sh = moe->sgate ? moe->sgate->rows : 0;
-    const size_t total = m * k, max_tiles = total / 32 + 1 + n;
+    const size_t total = m * k, max_tiles = prefill_max_tiles(total, n, 32);
     auto q = [](size_t a, size_t b) { return up256(a * b) + 2 * up256(4 * a * b / BLOCK); };
     size_t b = up256(4 * m * n) + 6 * up256(4 * total) + up256(4 * m) + up256(4 * (1 + 3 * max_tiles));
     b += q(m, hid) + 2 * up256(4 * total * inter) + q(total, inter) + up256(4 * total * hid);
@@ -591,6 +643,84 @@ int moe_run_device(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *o
 int route_device(kh_ctx *ctx, const kh_moe *moe, const float *logits, size_t m, int32_t *experts, float *weights,
                  int32_t *count) {
     return launch_route(ctx, route_args(moe, logits, experts, weights, count), (int)m);
+}
+
+int moe_picks(kh_ctx *ctx, const kh_moe *moe, size_t m, const MoePicks &o) {
+    const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
+    const size_t sh = moe->sgate ? moe->sgate->rows : 0, total = m * k;
+    if (m == 0) return KH_OK;
+    if (!ctx->moe.ptr || ctx->moe.bytes < workspace_bytes(moe, m))
+        return fail(KH_EINVAL, "moe picks: no run of this many tokens to read");
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    auto get = [&](const void *src, size_t bytes) {
+        std::vector<char> h(bytes);
+        if (bytes && hipMemcpy(h.data(), src, bytes, hipMemcpyDeviceToHost) != hipSuccess) h.clear();
+        return h;
+    };
+    auto f32 = [](const std::vector<char> &h) { return reinterpret_cast<const float *>(h.data()); };
+    auto i32 = [](const std::vector<char> &h) { return reinterpret_cast<const int32_t *>(h.data()); };
+    // per token: its count, then for pick j (expert order) the expert, the
+    // weight and the row holding its gate / up / hidden / output
+    std::vector<int32_t> cnt(m), expert(total, 0), row(total, -1);
+    std::vector<float> weight(total, 0.0f);
+    const float *g_d, *u_d, *y_d, *logits_d, *sg_d = nullptr, *su_d = nullptr, *ys_d = nullptr;
+    QAct rq{};
+    if (m == 1) {
+        const DecodeBufs b = decode_bufs(ctx, moe);
+        auto c = get(b.cnt, 4), e = get(b.se, 4 * k), w = get(b.sw, 4 * k);
+        if (c.empty() || e.empty() || w.empty()) return fail(KH_EINVAL, "moe picks: copy failed");
+        cnt[0] = i32(c)[0];
+        for (size_t j = 0; j < k; j++)
+            if ((int)j < cnt[0]) expert[j] = i32(e)[j], weight[j] = f32(w)[j], row[j] = (int)j;
+        g_d = b.g, u_d = b.u, y_d = b.y, logits_d = b.logits;
+        if (sh) sg_d = b.sg, su_d = b.su, ys_d = b.ys;
+    } else {
+        const PrefillBufs b = prefill_bufs(ctx, moe, m);
+        auto c = get(b.cnt, 4 * m), e = get(b.pe, 4 * total), p = get(b.pos, 4 * total), w = get(b.wpos, 4 * total);
+        if (c.empty() || e.empty() || p.empty() || w.empty()) return fail(KH_EINVAL, "moe picks: copy failed");
+        for (size_t t = 0; t < m; t++) {
+            cnt[t] = i32(c)[t];
+            std::vector<int32_t> xs(i32(e) + t * k, i32(e) + t * k + cnt[t]);
+            std::sort(xs.begin(), xs.end());
+            for (int j = 0; j < cnt[t]; j++) {
+                expert[t * k + j] = xs[j];
+                row[t * k + j] = i32(p)[t * k + j];
+                weight[t * k + j] = f32(w)[t * k + j];
+            }
+        }
+        g_d = b.g, u_d = b.u, y_d = b.y, logits_d = b.logits, rq = b.rq;
+        if (sh) sg_d = b.sg, su_d = b.su, ys_d = b.base;
+    }
+    if (o.count) std::copy(cnt.begin(), cnt.end(), o.count);
+    if (o.experts) std::copy(expert.begin(), expert.end(), o.experts);
+    if (o.weights) std::copy(weight.begin(), weight.end(), o.weights);
+    if (o.logits) KH_HIP(hipMemcpy(o.logits, logits_d, 4 * m * n, hipMemcpyDeviceToHost));
+    // the rows, gathered pick by pick (an unused pick's stay zero)
+    auto gather = [&](void *dst, const void *src, size_t row_bytes) -> int {
+        if (!dst) return KH_OK;
+        memset(dst, 0, total * row_bytes);
+        for (size_t i = 0; i < total; i++)
+            if (row[i] >= 0)
+                KH_HIP(hipMemcpy(static_cast<char *>(dst) + i * row_bytes,
+                                 static_cast<const char *>(src) + (size_t)row[i] * row_bytes, row_bytes,
+                                 hipMemcpyDeviceToHost));
+        return KH_OK;
+    };
+    int rc;
+    if ((rc = gather(o.gate, g_d, 4 * inter)) || (rc = gather(o.up, u_d, 4 * inter)) ||
+        (rc = gather(o.out, y_d, 4 * hid)))
+        return rc;
+    if (o.hidden_qs || o.hidden_scales) {
+        if (m == 1) return fail(KH_DECLINED, "moe picks: one token's hidden codes stay inside the down GEMV");
+        if ((rc = gather(o.hidden_qs, rq.qs, inter)) || (rc = gather(o.hidden_scales, rq.scales, 4 * inter / BLOCK)))
+            return rc;
+    }
+    if (sh) {
+        if (o.shared_gate) KH_HIP(hipMemcpy(o.shared_gate, sg_d, 4 * m * sh, hipMemcpyDeviceToHost));
+        if (o.shared_up) KH_HIP(hipMemcpy(o.shared_up, su_d, 4 * m * sh, hipMemcpyDeviceToHost));
+        if (o.shared_out) KH_HIP(hipMemcpy(o.shared_out, ys_d, 4 * m * hid, hipMemcpyDeviceToHost));
+    }
+    return KH_OK;
 }
 
 }  // namespace kh

@@ -180,12 +180,21 @@ int wide_input(kh_ctx *ctx, kh_llm *m, std::vector<std::pair<const kh_weight *, 
     return KH_OK;
 }
 
-// One token's launches, all on the context's stream.
-int step(kh_ctx *ctx, kh_llm *m) {
+// A copy of n floats of device memory to the trace's host buffer (null: none).
+int trace_copy(kh_ctx *ctx, float *dst, const float *src, size_t n) {
+    if (dst) KH_HIP(hipMemcpyAsync(dst, src, 4 * n, hipMemcpyDeviceToHost, ctx->stream));
+    return KH_OK;
+}
+
+// One token's launches, all on the context's stream.  With a trace (the
+// parity hook kh_debug_llm_trace; never under capture) each sub-block's
+// results are copied out as it ends.
+int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr) {
     const kh_llm_spec &s = m->spec;
     const size_t qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
     int rc;
     if ((rc = launch_dequant_row_dev(ctx, m->embed, m->token, m->x))) return rc;  // embed (llama.rs:384-391)
+    if (tr && (rc = trace_copy(ctx, tr->x_embed, m->x, s.n_embd))) return rc;
     for (size_t l = 0; l < s.n_layer; l++) {
         const kh_llm::Layer &L = m->layers[l];
         // ---- attention sub-block (llama.rs:241-276)
@@ -208,6 +217,15 @@ int step(kh_ctx *ctx, kh_llm *m) {
         jobs.clear();
         jobs.push_back({L.o, gemv_job(L.o, m->att, nullptr, nullptr, m->x, 1)});
         if ((rc = wide_input(ctx, m, jobs, m->att, qd)) || (rc = run_jobs(ctx, jobs))) return rc;
+        if (tr) {
+            const size_t n = m->len + 1;  // positions held after the push
+            if ((rc = trace_copy(ctx, tr->qkv ? tr->qkv + l * (qd + 2 * kvd) : nullptr, m->qkv, qd + 2 * kvd)) ||
+                (rc = trace_copy(ctx, tr->k_cache ? tr->k_cache + l * n * kvd : nullptr, m->kc[l], n * kvd)) ||
+                (rc = trace_copy(ctx, tr->v_cache ? tr->v_cache + l * n * kvd : nullptr, m->vc[l], n * kvd)) ||
+                (rc = trace_copy(ctx, tr->att ? tr->att + l * qd : nullptr, m->att, qd)) ||
+                (rc = trace_copy(ctx, tr->x_attn ? tr->x_attn + l * s.n_embd : nullptr, m->x, s.n_embd)))
+                return rc;
+        }
         // ---- MLP sub-block (llama.rs:278-285, Ffn::run ffn.rs:370-375)
         const bool fm = norm_fusable(L.gate) && norm_fusable(L.up);
         const float *min_ = fm ? m->x : m->h;
@@ -229,6 +247,12 @@ int step(kh_ctx *ctx, kh_llm *m) {
             jobs.push_back({L.down, j});
         }
         if ((rc = run_jobs(ctx, jobs))) return rc;
+        if (tr && L.down->precision != KH_F32) {  // (the f32 path leaves swiglu in g)
+            if ((rc = trace_copy(ctx, tr->gate ? tr->gate + l * s.n_ff : nullptr, m->g, s.n_ff)) ||
+                (rc = trace_copy(ctx, tr->up ? tr->up + l * s.n_ff : nullptr, m->u, s.n_ff)))
+                return rc;
+        }
+        if (tr && (rc = trace_copy(ctx, tr->x_mlp ? tr->x_mlp + l * s.n_embd : nullptr, m->x, s.n_embd))) return rc;
     }
     // ---- head (llama.rs:404-411)
     const kh_weight *head = m->head ? m->head : m->embed;
@@ -663,6 +687,23 @@ int kh_llm_forward(kh_ctx *ctx, kh_llm *m, int32_t token, float *logits, int32_t
     KH_HIP(hipStreamSynchronize(ctx->stream));
     m->len += 1;
     if (next) *next = nt;
+    return KH_OK;
+}
+
+int kh_debug_llm_trace(kh_ctx *ctx, kh_llm *m, int32_t token, const kh_llm_trace *tr) {
+    if (!ctx || !m || m->ctx != ctx || !tr) return fail(KH_EINVAL, "kh_debug_llm_trace: null argument");
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = ready(m);
+    if (rc) return rc;
+    if (token < 0 || (size_t)token >= m->spec.vocab) return fail(KH_EINVAL, "kh_debug_llm_trace: token out of range");
+    if (m->len >= m->spec.n_ctx) return fail(KH_EINVAL, "kh_debug_llm_trace: the context window is full");
+    const int32_t st[3] = {token, (int32_t)m->len, 0};
+    KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = step(ctx, m, tr))) return rc;
+    if (tr->logits) KH_HIP(hipMemcpyAsync(tr->logits, m->logits, 4 * m->spec.vocab, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    m->len += 1;
     return KH_OK;
 }
 

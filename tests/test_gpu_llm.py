@@ -8,8 +8,11 @@ layer, an activation requantised at the next projection can land on the
 neighbouring int8 code where it sits within rounding of a boundary.  Weights
 are N(0, 0.02), the benchmark's scale: with 0.08 the random model's attention
 is sharp enough that one such code moves the logits by up to 1.5e-2, and the
-oracle itself moves that much under 1e-5 relative noise on its projections.  The
-next token is the argmax of the step's own logits, exactly; the graph-replay
+oracle itself moves that much under 1e-5 relative noise on its projections.
+test_gpu_llm_stages.py holds every stage of every layer to 1e-5 on the
+device's own inputs, and test_oracle.py pins the oracle's composition to a
+float64 restatement at 1e-5.  The next token is the argmax of the step's own
+logits, exactly; the graph-replay
 path and the one-call-per-token path agree bit for bit; truncating and
 replaying repeats the logits bit for bit.
 """

@@ -7,9 +7,12 @@ with weights within 1e-6 (its exp and divide are the device's).  The layer's
 output agrees within 2e-3 x max|ref|: each of its GEMVs agrees with the
 oracle's to 1e-5, but the SwiGLU hidden is quantised again before the down
 projection, and a hidden value within rounding of a quantisation boundary
-takes the neighbouring int8 code on one side (about 1e-3 of codes at these
-shapes), a difference of one code step in that term.  The device's own
-decode and batched paths, and repeated runs, are compared as well.
+takes the neighbouring int8 code on one side, a difference of one code step
+in that term.  test_gpu_moe_stages.py holds every stage to 1e-5 on the
+device's own inputs and shows that the oracle's chain and the device's part
+only by such one-step codes (1 in 25344 hidden codes at DeepSeek-V2-Lite's
+shapes).  The device's own decode and batched paths, and repeated runs, are
+compared as well.
 """
 import numpy as np
 import pytest

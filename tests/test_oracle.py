@@ -712,3 +712,129 @@ def test_mla_oracle_drops_weights_below_1e_8():
     s = (ql[0].astype(np.float64) @ c.T.astype(np.float64)) * scale
     w = np.exp(s - s.max()) / np.exp(s - s.max()).sum()
     assert w[7] < 1e-8 < w.max()  # the skip does apply here
+
+
+# ---- the decoder's composition (O.Llm.forward) against a float64 restatement
+
+
+def _f64_llm(spec, layers, embed, final, head, cos_t, sin_t, tokens):
+    """The forward of llama.rs:224-289 between the embedding and the head
+    (:384-415), restated in float64 numpy from dequantised q8 weights.  Each
+    projection's input is quantised by the oracle's QActivation::new (the
+    reference quantises there too); everything else -- norms, RoPE, the
+    cache, attention with its 1e-8 skip (mod.rs:807), SwiGLU, the residual
+    adds -- is computed here in float64, independently of the oracle's C."""
+    e, hd, nh, nkv, eps = spec["n_embd"], spec["head_dim"], spec["n_head"], spec["n_kv_head"], spec["eps"]
+    half, group = hd // 2, nh // nkv
+    deq = lambda w, rows, cols: (np.repeat(np.asarray(w[0], np.float64).reshape(rows, cols // 32), 32, axis=1)
+                                 * np.asarray(w[1], np.float64).reshape(rows, cols))
+
+    def proj(w, rows, cols, x, bias=None):
+        xq, xs, _ = O.qact(np.asarray(x, np.float32))
+        y = deq(w, rows, cols) @ (np.repeat(np.asarray(xs, np.float64), 32) * xq)
+        return y if bias is None else y + np.asarray(bias, np.float64)
+
+    def norm(x, w):
+        x = np.asarray(x, np.float64)
+        return x / np.sqrt(np.mean(x * x) + eps) * np.asarray(w, np.float64)
+
+    def rope(x, pos):
+        c = np.asarray(cos_t, np.float64).reshape(-1, half)[pos]
+        s = np.asarray(sin_t, np.float64).reshape(-1, half)[pos]
+        if spec.get("rope_interleaved"):
+            a, b = x[0::2].copy(), x[1::2].copy()
+            x[0::2], x[1::2] = a * c - b * s, b * c + a * s
+        else:
+            a, b = x[:half].copy(), x[half:].copy()
+            x[:half], x[half:] = a * c - b * s, b * c + a * s
+        return x
+
+    qd, kvd = nh * hd, nkv * hd
+    kc = [[] for _ in layers]
+    vc = [[] for _ in layers]
+    out = []
+    for pos, tok in enumerate(tokens):
+        x = deq(embed, spec["vocab"], e)[tok]
+        for l, L in enumerate(layers):
+            h = norm(x, L["attn_norm"])
+            q = proj(L["q"], qd, e, h, L.get("q_b"))
+            k = proj(L["k"], kvd, e, h, L.get("k_b"))
+            v = proj(L["v"], kvd, e, h, L.get("v_b"))
+            for i in range(nh):
+                q[i * hd:(i + 1) * hd] = rope(q[i * hd:(i + 1) * hd], pos)
+            for i in range(nkv):
+                k[i * hd:(i + 1) * hd] = rope(k[i * hd:(i + 1) * hd], pos)
+            kc[l].append(k)
+            vc[l].append(v)
+            K_, V_ = np.array(kc[l]), np.array(vc[l])
+            att = np.zeros(qd)
+            for i in range(nh):
+                j = (i // group) * hd
+                sc = K_[:, j:j + hd] @ q[i * hd:(i + 1) * hd] / math.sqrt(hd)
+                w = np.exp(sc - sc.max())
+                w /= w.sum()
+                w[w < 1e-8] = 0.0
+                att[i * hd:(i + 1) * hd] = w @ V_[:, j:j + hd]
+            x = x + proj(L["o"], e, qd, att)
+            h = norm(x, L["mlp_norm"])
+            g = proj(L["gate"], spec["n_ff"], e, h)
+            u = proj(L["up"], spec["n_ff"], e, h)
+            x = x + proj(L["down"], e, spec["n_ff"], g / (1.0 + np.exp(-g)) * u)
+        out.append(proj(head, spec["vocab"], e, norm(x, final)))
+    return out
+
+
+def _two_layer_model(interleaved, seed=4000):
+    # a 2-layer q8 model with Qwen2-style biases; layer weights N(0, 0.1) and
+    # embeddings N(0, 0.05), so that every branch moves the logits by O(1)
+    rng = iter(range(seed, seed + 1000))
+    spec = dict(n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=32, n_ff=256, vocab=64, n_ctx=16, eps=1e-6,
+                rope_interleaved=int(interleaved))
+    qd, kvd, e = 128, 64, 128
+    q8 = lambda r, c, sc=0.1: O.quantize_q8(O.normal(next(rng), r * c, sc), r, c)
+    vec = lambda n, b=1.0: (b + O.normal(next(rng), n, 0.1)).astype(np.float32)
+    layers = []
+    for _ in range(2):
+        L = {n: q8(r, c) for n, (r, c) in dict(q=(qd, e), k=(kvd, e), v=(kvd, e), o=(e, qd), gate=(256, e),
+                                                up=(256, e), down=(e, 256)).items()}
+        L.update(attn_norm=vec(e), mlp_norm=vec(e), q_b=vec(qd, 0.0), k_b=vec(kvd, 0.0), v_b=vec(kvd, 0.0))
+        layers.append(L)
+    embed, final = q8(64, e, 0.05), vec(e)
+    cos_t, sin_t = O.rope_tables(32, 16, 1e6)
+    return spec, layers, embed, final, cos_t, sin_t
+
+
+TOKENS = [3, 17, 60, 42, 7, 7, 1]
+
+
+def _rel_errs(spec, layers, embed, final, cos_t, sin_t, oracle_layers=None):
+    want = _f64_llm(spec, layers, embed, final, embed, cos_t, sin_t, TOKENS)
+    ref = O.Llm(spec, oracle_layers or layers, embed, final, None, cos_t, sin_t)
+    return [float(np.max(np.abs(ref.forward(t).astype(np.float64) - want[i]))) / float(np.max(np.abs(want[i])))
+            for i, t in enumerate(TOKENS)]
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_the_oracles_decoder_is_the_float64_composition(interleaved):
+    # The oracle's logits agree with the float64 restatement to 1e-5 x max at
+    # every step (measured: under 3e-7 -- f32 rounding in the norms,
+    # attention and adds; no activation code moves across a boundary here).
+    errs = _rel_errs(*_two_layer_model(interleaved))
+    assert max(errs) <= 1e-5, errs
+
+
+@pytest.mark.parametrize("slip", ["down", "o", "attn_norm", "v_b"])
+def test_the_float64_composition_catches_a_wiring_slip(slip):
+    # the same check against an oracle whose second layer has one part
+    # planted wrong (its down / o projection zeroed, its attention norm
+    # weights all one, its v bias dropped) fails by far more than the bar
+    spec, layers, embed, final, cos_t, sin_t = _two_layer_model(False)
+    L = dict(layers[1])
+    if slip in ("down", "o"):
+        L[slip] = (np.zeros_like(L[slip][0]), L[slip][1])
+    elif slip == "attn_norm":
+        L[slip] = np.ones_like(L[slip])
+    else:
+        L[slip] = np.zeros_like(L[slip])
+    errs = _rel_errs(spec, layers, embed, final, cos_t, sin_t, oracle_layers=[layers[0], L])
+    assert max(errs) > 1e-2, errs
