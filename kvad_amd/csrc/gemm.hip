@@ -152,15 +152,17 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *part, in
     if ((N & 3) == 0) {  // the four outputs share a token
         const rsrc_t PT = rsrc(part, (size_t)ks * plane * 4);
         const unsigned o = (unsigned)(e0 * 4), step = (unsigned)(plane * 4);
+        // every split's load in flight at once (up to 32; those past ks read
+        // outside the buffer, as zeros), then the adds in split order
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int z0 = 0; z0 < ks; z0 += 8) {
-            float4 p[8];
+        for (int z0 = 0; z0 < ks; z0 += 32) {
+            float4 p[32];
 #pragma unroll
-            for (int j = 0; j < 8; j++)
+            for (int j = 0; j < 32; j++)
                 p[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                                       PT, z0 + j < ks ? o + (z0 + j) * step : 0xffffffffu, 0, 0));
 #pragma unroll
-            for (int j = 0; j < 8; j++)
+            for (int j = 0; j < 32; j++)
                 if (z0 + j < ks) x = make_float4(x.x + p[j].x, x.y + p[j].y, x.z + p[j].z, x.w + p[j].w);
         }
         const int r = (int)(e0 % N);
