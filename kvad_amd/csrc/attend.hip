@@ -118,7 +118,6 @@ __device__ __forceinline__ float rows_max(float x) {
 __device__ __forceinline__ float rows_min(float x) {
     return rows_reduce(x, [](float u, float v) { return fminf(u, v); });
 }
-
 // Split kernel, on matrix cores (v_mfma_f32_16x16x4_f32).  A workgroup of
 // four waves owns one KV head's G <= 16 query heads and P = 64 R positions;
 // wave w takes R tiles of 16 consecutive positions.  Per tile:
@@ -140,6 +139,103 @@ __device__ __forceinline__ float rows_min(float x) {
 // split covers the whole sequence, as the reference's exact weights
 // w = exp(s - M) * (1/S) with w < 1e-8 dropped (mod.rs:805-812).
 typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Fused RoPE (the session's step).  Wave w takes heads w, w + NW, ...: the
+// G query heads, then (in the workgroup holding the new position) the KV
+// head's new key as head G; lane l holds dims l (+ 64) of the head, loaded
+// ahead of the K and V loads and rotated while they fly.
+template <int HD, int NW>
+struct RopeIn {
+    static constexpr int RH = (16 + NW) / NW;  // heads per wave (at most G + 1 <= 17 heads)
+    static constexpr int HE = HD / 64;         // dims per lane
+    float x[RH][HE];
+};
+
+template <int HD, int NW>
+__device__ __forceinline__ void rope_load(const AttnArgs &a, RopeIn<HD, NW> &r, int wave, int lane, int G, int h0,
+                                          int kvh, bool holds) {
+#pragma unroll
+    for (int i = 0; i < RopeIn<HD, NW>::RH; i++) {
+        const int h = wave + i * NW;
+#pragma unroll
+        for (int e = 0; e < RopeIn<HD, NW>::HE; e++) r.x[i][e] = 0.0f;
+        if (h < G || (h == G && holds)) {  // uniform per wave
+            const float *src = h < G ? a.q + (size_t)(h0 + h) * HD : a.rope.kraw + (size_t)kvh * HD;
+#pragma unroll
+            for (int e = 0; e < RopeIn<HD, NW>::HE; e++) r.x[i][e] = src[lane + 64 * e];
+        }
+    }
+}
+
+// Per head: rms_norm with q_norm / k_norm (norm_heads, llama.rs:122-127),
+// then RoPE at position pos (Rope::apply / apply_interleaved,
+// tensor.rs:437-472), into s_rot[head]; when `holds`, the new key (s_rot[G])
+// and value (s_vnew) are also written into the caches at pos.  The caller
+// syncs the workgroup before reading s_rot / s_vnew.
+template <int HD, int NW>
+__device__ __forceinline__ void rope_apply(const AttnArgs &a, const RopeIn<HD, NW> &r, float (*s_rot)[HD],
+                                           float *s_vnew, int wave, int lane, int tid, int G, int kvh, int pos,
+                                           bool holds) {
+    constexpr int HE = RopeIn<HD, NW>::HE;
+    const int half = HD / 2;
+#pragma unroll
+    for (int i = 0; i < RopeIn<HD, NW>::RH; i++) {
+        const int h = wave + i * NW;
+        if (!(h < G || (h == G && holds))) continue;  // uniform per wave
+        float x[HE];
+#pragma unroll
+        for (int e = 0; e < HE; e++) x[e] = r.x[i][e];
+        const float *nw = h < G ? a.rope.q_norm : a.rope.k_norm;
+        if (nw) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < HE; e++) {
+                const float sq = x[e] * x[e];
+                ss = ss + sq;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + a.rope.eps);
+#pragma unroll
+            for (int e = 0; e < HE; e++) {
+                const float u = x[e] * inv;
+                x[e] = u * nw[lane + 64 * e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < HE; e++) {
+            const int d = lane + 64 * e;
+            // the pair partner: dim d +- half (half split) or d ^ 1 (interleaved)
+            float pv;
+            if (a.rope.interleaved) {
+                pv = __shfl_xor(x[e], 1);
+            } else {
+                if constexpr (HD == 128) pv = x[e ^ 1];  // d and d + 64 sit in one lane
+                else pv = __shfl_xor(x[e], 32);
+            }
+            const int ip = a.rope.interleaved ? d >> 1 : d % half;
+            const bool first = a.rope.interleaved ? (d & 1) == 0 : d < half;
+            const float c = a.rope.cos_t[(size_t)pos * half + ip], sn = a.rope.sin_t[(size_t)pos * half + ip];
+            float out;
+            if (first) {  // a = x, b = partner: a c - b s
+                const float ac = x[e] * c, bs = pv * sn;
+                out = ac - bs;
+            } else {      // b = x, a = partner: b c + a s
+                const float bc = x[e] * c, as = pv * sn;
+                out = bc + as;
+            }
+            s_rot[h][d] = out;
+            if (h == G) a.kw[(size_t)pos * a.kstride + (size_t)kvh * HD + d] = out;
+        }
+    }
+    if (holds) {
+        for (int d = tid; d < HD; d += 64 * NW) {
+            const float v = a.rope.vraw[(size_t)kvh * HD + d];
+            s_vnew[d] = v;
+            a.vw[(size_t)pos * a.vstride + (size_t)kvh * HD + d] = v;
+        }
+    }
+}
 
 template <int HD, int R, int NW, bool ROPE>
 __global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
@@ -184,28 +280,14 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
     // then values: loads complete in issue order
     const bool hv = j16 < G;
     f4v qb4[NQ4];
-    // Fused RoPE: wave w takes heads w, w + NW, ...: the G query heads, then
-    // (in the split holding the new position) the KV head's new key as head
-    // G; lane l holds dims l (+ 64) of the head, loaded now and rotated once
-    // the K and V loads are in flight.
+    // fused RoPE: the query heads (and, in the split holding the new
+    // position, the new key) loaded now, rotated once K and V are in flight
     constexpr bool rope = ROPE;  // launched with the rope argument set
     const int pos = L - 1;
     const bool holds = rope && pos >= t0 && pos < t0 + P;
-    constexpr int RH = (16 + NW) / NW;  // heads per wave (at most G + 1 <= 17 heads)
-    constexpr int HE = HD / 64;         // dims per lane
-    float xr[RH][HE];
+    RopeIn<HD, NW> xr;
     if (rope) {
-#pragma unroll
-        for (int i = 0; i < RH; i++) {
-            const int h = wave + i * NW;
-#pragma unroll
-            for (int e = 0; e < HE; e++) xr[i][e] = 0.0f;
-            if (h < G || (h == G && holds)) {  // uniform per wave
-                const float *src = h < G ? a.q + (size_t)(h0 + h) * HD : a.rope.kraw + (size_t)kvh * HD;
-#pragma unroll
-                for (int e = 0; e < HE; e++) xr[i][e] = src[lane + 64 * e];
-            }
-        }
+        rope_load<HD, NW>(a, xr, wave, lane, G, h0, kvh, holds);
     } else {
         const float *qh = a.q + (size_t)(h0 + (hv ? j16 : 0)) * HD + 4 * c4;
 #pragma unroll
@@ -236,70 +318,9 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
         }
 
     if (rope) {
-        // per head: rms_norm with q_norm / k_norm (norm_heads, llama.rs:122-127),
-        // then RoPE at the new position (Rope::apply / apply_interleaved,
-        // tensor.rs:437-472), into LDS; the new key and value also into the
-        // caches and into this workgroup's own registers for that position
         __shared__ __align__(16) float s_rot[17][HD];
         __shared__ __align__(16) float s_vnew[HD];
-        const int half = HD / 2;
-#pragma unroll
-        for (int i = 0; i < RH; i++) {
-            const int h = wave + i * NW;
-            if (!(h < G || (h == G && holds))) continue;  // uniform per wave
-            float x[HE];
-#pragma unroll
-            for (int e = 0; e < HE; e++) x[e] = xr[i][e];
-            const float *nw = h < G ? a.rope.q_norm : a.rope.k_norm;
-            if (nw) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int e = 0; e < HE; e++) {
-                    const float sq = x[e] * x[e];
-                    ss = ss + sq;
-                }
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
-                const float inv = 1.0f / sqrtf(ss / (float)HD + a.rope.eps);
-#pragma unroll
-                for (int e = 0; e < HE; e++) {
-                    const float u = x[e] * inv;
-                    x[e] = u * nw[lane + 64 * e];
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < HE; e++) {
-                const int d = lane + 64 * e;
-                // the pair partner: dim d +- half (half split) or d ^ 1 (interleaved)
-                float pv;
-                if (a.rope.interleaved) {
-                    pv = __shfl_xor(x[e], 1);
-                } else {
-                    if constexpr (HD == 128) pv = x[e ^ 1];  // d and d + 64 sit in one lane
-                    else pv = __shfl_xor(x[e], 32);
-                }
-                const int ip = a.rope.interleaved ? d >> 1 : d % half;
-                const bool first = a.rope.interleaved ? (d & 1) == 0 : d < half;
-                const float c = a.rope.cos_t[(size_t)pos * half + ip], sn = a.rope.sin_t[(size_t)pos * half + ip];
-                float out;
-                if (first) {  // a = x, b = partner: a c - b s
-                    const float ac = x[e] * c, bs = pv * sn;
-                    out = ac - bs;
-                } else {      // b = x, a = partner: b c + a s
-                    const float bc = x[e] * c, as = pv * sn;
-                    out = bc + as;
-                }
-                s_rot[h][d] = out;
-                if (h == G) a.kw[(size_t)pos * a.kstride + (size_t)kvh * HD + d] = out;
-            }
-        }
-        if (holds) {
-            for (int d = tid; d < HD; d += NTH) {
-                const float v = a.rope.vraw[(size_t)kvh * HD + d];
-                s_vnew[d] = v;
-                a.vw[(size_t)pos * a.vstride + (size_t)kvh * HD + d] = v;
-            }
-        }
+        rope_apply<HD, NW>(a, xr, s_rot, s_vnew, wave, lane, tid, G, kvh, pos, holds);
         __syncthreads();
         const float *qh = &s_rot[hv ? j16 : 0][4 * c4];
 #pragma unroll
@@ -749,6 +770,25 @@ void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
 
 namespace {
 
+// The longest sequence taken as one split (every load of the sequence in
+// flight in one workgroup): 256 positions at hd 64, 128 at hd 128, as
+// measured against split + merge on the box; KVAD_ATTN_SINGLE lowers it
+// (0: always split and merge).
+size_t single_max(int head_dim) {
+    const size_t hw = head_dim == 64 ? 256 : 128;
+    const int v = env_int("KVAD_ATTN_SINGLE", -1);
+    return v < 0 ? hw : std::min(hw, (size_t)v);
+}
+
+// Query heads per workgroup: the largest divisor of the group size that
+// fits the 16 columns of the score product.
+int heads_per_wg(int group) {
+    int gc = 1;
+    for (int c = 1; c <= 16; c++)
+        if (group % c == 0) gc = c;
+    return gc;
+}
+
 // The launch for n_positions (or, with a device length, for at most that
 // many): split size, partial buffers carved from ws.
 int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
@@ -768,12 +808,22 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     a.vstride = vstride;
     a.n_head = n_head;
     a.group = n_head / n_kv_head;
-    int gc = 1;  // query heads per workgroup: the 16 columns of the score product
-    for (int c = 1; c <= 16; c++)
-        if (a.group % c == 0) gc = c;
+    const int gc = heads_per_wg(a.group);
     a.gc = gc;
     const int n_hg = n_head / gc;
     a.L = (int)n_positions;
+    a.scale = 1.0f / sqrtf((float)head_dim);  // mod.rs:777
+    a.out = out;
+    // A short sequence runs as one split: the split kernel applies the
+    // reference's exact weights itself and no merge is launched.
+    if (n_positions <= single_max(head_dim)) {
+        int P = 64;
+        while ((size_t)P < n_positions) P *= 2;
+        a.P = P;
+        a.nw = P == 256 ? 8 : 4;
+        a.nsplit = 1;
+        return KH_OK;
+    }
     // positions per split: the largest rung that still gives a workgroup
     // per CU, or a larger one when the merge's split limit needs it
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -794,8 +844,6 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     const int fw = env_int("KVAD_ATTN_WAVES", 0);
     a.nw = P >= 128 && (fw == 8 || (fw != 4 && P == 256)) ? 8 : 4;
     a.nsplit = (int)((n_positions + P - 1) / P);
-    a.scale = 1.0f / sqrtf((float)head_dim);  // mod.rs:777
-    a.out = out;
     return KH_OK;
 }
 
@@ -833,6 +881,8 @@ int run(kh_ctx *ctx, const AttnArgs &a, int head_dim, int nb = 1) {
 }
 
 }  // namespace
+
+size_t attend_single_max(int head_dim) { return head_dim == 64 || head_dim == 128 ? single_max(head_dim) : 0; }
 
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions) {
     (void)n_kv_head;

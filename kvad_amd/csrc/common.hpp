@@ -124,7 +124,12 @@ struct kh_llm {
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     size_t len = 0;                                          // positions in the cache
-    hipGraphExec_t graph = nullptr;                          // one captured step
+    // one captured step per attention bucket, keyed by its launch maximum:
+    // powers of two from 64 up to attn_short (attention as one split, no
+    // merge launch), then n_ctx
+    std::map<size_t, hipGraphExec_t> graphs;
+    size_t attn_short = 0;                                   // attend_single_max, at most n_ctx
+    size_t attn_max = 0;                                     // the launch maximum of the step being issued
     // Session::park / resume (model/mod.rs:889-897): caches handed out and
     // not yet taken back or freed, and freed ones kept for the next park
     std::set<kh_llm_parked *> parked;
@@ -134,7 +139,7 @@ struct kh_llm {
     void *rows_buf = nullptr;
     size_t rows_cap = 0;
     std::vector<char> rows_host;
-    std::map<size_t, hipGraphExec_t> rows_graphs;            // the pass for n rows, captured once per n
+    std::map<std::pair<size_t, size_t>, hipGraphExec_t> rows_graphs;  // the pass for n rows, per (n, bucket)
 };
 
 // A conversation's cache set aside (Session::park, model/mod.rs:889-893): per
@@ -361,6 +366,9 @@ int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, c
                          const float *v, size_t kv_stride_k, size_t kv_stride_v, const int32_t *len_dev, int plus_one,
                          size_t max_positions, float *out, void *ws, const AttnRope *rope = nullptr);
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions);
+// The longest sequence the launches above take as one split (no partials,
+// no merge launch); 0 when none.
+size_t attend_single_max(int head_dim);
 // Attention with its partials in the library's static per-device scratch
 // array (attend.hip): no allocation.  scratch_init(device), with that device
 // current, looks up the array's device address once per device (kh_init

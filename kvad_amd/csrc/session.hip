@@ -212,7 +212,7 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr) {
         const AttnRope rp{m->qkv + qd, m->qkv + qd + kvd, m->rope_cos, m->rope_sin, L.q_norm, L.k_norm,
                           s.eps, s.rope_interleaved, 0};
         if ((rc = launch_attend_devlen(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, m->qkv, m->kc[l],
-                                       m->vc[l], kvd, kvd, m->pos, 1, s.n_ctx, m->att, m->attn_ws, &rp)))
+                                       m->vc[l], kvd, kvd, m->pos, 1, m->attn_max, m->att, m->attn_ws, &rp)))
             return rc;
         jobs.clear();
         jobs.push_back({L.o, gemv_job(L.o, m->att, nullptr, nullptr, m->x, 1)});
@@ -402,7 +402,7 @@ int norm_rows(kh_ctx *ctx, const float *x, const float *w, size_t n, size_t e, f
 // run_rows (llama.rs:224-289) with Rows::Each, then the head over every row
 // (llama.rs:404-416) and each row's greedy token.  The table (tokens, and per
 // layer each row's cache and length) is already on the device.
-int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
+int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len) {
     const kh_llm_spec &s = m->spec;
     const size_t e = s.n_embd, qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
     int rc;
@@ -423,7 +423,7 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b) {
         const AttnRow *tab = b.tab + l * n;
         const AttnRope rp{b.k, b.v, m->rope_cos, m->rope_sin, L.q_norm, L.k_norm, s.eps, s.rope_interleaved, kvd};
         if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
-                                     kvd, s.n_ctx, b.att, b.ws, b.ws_bytes, &rp)))
+                                     kvd, max_len, b.att, b.ws, b.ws_bytes, &rp)))
             return rc;
         if (L.o->precision != KH_F32 && n <= (size_t)MULTI_TOKENS && n <= rows_multi_max()) {
             // x += o(attn): the multi-token GEMV quantises the attention rows
@@ -503,11 +503,54 @@ void drop_cache(kh_llm *m, std::vector<float *> &k, std::vector<float *> &v) {
     v.clear();
 }
 
-void drop_graph(kh_llm *m) {  // the captured step names the held cache
-    if (m->graph) {
-        (void)hipGraphExecDestroy(m->graph);
-        m->graph = nullptr;
+void drop_graph(kh_llm *m) {  // the captured steps name the held cache
+    for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.second);
+    m->graphs.clear();
+}
+
+// The attention launch maximum for a step that ends with `len` positions
+// held: the next power of two from 64 while that is at most attn_short (one
+// split of the split kernel takes the whole sequence, no merge launch), else
+// n_ctx.  Per-token calls and captured steps pick alike, so their results
+// agree to the bit.
+size_t bucket_max(const kh_llm *m, size_t len) {
+    if (len > m->attn_short) return m->spec.n_ctx;
+    size_t b = 64;
+    while (b < len) b *= 2;
+    return std::min(b, m->attn_short);
+}
+
+// Capture the step of bucket bm unless it is held (the launches read pos and
+// token from the device, so one capture serves every step of the bucket).
+int capture_step(kh_ctx *ctx, kh_llm *m, size_t bm) {
+    if (m->graphs.count(bm)) return KH_OK;
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    m->attn_max = bm;
+    hipGraph_t g = nullptr;
+    KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = step(ctx, m);
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
     }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    m->graphs[bm] = x;
+    return KH_OK;
+}
+
+// n steps from m->len: capture the buckets they cross first, then replay.
+int replay_steps(kh_ctx *ctx, kh_llm *m, size_t n) {
+    int rc;
+    for (size_t i = 0; i < n; i++)
+        if ((rc = capture_step(ctx, m, bucket_max(m, m->len + i + 1)))) return rc;
+    for (size_t i = 0; i < n; i++)
+        KH_HIP(hipGraphLaunch(m->graphs.at(bucket_max(m, m->len + i + 1)), ctx->stream));
+    return KH_OK;
 }
 
 }  // namespace
@@ -552,6 +595,8 @@ int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out) {
     m->token = m->state, m->pos = m->state + 1, m->steps = m->state + 2;
     KH_HIP(hipMemset(m->state, 0, 3 * sizeof(int32_t)));
     m->attn_ws_bytes = attend_ws_bytes((int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, s.n_ctx);
+    m->attn_short = std::min(attend_single_max((int)s.head_dim), s.n_ctx);
+    m->attn_max = s.n_ctx;
     KH_HIP(hipMalloc(&m->attn_ws, m->attn_ws_bytes));
     *out = m.release();
     return KH_OK;
@@ -563,7 +608,7 @@ int kh_llm_free(kh_llm *m) {
         std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
         (void)hipSetDevice(m->ctx->device);
         (void)hipStreamSynchronize(m->ctx->stream);
-        if (m->graph) (void)hipGraphExecDestroy(m->graph);
+        drop_graph(m);
         drop_rows_graphs(m);
         for (auto p : m->kc) (void)hipFree(p);
         for (auto p : m->vc) (void)hipFree(p);
@@ -680,6 +725,7 @@ int kh_llm_forward(kh_ctx *ctx, kh_llm *m, int32_t token, float *logits, int32_t
     if (m->len >= m->spec.n_ctx) return fail(KH_EINVAL, "kh_llm_forward: the context window is full");
     const int32_t st[3] = {token, (int32_t)m->len, 0};
     KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
+    m->attn_max = bucket_max(m, m->len + 1);
     if ((rc = step(ctx, m))) return rc;
     if (logits) KH_HIP(hipMemcpyAsync(logits, m->logits, 4 * m->spec.vocab, hipMemcpyDeviceToHost, ctx->stream));
     int32_t nt = 0;
@@ -700,6 +746,7 @@ int kh_debug_llm_trace(kh_ctx *ctx, kh_llm *m, int32_t token, const kh_llm_trace
     if (m->len >= m->spec.n_ctx) return fail(KH_EINVAL, "kh_debug_llm_trace: the context window is full");
     const int32_t st[3] = {token, (int32_t)m->len, 0};
     KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
+    m->attn_max = bucket_max(m, m->len + 1);
     if ((rc = step(ctx, m, tr))) return rc;
     if (tr->logits) KH_HIP(hipMemcpyAsync(tr->logits, m->logits, 4 * m->spec.vocab, hipMemcpyDeviceToHost, ctx->stream));
     KH_HIP(hipStreamSynchronize(ctx->stream));
@@ -722,34 +769,13 @@ int kh_llm_generate(kh_ctx *ctx, kh_llm *m, int32_t token, size_t n, int32_t *to
             (void)hipFree(m->out);
             m->out = nullptr;
         }
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
         KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->out), 4 * n));
         m->out_cap = (int)n;
     }
     const int32_t st[3] = {token, (int32_t)m->len, 0};
     KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
-    if (!m->graph) {  // one token's launches, captured once (they read pos and token from the device)
-        KH_HIP(hipStreamSynchronize(ctx->stream));
-        hipGraph_t g = nullptr;
-        KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-        rc = step(ctx, m);
-        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
-        if (rc) {
-            if (g) (void)hipGraphDestroy(g);
-            return rc;
-        }
-        if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-        e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
-        if (e != hipSuccess) {
-            m->graph = nullptr;
-            return hip_fail(e, "hipGraphInstantiate");
-        }
-    }
-    for (size_t i = 0; i < n; i++) KH_HIP(hipGraphLaunch(m->graph, ctx->stream));
+    if ((rc = replay_steps(ctx, m, n))) return rc;
     KH_HIP(hipMemcpyAsync(tokens, m->out, 4 * n, hipMemcpyDeviceToHost, ctx->stream));
     KH_HIP(hipStreamSynchronize(ctx->stream));
     m->len += n;
@@ -759,10 +785,12 @@ int kh_llm_generate(kh_ctx *ctx, kh_llm *m, int32_t token, size_t n, int32_t *to
 int kh_llm_generate_launch(kh_ctx *ctx, kh_llm *m, size_t n) {
     // Replays n more steps of an already-captured graph from the device state
     // as it stands, without copying anything back (for timing).
-    if (!ctx || !m || !m->graph) return fail(KH_EINVAL, "kh_llm_generate_launch: no captured step");
+    if (!ctx || !m || m->graphs.empty())
+        return fail(KH_EINVAL, "kh_llm_generate_launch: no captured step");
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     if (m->len + n > m->spec.n_ctx) return fail(KH_EINVAL, "kh_llm_generate_launch: the steps would overrun the context");
-    for (size_t i = 0; i < n; i++) KH_HIP(hipGraphLaunch(m->graph, ctx->stream));
+    const int rc = replay_steps(ctx, m, n);
+    if (rc) return rc;
     m->len += n;
     return KH_OK;
 }
@@ -869,17 +897,21 @@ int kh_llm_forward_each(kh_ctx *ctx, kh_llm *m, size_t n, const int32_t *tokens,
     m->rows_host.resize(tok_bytes + tab_bytes);
     std::copy(tokens, tokens + n, reinterpret_cast<int32_t *>(m->rows_host.data()));
     AttnRow *tab = reinterpret_cast<AttnRow *>(m->rows_host.data() + tok_bytes);
+    size_t longest = 0;
+    for (size_t i = 0; i < n; i++) longest = std::max(longest, caches[i]->len + 1);
     for (size_t l = 0; l < s.n_layer; l++)
         for (size_t i = 0; i < n; i++) tab[l * n + i] = AttnRow{caches[i]->k[l], caches[i]->v[l], (int)caches[i]->len + 1};
     // the pass for n rows reads everything it varies on from the table, so
-    // it is captured once per n and replayed
-    auto it = m->rows_graphs.find(n);
+    // it is captured once per n and attention bucket (of the longest row) and replayed
+    const size_t bm = bucket_max(m, longest);
+    const std::pair<size_t, size_t> key{n, bm};
+    auto it = m->rows_graphs.find(key);
     if (it == m->rows_graphs.end()) {
         if ((rc = gemm_split_reserve(ctx))) return rc;
         KH_HIP(hipStreamSynchronize(ctx->stream));
         hipGraph_t g = nullptr;
         KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-        rc = step_rows(ctx, m, n, b);
+        rc = step_rows(ctx, m, n, b, bm);
         hipError_t e = hipStreamEndCapture(ctx->stream, &g);
         if (rc) {
             if (g) (void)hipGraphDestroy(g);
@@ -890,7 +922,7 @@ int kh_llm_forward_each(kh_ctx *ctx, kh_llm *m, size_t n, const int32_t *tokens,
         e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
-        it = m->rows_graphs.emplace(n, x).first;
+        it = m->rows_graphs.emplace(key, x).first;
     }
     KH_HIP(hipMemcpyAsync(b.tok, m->rows_host.data(), tok_bytes, hipMemcpyHostToDevice, ctx->stream));
     KH_HIP(hipMemcpyAsync(b.tab, tab, tab_bytes, hipMemcpyHostToDevice, ctx->stream));

@@ -139,13 +139,51 @@ def test_attend_rejects_more_positions_than_cached(ctx):
         K.attend(ctx, K.Spec(14, 3, 64), O.normal(1, 14 * 64), cache, 0, 5)
 
 
-@pytest.mark.parametrize("n_head,n_kv,L", [(4, 1, 3000), (4, 1, 20000), (14, 2, 32768)])
-def test_attend_skip_across_many_splits(ctx, n_head, n_kv, L):
+# KVAD_ATTN_SINGLE lowers the longest sequence taken as one split (256
+# positions at head_dim 64, 128 at 128): 0 makes every call split and merge.
+SINGLE, SPLIT = None, "0"
+
+
+def attn_mode(monkeypatch, mode):
+    if mode is None:
+        monkeypatch.delenv("KVAD_ATTN_SINGLE", raising=False)
+    else:
+        monkeypatch.setenv("KVAD_ATTN_SINGLE", mode)
+
+
+@pytest.mark.parametrize("spec,L", [(QWEN, 1), (QWEN, 17), (QWEN, 100), (QWEN, 200), (QWEN, 256), (LLAMA, 1),
+                                    (LLAMA, 100), (LLAMA, 128), (K.Spec(16, 1, 128), 128),
+                                    (K.Spec(4, 4, 64), 233), (K.Spec(24, 2, 64), 77)])
+def test_one_split_and_split_merge_agree(ctx, monkeypatch, spec, L):
+    # the whole sequence as one split (the reference's exact weights, no
+    # merge launch) against the same call split and merged, both against
+    # the oracle; at one position both are exact
+    say("attend single vs split", spec, L)
+    cache, ks, vs = filled_cache(ctx, spec, L, seed=L + 5)
+    q = O.normal(L + 105, spec.n_head * spec.head_dim)
+    want = O.attend(spec.n_head, spec.n_kv_head, spec.head_dim, q, ks[0], vs[0], L)
+    attn_mode(monkeypatch, SINGLE)
+    single = K.attend(ctx, spec, q, cache, 0, L)
+    attn_mode(monkeypatch, SPLIT)
+    split = K.attend(ctx, spec, q, cache, 0, L)
+    close(single, want)
+    close(split, want)
+    if L == 1:
+        np.testing.assert_array_equal(single, want)
+        np.testing.assert_array_equal(split, want)
+
+
+@pytest.mark.parametrize("n_head,n_kv,L,mode", [(4, 1, 3000, SPLIT), (4, 1, 20000, SPLIT), (14, 2, 32768, SPLIT),
+                                                (4, 1, 256, SPLIT), (4, 1, 256, SINGLE), (14, 2, 250, SINGLE),
+                                                (16, 1, 200, SINGLE)])
+def test_attend_skip_across_many_splits(ctx, monkeypatch, n_head, n_kv, L, mode):
     # A few dominant positions; the rest spread across the 1e-8 line, so some
     # splits are left out whole, some kept whole and most straddle it.  Values
     # are large, so a skipped term wrongly kept (or a kept one dropped) shows.
-    # Qwen's geometry at 32768 positions runs the 256-position splits.
-    say("attend skip, many splits", n_head, n_kv, L)
+    # Qwen's geometry at 32768 positions runs the 256-position splits; a
+    # single split drops the same weights itself.
+    attn_mode(monkeypatch, mode)
+    say("attend skip, many splits", n_head, n_kv, L, mode)
     spec = K.Spec(n_head, n_kv, 64)
     kvd = n_kv * 64
     rng = np.random.default_rng(L)

@@ -66,9 +66,13 @@ VARIANTS = {
 }
 
 
+@pytest.mark.parametrize("attn", ["single", "split"])
 @pytest.mark.parametrize("variant", list(VARIANTS))
-def test_several_conversations_at_once_say_what_each_says_alone(ctx, variant):
-    say("forward_each vs alone", variant)
+def test_several_conversations_at_once_say_what_each_says_alone(ctx, monkeypatch, variant, attn):
+    # every row's attention as one split, or (KVAD_ATTN_SINGLE=0) split and merged
+    if attn == "split":
+        monkeypatch.setenv("KVAD_ATTN_SINGLE", "0")
+    say("forward_each vs alone", variant, attn)
     one, mk = build(ctx, 700, **VARIANTS[variant])
     alle, _ = build(ctx, 700, **VARIANTS[variant])
     theirs, ours = set_aside(one, PROMPTS), set_aside(alle, PROMPTS)
@@ -173,11 +177,15 @@ def test_many_rows_on_the_multi_token_gemv_and_the_gemm(ctx, case):
             assert nxt[i] == O.argmax(got[i])
 
 
-def test_long_conversations_attend_across_many_splits(ctx):
-    # lengths 1..300 in one pass: rows of one split and rows of several
-    say("forward_each long")
+@pytest.mark.parametrize("attn", ["single", "split"])
+def test_long_conversations_attend_across_many_splits(ctx, monkeypatch, attn):
+    # lengths 1..300 in one pass: rows of one split and rows of several; or
+    # lengths 1..251, every row's attention one split (the pass is bucketed
+    # by its longest row)
+    monkeypatch.delenv("KVAD_ATTN_SINGLE", raising=False)
+    say("forward_each long", attn)
     m, mk = build(ctx, 760, n_ctx=512)
-    lens = [300, 1, 129, 64, 65]
+    lens = [300, 1, 129, 64, 65] if attn == "split" else [250, 1, 129, 64, 65]
     prompts = [[(13 * i + 5 * j) % 512 for j in range(L)] for i, L in enumerate(lens)]
     parked = set_aside(m, prompts)
     refs = [mk() for _ in prompts]

@@ -95,16 +95,19 @@ def run_both(m, ref, tokens):
     return worst
 
 
-@pytest.mark.parametrize("variant", ["qwen2", "qwen3", "llama_interleaved", "qwen2_f32", "llama_q4k"])
+FORWARD_VARIANTS = {
+    "qwen2": dict(bias=True), "qwen3": dict(bias=False, qk_norm=True, tied=False),
+    "llama_interleaved": dict(bias=False, interleaved=True, n_head=8, n_kv_head=2, head_dim=128, n_embd=256),
+    "qwen2_f32": dict(bias=True, tied=False, prec="f32"),
+    # Q4_K layer weights (GGUF-style): q/k/v take the fused rms_norm
+    # input, down swiglu(gate, up), o and down add the residual
+    "llama_q4k": dict(bias=False, interleaved=True, n_head=16, n_kv_head=4, head_dim=128, n_embd=2048,
+                      n_ff=2048, prec="q4k")}
+
+
+@pytest.mark.parametrize("variant", list(FORWARD_VARIANTS))
 def test_forward_matches_the_oracle(ctx, variant):
-    kw = {"qwen2": dict(bias=True), "qwen3": dict(bias=False, qk_norm=True, tied=False),
-          "llama_interleaved": dict(bias=False, interleaved=True, n_head=8, n_kv_head=2, head_dim=128,
-                                    n_embd=256),
-          "qwen2_f32": dict(bias=True, tied=False, prec="f32"),
-          # Q4_K layer weights (GGUF-style): q/k/v take the fused rms_norm
-          # input, down swiglu(gate, up), o and down add the residual
-          "llama_q4k": dict(bias=False, interleaved=True, n_head=16, n_kv_head=4, head_dim=128, n_embd=2048,
-                            n_ff=2048, prec="q4k")}[variant]
+    kw = FORWARD_VARIANTS[variant]
     say("llm forward", variant)
     m, mk = build(ctx, 100, **kw)
     ref = mk()
@@ -191,3 +194,27 @@ def test_new_rope_tables_reach_the_captured_step(ctx):
     m2, _ = build(ctx, 600)
     m2.set_rope(cos_t, sin_t, 64)
     np.testing.assert_array_equal(m1.generate(5, 6), m2.generate(5, 6))
+
+
+@pytest.mark.parametrize("single,variant", [("0", "qwen3"), ("0", "llama_interleaved"), ("16", "qwen2"),
+                                            ("16", "llama_interleaved"), ("16", "qwen2_f32")])
+def test_attention_buckets(ctx, monkeypatch, single, variant):
+    # The step's attention runs as one split (RoPE and the cache push inside,
+    # no merge launch) while the sequence is short, and split + merge past
+    # that, one token at a time and in the captured steps alike.
+    # KVAD_ATTN_SINGLE moves the line: 0 splits from the first token, 16
+    # switches after 16 positions.
+    monkeypatch.setenv("KVAD_ATTN_SINGLE", single)
+    say("llm attention buckets", single, variant)
+    m, mk = build(ctx, 140, **FORWARD_VARIANTS[variant])
+    tokens = [3, 17, 500, 42, 7, 7, 99, 1, 256, 12, 5, 6, 7, 8, 9, 10, 11, 300, 301, 302, 2, 4]
+    run_both(m, mk(), tokens)
+    m1, _ = build(ctx, 140, **FORWARD_VARIANTS[variant])
+    m2, _ = build(ctx, 140, **FORWARD_VARIANTS[variant])
+    got = m1.generate(5, 12)
+    got = np.concatenate([got, m1.generate(int(got[-1]), 12)])  # across the line, both steps captured
+    t, want = 5, []
+    for _ in range(24):
+        _, t = m2.forward(t)
+        want.append(t)
+    np.testing.assert_array_equal(got, want)
