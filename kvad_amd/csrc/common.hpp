@@ -209,6 +209,11 @@ size_t fuse_max_cols(int precision);
 
 // Runs every job in one launch per input kind (all jobs share `precision`).
 int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs);
+struct RouteArgs;
+// One launch of `jobs` (f32 inputs, q8) whose job route_job is a router:
+// its one workgroup computes the token's logits and routes them (r.logits
+// unused); KH_DECLINED where no such kernel is built for the launch's shape.
+int launch_gemv_route(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs, int route_job, const RouteArgs &r);
 
 // y[m, rows] = x W^T (+bias) for a few quantised token rows (m small): the
 // weights stream once for all of them.  x holds the rows' codes.

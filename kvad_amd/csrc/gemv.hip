@@ -28,6 +28,7 @@
 // rows per wave (R), so a row computed in a matvec_many launch equals the
 // same row computed alone, to the bit.
 #include "gemv_core.hpp"
+#include "route.hpp"
 
 #include <vector>
 
@@ -134,10 +135,13 @@ __global__ __launch_bounds__(256) void norm_qact_kernel(const float *__restrict_
 // jobs in proportion to their rows; each wave walks the row groups
 // lw, lw + nw, ... of its job, loading the next group's weights before it
 // computes the current one.  The first group's loads are issued before the
-// activation is staged, so they fly while the workgroup quantises.
-template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB>
+// activation is staged, so they fly while the workgroup quantises.  With
+// ROUTE, the router job (one workgroup, every router row) also keeps its
+// outputs in LDS and its first wave routes them (MoE decode).
+template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB, bool ROUTE = false>
 __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ float s_lg[ROUTE ? MAX_EXPERTS : 1];  // the router's logits
     const int tid = threadIdx.x;
     const int lane = tid & (WAVE - 1);
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -146,6 +150,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     for (int i = 1; i < tab.n; i++)
         if (blk >= tab.j[i].wave0) ji = i;
     const GemvJob &job = tab.j[ji];
+    const bool routes = ROUTE && ji == tab.route_job - 1;  // uniform per workgroup
     const int rows = job.rows, cols = job.cols, nb = cols / BLOCK;
     const int C = chunks_per_row(PREC, cols);
     const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
@@ -234,6 +239,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
                     float out = job.bias ? v + b : v;
                     if (job.accumulate) out = y0 + out;  // x += proj (llama.rs:273-276)
                     job.y[r] = out;
+                    if (routes) s_lg[r] = out;
                 }
                 acc[i] = 0.0f;
             }
@@ -248,6 +254,12 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
         run_step(ca, step);
         load_step(ca, step + 2);
         if (step + 1 < steps) run_step(cb, step + 1);
+    }
+    if constexpr (ROUTE) {
+        if (routes) {
+            __syncthreads();  // every wave's logits are in LDS
+            if (wv == 0) route_one(tab.route, 0, s_lg);
+        }
     }
 }
 
@@ -596,7 +608,7 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
         const int want = (groups + p.nwv - 1) / p.nwv;
         int share = (int)((long long)cap_wg * tab.j[i].rows / (rows_total > 0 ? rows_total : 1));
         if (share < 1) share = 1;
-        const int nwg = want < share ? want : share;
+        const int nwg = i == tab.route_job - 1 ? 1 : want < share ? want : share;  // the router: one workgroup
         tab.j[i].wave0 = blocks;  // first workgroup of the job
         tab.j[i].nwaves = nwg * p.nwv;
         blocks += nwg;
@@ -631,6 +643,22 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
         launch_kind<PREC, CPL, 1, true>(ctx, tab, blocks, lds, kind);         \
         KH_HIP(hipGetLastError());                                            \
         return KH_OK;                                                         \
+    }
+    if (tab.route_job) {  // the MoE decode step's router with its routing
+#define KH_ROUTE(CPL, R)                                                                                       \
+    if (p.cpl == CPL && p.r == R) {                                                                            \
+        hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_F32, false, false, WPB, true>), dim3(blocks),         \
+                           dim3(WAVE * WPB), lds, ctx->stream, tab);                                           \
+        KH_HIP(hipGetLastError());                                                                             \
+        return KH_OK;                                                                                          \
+    }
+        if constexpr (PREC == KH_Q8) {
+            if (kind == IN_F32 && !wide && p.nwv == WPB) {
+                KH_ROUTE(1, 4) KH_ROUTE(1, 2) KH_ROUTE(2, 2) KH_ROUTE(2, 1) KH_ROUTE(4, 1)
+            }
+        }
+#undef KH_ROUTE
+        return fail(KH_DECLINED, "matvec: no routing kernel for this plan");
     }
     if (p.nwv == 16) {
         if (p.cpl != 2 || p.r != 1 || wide) return fail(KH_EINVAL, "matvec: no 16-wave kernel for this plan");
@@ -844,6 +872,29 @@ int launch_gemv(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs) {
         if (precision == KH_F32) break;
     }
     return KH_OK;
+}
+
+int launch_gemv_route(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs, int route_job,
+                      const RouteArgs &r) {
+    if (njobs <= 0 || njobs > MAX_JOBS || route_job < 0 || route_job >= njobs)
+        return fail(KH_EINVAL, "matvec: bad routed job table");
+    if (r.n > MAX_EXPERTS || r.top_k > MAX_TOPK || r.n_group > MAX_GROUPS || jobs[route_job].rows != r.n)
+        return fail(KH_DECLINED, "matvec: a router the fused routing does not take");
+    if (precision != KH_Q8) return fail(KH_DECLINED, "matvec: routed launches are built for q8");
+    JobTable tab{};
+    tab.n = njobs;
+    tab.route_job = route_job + 1;
+    tab.route = r;
+    int maxC = 0, maxCols = 0, rows_total = 0;
+    for (int i = 0; i < njobs; i++) {
+        tab.j[i] = jobs[i];
+        if (input_kind(jobs[i]) != IN_F32 || jobs[i].dots) return fail(KH_DECLINED, "matvec: routed jobs take f32 x");
+        const int c = chunks_per_row(precision, jobs[i].cols);
+        maxC = c > maxC ? c : maxC;
+        maxCols = jobs[i].cols > maxCols ? jobs[i].cols : maxCols;
+        rows_total += jobs[i].rows;
+    }
+    return launch_prec<KH_Q8>(ctx, tab, maxC, maxCols, rows_total, false, IN_F32);
 }
 
 int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,

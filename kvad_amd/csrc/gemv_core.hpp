@@ -19,6 +19,10 @@ constexpr int MAX_JOBS = 24;
 struct JobTable {
     GemvJob j[MAX_JOBS];
     int n;
+    // ROUTE kernels: 1 + the job whose one workgroup, having computed a
+    // token's router logits, also routes them (route.hpp); 0: none
+    int route_job;
+    RouteArgs route;
 };
 
 // Chunks of 16 bytes per weight row.

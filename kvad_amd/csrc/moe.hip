@@ -2,12 +2,13 @@
 // ffn.rs:615-708) with Router::route (ffn.rs:256-349), mix (ffn.rs:744-806),
 // decode_together (ffn.rs:820-842) and SharedExpert::run (ffn.rs:437-451).
 //
-// Decode (one token) is four launches and no host round trip: (1) one GEMV
-// launch for the router and the shared expert's gate and up, which read the
-// same input; (2) the router, one wave, which writes the chosen experts in
-// expert order; (3) one GEMV launch for every chosen expert's gate and up,
-// each job reading its weight through a device table indexed by the router's
-// pick; (4) one GEMV launch for every down projection, the shared expert's
+// Decode (one token) is three GEMV launches and the combine, with no host
+// round trip: (1) one GEMV launch for the router and the shared expert's
+// gate and up, which read the same input, (2) in whose router workgroup one
+// wave routes the logits and writes the chosen experts in expert order (a
+// launch of its own where the GEMV has no routing build for the shape);
+// (3) one GEMV launch for every chosen expert's gate and up, each job
+// reading its weight through a device table indexed by the router's pick; (4) one GEMV launch for every down projection, the shared expert's
 // included, each staging swiglu(gate, up) as its input; then the combine,
 // which adds the weighted expert outputs to the shared expert's in expert
 // order -- the order mix() adds them, so the sum rounds as the reference's.
@@ -21,179 +22,15 @@
 #include <vector>
 
 #include "common.hpp"
+#include "route.hpp"
 
 namespace kh {
 namespace {
 
-constexpr int MAX_EXPERTS = 512;
-constexpr int MAX_TOPK = 16;
-constexpr int MAX_GROUPS = 64;
 
-// f32::total_cmp as an integer key (-0.0 < +0.0; a total order).
-__device__ __forceinline__ int total_key(float f) {
-    const int b = __builtin_bit_cast(int, f);
-    return b ^ (int)(((unsigned)(b >> 31)) >> 1);
-}
-
-// Router::route for one token per wave (ffn.rs:256-309).  The softmax's sum
-// and the normalisation run in one lane in index order, as the reference
-// sums them; the top-k picks the largest choice, the lowest index on ties.
+// Router::route for one token per wave (route.hpp).
 __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
-    const int tok = blockIdx.x, lane = threadIdx.x, n = r.n;
-    __shared__ __align__(16) float s_score[MAX_EXPERTS], s_choice[MAX_EXPERTS];  // padded to n16
-    __shared__ float s_inv;
-    __shared__ int s_order[MAX_GROUPS];
-    __shared__ float s_str[MAX_GROUPS];
-    __shared__ int s_pick_e[MAX_TOPK];
-    __shared__ float s_pick_w[MAX_TOPK];
-    __shared__ int s_best;
-    const float *lg = r.logits + (size_t)tok * n;
-    // Serial loops over the experts read 16 values at a time (four 16-byte
-    // LDS reads in flight) and then use them in index order: one LDS round
-    // trip per 16 experts rather than per expert.  Padding past n reads as
-    // 0 (adding 0.0f to a positive sum is exact) or -inf (never a choice).
-    const int n16 = (n + 15) & ~15;
-    auto batch = [&](const float *a, int i0, float (&v)[16]) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 f = reinterpret_cast<const float4 *>(a + i0)[q];
-            v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
-        }
-    };
-
-    if (r.scoring == 0) {  // softmax_inplace (tensor.rs:297-308)
-        float mx = -INFINITY;
-        for (int i = lane; i < n; i += 64) mx = fmaxf(mx, lg[i]);
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        for (int i = lane; i < n16; i += 64) s_score[i] = i < n ? expf(lg[i] - mx) : 0.0f;
-        __syncthreads();
-        if (lane == 0) {  // summed in index order, as the reference does
-            float sum = 0.0f;
-            for (int i0 = 0; i0 < n16; i0 += 16) {
-                float v[16];
-                batch(s_score, i0, v);
-#pragma unroll
-                for (int t = 0; t < 16; t++) sum += v[t];
-            }
-            s_inv = 1.0f / sum;
-        }
-        __syncthreads();
-        for (int i = lane; i < n; i += 64) s_score[i] *= s_inv;
-    } else {  // sigmoid (ffn.rs:262-266)
-        for (int i = lane; i < n; i += 64) s_score[i] = 1.0f / (1.0f + expf(-lg[i]));
-    }
-    __syncthreads();
-    for (int i = lane; i < n16; i += 64)
-        s_choice[i] = i >= n ? -INFINITY : r.bias ? s_score[i] + r.bias[i] : s_score[i];
-    __syncthreads();
-
-    // mask_to_best_groups (ffn.rs:312-349)
-    if (r.select != 0 && r.n_group > 1) {
-        const int per = n / r.n_group;
-        if (lane < r.n_group) {
-            const float *grp = s_choice + lane * per;
-            float st;
-            if (r.select == 1) {
-                st = -INFINITY;
-                for (int i = 0; i < per; i++) st = fmaxf(st, grp[i]);
-            } else {
-                float a = -INFINITY, b = -INFINITY;
-                for (int i = 0; i < per; i++) {
-                    const float v = grp[i];
-                    if (v > a) {
-                        b = a;
-                        a = v;
-                    } else if (v > b) {
-                        b = v;
-                    }
-                }
-                st = a + b;
-            }
-            s_str[lane] = st;
-        }
-        __syncthreads();
-        if (lane == 0) {  // stable sort, descending by total_cmp
-            for (int g = 0; g < r.n_group; g++) s_order[g] = g;
-            for (int i = 1; i < r.n_group; i++) {
-                const int x = s_order[i];
-                int j = i;
-                while (j > 0 && total_key(s_str[s_order[j - 1]]) < total_key(s_str[x])) {
-                    s_order[j] = s_order[j - 1];
-                    j--;
-                }
-                s_order[j] = x;
-            }
-        }
-        __syncthreads();
-        const int keep = r.topk_group < r.n_group ? r.topk_group : r.n_group;
-        for (int o = keep; o < r.n_group; o++)
-            for (int i = lane; i < per; i += 64) s_choice[s_order[o] * per + i] = -INFINITY;
-        __syncthreads();
-    }
-
-    // the picks (ffn.rs:279-293): the reference takes the largest choice,
-    // the lowest index on ties, until top_k are taken or none is left; that
-    // is the order of each valid expert's rank among the valid choices
-    const int k = r.top_k < n ? r.top_k : n;
-    if (lane == 0) s_best = 0;
-    __syncthreads();
-    for (int i = lane; i < n; i += 64) {
-        const float v = s_choice[i];
-        if (!(v > -INFINITY)) continue;
-        int rank = 0;
-        for (int j0 = 0; j0 < n16; j0 += 16) {
-            float u[16];
-            batch(s_choice, j0, u);
-#pragma unroll
-            for (int t = 0; t < 16; t++) rank += u[t] > -INFINITY && (u[t] > v || (u[t] == v && j0 + t < i));
-        }
-        if (rank < k) {
-            s_pick_e[rank] = i;
-            s_pick_w[rank] = s_score[i];
-            atomicAdd(&s_best, 1);
-        }
-    }
-    __syncthreads();
-    const int got = s_best;
-
-    if (lane == 0) {
-        const bool normalised = r.norm_topk && r.top_k > 1;
-        if (normalised) {  // ffn.rs:296-302
-            float total = 0.0f;
-            for (int i = 0; i < got; i++) total += s_pick_w[i];
-            total += 1e-20f;
-            for (int i = 0; i < got; i++) s_pick_w[i] /= total;
-        }
-        if (r.always_scale || !normalised)
-            for (int i = 0; i < got; i++) s_pick_w[i] *= r.scale;
-        int32_t *e = r.experts + (size_t)tok * r.top_k;
-        float *w = r.weights + (size_t)tok * r.top_k;
-        for (int i = 0; i < r.top_k; i++) {
-            e[i] = i < got ? s_pick_e[i] : -1;
-            w[i] = i < got ? s_pick_w[i] : 0.0f;
-        }
-        r.count[tok] = got;
-        if (r.sorted_experts) {
-            // the picks in expert order; unused slots name expert 0 with
-            // weight 0, so a kernel that reads every slot stays in bounds
-            int se[MAX_TOPK];
-            float sw[MAX_TOPK];
-            for (int i = 0; i < got; i++) {
-                int j = i;
-                while (j > 0 && se[j - 1] > s_pick_e[i]) {
-                    se[j] = se[j - 1];
-                    sw[j] = sw[j - 1];
-                    j--;
-                }
-                se[j] = s_pick_e[i];
-                sw[j] = s_pick_w[i];
-            }
-            for (int i = 0; i < r.top_k; i++) {
-                r.sorted_experts[(size_t)tok * r.top_k + i] = i < got ? se[i] : 0;
-                r.sorted_weights[(size_t)tok * r.top_k + i] = i < got ? sw[i] : 0.0f;
-            }
-        }
-    }
+    route_one(r, blockIdx.x, r.logits + (size_t)blockIdx.x * r.n);
 }
 
 // by_expert (ffn.rs:627-640): the picks' rows grouped by expert, experts in
@@ -449,18 +286,35 @@ int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
         w.push_back(moe->sup), xs.push_back(x), ys1.push_back(su);
     }
     int rc;
-    if (moe->router->precision == KH_F32) {  // matvec_many declines f32: run the router alone
-        if ((rc = matvec_device(ctx, moe->router, x, nullptr, logits, nullptr))) return rc;
-        if (sh && (rc = matvec_many_device(ctx, w.size() - 1, w.data() + 1, xs.data() + 1, ys1.data() + 1)))
-            return rc;
-    } else if ((rc = matvec_many_device(ctx, w.size(), w.data(), xs.data(), ys1.data()))) {
-        return rc;
-    }
-    // (2) the router
     RouteArgs r = route_args(moe, logits, pe, pw, cnt);
     r.sorted_experts = se;
     r.sorted_weights = sw;
-    if ((rc = launch_route(ctx, r, 1))) return rc;
+    // (1) + (2) in one launch where the GEMV has a routing build for it: the
+    // router's one workgroup routes its own logits while the shared expert's
+    // rows stream (q8, inputs the kernel stages itself)
+    bool routed = false;
+    if (moe->router->precision == KH_Q8 && !dequant_selected()) {
+        bool plain = true;
+        for (const kh_weight *v : w) plain = plain && v->precision == KH_Q8 && v->cols <= fuse_max_cols(KH_Q8);
+        if (plain) {
+            std::vector<GemvJob> j1;
+            for (size_t i = 0; i < w.size(); i++) j1.push_back(plain_job(w[i], xs[i], nullptr, ys1[i]));
+            rc = launch_gemv_route(ctx, KH_Q8, j1.data(), (int)j1.size(), 0, r);
+            if (rc != KH_OK && rc != KH_DECLINED) return rc;
+            routed = rc == KH_OK;
+        }
+    }
+    if (!routed) {
+        if (moe->router->precision == KH_F32) {  // matvec_many declines f32: run the router alone
+            if ((rc = matvec_device(ctx, moe->router, x, nullptr, logits, nullptr))) return rc;
+            if (sh && (rc = matvec_many_device(ctx, w.size() - 1, w.data() + 1, xs.data() + 1, ys1.data() + 1)))
+                return rc;
+        } else if ((rc = matvec_many_device(ctx, w.size(), w.data(), xs.data(), ys1.data()))) {
+            return rc;
+        }
+        // (2) the router
+        if ((rc = launch_route(ctx, r, 1))) return rc;
+    }
     // (3) every chosen expert's gate and up, through the device tables
     std::vector<GemvJob> jobs;
     for (size_t i = 0; i < k; i++) {
