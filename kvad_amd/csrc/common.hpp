@@ -120,6 +120,7 @@ struct kh_llm {
     int32_t *out = nullptr;                                  // generated tokens
     float *arg_v = nullptr;                                  // argmax partials
     int *arg_i = nullptr;
+    int *arg_n = nullptr;                                    // how many the head GEMV wrote
     int out_cap = 0;
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -214,6 +215,11 @@ struct RouteArgs;
 // its one workgroup computes the token's logits and routes them (r.logits
 // unused); KH_DECLINED where no such kernel is built for the launch's shape.
 int launch_gemv_route(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs, int route_job, const RouteArgs &r);
+// One GEMV whose workgroups also keep the greedy choice over their rows
+// r >= 1 (workgroup g: arg_v[g], arg_i[g]; their count to *arg_n);
+// KH_DECLINED for f32 weights or more than `cap` workgroups.
+int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *arg_v, int *arg_i, int *arg_n,
+                       int cap);
 
 // y[m, rows] = x W^T (+bias) for a few quantised token rows (m small): the
 // weights stream once for all of them.  x holds the rows' codes.

@@ -1,5 +1,6 @@
-// Device helpers shared by the GEMV kernels (gemv.hip, dequant.hip): buffer
-// loads, DPP lane moves, the wave sum and the Q4_K header decode.
+// Device helpers shared by the GEMV kernels (gemv.hip, dequant.hip) and the
+// session (session.hip): buffer loads, DPP lane moves, the wave sum, the
+// Q4_K header decode and the dequantised weight element.
 #pragma once
 
 #include "common.hpp"
@@ -95,6 +96,42 @@ __device__ __forceinline__ void q4k_scale_min(const int4 &h, int sh, unsigned hi
     const unsigned X = A ^ ((A ^ Cw) & hij), Y = B ^ ((B ^ (Cw >> 4)) & hij);
     sc = (X & 0xfu) | ((A >> s2) & 0x30u);
     mn = (Y & 0xfu) | ((B >> s2) & 0x30u);
+}
+
+// Element k of row r of a weight, dequantised: Weight::row (quant.rs:374-402)
+// for q8 ((f32)q * s) and q4 ((f32)(nibble - 8) * s), the Q4_K decoder
+// (mpp.rs:304-315: (f32(d) * sc) * q - f32(dmin) * m), or the f32 value.
+__device__ __forceinline__ float dequant_elem(int prec, const void *qs, const float *scales, size_t cols, size_t r,
+                                              size_t k) {
+    const size_t nb = cols / BLOCK;
+    if (prec == KH_Q8) {
+        const int8_t *q = static_cast<const int8_t *>(qs) + r * cols;
+        return (float)q[k] * scales[r * nb + k / BLOCK];
+    } else if (prec == KH_Q4) {
+        const uint8_t *q = static_cast<const uint8_t *>(qs) + r * cols / 2;
+        const size_t b = k / BLOCK, o = k % BLOCK;
+        const uint8_t byte = q[b * 16 + (o & 15)];
+        const int code = o < 16 ? (byte & 0x0f) : (byte >> 4);
+        return (float)(code - 8) * scales[r * nb + b];
+    } else if (prec == KH_Q4K) {
+        const uint8_t *blk = static_cast<const uint8_t *>(qs) + (r * (cols / QK_K) + k / QK_K) * Q4K_BYTES;
+        const int p = (int)(k % QK_K), j = p / 32, c = p / 64, h = (p / 32) & 1, l = p % 32;
+        const uint8_t *s = blk + 4;
+        int sc, mn;
+        if (j < 4) {
+            sc = s[j] & 63;
+            mn = s[j + 4] & 63;
+        } else {
+            sc = (s[j + 4] & 0xf) | ((s[j - 4] >> 6) << 4);
+            mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const float dl = half_bits_to_float(blk[0] | (blk[1] << 8)) * (float)sc;
+        const float ml = half_bits_to_float(blk[2] | (blk[3] << 8)) * (float)mn;
+        const int q = (blk[16 + 32 * c + l] >> (4 * h)) & 0xf;
+        const float t = dl * (float)q;
+        return t - ml;
+    }
+    return static_cast<const float *>(qs)[r * cols + k];
 }
 
 }  // namespace dev

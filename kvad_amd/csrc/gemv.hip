@@ -151,6 +151,9 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
         if (blk >= tab.j[i].wave0) ji = i;
     const GemvJob &job = tab.j[ji];
     const bool routes = ROUTE && ji == tab.route_job - 1;  // uniform per workgroup
+    const bool argm = ji == tab.arg_job - 1;              // uniform per workgroup
+    float arg_bv = -INFINITY;                             // the wave's greedy choice (lane 0)
+    int arg_bi = -1;
     const int rows = job.rows, cols = job.cols, nb = cols / BLOCK;
     const int C = chunks_per_row(PREC, cols);
     const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
@@ -240,6 +243,8 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
                     if (job.accumulate) out = y0 + out;  // x += proj (llama.rs:273-276)
                     job.y[r] = out;
                     if (routes) s_lg[r] = out;
+                    // rows in increasing order: a later equal value never wins
+                    if (argm && r >= 1 && out == out && (arg_bi < 0 || out > arg_bv)) arg_bv = out, arg_bi = r;
                 }
                 acc[i] = 0.0f;
             }
@@ -254,6 +259,25 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
         run_step(ca, step);
         load_step(ca, step + 2);
         if (step + 1 < steps) run_step(cb, step + 1);
+    }
+    if (argm) {  // the workgroup's choice: its waves' in wave order, the lowest index on ties
+        __shared__ float s_av[NWV];
+        __shared__ int s_ai[NWV];
+        if (lane == 0) s_av[wv] = arg_bv, s_ai[wv] = arg_bi;
+        __syncthreads();
+        if (tid == 0) {
+            float bv = s_av[0];
+            int bi = s_ai[0];
+            for (int w = 1; w < NWV; w++) {
+                const float v = s_av[w];
+                const int i = s_ai[w];
+                if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) bv = v, bi = i;
+            }
+            const int g = blk - job.wave0;
+            tab.arg_v[g] = bv;
+            tab.arg_i[g] = bi;
+            if (g == 0) *tab.arg_n = nw / NWV;
+        }
     }
     if constexpr (ROUTE) {
         if (routes) {
@@ -614,6 +638,8 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
         blocks += nwg;
     }
     if (blocks == 0) return KH_OK;
+    if (tab.arg_job && tab.j[tab.arg_job - 1].nwaves / p.nwv > tab.arg_cap)
+        return fail(KH_DECLINED, "matvec: more workgroups than greedy partials");
     const int pb = padded_blocks(PREC, maxC, p.cpl);
     const size_t lds = (size_t)pb * 32 + 8 * (size_t)pb;
     if (lds > 64 * 1024) return fail(KH_DECLINED, "matvec: activation too wide for the LDS stage");
@@ -707,36 +733,7 @@ __global__ void dequant_row_kernel(int prec, const void *qs, const float *scales
     const size_t r = r_dev ? (size_t)*r_dev : r_host;
     size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= cols) return;
-    const size_t nb = cols / BLOCK;
-    if (prec == KH_Q8) {
-        const int8_t *q = static_cast<const int8_t *>(qs) + r * cols;
-        out[k] = (float)q[k] * scales[r * nb + k / BLOCK];
-    } else if (prec == KH_Q4) {
-        const uint8_t *q = static_cast<const uint8_t *>(qs) + r * cols / 2;
-        size_t b = k / BLOCK, o = k % BLOCK;
-        uint8_t byte = q[b * 16 + (o & 15)];
-        int code = o < 16 ? (byte & 0x0f) : (byte >> 4);
-        out[k] = (float)(code - 8) * scales[r * nb + b];
-    } else if (prec == KH_Q4K) {
-        const uint8_t *blk = static_cast<const uint8_t *>(qs) + (r * (cols / QK_K) + k / QK_K) * Q4K_BYTES;
-        int p = (int)(k % QK_K), j = p / 32, c = p / 64, h = (p / 32) & 1, l = p % 32;
-        const uint8_t *s = blk + 4;
-        int sc, mn;
-        if (j < 4) {
-            sc = s[j] & 63;
-            mn = s[j + 4] & 63;
-        } else {
-            sc = (s[j + 4] & 0xf) | ((s[j - 4] >> 6) << 4);
-            mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-        }
-        float dl = half_bits_to_float(blk[0] | (blk[1] << 8)) * (float)sc;
-        float ml = half_bits_to_float(blk[2] | (blk[3] << 8)) * (float)mn;
-        int q = (blk[16 + 32 * c + l] >> (4 * h)) & 0xf;
-        float t = dl * (float)q;
-        out[k] = t - ml;
-    } else {
-        out[k] = static_cast<const float *>(qs)[r * cols + k];
-    }
+    out[k] = dequant_elem(prec, qs, scales, cols, r, k);
 }
 
 }  // namespace
@@ -895,6 +892,26 @@ int launch_gemv_route(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs
         rows_total += jobs[i].rows;
     }
     return launch_prec<KH_Q8>(ctx, tab, maxC, maxCols, rows_total, false, IN_F32);
+}
+
+int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *arg_v, int *arg_i, int *arg_n,
+                       int cap) {
+    if (precision == KH_F32 || job.dots) return fail(KH_DECLINED, "matvec: the greedy epilogue is built for quantised weights");
+    JobTable tab{};
+    tab.n = 1;
+    tab.j[0] = job;
+    tab.arg_job = 1;
+    tab.arg_cap = cap;
+    tab.arg_v = arg_v;
+    tab.arg_i = arg_i;
+    tab.arg_n = arg_n;
+    const int maxC = chunks_per_row(precision, job.cols), kind = input_kind(job);
+    switch (precision) {
+        case KH_Q8: return launch_prec<KH_Q8>(ctx, tab, maxC, job.cols, job.rows, false, kind);
+        case KH_Q4: return launch_prec<KH_Q4>(ctx, tab, maxC, job.cols, job.rows, false, kind);
+        case KH_Q4K: return launch_prec<KH_Q4K>(ctx, tab, maxC, job.cols, job.rows, false, kind);
+        default: return fail(KH_EINVAL, "unknown precision");
+    }
 }
 
 int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,

@@ -23,6 +23,13 @@ struct JobTable {
     // token's router logits, also routes them (route.hpp); 0: none
     int route_job;
     RouteArgs route;
+    // 1 + the job whose workgroups also keep the greedy choice over their
+    // rows r >= 1 (the largest, the lowest index on ties, NaN never):
+    // workgroup g writes arg_v[g], arg_i[g] and workgroup 0 the count to
+    // *arg_n; 0: none
+    int arg_job, arg_cap;
+    float *arg_v;
+    int *arg_i, *arg_n;
 };
 
 // Chunks of 16 bytes per weight row.

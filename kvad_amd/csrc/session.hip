@@ -18,6 +18,7 @@
 #include <memory>
 
 #include "common.hpp"
+#include "device.hpp"
 
 namespace kh {
 namespace {
@@ -28,6 +29,7 @@ namespace {
 // one workgroup reduces the runs, compares with entry 0, and makes the next
 // token the input, advances the position and records the step's token.
 constexpr int ARGMAX_BLOCKS = 256;
+constexpr int ARGMAX_CAP = 16384;  // greedy partials the head GEMV's workgroups may write
 
 __device__ __forceinline__ void better(float &bv, int &bi, float ov, int oi) {
     if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) bv = ov, bi = oi;
@@ -87,22 +89,55 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float *v, int n,
     if (threadIdx.x == 0) next[row] = pick(v + (size_t)row * n, n, bv, bi);
 }
 
+// The embedding the next step starts from: the chosen token's row of the
+// embedding weight (Weight::row, llama.rs:384-391).
+struct NextEmbed {
+    int prec;
+    const void *qs;
+    const float *scales;
+    size_t cols;
+    float *x;
+};
+
+// The partials' count is *pn (the head GEMV's workgroups) or, without pn,
+// ARGMAX_BLOCKS (argmax_partial_kernel).  The chosen token becomes the next
+// input, the position advances, the step is recorded, and the token's
+// embedding row is written to e.x, so a captured step needs no launch of its
+// own for it.
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float *v, int n, const float *pv, const int *pi,
-                                                          int32_t *token, int32_t *pos, int32_t *step, int32_t *out,
-                                                          int out_cap) {
+                                                          const int *pn, int32_t *token, int32_t *pos, int32_t *step,
+                                                          int32_t *out, int out_cap, NextEmbed e) {
     __shared__ float s_v[256];
     __shared__ int s_i[256];
-    float bv = pv[threadIdx.x];
-    int bi = pi[threadIdx.x];
+    __shared__ int s_best;
+    const int np = pn ? min(*pn, ARGMAX_CAP) : ARGMAX_BLOCKS;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int t0 = 0; t0 < np; t0 += 8 * 256) {  // eight loads in flight per thread
+        float v8[8];
+        int i8[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int t = t0 + u * 256 + (int)threadIdx.x;
+            v8[u] = t < np ? pv[t] : -INFINITY;
+            i8[u] = t < np ? pi[t] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) better(bv, bi, v8[u], i8[u]);
+    }
     block_best(bv, bi, s_v, s_i);
     if (threadIdx.x == 0) {
         const int best = pick(v, n, bv, bi);
+        s_best = best;
         *token = best;
         *pos = *pos + 1;
         const int k = *step;
         if (out && k < out_cap) out[k] = best;
         *step = k + 1;
     }
+    __syncthreads();
+    const size_t r = (size_t)s_best;
+    for (size_t k = threadIdx.x; k < e.cols; k += 256) e.x[k] = dev::dequant_elem(e.prec, e.qs, e.scales, e.cols, r, k);
 }
 
 template <typename T>
@@ -186,14 +221,16 @@ int trace_copy(kh_ctx *ctx, float *dst, const float *src, size_t n) {
     return KH_OK;
 }
 
-// One token's launches, all on the context's stream.  With a trace (the
-// parity hook kh_debug_llm_trace; never under capture) each sub-block's
-// results are copied out as it ends.
-int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr) {
+// One token's launches, all on the context's stream.  With `embed` the
+// step starts from the token's embedding row (llama.rs:384-391); without,
+// from the row the previous step's argmax wrote into x (captured steps).
+// With a trace (the parity hook kh_debug_llm_trace; never under capture)
+// each sub-block's results are copied out as it ends.
+int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr, bool embed = true) {
     const kh_llm_spec &s = m->spec;
     const size_t qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
     int rc;
-    if ((rc = launch_dequant_row_dev(ctx, m->embed, m->token, m->x))) return rc;  // embed (llama.rs:384-391)
+    if (embed && (rc = launch_dequant_row_dev(ctx, m->embed, m->token, m->x))) return rc;
     if (tr && (rc = trace_copy(ctx, tr->x_embed, m->x, s.n_embd))) return rc;
     for (size_t l = 0; l < s.n_layer; l++) {
         const kh_llm::Layer &L = m->layers[l];
@@ -260,12 +297,25 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr) {
     if (!fh && (rc = launch_rms_norm(ctx, m->x, m->final_norm, 1, s.n_embd, s.eps, m->h))) return rc;
     std::vector<std::pair<const kh_weight *, GemvJob>> jobs{
         {head, normed(gemv_job(head, fh ? m->x : m->h, nullptr, nullptr, m->logits, 0), fh, m->final_norm, s.eps)}};
-    if ((!fh && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) || (rc = run_jobs(ctx, jobs))) return rc;
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(ARGMAX_BLOCKS), dim3(256), 0, ctx->stream, m->logits,
-                       (int)s.vocab, m->arg_v, m->arg_i);
-    KH_HIP(hipGetLastError());
+    if (!fh && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) return rc;
+    // the greedy choice (sampler.rs:217-226): each workgroup of the head GEMV
+    // keeps its best row, one workgroup then takes the best of them; f32
+    // heads, or launches of more workgroups than partials, run a partial pass
+    bool kept = false;
+    if (head->precision != KH_F32) {
+        rc = launch_gemv_argmax(ctx, head->precision, jobs[0].second, m->arg_v, m->arg_i, m->arg_n, ARGMAX_CAP);
+        if (rc != KH_OK && rc != KH_DECLINED) return rc;
+        kept = rc == KH_OK;
+    }
+    if (!kept) {
+        if ((rc = run_jobs(ctx, jobs))) return rc;
+        hipLaunchKernelGGL(argmax_partial_kernel, dim3(ARGMAX_BLOCKS), dim3(256), 0, ctx->stream, m->logits,
+                           (int)s.vocab, m->arg_v, m->arg_i);
+        KH_HIP(hipGetLastError());
+    }
+    const NextEmbed ne{m->embed->precision, m->embed->qs, m->embed->scales, m->embed->cols, m->x};
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, ctx->stream, m->logits, (int)s.vocab, m->arg_v,
-                       m->arg_i, m->token, m->pos, m->steps, m->out, m->out_cap);
+                       m->arg_i, kept ? m->arg_n : nullptr, m->token, m->pos, m->steps, m->out, m->out_cap, ne);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -528,7 +578,7 @@ int capture_step(kh_ctx *ctx, kh_llm *m, size_t bm) {
     m->attn_max = bm;
     hipGraph_t g = nullptr;
     KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    const int rc = step(ctx, m);
+    const int rc = step(ctx, m, nullptr, false);  // x: the previous step's argmax wrote it
     hipError_t e = hipStreamEndCapture(ctx->stream, &g);
     if (rc) {
         if (g) (void)hipGraphDestroy(g);
@@ -543,11 +593,14 @@ int capture_step(kh_ctx *ctx, kh_llm *m, size_t bm) {
     return KH_OK;
 }
 
-// n steps from m->len: capture the buckets they cross first, then replay.
+// n steps from m->len: capture the buckets they cross first, then replay;
+// the first step's input is the embedding row of the token held on the
+// device (the captured steps take the row their argmax wrote).
 int replay_steps(kh_ctx *ctx, kh_llm *m, size_t n) {
     int rc;
     for (size_t i = 0; i < n; i++)
         if ((rc = capture_step(ctx, m, bucket_max(m, m->len + i + 1)))) return rc;
+    if ((rc = launch_dequant_row_dev(ctx, m->embed, m->token, m->x))) return rc;
     for (size_t i = 0; i < n; i++)
         KH_HIP(hipGraphLaunch(m->graphs.at(bucket_max(m, m->len + i + 1)), ctx->stream));
     return KH_OK;
@@ -590,7 +643,8 @@ int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out) {
         (rc = dev_alloc(&m->u, s.n_ff)) || (rc = dev_alloc(&m->logits, s.vocab)) ||
         (rc = dev_alloc(&m->hq.qs, hq_n)) || (rc = dev_alloc(&m->hq.scales, hq_n / BLOCK)) ||
         (rc = dev_alloc(&m->hq.sums, hq_n / BLOCK)) || (rc = dev_alloc(&m->state, 3)) ||
-        (rc = dev_alloc(&m->arg_v, ARGMAX_BLOCKS)) || (rc = dev_alloc(&m->arg_i, ARGMAX_BLOCKS)))
+        (rc = dev_alloc(&m->arg_v, ARGMAX_CAP)) || (rc = dev_alloc(&m->arg_i, ARGMAX_CAP)) ||
+        (rc = dev_alloc(&m->arg_n, 1)))
         return rc;
     m->token = m->state, m->pos = m->state + 1, m->steps = m->state + 2;
     KH_HIP(hipMemset(m->state, 0, 3 * sizeof(int32_t)));
@@ -624,7 +678,7 @@ int kh_llm_free(kh_llm *m) {
         for (void *p : {(void *)m->x, (void *)m->h, (void *)m->qkv, (void *)m->att, (void *)m->g, (void *)m->u,
                         (void *)m->logits, (void *)m->hq.qs, (void *)m->hq.scales, (void *)m->hq.sums,
                         (void *)m->state, (void *)m->final_norm, (void *)m->rope_cos, (void *)m->rope_sin,
-                        m->attn_ws, (void *)m->out, (void *)m->arg_v, (void *)m->arg_i})
+                        m->attn_ws, (void *)m->out, (void *)m->arg_v, (void *)m->arg_i, (void *)m->arg_n})
             if (p) (void)hipFree(p);
     }
     delete m;
