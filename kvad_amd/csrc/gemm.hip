@@ -259,59 +259,58 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
     int4 ra[A_PT], rb[B_PT], rh;
     float rws[WS_PT], rxs[XS_PT], rxsum[XS_PT];
 
+    // Every load is issued, the ones past a tail with an offset past the
+    // buffer's end, which reads zeros: no branch around any load.
+    constexpr unsigned OOB = 0xffffffffu;
     auto load_stage = [&](int k0) {
 #pragma unroll
         for (int u = 0; u < A_PT; u++) {
             const int c = tid + u * THREADS;
-            int4 v = {0, 0, 0, 0};
-            if (c < A_CH) {
-                if constexpr (PREC == KH_Q8) {
-                    const int row = c >> 3, kc = c & 7;
-                    if (k0 + 16 * kc < K) v = ld16(W, (unsigned)(n0 + row) * (unsigned)K + (unsigned)(k0 + 16 * kc));
-                } else if constexpr (PREC == KH_Q4) {
-                    const int row = c / NBS, blk = c % NBS;
-                    if (k0 / BLOCK + blk < nb)
-                        v = ld16(W, (unsigned)(n0 + row) * (unsigned)(K / 2) + (unsigned)((k0 / BLOCK + blk) * 16));
-                } else {
-                    const int row = c / NBS, q = c % NBS;
-                    const unsigned sb = (unsigned)(k0 / QK_K), h = (unsigned)((k0 % QK_K) / BK);
-                    v = ld16(W, (unsigned)(n0 + row) * (unsigned)(K / QK_K) * Q4K_BYTES + sb * Q4K_BYTES + 16 + 64 * h +
-                                    16 * q);
-                }
+            unsigned off;
+            if constexpr (PREC == KH_Q8) {
+                const int row = c >> 3, kc = c & 7;
+                off = c < A_CH && k0 + 16 * kc < K ? (unsigned)(n0 + row) * (unsigned)K + (unsigned)(k0 + 16 * kc) : OOB;
+            } else if constexpr (PREC == KH_Q4) {
+                const int row = c / NBS, blk = c % NBS;
+                off = c < A_CH && k0 / BLOCK + blk < nb
+                          ? (unsigned)(n0 + row) * (unsigned)(K / 2) + (unsigned)((k0 / BLOCK + blk) * 16)
+                          : OOB;
+            } else {
+                const int row = c / NBS, q = c % NBS;
+                const unsigned sb = (unsigned)(k0 / QK_K), h = (unsigned)((k0 % QK_K) / BK);
+                off = c < A_CH ? (unsigned)(n0 + row) * (unsigned)(K / QK_K) * Q4K_BYTES + sb * Q4K_BYTES + 16 +
+                                     64 * h + 16 * q
+                               : OOB;
             }
-            ra[u] = v;
+            ra[u] = ld16(W, off);
         }
-        if constexpr (PREC == KH_Q4K) {
-            rh = int4{0, 0, 0, 0};
-            if (tid < BN)
-                rh = ld16(W, (unsigned)(n0 + tid) * (unsigned)(K / QK_K) * Q4K_BYTES +
-                                 (unsigned)(k0 / QK_K) * Q4K_BYTES);
-        }
+        if constexpr (PREC == KH_Q4K)
+            rh = ld16(W, tid < BN ? (unsigned)(n0 + tid) * (unsigned)(K / QK_K) * Q4K_BYTES +
+                                        (unsigned)(k0 / QK_K) * Q4K_BYTES
+                                  : OOB);
 #pragma unroll
         for (int u = 0; u < B_PT; u++) {
             const int kc = (tid + u * THREADS) & 7;
-            int4 v = {0, 0, 0, 0};
-            if (brow[u] >= 0 && k0 + 16 * kc < K)
-                v = ld16(X, (unsigned)brow[u] * (unsigned)K + (unsigned)(k0 + 16 * kc));
-            rb[u] = v;
+            rb[u] = ld16(X, brow[u] >= 0 && k0 + 16 * kc < K ? (unsigned)brow[u] * (unsigned)K + (unsigned)(k0 + 16 * kc)
+                                                            : OOB);
         }
         if constexpr (PREC != KH_Q4K) {
 #pragma unroll
             for (int u = 0; u < WS_PT; u++) {
                 const int c = tid + u * THREADS;
                 const int row = c / NBS, blk = c % NBS;
-                rws[u] = c < BN * NBS && k0 / BLOCK + blk < nb
-                             ? ldf(WS, ((unsigned)(n0 + row) * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u)
-                             : 0.0f;
+                rws[u] = ldf(WS, c < BN * NBS && k0 / BLOCK + blk < nb
+                                     ? ((unsigned)(n0 + row) * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u
+                                     : OOB);
             }
         }
 #pragma unroll
         for (int u = 0; u < XS_PT; u++) {
             const int blk = (tid + u * THREADS) % NBS;
             const bool ok = srow[u] >= 0 && k0 / BLOCK + blk < nb;
-            const unsigned off = ((unsigned)srow[u] * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u;
-            rxs[u] = ok ? ldf(XS, off) : 0.0f;
-            if constexpr (PREC == KH_Q4K) rxsum[u] = ok ? (float)ldi(XSUM, off) : 0.0f;
+            const unsigned off = ok ? ((unsigned)srow[u] * (unsigned)nb + (unsigned)(k0 / BLOCK + blk)) * 4u : OOB;
+            rxs[u] = ldf(XS, off);
+            if constexpr (PREC == KH_Q4K) rxsum[u] = (float)ldi(XSUM, off);
         }
     };
 
@@ -445,9 +444,15 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             // Q4_K: d*sc * xs) as an outer product on the matrix core: k-slot 0
             // holds the 32 rows' (tokens') scales, k-slot 1 zeros
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) wa[f][rt] = lo ? sW[b][wr0 + rt * 32 + lane] : 0.0f;
+            for (int rt = 0; rt < RT; rt++) {
+                const float x = sW[b][wr0 + rt * 32 + (lane & 31)];  // read by every lane, kept by the low half
+                wa[f][rt] = lo ? x : 0.0f;
+            }
 #pragma unroll
-            for (int tt = 0; tt < TT; tt++) xb[f][tt] = lo ? sX[b][wm0 + tt * 32 + lane] : 0.0f;
+            for (int tt = 0; tt < TT; tt++) {
+                const float x = sX[b][wm0 + tt * 32 + (lane & 31)];
+                xb[f][tt] = lo ? x : 0.0f;
+            }
         };
         frags(0, 0);
 #pragma unroll
