@@ -253,8 +253,10 @@ def main() -> int:
     log(f"dequant q4k step: {dequant_step}")
 
     # ---- batched decode (forward_each, llama.rs:418-434): m tokens through
-    # the same 32 layers, one matmul_bt per projection (each quantises its m
-    # rows, then one multi-token GEMV streams the weights once) -------------
+    # the same 32 layers, one matmul_bt per projection: one multi-token GEMV
+    # launch streams the weights once, quantising the m rows in every
+    # workgroup while 2/4/8 token slots x cols <= 12288, else after a
+    # quantising launch of its own -------------------------------------------
     batched = {}
     xs_m = torch.randn(8 * 14336, device=dev, generator=gen)
     ys_m = torch.empty(8 * 14336, device=dev)
@@ -268,7 +270,9 @@ def main() -> int:
         s = g.time(max(3, args.steps // 2), args.warmup)
         bb = args.layers * sum(144 * r * c // 256 + 4 * m * (r + c) for r, c in LLAMA_LAYER.values())
         batched[str(m)] = {"ms_per_step": round(s * 1e3, 4), "GBps": round(bb / s / 1e9, 1),
-                           "token_rows_per_s": round(m / s, 1), "launches_per_step": 2 * 7 * args.layers}
+                           "token_rows_per_s": round(m / s, 1),
+                           "launches_per_step": args.layers * sum(1 if (2 if m <= 2 else 4 if m <= 4 else 8) * c <= 12288
+                                                                  else 2 for _, c in LLAMA_LAYER.values())}
         del g
     log(f"batched decode q4k: {batched}")
 

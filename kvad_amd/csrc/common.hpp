@@ -231,6 +231,10 @@ int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, 
 // With xf set, the rows are f32 ([m][cols]) and every workgroup quantises
 // them as it stages them (the same codes as launch_qact); x is then unused.
 constexpr int MULTI_JOBS = 3;
+// Whether the multi-token GEMV should stage m f32 rows of `cols` itself
+// (quantising them in every workgroup) rather than read codes quantised once
+// by a launch of their own: only while the stage is small.
+bool multi_stages_f32(int precision, size_t m, size_t cols);
 int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,
                            float *const *y, const int *accumulate, const QAct &x, size_t m,
                            const float *xf = nullptr);

@@ -695,13 +695,7 @@ int matmul_rows(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, cons
 
 namespace {
 // KVAD_MATMUL_GEMM=1 sends every m > 1 to the MFMA GEMM (for comparisons).
-bool matmul_force_gemm() {
-    static const bool v = [] {
-        const char *e = getenv("KVAD_MATMUL_GEMM");
-        return e && *e == '1';
-    }();
-    return v;
-}
+bool matmul_force_gemm() { return env_int("KVAD_MATMUL_GEMM", 0) == 1; }
 }  // namespace
 
 namespace {
@@ -778,8 +772,9 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
         return launch_f32gemm(ctx, a);
     }
     // up to eight rows: the multi-token GEMV quantises them as it stages them
-    // (QActBatch::new's codes, one launch fewer)
-    if (m <= (size_t)MULTI_TOKENS && !matmul_force_gemm())
+    // (QActBatch::new's codes, one launch fewer) while they are few values
+    const bool multi = m <= (size_t)MULTI_TOKENS && !matmul_force_gemm();
+    if (multi && multi_stages_f32(w->precision, m, cols))
         return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, QAct{}, m, xs);
     // QActBatch::new (quant.rs:693-714): the activation rows quantised per block
     const size_t qb = (m * cols + 255) / 256 * 256, sb = (4 * m * cols / BLOCK + 255) / 256 * 256;

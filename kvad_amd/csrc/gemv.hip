@@ -950,6 +950,17 @@ int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, 
     return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, nullptr, x, m);
 }
 
+bool multi_stages_f32(int precision, size_t m, size_t cols) {
+    // Every workgroup quantises its token slots' rows (2, 4 or 8 slots); past
+    // about 12K values that costs more than a quantising launch of its own
+    // plus a stage of codes (measured over q8 and Q4_K weights of 896 to
+    // 14336 columns at m = 2..8).
+    const size_t slots = m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    const int lim = env_int("KVAD_MULTI_STAGE_F32", 12288);  // tuning knob
+    (void)precision;
+    return slots * cols <= (size_t)lim;
+}
+
 size_t fuse_max_cols(int precision) {
     static const size_t forced = [] {
         const char *e = getenv("KVAD_FUSE_MAX_COLS");

@@ -475,11 +475,13 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len
         if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
                                      kvd, max_len, b.att, b.ws, b.ws_bytes, &rp)))
             return rc;
-        if (L.o->precision != KH_F32 && n <= (size_t)MULTI_TOKENS && n <= rows_multi_max()) {
+        if (L.o->precision != KH_F32 && n <= (size_t)MULTI_TOKENS && n <= rows_multi_max() &&
+            multi_stages_f32(L.o->precision, n, qd)) {
             // x += o(attn): the multi-token GEMV quantises the attention rows
-            // itself, in its one launch (past eight rows it takes several, each
-            // quantising its rows in every workgroup: measured slower than one
-            // quantisation launch at 32 rows)
+            // itself, in its one launch, while they are narrow (past eight
+            // rows it takes several, each quantising its rows in every
+            // workgroup: measured slower than one quantisation launch at 32
+            // rows)
             const float *no_bias = nullptr;
             const int acc = 1;
             if ((rc = launch_gemv_multi_jobs(ctx, 1, &L.o, &no_bias, &b.x, &acc, b.qa, n, b.att))) return rc;
