@@ -59,6 +59,9 @@ const char *kh_version(void);
 /* A device and a stream: the per-session state CpuSession keeps as its rayon
  * pool (model/mod.rs:979-1072). */
 int kh_init(int device, kh_ctx **out);
+/* Frees the context.  Every weight, cache, MoE layer, session and parked
+ * conversation made on it must be freed first: their frees lock the
+ * context. */
 int kh_free(kh_ctx *ctx);
 /* Launch on `hip_stream` (a hipStream_t) instead of the context's own; NULL
  * restores the own stream.  The caller keeps ownership of the stream. */

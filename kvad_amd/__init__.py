@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -191,9 +192,21 @@ class Context:
         h = C.c_void_p()
         _check(lib.kh_init(device, C.byref(h)))
         self.h = h
+        self._objects = weakref.WeakSet()  # live handles made on this context
+
+    def _own(self, obj) -> None:
+        self._objects.add(obj)
 
     def close(self) -> None:
+        """kh_free, after every live object made on this context: their frees
+        lock the context, so none may outlive it (parked conversations before
+        their session, sessions and MoE layers before the weights they name)."""
         if self.h:
+            live = list(self._objects)
+            for kind in (Parked, Llm, Moe, KvCache, Weight):
+                for obj in live:
+                    if isinstance(obj, kind):
+                        obj.free()
             lib.kh_free(self.h)
             self.h = None
 
@@ -219,6 +232,7 @@ class Weight:
     def __init__(self, ctx: Context, handle: C.c_void_p, keep=None):
         self.ctx = ctx
         self.h = handle
+        ctx._own(self)
         rows, cols, prec, nbytes = _sz(), _sz(), C.c_int(), _sz()
         _check(lib.kh_weight_info(handle, C.byref(rows), C.byref(cols), C.byref(prec), C.byref(nbytes)))
         self.rows, self.cols, self.precision, self.bytes = rows.value, cols.value, prec.value, nbytes.value
@@ -451,6 +465,7 @@ class KvCache:
         h = C.c_void_p()
         _check(lib.kh_kv_new(ctx.h, n_layer, k_dim, v_dim, capacity, C.byref(h)))
         self.ctx, self.h = ctx, h
+        ctx._own(self)
         self.n_layer, self.k_dim, self.v_dim = n_layer, k_dim, v_dim
 
     def free(self) -> None:
@@ -554,6 +569,7 @@ class Moe:
         self.h = C.c_void_p()
         _check(lib.kh_moe_new(ctx.h, n_experts, top_k, hidden, inter, scoring, select, n_group, topk_group,
                               int(norm_topk), scale, _ptr(b), C.byref(self.h)))
+        ctx._own(self)
         self._keep = {}
 
     def set_router(self, w: Weight) -> None:
@@ -658,6 +674,7 @@ class Llm:
         self.spec = LlmSpec(**spec)
         self.h = C.c_void_p()
         _check(lib.kh_llm_new(ctx.h, C.byref(self.spec), C.byref(self.h)))
+        ctx._own(self)
         self._keep = {}
 
     def set_layer(self, l: int, q, k, v, o, gate, up, down, attn_norm, mlp_norm, q_b=None, k_b=None, v_b=None,
@@ -721,7 +738,7 @@ class Llm:
         far, set aside; the session is left with an empty one."""
         h = C.c_void_p()
         _check(lib.kh_llm_park(self.h, C.byref(h)))
-        return Parked(h)
+        return Parked(h, self.ctx)
 
     def resume(self, parked: "Parked") -> None:
         """Session::resume (model/mod.rs:895-897): `parked` back in place of
@@ -760,8 +777,10 @@ class Parked:
     """A conversation set aside by Llm.park (the Session trait's Parked,
     model/mod.rs:837): its device cache and length."""
 
-    def __init__(self, h):
+    def __init__(self, h, ctx: Context | None = None):
         self.h = h
+        if ctx is not None:
+            ctx._own(self)
 
     def __len__(self) -> int:
         n = _sz()

@@ -223,7 +223,9 @@ int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *ar
 
 // y[m, rows] = x W^T (+bias) for a few quantised token rows (m small): the
 // weights stream once for all of them.  x holds the rows' codes.
-constexpr int MULTI_TOKENS = 8;  // launch_matmul takes this path up to here
+constexpr int MULTI_TOKENS = 8;  // token slots of one VALU multi-token launch
+// Whether kh_matmul takes the multi-token GEMV (else the GEMM) for m rows.
+bool matmul_takes_multi(size_t m, size_t cols);
 int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, const float *bias, float *y);
 // The same for up to MULTI_JOBS weights of one precision and width over the
 // same rows of codes, in one launch: y[i] (+)= x W_i^T (+ bias[i]), adding
@@ -235,6 +237,13 @@ constexpr int MULTI_JOBS = 3;
 // (quantising them in every workgroup) rather than read codes quantised once
 // by a launch of their own: only while the stage is small.
 bool multi_stages_f32(int precision, size_t m, size_t cols);
+// Token rows from which the multi-token GEMV runs on the matrix cores
+// (launch_gemv_mma) when it is given codes.
+size_t mma_min_tokens();
+// The multi-token GEMV on the matrix cores (gemv_mma.hip): the same
+// contract as launch_gemv_multi_jobs over codes, 16 token rows a launch.
+int launch_gemv_mma(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias, float *const *y,
+                    const int *accumulate, const QAct &x, size_t m);
 int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,
                            float *const *y, const int *accumulate, const QAct &x, size_t m,
                            const float *xf = nullptr);
@@ -273,13 +282,14 @@ struct GemmArgs {
     int ksplit;
     float *part;
 };
-int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m);
+// tile_n: weight rows per tile (128, or 64 with 64-token tiles, ungrouped)
+int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m, int tile_n = 128);
 // Allocates the split-K workspace now (a GEMM captured into a graph splits
 // only when it was allocated before the capture).
 int gemm_split_reserve(kh_ctx *ctx);
 // Sets a's split-K fields for an ungrouped launch of tile_m-token tiles when
 // splitting its k-stages pays (ksplit 0: no split).
-int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m);
+int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m, int tile_n = 128);
 // Tokens per tile for an ungrouped M x N launch of the int8 GEMM.
 int gemm_tile_m(kh_ctx *ctx, int M, int N);
 

@@ -594,12 +594,20 @@ __global__ __launch_bounds__(THREADS) void gemm_f32_kernel(GemmArgs a) {
 
 // Tile shape for a problem: the largest tile that still gives every CU a
 // workgroup, else the smallest.
-enum Shape { T128x128, T128x64, T128x32 };
+enum Shape { T128x128, T128x64, T128x32, T64x64 };
 
 Shape pick_shape(int M, int N, int cu) {
-    const int forced = env_int("KVAD_GEMM_TILE_M", 0);  // tuning knob: tokens per tile
+    const int forced = env_int("KVAD_GEMM_TILE_M", 0);  // tuning knob: tokens per tile (6464: 64 x 64)
+    if (forced == 6464) return T64x64;
     if (forced == 128 || forced == 64 || forced == 32) return forced == 128 ? T128x128 : forced == 64 ? T128x64 : T128x32;
     const long long nt = (N + 127) / 128;
+    // 128 x 128 tiles while they give four workgroups per CU; below that,
+    // 64 x 64 tiles while they give one per two CUs (more, smaller
+    // workgroups hide the k-stages' load latency: (512, 896, 4864) 31.0 ->
+    // 28.3 us, (1024, 896, 4864) 45.0 -> 41.2, (512, 2048, 1408) 32.6 ->
+    // 31.0; at (2048, 4096, 14336) they lose, 461 -> 597)
+    if (nt * ((M + 127) / 128) >= 4LL * cu) return T128x128;
+    if ((long long)((N + 63) / 64) * ((M + 63) / 64) >= cu / 2) return T64x64;
     if (nt * ((M + 127) / 128) >= cu) return T128x128;
     if (nt * ((M + 63) / 64) >= cu) return T128x64;
     return T128x32;
@@ -609,18 +617,21 @@ Shape pick_shape(int M, int N, int cu) {
 
 int gemm_tile_m(kh_ctx *ctx, int M, int N) {
     const Shape sh = pick_shape(M, N, ctx->cu_count > 0 ? ctx->cu_count : 256);
-    return sh == T128x128 ? 128 : sh == T128x64 ? 64 : 32;
+    return sh == T128x128 ? 128 : sh == T128x32 ? 32 : 64;
 }
 
 namespace {
 
 template <int PREC>
-int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m) {
-    const unsigned gx = (unsigned)((a.N + 127) / 128);
+int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m, int tile_n) {
+    const unsigned gx = (unsigned)((a.N + tile_n - 1) / tile_n);
     const unsigned gy = a.tiles ? (unsigned)max_tiles : (unsigned)((a.M + tile_m - 1) / tile_m);
     if (gy == 0) return KH_OK;
     const dim3 grid(gx, gy, a.ksplit > 1 ? (unsigned)a.ksplit : 1u);
-    switch (tile_m) {
+    if (tile_n == 64) {
+        if (tile_m != 64 || a.tiles) return fail(KH_EINVAL, "gemm: 64-row tiles are 64 tokens wide and ungrouped");
+        hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 1, 1>), grid, dim3(THREADS), 0, ctx->stream, a);
+    } else switch (tile_m) {
         case 128:
             hipLaunchKernelGGL((gemm_i8_kernel<PREC, 2, 2, 2, 2>), grid, dim3(THREADS), 0, ctx->stream, a);
             break;
@@ -715,7 +726,7 @@ int gemm_split_reserve(kh_ctx *ctx) {
     return KH_OK;
 }
 
-int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m) {
+int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m, int tile_n) {
     a.ksplit = 0;
     if (a.tiles) return KH_OK;  // grouped launches are not split
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -724,7 +735,7 @@ int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m) {
     // another's MFMAs run), with at least SPLIT_MIN_STAGES stages a split,
     // at most SPLIT_MAX splits, and partials (4 M N bytes a split, written
     // and read again) of at most the weights' N K bytes.
-    const long long tiles = (long long)((a.N + 127) / 128) * ((a.M + tile_m - 1) / tile_m);
+    const long long tiles = (long long)((a.N + tile_n - 1) / tile_n) * ((a.M + tile_m - 1) / tile_m);
     const int S = (a.K + BK - 1) / BK;
     const size_t plane = (size_t)a.M * a.N * 4;
     long long ks = ((long long)SPLIT_PER_CU * cu + tiles / 2) / tiles;
@@ -773,7 +784,7 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     }
     // up to eight rows: the multi-token GEMV quantises them as it stages them
     // (QActBatch::new's codes, one launch fewer) while they are few values
-    const bool multi = m <= (size_t)MULTI_TOKENS && !matmul_force_gemm();
+    const bool multi = matmul_takes_multi(m, cols) && !matmul_force_gemm();
     if (multi && multi_stages_f32(w->precision, m, cols))
         return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, QAct{}, m, xs);
     // QActBatch::new (quant.rs:693-714): the activation rows quantised per block
@@ -794,7 +805,7 @@ int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, co
         rows > 0x7fffffff || m > 0x7fffffff)
         return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
     // a few tokens: stream the weights once through the multi-token GEMV
-    if (m <= (size_t)MULTI_TOKENS && !matmul_force_gemm())
+    if (matmul_takes_multi(m, cols) && !matmul_force_gemm())
         return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, q, m);
     GemmArgs a{};
     a.w = w->qs;
@@ -810,18 +821,18 @@ int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, co
     a.xsum = q.sums;
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const Shape sh = pick_shape(a.M, a.N, cu);
-    const int tile_m = sh == T128x128 ? 128 : sh == T128x64 ? 64 : 32;
-    int rc = plan_split(ctx, a, tile_m);
+    const int tile_m = sh == T128x128 ? 128 : sh == T128x32 ? 32 : 64, tile_n = sh == T64x64 ? 64 : 128;
+    int rc = plan_split(ctx, a, tile_m, tile_n);
     if (rc) return rc;
-    return launch_gemm_q(ctx, w->precision, a, 0, tile_m);
+    return launch_gemm_q(ctx, w->precision, a, 0, tile_m, tile_n);
 }
 
-int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m) {
+int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m, int tile_n) {
     if (a.tiles && (!a.wtab || !a.wstab)) return fail(KH_EINVAL, "gemm: grouped launch without weight tables");
     switch (precision) {
-        case KH_Q8: return launch_i8<KH_Q8>(ctx, a, max_tiles, tile_m);
-        case KH_Q4: return launch_i8<KH_Q4>(ctx, a, max_tiles, tile_m);
-        case KH_Q4K: return launch_i8<KH_Q4K>(ctx, a, max_tiles, tile_m);
+        case KH_Q8: return launch_i8<KH_Q8>(ctx, a, max_tiles, tile_m, tile_n);
+        case KH_Q4: return launch_i8<KH_Q4>(ctx, a, max_tiles, tile_m, tile_n);
+        case KH_Q4K: return launch_i8<KH_Q4K>(ctx, a, max_tiles, tile_m, tile_n);
         default: return fail(KH_EINVAL, "gemm: the grouped kernel takes quantised weights");
     }
 }

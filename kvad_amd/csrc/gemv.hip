@@ -917,6 +917,8 @@ int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *ar
 int launch_gemv_multi_jobs(kh_ctx *ctx, int njobs, const kh_weight *const *w, const float *const *bias,
                            float *const *y, const int *accumulate, const QAct &x, size_t m, const float *xf) {
     if (m == 0) return KH_OK;
+    if (!xf && m >= mma_min_tokens() && w[0]->precision != KH_F32)
+        return launch_gemv_mma(ctx, njobs, w, bias, y, accumulate, x, m);
     if (njobs < 1 || njobs > MULTI_JOBS) return fail(KH_EINVAL, "matmul: one to three weights per launch");
     MultiArgs a{};
     a.xq = x.qs;
@@ -955,10 +957,23 @@ bool multi_stages_f32(int precision, size_t m, size_t cols) {
     // about 12K values that costs more than a quantising launch of its own
     // plus a stage of codes (measured over q8 and Q4_K weights of 896 to
     // 14336 columns at m = 2..8).
+    // From mma_min_tokens() rows the matrix-core kernel takes the rows' codes.
+    if (m >= mma_min_tokens()) return false;
     const size_t slots = m <= 2 ? 2 : m <= 4 ? 4 : 8;
     const int lim = env_int("KVAD_MULTI_STAGE_F32", 12288);  // tuning knob
     (void)precision;
     return slots * cols <= (size_t)lim;
+}
+
+size_t mma_min_tokens() { return (size_t)env_int("KVAD_MMA_MIN", 5); }  // tuning knob
+
+bool matmul_takes_multi(size_t m, size_t cols) {
+    const int forced = env_int("KVAD_MULTI_TOKENS", 0);  // tuning knob: the multi-token GEMV up to this many rows
+    if (forced > 0) return m <= (size_t)forced;
+    // past eight rows the matrix-core kernel (16 rows a launch) beats the
+    // GEMM only over narrow rows (measured: 4864x896 at 16 rows 10.1 against
+    // 12.4 us; 896x4864 18.1 against 12.0)
+    return m <= (size_t)MULTI_TOKENS || (m <= 16 && cols <= 2048);
 }
 
 size_t fuse_max_cols(int precision) {

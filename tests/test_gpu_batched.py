@@ -146,20 +146,21 @@ def test_a_batch_of_one_is_a_token_and_a_batch_of_none_is_nothing(ctx):
 
 
 ROW_CASES = {
-    "q8_8": (8, {}), "q8_13": (13, {}), "q8_40": (40, {}),
+    "q8_8": (8, {}), "q8_13": (13, {}), "q8_20": (20, {}), "q8_40": (40, {}),
     # the down projection's 1024-wide input is eight k-stages: at 40 rows the
     # GEMM splits them over the grid and the last split adds the residual
     "q8_40_split": (40, dict(n_ff=1024)),
-    "q4k_5": (5, dict(prec="q4k", n_embd=256, n_ff=512)), "q4k_40": (40, dict(prec="q4k", n_embd=256, n_ff=1024)),
+    "q4k_5": (5, dict(prec="q4k", n_embd=256, n_ff=512)), "q4k_20": (20, dict(prec="q4k", n_embd=256, n_ff=512)),
+    "q4k_40": (40, dict(prec="q4k", n_embd=256, n_ff=1024)),
     "q4_6": (6, dict(prec="q4")), "q4_40": (40, dict(prec="q4", n_ff=1024)),
 }
 
 
 @pytest.mark.parametrize("case", list(ROW_CASES))
 def test_many_rows_on_the_multi_token_gemv_and_the_gemm(ctx, case):
-    # up to 8 rows: one multi-token GEMV launch per projection group; 13:
-    # two launches of up to eight rows; 40: the int8 GEMM, residual added in
-    # its epilogue (q8, q4 and Q4_K layer weights)
+    # up to 16 rows: one multi-token GEMV launch per projection group (on
+    # the matrix cores from five rows); 20: two launches; 40: the int8 GEMM,
+    # residual added in its epilogue (q8, q4 and Q4_K layer weights)
     n, kw = ROW_CASES[case]
     say("forward_each rows", case)
     m, mk = build(ctx, 740 + n, **kw)

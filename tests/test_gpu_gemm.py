@@ -51,6 +51,24 @@ def test_matmul_matches_the_oracle(ctx, prec):
         close(w.matmul_bt(xs, m, bias), oracle_matmul(prec, parts, rows, cols, xs, m, bias))
 
 
+@pytest.mark.parametrize("tile", ["32", "64", "128", "6464"])
+@pytest.mark.parametrize("prec", ["q8", "q4", "q4k"])
+def test_every_tile_shape_matches_the_oracle(ctx, monkeypatch, prec, tile):
+    # 128 weight rows by 32 / 64 / 128 tokens, or 64 by 64 (KVAD_GEMM_TILE_M):
+    # edge tiles in both directions, k tails, the k-stages split or not
+    monkeypatch.setenv("KVAD_GEMM_TILE_M", tile)
+    for m, rows, cols in [(33, 130, 96 if prec != "q4k" else 256), (65, 257, 288 if prec != "q4k" else 768),
+                          (100, 200, 1024)]:
+        w, parts = make(ctx, prec, rows, cols, seed=m + 2 * rows + cols)
+        xs = O.normal(m * 5 + rows, m * cols)
+        bias = O.normal(rows + 9, rows)
+        want = oracle_matmul(prec, parts, rows, cols, xs, m, bias)
+        for ks in ("", "3"):
+            say("matmul tile", prec, tile, m, rows, cols, ks or "auto")
+            monkeypatch.setenv("KVAD_GEMM_KSPLIT", ks)
+            close(w.matmul_bt(xs, m, bias), want)
+
+
 @pytest.mark.parametrize("prec", ["q8", "f32"])
 def test_qwen_prefill_shape(ctx, prec):
     # M = 512 tokens, K = 896, N = 4864

@@ -207,3 +207,18 @@ def test_device_quantiser_is_bit_exact(ctx, prec):
     np.testing.assert_array_equal(qs, q2)
     if s2 is not None:
         np.testing.assert_array_equal(sc.view(np.uint32), s2.view(np.uint32))
+
+
+def test_closing_a_context_frees_its_objects_first():
+    # objects still alive when their context closes are freed with it (their
+    # frees lock the context, so they may not outlive it); freeing them again
+    # afterwards, or collecting them, does nothing
+    say("context close with live objects")
+    c = K.Context(0)
+    w, _ = make(c, "q8", 64, 64, seed=1)
+    kv = K.KvCache(c, 1, 64, 64, 4)
+    c.close()
+    assert w.h is None and kv.h is None and c.h is None
+    w.free()
+    kv.free()
+    del w, kv
