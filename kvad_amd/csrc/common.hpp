@@ -224,8 +224,9 @@ int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *ar
 // y[m, rows] = x W^T (+bias) for a few quantised token rows (m small): the
 // weights stream once for all of them.  x holds the rows' codes.
 constexpr int MULTI_TOKENS = 8;  // token slots of one VALU multi-token launch
-// Whether kh_matmul takes the multi-token GEMV (else the GEMM) for m rows.
-bool matmul_takes_multi(size_t m, size_t cols);
+// Whether m token rows against a rows x cols weight take the multi-token
+// GEMV (else the GEMM): kh_matmul, and the session's single projections.
+bool matmul_takes_multi(size_t m, size_t rows, size_t cols);
 int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, const float *bias, float *y);
 // The same for up to MULTI_JOBS weights of one precision and width over the
 // same rows of codes, in one launch: y[i] (+)= x W_i^T (+ bias[i]), adding

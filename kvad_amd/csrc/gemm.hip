@@ -784,7 +784,7 @@ int launch_matmul(kh_ctx *ctx, const kh_weight *w, const float *xs, size_t m, co
     }
     // up to eight rows: the multi-token GEMV quantises them as it stages them
     // (QActBatch::new's codes, one launch fewer) while they are few values
-    const bool multi = matmul_takes_multi(m, cols) && !matmul_force_gemm();
+    const bool multi = matmul_takes_multi(m, rows, cols) && !matmul_force_gemm();
     if (multi && multi_stages_f32(w->precision, m, cols))
         return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, QAct{}, m, xs);
     // QActBatch::new (quant.rs:693-714): the activation rows quantised per block
@@ -805,7 +805,7 @@ int launch_matmul_q(kh_ctx *ctx, const kh_weight *w, const QAct &q, size_t m, co
         rows > 0x7fffffff || m > 0x7fffffff)
         return fail(KH_DECLINED, "matmul: operands of 4 GiB or more are not addressed here");
     // a few tokens: stream the weights once through the multi-token GEMV
-    if (matmul_takes_multi(m, cols) && !matmul_force_gemm())
+    if (matmul_takes_multi(m, rows, cols) && !matmul_force_gemm())
         return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, q, m);
     GemmArgs a{};
     a.w = w->qs;

@@ -967,13 +967,15 @@ bool multi_stages_f32(int precision, size_t m, size_t cols) {
 
 size_t mma_min_tokens() { return (size_t)env_int("KVAD_MMA_MIN", 5); }  // tuning knob
 
-bool matmul_takes_multi(size_t m, size_t cols) {
+bool matmul_takes_multi(size_t m, size_t rows, size_t cols) {
     const int forced = env_int("KVAD_MULTI_TOKENS", 0);  // tuning knob: the multi-token GEMV up to this many rows
     if (forced > 0) return m <= (size_t)forced;
-    // past eight rows the matrix-core kernel (16 rows a launch) beats the
-    // GEMM only over narrow rows (measured: 4864x896 at 16 rows 10.1 against
-    // 12.4 us; 896x4864 18.1 against 12.0)
-    return m <= (size_t)MULTI_TOKENS || (m <= 16 && cols <= 2048);
+    // Past eight rows the matrix-core kernel (16 rows a launch) beats the
+    // GEMM only over narrow rows of a not-too-tall matrix; the GEMM's time is
+    // nearly flat in m.  Measured (us): 4864x896 at 16 rows 10.1 against
+    // 12.4; 896x896 7.9 / 12.1; 896x4864 18.1 / 12.0; 151936x896 (a
+    // vocabulary head) 95.9 / 72.7, at 8 rows 49.7 / 72.0.
+    return m <= (size_t)MULTI_TOKENS || (m <= 16 && cols <= 2048 && rows <= 16384);
 }
 
 size_t fuse_max_cols(int precision) {

@@ -405,9 +405,11 @@ int ensure_rows(kh_llm *m, size_t n) {
 // y[n][rows] (+)= xs W^T (+bias): f32 weights on the f32 GEMM, quantised
 // ones from the rows' codes in qa (matmul_bt, quant.rs:751; tensor.rs:102);
 // with accumulate the product is added into y (the residual add).
-// Rows up to this many take the multi-token GEMV, eight rows a launch (the
-// weights stream once per launch): at decode's small matrices that beats a
-// GEMM whose 128-row tiles leave most CUs idle.
+// Projections of the same input (q/k/v, gate/up) take one multi-token GEMV
+// launch up to this many rows (the weights stream once per launch; the GEMM
+// would take a launch per weight, and at decode's small matrices its
+// 128-row tiles leave most CUs idle).  A single projection (o, down, the
+// head) follows kh_matmul's rule.
 size_t rows_multi_max() {
     static const size_t v = (size_t)env_int("KVAD_ROWS_MULTI", 32);  // tuning knob
     return v;
@@ -416,7 +418,8 @@ size_t rows_multi_max() {
 int project(kh_ctx *ctx, const kh_weight *w, const float *xs, const QAct &qa, size_t n, const float *bias, float *y,
             int accumulate = 0) {
     if (w->precision == KH_F32) return launch_matmul(ctx, w, xs, n, bias, y, accumulate);
-    if (n <= rows_multi_max()) return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, qa, n);
+    if (n <= rows_multi_max() && matmul_takes_multi(n, w->rows, w->cols))
+        return launch_gemv_multi_jobs(ctx, 1, &w, &bias, &y, &accumulate, qa, n);
     return launch_matmul_q(ctx, w, qa, n, bias, y, accumulate);
 }
 
