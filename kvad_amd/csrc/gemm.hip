@@ -602,12 +602,13 @@ Shape pick_shape(int M, int N, int cu) {
     if (forced == 128 || forced == 64 || forced == 32) return forced == 128 ? T128x128 : forced == 64 ? T128x64 : T128x32;
     const long long nt = (N + 127) / 128;
     // 128 x 128 tiles while they give four workgroups per CU; below that,
-    // 64 x 64 tiles while they give one per two CUs (more, smaller
-    // workgroups hide the k-stages' load latency: (512, 896, 4864) 31.0 ->
-    // 28.3 us, (1024, 896, 4864) 45.0 -> 41.2, (512, 2048, 1408) 32.6 ->
-    // 31.0; at (2048, 4096, 14336) they lose, 461 -> 597)
+    // from 128 tokens, 64 x 64 tiles while they give one per two CUs (more,
+    // smaller workgroups hide the k-stages' load latency: (512, 896, 4864)
+    // 31.0 -> 28.3 us, (1024, 896, 4864) 45.0 -> 41.2, (512, 2048, 1408)
+    // 32.6 -> 31.0; at (2048, 4096, 14336) they lose, 461 -> 597, and at 16
+    // tokens over 14336x4096 29 -> 45 against 32-token tiles split over k)
     if (nt * ((M + 127) / 128) >= 4LL * cu) return T128x128;
-    if ((long long)((N + 63) / 64) * ((M + 63) / 64) >= cu / 2) return T64x64;
+    if (M >= 128 && (long long)((N + 63) / 64) * ((M + 63) / 64) >= cu / 2) return T64x64;
     if (nt * ((M + 127) / 128) >= cu) return T128x128;
     if (nt * ((M + 63) / 64) >= cu) return T128x64;
     return T128x32;

@@ -427,11 +427,12 @@ int launch_gemv_mma(kh_ctx *ctx, int njobs, const kh_weight *const *w, const flo
                         accumulate ? accumulate[i] : 0, nwg};
         nwg += (int)((w[i]->rows + 15) / 16);
     }
-    // waves per workgroup: enough that each takes a few units (R per round),
-    // more while the launch has few workgroups
-    const int R = prec == KH_Q4K ? 2 : 4;
+    // Four waves per workgroup, each taking several rounds of R units when
+    // the rows are long: measured at or ahead of 8 and 16 waves at every
+    // shape (m = 8, us for 4 / 8 / 16 waves: Q4_K 14336x4096 23.1 / 22.8 /
+    // 33.3, 4096x14336 20.7 / 21.2 / 21.9; q8 896x4864 10.8 / 11.3 / 11.9,
+    // 151936x896 49.4 / 78.1 / 91.9)
     int nw = 4;
-    while (nw < 16 && (a.units > nw * R || (long long)nwg * nw < 2048) && a.units >= 2 * nw) nw *= 2;
     const int forced = env_int("KVAD_MMA_WAVES", 0);  // tuning knob
     if (forced == 4 || forced == 8 || forced == 16) nw = forced;
     for (size_t t0 = 0; t0 < m; t0 += MMA_TOKENS) {
@@ -442,9 +443,11 @@ int launch_gemv_mma(kh_ctx *ctx, int njobs, const kh_weight *const *w, const flo
         b.xsum = x.sums + t0 * nb;
         for (int i = 0; i < njobs; i++) b.j[i].y = a.j[i].y + t0 * a.j[i].rows;
         int rc;
+        // two units a round (measured against 1, 4 and 8 at m = 8: q8
+        // 151936x896 37.2 against 49.5 us at 4; Q4_K level with 1, 4 slower)
         switch (prec) {
-            case KH_Q8: rc = launch_mode<KH_Q8, 4>(ctx, b, nwg, nw); break;
-            case KH_Q4: rc = launch_mode<KH_Q4, 4>(ctx, b, nwg, nw); break;
+            case KH_Q8: rc = launch_mode<KH_Q8, 2>(ctx, b, nwg, nw); break;
+            case KH_Q4: rc = launch_mode<KH_Q4, 2>(ctx, b, nwg, nw); break;
             default: rc = launch_mode<KH_Q4K, 2>(ctx, b, nwg, nw); break;
         }
         if (rc) return rc;
