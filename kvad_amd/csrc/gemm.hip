@@ -607,10 +607,13 @@ Shape pick_shape(int M, int N, int cu) {
     // 31.0 -> 28.3 us, (1024, 896, 4864) 45.0 -> 41.2, (512, 2048, 1408)
     // 32.6 -> 31.0; at (2048, 4096, 14336) they lose, 461 -> 597, and at 16
     // tokens over 14336x4096 29 -> 45 against 32-token tiles split over k)
-    if (nt * ((M + 127) / 128) >= 4LL * cu) return T128x128;
+    // Token tiles no wider than the tokens need: a tall matrix at 16 or 32
+    // tokens (a vocabulary head) gives enough workgroups with 32-token
+    // tiles, and 128-token ones would leave three quarters of every tile idle.
+    if (M > 64 && nt * ((M + 127) / 128) >= 4LL * cu) return T128x128;
     if (M >= 128 && (long long)((N + 63) / 64) * ((M + 63) / 64) >= cu / 2) return T64x64;
-    if (nt * ((M + 127) / 128) >= cu) return T128x128;
-    if (nt * ((M + 63) / 64) >= cu) return T128x64;
+    if (M > 64 && nt * ((M + 127) / 128) >= cu) return T128x128;
+    if (M > 32 && nt * ((M + 63) / 64) >= cu) return T128x64;
     return T128x32;
 }
 
