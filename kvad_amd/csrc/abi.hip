@@ -826,6 +826,8 @@ int kh_moe_new(kh_ctx *ctx, size_t n_experts, size_t top_k, size_t hidden, size_
     m->down.assign(n_experts, nullptr);
     KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->tab), sizeof(void *) * 3 * n_experts));
     KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->stab), sizeof(float *) * 3 * n_experts));
+    KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->arrivals), sizeof(unsigned)));
+    KH_HIP(hipMemset(m->arrivals, 0, sizeof(unsigned)));  // the decode step's router leaves it at zero
     if (bias) {
         KH_HIP(hipMalloc(reinterpret_cast<void **>(&m->bias), 4 * n_experts));
         KH_HIP(hipMemcpy(m->bias, bias, 4 * n_experts, hipMemcpyHostToDevice));
@@ -841,6 +843,7 @@ int kh_moe_free(kh_moe *moe) {
         (void)hipStreamSynchronize(moe->ctx->stream);
         if (moe->tab) (void)hipFree(moe->tab);
         if (moe->stab) (void)hipFree(moe->stab);
+        if (moe->arrivals) (void)hipFree(moe->arrivals);
         if (moe->bias) (void)hipFree(moe->bias);
     }
     delete moe;

@@ -93,6 +93,7 @@ struct kh_moe {
     int precision = -1;                        // of every expert weight
     void **tab = nullptr;                      // device: [gate qs | up qs | down qs] x n_experts
     float **stab = nullptr;                    // device: the same for scales
+    unsigned *arrivals = nullptr;              // device: router workgroups done this step (zero between steps)
     bool dirty = true;                         // tables need uploading
 };
 
@@ -339,6 +340,11 @@ struct RouteArgs {
     int32_t *count;
     int32_t *sorted_experts;  // optional, [m, top_k]
     float *sorted_weights;
+    // Fused into the router's GEMV (launch_gemv_route): with `arrivals` set,
+    // the router's rows are spread over `groups` workgroups and the last to
+    // finish routes; without, one workgroup computes them all and routes.
+    unsigned *arrivals;
+    int groups;
 };
 int launch_route(kh_ctx *ctx, const RouteArgs &r, int m);
 // Groups m tokens' picks by expert (expert order, then token order): rows

@@ -241,7 +241,10 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
                 if (lane == 0 && r < rows) {
                     float out = job.bias ? v + b : v;
                     if (job.accumulate) out = y0 + out;  // x += proj (llama.rs:273-276)
-                    job.y[r] = out;
+                    if (routes && tab.route.arrivals)  // read back by another workgroup: past the L2
+                        __hip_atomic_store(job.y + r, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else
+                        job.y[r] = out;
                     if (routes) s_lg[r] = out;
                     // rows in increasing order: a later equal value never wins
                     if (argm && r >= 1 && out == out && (arg_bi < 0 || out > arg_bv)) arg_bv = out, arg_bi = r;
@@ -280,7 +283,29 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
         }
     }
     if constexpr (ROUTE) {
-        if (routes) {
+        if (routes && tab.route.arrivals) {
+            // The router's rows are spread over route.groups workgroups; the
+            // last to finish routes.  Each wave's logit stores (device scope,
+            // past the per-XCD L2) have completed before the workgroup counts
+            // its arrival, and the last reads them back at device scope, so no
+            // cache-wide fence is needed.  Nothing waits on another
+            // workgroup: every workgroup counts itself once and leaves.
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (wv == 0) {
+                unsigned old = 0;
+                if (lane == 0)
+                    old = __hip_atomic_fetch_add(tab.route.arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);
+                if (old == (unsigned)tab.route.groups - 1) {
+                    for (int i = lane; i < rows; i += WAVE)
+                        s_lg[i] = __hip_atomic_load(job.y + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    wave_lds_sync();
+                    route_one(tab.route, 0, s_lg);
+                    if (lane == 0) __hip_atomic_store(tab.route.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        } else if (routes) {
             __syncthreads();  // every wave's logits are in LDS
             if (wv == 0) route_one(tab.route, 0, s_lg);
         }
@@ -632,7 +657,12 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
         const int want = (groups + p.nwv - 1) / p.nwv;
         int share = (int)((long long)cap_wg * tab.j[i].rows / (rows_total > 0 ? rows_total : 1));
         if (share < 1) share = 1;
-        const int nwg = i == tab.route_job - 1 ? 1 : want < share ? want : share;  // the router: one workgroup
+        // the router: one workgroup, or (counting arrivals) as many as its rows need
+        int nwg = want < share ? want : share;
+        if (i == tab.route_job - 1) {
+            nwg = tab.route.arrivals ? want : 1;
+            tab.route.groups = nwg;
+        }
         tab.j[i].wave0 = blocks;  // first workgroup of the job
         tab.j[i].nwaves = nwg * p.nwv;
         blocks += nwg;

@@ -289,6 +289,7 @@ int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
     RouteArgs r = route_args(moe, logits, pe, pw, cnt);
     r.sorted_experts = se;
     r.sorted_weights = sw;
+    r.arrivals = moe->arrivals;
     // (1) + (2) in one launch where the GEMV has a routing build for it: the
     // router's one workgroup routes its own logits while the shared expert's
     // rows stream (q8, inputs the kernel stages itself)
