@@ -292,8 +292,9 @@ int gemm_split_reserve(kh_ctx *ctx);
 // Sets a's split-K fields for an ungrouped launch of tile_m-token tiles when
 // splitting its k-stages pays (ksplit 0: no split).
 int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m, int tile_n = 128);
-// Tokens per tile for an ungrouped M x N launch of the int8 GEMM.
-int gemm_tile_m(kh_ctx *ctx, int M, int N);
+// Tokens per tile (returned) and weight rows per tile (*tile_n) for an
+// ungrouped M x N launch of the int8 GEMM.
+int gemm_tiles(kh_ctx *ctx, int M, int N, int *tile_n);
 
 // Operator bodies on device pointers (abi.hip), for the layers built on them.
 int matvec_device(kh_ctx *ctx, const kh_weight *w, const float *x, const float *bias, float *y, int32_t *dots);

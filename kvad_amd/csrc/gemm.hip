@@ -619,8 +619,9 @@ Shape pick_shape(int M, int N, int cu) {
 
 }  // namespace
 
-int gemm_tile_m(kh_ctx *ctx, int M, int N) {
+int gemm_tiles(kh_ctx *ctx, int M, int N, int *tile_n) {
     const Shape sh = pick_shape(M, N, ctx->cu_count > 0 ? ctx->cu_count : 256);
+    *tile_n = sh == T64x64 ? 64 : 128;
     return sh == T128x128 ? 128 : sh == T128x32 ? 32 : 64;
 }
 
@@ -738,14 +739,16 @@ int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m, int tile_n) {
     // workgroups per CU (a CU holds several: one's loads wait while
     // another's MFMAs run), with at least SPLIT_MIN_STAGES stages a split,
     // at most SPLIT_MAX splits, and partials (4 M N bytes a split, written
-    // and read again) of at most the weights' N K bytes.
+    // and read again) of at most the weights' N K bytes or 4 MiB, whichever
+    // is more (a small weight such as a router's 64 rows would otherwise
+    // never split: 512 tokens x 64 x 2048, 16 workgroups, 22.6 us unsplit).
     const long long tiles = (long long)((a.N + tile_n - 1) / tile_n) * ((a.M + tile_m - 1) / tile_m);
     const int S = (a.K + BK - 1) / BK;
     const size_t plane = (size_t)a.M * a.N * 4;
     long long ks = ((long long)SPLIT_PER_CU * cu + tiles / 2) / tiles;
     ks = std::min<long long>(ks, S / SPLIT_MIN_STAGES);
     ks = std::min<long long>(ks, SPLIT_MAX);
-    ks = std::min<long long>(ks, (long long)((size_t)a.K / (4 * (size_t)a.M)));
+    ks = std::min<long long>(ks, (long long)(std::max((size_t)a.N * a.K, (size_t)4 << 20) / plane));
     const int forced = env_int("KVAD_GEMM_KSPLIT", 0);  // tuning knob: k splits (1: none)
     if (forced > 0) ks = std::min(forced, S);
     ks = std::min<long long>(ks, (long long)(SPLIT_BYTES / plane));

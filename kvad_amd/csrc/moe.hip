@@ -345,20 +345,22 @@ int ffn_rows(kh_ctx *ctx, const kh_weight *gate, const kh_weight *up, const kh_w
     GemmArgs a{};
     a.xq = xq.qs, a.xs = xq.scales, a.xsum = xq.sums;
     a.M = (int)m, a.K = (int)gate->cols;
-    const int tm = gemm_tile_m(ctx, (int)m, (int)gate->rows);
+    int tn;
+    const int tm = gemm_tiles(ctx, (int)m, (int)gate->rows, &tn);
     int rc;
     a.w = gate->qs, a.ws = gate->scales, a.N = (int)gate->rows, a.y = g;
-    if ((rc = plan_split(ctx, a, tm)) || (rc = launch_gemm_q(ctx, gate->precision, a, 0, tm))) return rc;
+    if ((rc = plan_split(ctx, a, tm, tn)) || (rc = launch_gemm_q(ctx, gate->precision, a, 0, tm, tn))) return rc;
     a.w = up->qs, a.ws = up->scales, a.N = (int)up->rows, a.y = u;
-    if ((rc = plan_split(ctx, a, tm)) || (rc = launch_gemm_q(ctx, up->precision, a, 0, tm))) return rc;
+    if ((rc = plan_split(ctx, a, tm, tn)) || (rc = launch_gemm_q(ctx, up->precision, a, 0, tm, tn))) return rc;
     if ((rc = launch_swiglu_qact(ctx, g, u, m, gate->rows, hq))) return rc;
     GemmArgs d{};
     d.xq = hq.qs, d.xs = hq.scales, d.xsum = hq.sums;
     d.M = (int)m, d.K = (int)down->cols, d.N = (int)down->rows;
     d.w = down->qs, d.ws = down->scales, d.y = y;
-    const int td = gemm_tile_m(ctx, (int)m, (int)down->rows);
-    if ((rc = plan_split(ctx, d, td))) return rc;
-    return launch_gemm_q(ctx, down->precision, d, 0, td);
+    int tdn;
+    const int td = gemm_tiles(ctx, (int)m, (int)down->rows, &tdn);
+    if ((rc = plan_split(ctx, d, td, tdn))) return rc;
+    return launch_gemm_q(ctx, down->precision, d, 0, td, tdn);
 }
 
 // A batch: Moe::run for m > 1 (ffn.rs:615-708, mix ffn.rs:788-805).
