@@ -283,6 +283,15 @@ struct GemmArgs {
     // the splits in order, then bias and residual
     int ksplit;
     float *part;
+    // a second weight of the same shape over the same activations (gate and
+    // up): when y2 is set the grid holds both weights' row tiles, the first
+    // weight's then the second's, and the second writes y2 (split-K partials
+    // of the second take the plane after the first's)
+    const void *w2;
+    const float *ws2;
+    const void *const *wtab2;
+    const float *const *wstab2;
+    float *y2;
 };
 // tile_n: weight rows per tile (128, or 64 with 64-token tiles, ungrouped)
 int launch_gemm_q(kh_ctx *ctx, int precision, const GemmArgs &a, int max_tiles, int tile_m, int tile_n = 128);

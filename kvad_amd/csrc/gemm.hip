@@ -214,8 +214,15 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr0 = (wave / WT) * RT * 32, wm0 = (wave % WT) * TT * 32;
-    const int n0 = blockIdx.x * BN;
     const int K = a.K, nb = K / BLOCK;
+    // a paired launch: row tiles past the first weight's are the second's
+    const int nx = (a.N + BN - 1) / BN;
+    const bool second = a.y2 && (int)blockIdx.x >= nx;
+    const int n0 = ((int)blockIdx.x - (second ? nx : 0)) * BN;
+    if (second) {
+        a.w = a.w2, a.ws = a.ws2, a.wtab = a.wtab2, a.wstab = a.wstab2, a.y = a.y2;
+        if (a.ksplit > 1) a.part += (size_t)a.ksplit * a.M * a.N;
+    }
 
     // the workgroup's rows of activations (and, grouped, its expert)
     int m0, m_end;
@@ -629,7 +636,7 @@ namespace {
 
 template <int PREC>
 int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m, int tile_n) {
-    const unsigned gx = (unsigned)((a.N + tile_n - 1) / tile_n);
+    const unsigned gx = (unsigned)((a.N + tile_n - 1) / tile_n) * (a.y2 ? 2u : 1u);
     const unsigned gy = a.tiles ? (unsigned)max_tiles : (unsigned)((a.M + tile_m - 1) / tile_m);
     if (gy == 0) return KH_OK;
     const dim3 grid(gx, gy, a.ksplit > 1 ? (unsigned)a.ksplit : 1u);
@@ -653,6 +660,12 @@ int launch_i8(kh_ctx *ctx, const GemmArgs &a, int max_tiles, int tile_m, int til
         hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, ctx->stream,
                            a.part, a.ksplit, a.M, a.N, a.bias, a.accumulate, a.y);
         KH_HIP(hipGetLastError());
+        if (a.y2) {  // the second weight's splits, in the plane after the first's
+            hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                               ctx->stream, a.part + (size_t)a.ksplit * a.M * a.N, a.ksplit, a.M, a.N, a.bias,
+                               a.accumulate, a.y2);
+            KH_HIP(hipGetLastError());
+        }
     }
     return KH_OK;
 }
@@ -742,13 +755,15 @@ int plan_split(kh_ctx *ctx, GemmArgs &a, int tile_m, int tile_n) {
     // and read again) of at most the weights' N K bytes or 4 MiB, whichever
     // is more (a small weight such as a router's 64 rows would otherwise
     // never split: 512 tokens x 64 x 2048, 16 workgroups, 22.6 us unsplit).
-    const long long tiles = (long long)((a.N + tile_n - 1) / tile_n) * ((a.M + tile_m - 1) / tile_m);
+    // a paired launch (a.y2) holds both weights' tiles and partial planes
+    const int pair = a.y2 ? 2 : 1;
+    const long long tiles = (long long)((a.N + tile_n - 1) / tile_n) * ((a.M + tile_m - 1) / tile_m) * pair;
     const int S = (a.K + BK - 1) / BK;
-    const size_t plane = (size_t)a.M * a.N * 4;
+    const size_t plane = (size_t)a.M * a.N * 4 * pair;
     long long ks = ((long long)SPLIT_PER_CU * cu + tiles / 2) / tiles;
     ks = std::min<long long>(ks, S / SPLIT_MIN_STAGES);
     ks = std::min<long long>(ks, SPLIT_MAX);
-    ks = std::min<long long>(ks, (long long)(std::max((size_t)a.N * a.K, (size_t)4 << 20) / plane));
+    ks = std::min<long long>(ks, (long long)(std::max((size_t)a.N * a.K * pair, (size_t)4 << 20) / plane));
     const int forced = env_int("KVAD_GEMM_KSPLIT", 0);  // tuning knob: k splits (1: none)
     if (forced > 0) ks = std::min(forced, S);
     ks = std::min<long long>(ks, (long long)(SPLIT_BYTES / plane));

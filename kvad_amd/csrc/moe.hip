@@ -14,9 +14,11 @@
 // order -- the order mix() adds them, so the sum rounds as the reference's.
 //
 // Prefill groups the tokens by expert (expert order, then token order, as
-// by_expert is filled, ffn.rs:627-640), runs each expert's gate/up and down as
-// one grouped int8 GEMM over tiles of its rows, and combines per token in
-// expert order after the shared expert (which runs on every token).
+// by_expert is filled, ffn.rs:627-640), runs every expert's gate and up as
+// one grouped int8 GEMM launch over tiles of its rows (the two weight tables
+// paired) and every down as another, and combines per token in expert order
+// after the shared expert (which runs on every token, its gate and up paired
+// the same way).  The input rows are quantised once, for the router too.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -349,9 +351,15 @@ int ffn_rows(kh_ctx *ctx, const kh_weight *gate, const kh_weight *up, const kh_w
     const int tm = gemm_tiles(ctx, (int)m, (int)gate->rows, &tn);
     int rc;
     a.w = gate->qs, a.ws = gate->scales, a.N = (int)gate->rows, a.y = g;
-    if ((rc = plan_split(ctx, a, tm, tn)) || (rc = launch_gemm_q(ctx, gate->precision, a, 0, tm, tn))) return rc;
-    a.w = up->qs, a.ws = up->scales, a.N = (int)up->rows, a.y = u;
-    if ((rc = plan_split(ctx, a, tm, tn)) || (rc = launch_gemm_q(ctx, up->precision, a, 0, tm, tn))) return rc;
+    if (gate->precision == up->precision && gate->rows == up->rows && gate->cols == up->cols) {
+        // gate and up in one launch over the same activation tiles
+        a.w2 = up->qs, a.ws2 = up->scales, a.y2 = u;
+        if ((rc = plan_split(ctx, a, tm, tn)) || (rc = launch_gemm_q(ctx, gate->precision, a, 0, tm, tn))) return rc;
+    } else {
+        if ((rc = plan_split(ctx, a, tm, tn)) || (rc = launch_gemm_q(ctx, gate->precision, a, 0, tm, tn))) return rc;
+        a.w = up->qs, a.ws = up->scales, a.N = (int)up->rows, a.y = u;
+        if ((rc = plan_split(ctx, a, tm, tn)) || (rc = launch_gemm_q(ctx, up->precision, a, 0, tm, tn))) return rc;
+    }
     if ((rc = launch_swiglu_qact(ctx, g, u, m, gate->rows, hq))) return rc;
     GemmArgs d{};
     d.xq = hq.qs, d.xs = hq.scales, d.xsum = hq.sums;
@@ -422,15 +430,20 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     int32_t *pe = b.pe, *cnt = b.cnt, *pos = b.pos, *row_token = b.row_token, *tiles = b.tiles;
     const QAct hq = b.hq, rq = b.rq, sq = b.sq;
     int rc;
-    // router logits (any precision), then the routes
-    if ((rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits))) return rc;
-    if ((rc = launch_route(ctx, route_args(moe, logits, pe, pw, cnt), (int)m))) return rc;
+    // the activations, quantised once for the router, every expert and the
+    // shared one (QActBatch::new, quant.rs:693-714)
+    if ((rc = launch_qact(ctx, hs, m, hid, hq))) return rc;
+    // router logits (any precision; quantised weights read the codes above,
+    // the ones matmul_bt would make), then the routes
+    if (moe->router->precision != KH_F32 && moe->router->cols == hid)
+        rc = launch_matmul_q(ctx, moe->router, hq, m, nullptr, logits, 0);
+    else
+        rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits);
+    if (rc || (rc = launch_route(ctx, route_args(moe, logits, pe, pw, cnt), (int)m))) return rc;
     // by_expert, and the tiles of the grouped GEMMs
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), 0, ctx->stream, pe, pw, cnt, (int)m, (int)k,
                        (int)n, tile_m, row_token, row_weight, pos, wpos, tiles);
     KH_HIP(hipGetLastError());
-    // the activations, quantised once for every expert and the shared one
-    if ((rc = launch_qact(ctx, hs, m, hid, hq))) return rc;
     // the shared expert on every token (SharedExpert::run, ffn.rs:437-451)
     if (sh && (rc = ffn_rows(ctx, moe->sgate, moe->sup, moe->sdown, hq, m, sg, su, sq, base))) return rc;
     // each expert's gate and up over its own rows
@@ -441,10 +454,10 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     a.wtab = const_cast<const void *const *>(moe->tab);
     a.wstab = const_cast<const float *const *>(moe->stab);
     a.y = g;
-    if ((rc = launch_gemm_q(ctx, moe->precision, a, (int)max_tiles, tile_m))) return rc;
-    a.wtab = const_cast<const void *const *>(moe->tab + n);
-    a.wstab = const_cast<const float *const *>(moe->stab + n);
-    a.y = u;
+    // and up in the same launch (the second weight table)
+    a.wtab2 = const_cast<const void *const *>(moe->tab + n);
+    a.wstab2 = const_cast<const float *const *>(moe->stab + n);
+    a.y2 = u;
     if ((rc = launch_gemm_q(ctx, moe->precision, a, (int)max_tiles, tile_m))) return rc;
     if ((rc = launch_swiglu_qact(ctx, g, u, total, inter, rq))) return rc;
     // each expert's down over its rows of swiglu(gate, up)
