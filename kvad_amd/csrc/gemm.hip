@@ -15,8 +15,9 @@
 //
 // The per-block scaling is the bound: with 32-wide scale blocks on both
 // operands every output takes a scaled term per block.  The scale products
-// ws[r] * xs[t] of a tile are an outer product, computed on the matrix core
-// (v_mfma_f32_32x32x2_f32 with one k-slot zero); Q4_K's minimum terms
+// ws[r] * xs[t] of a tile are an outer product, computed on the matrix core,
+// two tiles per v_mfma_f32_32x32x1_2b_f32 (half the matrix-core time of one
+// 32x32x2 product per tile with a k-slot zeroed); Q4_K's minimum terms
 // sum_b dmin*m * xs*sum are a true product over the block index and go into
 // the accumulators by MFMA as well.  Two VALU operations per output per
 // block remain (convert the i32 dot, fused multiply-add); matrix-core
@@ -44,6 +45,14 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+__device__ __forceinline__ v16f lo16(const v32f &x) {
+    return __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
+__device__ __forceinline__ v16f hi16(const v32f &x) {
+    return __builtin_shufflevector(x, x, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
+}
 
 constexpr unsigned RSRC_WORD3 = 0x00020000;  // raw buffer, gfx9 family
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -407,7 +416,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             for (int v = 0; v < 16; v++) acc[rt][tt][v] = 0.0f;
 
     const v16i zero = {};
-    const v16f fzero = {};
+    const v32f fzero32 = {};
     // One tile pair's products are held while the next pair's are issued:
     // the matrix core works on tile i while the VALU scales tile i - 1
     // (otherwise every convert waits out its own MFMA).  The pair still
@@ -436,8 +445,14 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
         // block b's fragments (and its scale columns) from LDS; the next
         // block's are read while this one's products are scaled
         v4i af[2][RT], bf[2][TT];
-        float wa[2][RT], xb[2][TT];
-        const bool lo = lane < 32;
+        // The block's scale products p[r][t] = ws[r] * xs[t] (quant.rs:903;
+        // Q4_K: d*sc * xs) are outer products on the matrix core, two 32 x 32
+        // tiles per v_mfma_f32_32x32x1_2b_f32 (tile k from lanes 32k..32k+31
+        // of both operands, its products in elements 16k..16k+15): the two
+        // token tiles of a row tile (TT = 2), else the two row tiles (RT = 2),
+        // else two consecutive blocks of the one tile (issued at even blocks).
+        constexpr int PR = TT == 2 ? RT : 1;  // pair products per block
+        float wa[2][PR], xb[2];
         auto frags = [&](int b, int f) {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
@@ -447,20 +462,20 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             for (int tt = 0; tt < TT; tt++)
                 bf[f][tt] = *reinterpret_cast<const v4i *>(sB + (wm0 + tt * 32 + (lane & 31)) * ASTR + b * 32 +
                                                            16 * (lane >> 5));
-            // the block's scale products p[r][t] = ws[r] * xs[t] (quant.rs:903;
-            // Q4_K: d*sc * xs) as an outer product on the matrix core: k-slot 0
-            // holds the 32 rows' (tokens') scales, k-slot 1 zeros
+            if constexpr (TT == 2) {
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                const float x = sW[b][wr0 + rt * 32 + (lane & 31)];  // read by every lane, kept by the low half
-                wa[f][rt] = lo ? x : 0.0f;
-            }
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++) {
-                const float x = sX[b][wm0 + tt * 32 + (lane & 31)];
-                xb[f][tt] = lo ? x : 0.0f;
+                for (int rt = 0; rt < RT; rt++) wa[f][rt] = sW[b][wr0 + rt * 32 + (lane & 31)];
+                xb[f] = sX[b][wm0 + lane];
+            } else if constexpr (RT == 2) {
+                wa[f][0] = sW[b][wr0 + lane];
+                xb[f] = sX[b][wm0 + (lane & 31)];
+            } else if ((b & 1) == 0) {  // blocks b and b + 1 (b + 1 < NBS: NBS is even)
+                wa[f][0] = sW[b + (lane >> 5)][wr0 + (lane & 31)];
+                xb[f] = sX[b + (lane >> 5)][wm0 + (lane & 31)];
             }
         };
+        static_assert(NBS % 2 == 0, "block pairs stay within a stage");
+        v32f P = {};  // the current pair product (both halves)
         frags(0, 0);
 #pragma unroll
         for (int b = 0; b < NBS; b++) {
@@ -471,16 +486,22 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++) {
                     const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[f][rt], bf[f][tt], zero, 0, 0, 0);
-                    const v16f p = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[f][rt], xb[f][tt], fzero, 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
                     if (rt == 0 && tt == 0 && b + 1 < NBS && b + 1 < nblk) frags(b + 1, f ^ 1);
-                    // the previous pair: (rt, tt - 1), (rt - 1, TT - 1), or the last block's last
+                    // the previous tile: (rt, tt - 1), (rt - 1, TT - 1), or the last block's last
                     if (tt > 0) scale_into(acc[rt][tt - 1], pq, dq);
                     else if (rt > 0) scale_into(acc[rt - 1][TT - 1], pq, dq);
                     else if (pending) scale_into(acc[RT - 1][TT - 1], pq, dq);
+                    // a pair's product is issued at its first tile, once the
+                    // previous pair's last half is used (one pair live at a time)
+                    const int half = TT == 2 ? tt : RT == 2 ? rt : b & 1;
+                    if (half == 0) {
+                        const float wv = TT == 2 ? wa[f][rt] : wa[f][0];
+                        P = __builtin_amdgcn_mfma_f32_32x32x1f32(wv, xb[f], fzero32, 0, 0, 0);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                     dq = d;
-                    pq = p;
+                    pq = half ? hi16(P) : lo16(P);
                     pending = true;
                 }
             if constexpr (PREC == KH_Q4K) {
