@@ -47,12 +47,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-__device__ __forceinline__ v16f lo16(const v32f &x) {
-    return __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
-}
-__device__ __forceinline__ v16f hi16(const v32f &x) {
-    return __builtin_shufflevector(x, x, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
-}
 
 constexpr unsigned RSRC_WORD3 = 0x00020000;  // raw buffer, gfx9 family
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -368,20 +362,21 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
                 const unsigned hb[4] = {(unsigned)rh.x, (unsigned)rh.y, (unsigned)rh.z, (unsigned)rh.w};
                 auto byte = [&](int i) { return (hb[i >> 2] >> (8 * (i & 3))) & 0xffu; };  // block byte i
                 const float d = half_bits_to_float(hb[0]), dmin = half_bits_to_float(hb[0] >> 16);
-                const int h = (k0 % QK_K) / BK;
-#pragma unroll
-                for (int jj = 0; jj < 4; jj++) {
-                    const int j = 4 * h + jj;
-                    unsigned sc, mn;
-                    if (j < 4) {
-                        sc = byte(4 + j) & 63;
-                        mn = byte(4 + j + 4) & 63;
-                    } else {
-                        sc = (byte(4 + j + 4) & 0xf) | ((byte(4 + j - 4) >> 6) << 4);
-                        mn = (byte(4 + j + 4) >> 4) | ((byte(4 + j) >> 6) << 4);
-                    }
+                // sub-blocks j = 4 h + jj, h the stage's half of the super-block;
+                // each branch indexes the header with constants (a runtime index
+                // would put it in scratch memory)
+                auto put = [&](int jj, unsigned sc, unsigned mn) {
                     sW[jj][tid] = d * (float)sc;
                     sWm[jj][tid] = dmin * (float)mn;
+                };
+                if ((k0 % QK_K) / BK == 0) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) put(j, byte(4 + j) & 63, byte(8 + j) & 63);
+                } else {
+#pragma unroll
+                    for (int j = 4; j < 8; j++)
+                        put(j - 4, (byte(4 + j + 4) & 0xf) | ((byte(4 + j - 4) >> 6) << 4),
+                            (byte(4 + j + 4) >> 4) | ((byte(4 + j) >> 6) << 4));
                 }
             }
         }
@@ -417,17 +412,22 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
 
     const v16i zero = {};
     const v32f fzero32 = {};
-    // One tile pair's products are held while the next pair's are issued:
-    // the matrix core works on tile i while the VALU scales tile i - 1
-    // (otherwise every convert waits out its own MFMA).  The pair still
-    // pending at any block's end is (RT - 1, TT - 1).
-    v16i dq = {};
-    v16f pq = {};
+    // One tile's products are held while the next tile's are issued: the
+    // matrix core works on tile i while the VALU scales tile i - 1
+    // (otherwise every convert waits out its own MFMA).  Tile s of a stage
+    // (s = (b RT + rt) TT + tt) keeps its dots in D[s & 1] and its scale
+    // products in half h of the pair product P, so nothing is copied
+    // between steps; every index is a constant of the unrolled stage (a
+    // stage holds an even number of tiles, so the tile pending at a full
+    // stage's end is always D[1], half 1).
+    v16i D[2] = {};
+    v32f P = {};
     bool pending = false;
-    auto scale_into = [&](v16f &c, const v16f &p, const v16i &d) {
+    auto scale_into = [&](v16f &c, const v32f &pp, int h, const v16i &d) {
 #pragma unroll
-        for (int v = 0; v < 16; v++) c[v] = __builtin_fmaf(p[v], (float)d[v], c[v]);
+        for (int v = 0; v < 16; v++) c[v] = __builtin_fmaf(pp[16 * h + v], (float)d[v], c[v]);
     };
+    static_assert((NBS * RT * TT) % 2 == 0, "an even number of tiles a stage");
     // split z's stages (all of them without a split)
     int k_begin = 0, k_end = K;
     if (a.ksplit > 1) {
@@ -475,33 +475,38 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             }
         };
         static_assert(NBS % 2 == 0, "block pairs stay within a stage");
-        v32f P = {};  // the current pair product (both halves)
+        // the half of its pair product that tile (b, rt, tt) takes
+        auto half_of = [](int b, int rt, int tt) { return TT == 2 ? tt : RT == 2 ? rt : b & 1; };
         frags(0, 0);
 #pragma unroll
         for (int b = 0; b < NBS; b++) {
-            if (b >= nblk) break;
+            if (b >= nblk) {  // a k tail (the last stage only): its last tile is scaled now
+                const int sp = b * RT * TT - 1;
+                scale_into(acc[RT - 1][TT - 1], P, half_of(b - 1, RT - 1, TT - 1), D[sp & 1]);
+                pending = false;
+                break;
+            }
             const int f = b & 1;
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++) {
-                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[f][rt], bf[f][tt], zero, 0, 0, 0);
+                    const int st = (b * RT + rt) * TT + tt;
+                    D[st & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[f][rt], bf[f][tt], zero, 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
                     if (rt == 0 && tt == 0 && b + 1 < NBS && b + 1 < nblk) frags(b + 1, f ^ 1);
                     // the previous tile: (rt, tt - 1), (rt - 1, TT - 1), or the last block's last
-                    if (tt > 0) scale_into(acc[rt][tt - 1], pq, dq);
-                    else if (rt > 0) scale_into(acc[rt - 1][TT - 1], pq, dq);
-                    else if (pending) scale_into(acc[RT - 1][TT - 1], pq, dq);
+                    const int sp = (st + 1) & 1;
+                    if (tt > 0) scale_into(acc[rt][tt - 1], P, half_of(b, rt, tt - 1), D[sp]);
+                    else if (rt > 0) scale_into(acc[rt - 1][TT - 1], P, half_of(b, rt - 1, TT - 1), D[sp]);
+                    else if (pending) scale_into(acc[RT - 1][TT - 1], P, half_of(b - 1, RT - 1, TT - 1), D[sp]);
                     // a pair's product is issued at its first tile, once the
                     // previous pair's last half is used (one pair live at a time)
-                    const int half = TT == 2 ? tt : RT == 2 ? rt : b & 1;
-                    if (half == 0) {
+                    if (half_of(b, rt, tt) == 0) {
                         const float wv = TT == 2 ? wa[f][rt] : wa[f][0];
                         P = __builtin_amdgcn_mfma_f32_32x32x1f32(wv, xb[f], fzero32, 0, 0, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
-                    dq = d;
-                    pq = half ? hi16(P) : lo16(P);
                     pending = true;
                 }
             if constexpr (PREC == KH_Q4K) {
@@ -524,7 +529,7 @@ __global__ __launch_bounds__(THREADS) void gemm_i8_kernel(GemmArgs a) {
             }
         }
     }
-    if (pending) scale_into(acc[RT - 1][TT - 1], pq, dq);
+    if (pending) scale_into(acc[RT - 1][TT - 1], P, 1, D[1]);
     if (a.ksplit > 1) store_partials<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane);
     else store_tiles<RT, TT>(a, acc, n0 + wr0, m0 + wm0, m_end, lane);
 }

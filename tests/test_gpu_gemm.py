@@ -58,7 +58,7 @@ def test_every_tile_shape_matches_the_oracle(ctx, monkeypatch, prec, tile):
     # edge tiles in both directions, k tails, the k-stages split or not
     monkeypatch.setenv("KVAD_GEMM_TILE_M", tile)
     for m, rows, cols in [(33, 130, 96 if prec != "q4k" else 256), (65, 257, 288 if prec != "q4k" else 768),
-                          (100, 200, 1024)]:
+                          (40, 129, 192 if prec != "q4k" else 512), (100, 200, 1024)]:
         w, parts = make(ctx, prec, rows, cols, seed=m + 2 * rows + cols)
         xs = O.normal(m * 5 + rows, m * cols)
         bias = O.normal(rows + 9, rows)
