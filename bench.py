@@ -97,13 +97,22 @@ class Graph:
             fn()
         torch.cuda.synchronize()
 
-    def time(self, reps: int, warmup: int) -> float:
-        """Seconds per replay, HIP events on the graph's stream."""
+    def time(self, reps: int, warmup: int, settle: float = 0.0) -> float:
+        """Seconds per replay, HIP events on the graph's stream.  With settle
+        > 0 the graph is also replayed for that many seconds first: the
+        matrix-core clocks rise over the first second or so of sustained
+        load (a compute-bound GEMM measured 468, 394, 381 us on one box as
+        it warmed), so compute-bound figures are taken once they hold."""
         torch = self.torch
         with torch.cuda.stream(self.stream):
             for _ in range(warmup):
                 self.g.replay()
             torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < settle:
+                for _ in range(4):
+                    self.g.replay()
+                torch.cuda.synchronize()
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record(self.stream)
@@ -569,7 +578,7 @@ def prefill(torch, K, ctx, stream, dev, gen, args):
                     w.matmul_bt_dev(xs.data_ptr(), m, y.data_ptr())
 
             g = Graph(torch, ctx, stream, run)
-            s = g.time(max(3, args.steps // 10), 2) / 4
+            s = g.time(max(5, args.steps // 5), 2, settle=1.0) / 4
             peak = 5000.0 if prec == "q8" else 157.3
             tops = ops / s / 1e12
             res[f"{prec}_{m}x{k}x{n}"] = {"us": round(s * 1e6, 2), "TOPS": round(tops, 2),
@@ -594,7 +603,7 @@ def prefill(torch, K, ctx, stream, dev, gen, args):
                 w.matmul_bt_dev(xs.data_ptr(), m, y.data_ptr())
 
         g = Graph(torch, ctx, stream, run)
-        s = g.time(max(3, args.steps // 10), 2) / 8
+        s = g.time(max(5, args.steps // 5), 2, settle=0.3) / 8
         sweep[str(m)] = {"us": round(s * 1e6, 2), "GMACps": round(m * n * k / s / 1e9, 1),
                          "TOPS": round(2 * m * n * k / s / 1e12, 2),
                          "path": "multi-token GEMV" if m <= 8 else "int8 MFMA GEMM",
@@ -654,7 +663,7 @@ def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8):
         m0.run_dev(hs.data_ptr(), M, ys.data_ptr())
 
     g = Graph(torch, ctx, stream, pre)
-    s = g.time(max(3, args.steps // 10), 2)
+    s = g.time(max(5, args.steps // 5), 2, settle=1.0)
     ops = 2 * M * k * 3 * inter * hidden + 2 * M * 3 * sh * hidden
     res["prefill_512tok"] = {"us": round(s * 1e6, 1), "TOPS": round(ops / s / 1e12, 2), "ops": ops}
     del g
