@@ -129,7 +129,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU; --gpus N > 1 is not supported "
-              "(the sharding design is described in DESIGN.md)", file=sys.stderr)
+              "(value is one GPU's throughput on its share of the path)", file=sys.stderr)
         return 2
 
     import torch
