@@ -1022,7 +1022,15 @@ namespace {
 constexpr int MLA_LAT = 512, MLA_ROPE = 64, MLA_K = MLA_LAT + MLA_ROPE;
 constexpr int MLA_QSTR = MLA_K + 4;  // LDS row stride (floats) of the staged queries
 constexpr int MLA_P = 64;            // positions per workgroup: one tile of 16 per wave
-constexpr int MLA_MERGE_D = 128;     // dims per merge workgroup (four per head)
+// dims per merge workgroup: 128 (four per head) for a few splits, 64 from
+// 64 splits on, where each workgroup's partials are what it waits for
+// (measured at L = 1024 / 8192 / 32768: 18.9 / 24.6 / 44.2 us per layer at
+// 128, 19.0 / 24.3 / 42.8 at 64, 19.4 / 24.8 / 43.0 at 32)
+int mla_merge_dims(int nsplit) {
+    const int forced = env_int("KVAD_MLA_MERGE_D", 0);  // tuning knob: 32, 64 or 128
+    if (forced == 32 || forced == 64 || forced == 128) return forced;
+    return nsplit >= 64 ? 64 : 128;
+}
 
 struct MlaArgs {
     const float *q_lat, *q_pe;  // [n_head][512], [n_head][64]
@@ -1188,6 +1196,7 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
 }
 
 // Merge, one workgroup per head and 128 dims (merge_head): the value row of position t is c_t.
+template <int D>
 __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
     const int h = blockIdx.x;
     const rsrc_t C = rsrc(a.c, (size_t)a.L * a.cstride * 4);
@@ -1195,8 +1204,8 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               C, (unsigned)(((size_t)t * a.cstride + 4 * d4) * 4), 0, 0));
     };
-    merge_head<MLA_LAT, MLA_MERGE_D>(a.pm, a.pl, a.pmin, a.pacc, a.psc, a.nsplit, a.n_head, h,
-                                     MLA_MERGE_D * blockIdx.y, MLA_P, a.L, vrow, a.out);
+    merge_head<MLA_LAT, D>(a.pm, a.pl, a.pmin, a.pacc, a.psc, a.nsplit, a.n_head, h, D * blockIdx.y, MLA_P, a.L,
+                           vrow, a.out);
 }
 
 }  // namespace
@@ -1229,7 +1238,13 @@ int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, c
     hipLaunchKernelGGL(mla_split_kernel, dim3(a.nsplit, (n_head + 15) / 16), dim3(256), 0, ctx->stream, a);
     KH_HIP(hipGetLastError());
     if (a.nsplit > 1) {
-        hipLaunchKernelGGL(mla_merge_kernel, dim3(n_head, MLA_LAT / MLA_MERGE_D), dim3(256), 0, ctx->stream, a);
+        const int fd = mla_merge_dims(a.nsplit);
+        if (fd == 32)
+            hipLaunchKernelGGL((mla_merge_kernel<32>), dim3(n_head, MLA_LAT / 32), dim3(256), 0, ctx->stream, a);
+        else if (fd == 64)
+            hipLaunchKernelGGL((mla_merge_kernel<64>), dim3(n_head, MLA_LAT / 64), dim3(256), 0, ctx->stream, a);
+        else
+            hipLaunchKernelGGL((mla_merge_kernel<128>), dim3(n_head, MLA_LAT / 128), dim3(256), 0, ctx->stream, a);
         KH_HIP(hipGetLastError());
     }
     return KH_OK;

@@ -88,3 +88,27 @@ def test_skip_across_many_splits(ctx, L):
     got = _run(ctx, ql, qp, c, pe, H, L)
     want = O.mla_attend(H, 512, 64, ql, qp, c, pe, L, SCALE).reshape(H, 512)
     assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("dims", ["32", "64", "128"])
+def test_every_merge_width_matches_the_oracle(ctx, monkeypatch, dims):
+    # the merge cut into 32-, 64- or 128-dim workgroups per head, over many
+    # splits: random rows, and dominant positions with a spread across the
+    # 1e-8 line (as test_skip_across_many_splits builds them)
+    monkeypatch.setenv("KVAD_MLA_MERGE_D", dims)
+    H, L = 16, 4500
+    ql, qp, c, pe = _case(H * 31 + L, H, L)
+    got = _run(ctx, ql, qp, c, pe, H, L)
+    want = O.mla_attend(H, 512, 64, ql, qp, c, pe, L, SCALE).reshape(H, 512)
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), (dims, "random")
+    rng = np.random.default_rng(L + 7)
+    ql = np.zeros((H, 512), np.float32)
+    qp = np.zeros((H, 64), np.float32)
+    qp[:, 0] = np.sqrt(192.0)  # score_t = pe_t[0]
+    c = (rng.standard_normal((L, 512)) * 100.0).astype(np.float32)
+    pe = np.zeros((L, 64), np.float32)
+    pe[:, 0] = rng.uniform(-4.0, 10.0, L)
+    pe[rng.choice(L, 3, replace=False), 0] = 24.0
+    got = _run(ctx, ql, qp, c, pe, H, L)
+    want = O.mla_attend(H, 512, 64, ql, qp, c, pe, L, SCALE).reshape(H, 512)
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), (dims, "skip")
