@@ -1038,8 +1038,9 @@ struct MlaArgs {
     size_t cstride, pestride;
     int n_head, L, nsplit;
     float scale;
-    float *pm, *pl, *pmin, *pacc, *psc;  // per split: [nsplit][n_head]; acc [..][512]; scores [..][64]
+    float *pm, *pl, *pmin, *pacc, *psc;  // per split: [nsplit][n_head]; acc [..][512]; scores [..][P]
     float *out;                    // [n_head][512]
+    int P;                         // positions per split: 16 per wave
 };
 
 // Split kernel.  Wave w scores positions t0 + 16w .. +15 for the 16 heads:
@@ -1051,18 +1052,22 @@ struct MlaArgs {
 // The workgroup takes one maximum per head, so every wave's exponentials
 // share it; the probabilities go to LDS and wave w then forms
 // O[heads][dims 128w .. 128w + 127] = P V over all 64 positions.
-__global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void mla_split_kernel(MlaArgs a) {
+    constexpr int P = 16 * NW;       // positions: one tile of 16 per wave
+    constexpr int DW = MLA_LAT / NW;  // value dims each wave forms
+    constexpr int VG = DW / 64;       // 64-dim groups of them
     const int split = blockIdx.x, h0 = blockIdx.y * 16;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j16 = lane & 15, c4 = lane >> 4;
     const int L = a.L;
-    const int t0 = split * MLA_P, n = min(L - t0, MLA_P);
+    const int t0 = split * P, n = min(L - t0, P);
     const bool whole = a.nsplit == 1;
     const int H = min(a.n_head - h0, 16);
     __shared__ __align__(16) float sQ[16 * MLA_QSTR];
-    __shared__ float sP[16][MLA_P + 4];
-    __shared__ float s_st[3][4][16];
+    __shared__ float sP[16][P + 4];
+    __shared__ float s_st[3][NW][16];
     const rsrc_t C = rsrc(a.c, (size_t)L * a.cstride * 4), PE = rsrc(a.pe, (size_t)L * a.pestride * 4);
 
     // the tile's key rows (the long-latency loads) first
@@ -1083,7 +1088,7 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
             kq[8][i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(PE, poff, 64 * i, 0));
     }
     // the queries [q_lat | q_pe] of the group's heads, zero rows past H
-    for (int i = tid; i < 16 * (MLA_K / 4); i += 256) {
+    for (int i = tid; i < 16 * (MLA_K / 4); i += 64 * NW) {
         const int h = i / (MLA_K / 4), d4 = i % (MLA_K / 4);
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (h < H)
@@ -1120,7 +1125,19 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
         s_st[2][wave][j16] = mn;
     }
     __syncthreads();
-    const float M = fmaxf(fmaxf(s_st[0][0][j16], s_st[0][1][j16]), fmaxf(s_st[0][2][j16], s_st[0][3][j16]));
+    auto wmax = [&](int st, int h) {
+        float x = s_st[st][0][h];
+#pragma unroll
+        for (int w = 1; w < NW; w++) x = fmaxf(x, s_st[st][w][h]);
+        return x;
+    };
+    auto wsum = [&](int h) {  // in wave order
+        float x = s_st[1][0][h];
+#pragma unroll
+        for (int w = 1; w < NW; w++) x = x + s_st[1][w][h];
+        return x;
+    };
+    const float M = wmax(0, j16);
     float e[4], l = 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -1130,7 +1147,7 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
     l = rows_sum(l);
     if (c4 == 0) s_st[1][wave][j16] = l;
     __syncthreads();
-    const float S = ((s_st[1][0][j16] + s_st[1][1][j16]) + s_st[1][2][j16]) + s_st[1][3][j16];
+    const float S = wsum(j16);
     if (whole) {
         // the reference's own weights: w = exp(s - M) * (1/S), dropping w < 1e-8
         // (softmax_inplace, tensor.rs:297-308; deepseek.rs:576-579)
@@ -1145,28 +1162,29 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
     for (int r = 0; r < 4; r++) sP[j16][16 * wave + 4 * c4 + r] = e[r];
     __syncthreads();
 
-    // values: wave w forms dims 128 w .. 128 w + 127 for every position of the split
-    const int D0 = 128 * wave;
-    f4v vv[4][4][2];
+    // values: wave w forms dims DW w .. DW w + DW - 1 for every position of the split
+    const int D0 = DW * wave;
+    f4v vv[NW][4][VG];
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < NW; u++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const size_t p = (size_t)(t0 + 16 * u + 4 * c4 + r);
             const unsigned off = (unsigned)((p * a.cstride + D0 + 4 * j16) * 4);
-            vv[u][r][0] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 0, 0));
-            vv[u][r][1] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 256, 0));
+#pragma unroll
+            for (int v = 0; v < VG; v++)
+                vv[u][r][v] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 256 * v, 0));
         }
-    f4v acc[8];
+    f4v acc[4 * VG];
 #pragma unroll
-    for (int q = 0; q < 8; q++) acc[q] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < 4 * VG; q++) acc[q] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < NW; u++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const float pa = sP[j16][16 * u + 4 * c4 + r];  // head j16, position 4 c4 + r of tile u
 #pragma unroll
-            for (int v = 0; v < 2; v++)
+            for (int v = 0; v < VG; v++)
 #pragma unroll
                 for (int q = 0; q < 4; q++)
                     acc[4 * v + q] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vv[u][r][v][q], acc[4 * v + q], 0, 0, 0);
@@ -1179,19 +1197,22 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
         float *dst = whole ? a.out + (size_t)(h0 + h) * MLA_LAT
                            : a.pacc + ((size_t)split * a.n_head + h0 + h) * MLA_LAT;
 #pragma unroll
-        for (int v = 0; v < 2; v++)
+        for (int v = 0; v < VG; v++)
             *reinterpret_cast<float4 *>(dst + D0 + 64 * v + 4 * j16) =
                 make_float4(acc[4 * v][i], acc[4 * v + 1][i], acc[4 * v + 2][i], acc[4 * v + 3][i]);
     }
     if (!whole && tid < H) {
         const int h = tid;
         const size_t o = (size_t)split * a.n_head + h0 + h;
-        a.pm[o] = fmaxf(fmaxf(s_st[0][0][h], s_st[0][1][h]), fmaxf(s_st[0][2][h], s_st[0][3][h]));
-        a.pl[o] = ((s_st[1][0][h] + s_st[1][1][h]) + s_st[1][2][h]) + s_st[1][3][h];
-        a.pmin[o] = fminf(fminf(s_st[2][0][h], s_st[2][1][h]), fminf(s_st[2][2][h], s_st[2][3][h]));
+        a.pm[o] = wmax(0, h);
+        a.pl[o] = wsum(h);
+        float mnv = s_st[2][0][h];
+#pragma unroll
+        for (int w = 1; w < NW; w++) mnv = fminf(mnv, s_st[2][w][h]);
+        a.pmin[o] = mnv;
     }
     if (!whole && j16 < H)  // the scores, for the merge's decision on the 1e-8 skip (stored last)
-        *reinterpret_cast<float4 *>(a.psc + ((size_t)split * a.n_head + h0 + j16) * MLA_P + 16 * wave + 4 * c4) =
+        *reinterpret_cast<float4 *>(a.psc + ((size_t)split * a.n_head + h0 + j16) * P + 16 * wave + 4 * c4) =
             make_float4(s[0], s[1], s[2], s[3]);
 }
 
@@ -1204,7 +1225,7 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               C, (unsigned)(((size_t)t * a.cstride + 4 * d4) * 4), 0, 0));
     };
-    merge_head<MLA_LAT, D>(a.pm, a.pl, a.pmin, a.pacc, a.psc, a.nsplit, a.n_head, h, D * blockIdx.y, MLA_P, a.L,
+    merge_head<MLA_LAT, D>(a.pm, a.pl, a.pmin, a.pacc, a.psc, a.nsplit, a.n_head, h, D * blockIdx.y, a.P, a.L,
                            vrow, a.out);
 }
 
@@ -1226,16 +1247,26 @@ int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, c
     a.q_lat = q_lat, a.q_pe = q_pe, a.c = c, a.pe = pe, a.cstride = cstride, a.pestride = pestride;
     a.n_head = n_head;
     a.L = (int)n_positions;
-    a.nsplit = (int)((n_positions + MLA_P - 1) / MLA_P);
+    // positions per split: 128 (eight waves) while that still gives a
+    // workgroup per CU -- half the partials to write and merge -- else 64
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int hg = (n_head + 15) / 16;
+    const int forced = env_int("KVAD_MLA_SPLIT", 0);  // tuning knob: positions per split (64 / 128)
+    a.P = forced == 64 || forced == 128 ? forced
+          : (long long)((n_positions + 127) / 128) * hg >= cu ? 128 : MLA_P;
+    a.nsplit = (int)((n_positions + a.P - 1) / a.P);
     if (a.nsplit > MAX_SPLITS) return fail(KH_DECLINED, "mla_attend: sequence longer than the split merge takes");
     a.scale = scale;
     a.out = out;
     if (a.nsplit > 1) {
-        int rc = ensure(ctx, ctx->ws, 4 * partial_floats(a.nsplit, n_head, MLA_LAT, MLA_P) + 1024);
+        int rc = ensure(ctx, ctx->ws, 4 * partial_floats(a.nsplit, n_head, MLA_LAT, a.P) + 1024);
         if (rc) return rc;
         carve_partials(a, ctx->ws.ptr, MLA_LAT);
     }
-    hipLaunchKernelGGL(mla_split_kernel, dim3(a.nsplit, (n_head + 15) / 16), dim3(256), 0, ctx->stream, a);
+    if (a.P == 128)
+        hipLaunchKernelGGL((mla_split_kernel<8>), dim3(a.nsplit, hg), dim3(512), 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL((mla_split_kernel<4>), dim3(a.nsplit, hg), dim3(256), 0, ctx->stream, a);
     KH_HIP(hipGetLastError());
     if (a.nsplit > 1) {
         const int fd = mla_merge_dims(a.nsplit);

@@ -112,3 +112,25 @@ def test_every_merge_width_matches_the_oracle(ctx, monkeypatch, dims):
     got = _run(ctx, ql, qp, c, pe, H, L)
     want = O.mla_attend(H, 512, 64, ql, qp, c, pe, L, SCALE).reshape(H, 512)
     assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), (dims, "skip")
+
+
+@pytest.mark.parametrize("L", [1, 100, 129, 3000])
+def test_128_position_splits_match_the_oracle(ctx, monkeypatch, L):
+    # eight-wave splits of 128 positions (taken on their own past 32768
+    # positions): one split, a ragged last split, and the 1e-8 skip across
+    # many splits
+    monkeypatch.setenv("KVAD_MLA_SPLIT", "128")
+    H = 16
+    ql, qp, c, pe = _case(H * 13 + L, H, L)
+    if L == 3000:
+        rng = np.random.default_rng(L + 11)
+        ql = np.zeros((H, 512), np.float32)
+        qp = np.zeros((H, 64), np.float32)
+        qp[:, 0] = np.sqrt(192.0)  # score_t = pe_t[0]
+        c = (rng.standard_normal((L, 512)) * 100.0).astype(np.float32)
+        pe = np.zeros((L, 64), np.float32)
+        pe[:, 0] = rng.uniform(-4.0, 10.0, L)
+        pe[rng.choice(L, 3, replace=False), 0] = 24.0
+    got = _run(ctx, ql, qp, c, pe, H, L)
+    want = O.mla_attend(H, 512, 64, ql, qp, c, pe, L, SCALE).reshape(H, 512)
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), L
