@@ -1248,12 +1248,17 @@ int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, c
     a.n_head = n_head;
     a.L = (int)n_positions;
     // positions per split: 128 (eight waves) while that still gives a
-    // workgroup per CU -- half the partials to write and merge -- else 64
+    // workgroup per CU -- half the partials to write and merge; 32 (two
+    // waves) for short sequences past one split, twice the workgroups
+    // (measured at L = 1024 / 8192 / 32768: 18.9 / 24.4 / 40.8 us per layer
+    // by this rule, 17.7 / 27.2 / 51.0 with 32 everywhere); else 64
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int hg = (n_head + 15) / 16;
-    const int forced = env_int("KVAD_MLA_SPLIT", 0);  // tuning knob: positions per split (64 / 128)
-    a.P = forced == 64 || forced == 128 ? forced
-          : (long long)((n_positions + 127) / 128) * hg >= cu ? 128 : MLA_P;
+    const int forced = env_int("KVAD_MLA_SPLIT", 0);  // tuning knob: positions per split (32 / 64 / 128)
+    a.P = forced == 32 || forced == 64 || forced == 128 ? forced
+          : (long long)((n_positions + 127) / 128) * hg >= cu ? 128
+          : n_positions > (size_t)MLA_P && n_positions <= 1024 ? 32
+                                                               : MLA_P;
     a.nsplit = (int)((n_positions + a.P - 1) / a.P);
     if (a.nsplit > MAX_SPLITS) return fail(KH_DECLINED, "mla_attend: sequence longer than the split merge takes");
     a.scale = scale;
@@ -1265,6 +1270,8 @@ int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, c
     }
     if (a.P == 128)
         hipLaunchKernelGGL((mla_split_kernel<8>), dim3(a.nsplit, hg), dim3(512), 0, ctx->stream, a);
+    else if (a.P == 32)
+        hipLaunchKernelGGL((mla_split_kernel<2>), dim3(a.nsplit, hg), dim3(128), 0, ctx->stream, a);
     else
         hipLaunchKernelGGL((mla_split_kernel<4>), dim3(a.nsplit, hg), dim3(256), 0, ctx->stream, a);
     KH_HIP(hipGetLastError());
