@@ -748,7 +748,9 @@ template <int HD, bool ROPE>
 void launch_split_r(const AttnArgs &a, dim3 grid, hipStream_t stream) {
     const int r = a.P / (16 * a.nw);
     const dim3 block(64 * a.nw);
-    if (a.nw == 8) {
+    if (a.nw == 2) {
+        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 2, ROPE>), grid, block, 0, stream, a);
+    } else if (a.nw == 8) {
         if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1, 8, ROPE>), grid, block, 0, stream, a);
         else hipLaunchKernelGGL((attn_split_kernel<64, 2, 8, ROPE>), grid, block, 0, stream, a);
     } else if (r == 1) {
@@ -779,6 +781,9 @@ size_t single_max(int head_dim) {
     const int v = env_int("KVAD_ATTN_SINGLE", -1);
     return v < 0 ? hw : std::min(hw, (size_t)v);
 }
+
+// The longest single sequence split into 32-position splits.
+size_t short_split_max(int head_dim) { return head_dim == 64 ? 1024 : 512; }
 
 // Query heads per workgroup: the largest divisor of the group size that
 // fits the 16 columns of the score product.
@@ -831,9 +836,18 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     const int ladder[3] = {64, 128, 256};
     int step = rungs - 1;
     while (step > 0 && (long long)((n_positions + ladder[step] - 1) / ladder[step]) * n_hg * nb < cu) step--;
-    const int forced = env_int("KVAD_ATTN_SPLIT", 0);  // tuning knob: positions per split
+    const int forced = env_int("KVAD_ATTN_SPLIT", 0);  // tuning knob: positions per split (32 .. 256)
     for (int i = 0; i < rungs; i++)
         if (ladder[i] == forced) step = i;
+    // short sequences past one split: 32 positions on two waves, twice the
+    // workgroups (measured: Qwen geometry L = 1024 9.78 -> 9.52 us per layer,
+    // Llama-8B L = 512 11.93 -> 11.54; from 2048 positions they lose)
+    if (forced == 32 || (forced == 0 && nb == 1 && n_positions <= short_split_max(head_dim))) {
+        a.P = 32;
+        a.nw = 2;
+        a.nsplit = (int)((n_positions + 31) / 32);
+        return KH_OK;
+    }
     while (step < rungs - 1 && (n_positions + ladder[step] - 1) / ladder[step] > (size_t)MAX_SPLITS) step++;
     const int P = ladder[step];
     if ((n_positions + P - 1) / P > (size_t)MAX_SPLITS)
@@ -886,15 +900,22 @@ size_t attend_single_max(int head_dim) { return head_dim == 64 || head_dim == 12
 
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions) {
     (void)n_kv_head;
-    // the smallest split size (64) bounds the count; scores take P per split
+    // splits of 64 or more, or of 32 up to short_split_max: the smallest
+    // bounds the count; scores take P per split
     const size_t nsplit = (max_positions + 63) / 64;
-    return 4 * partial_floats(nsplit, n_head, head_dim, 64) + 4 * (max_positions + 256) * (size_t)n_head + 1024;
+    size_t f = partial_floats(nsplit, n_head, head_dim, 64);
+    const size_t n32 = (std::min(max_positions, short_split_max(head_dim)) + 31) / 32;
+    f = std::max(f, partial_floats(n32, n_head, head_dim, 32));
+    return 4 * f + 4 * (max_positions + 256) * (size_t)n_head + 1024;
 }
 
 size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size_t nb) {
     // per row as attend_ws_bytes: any split size the launch picks fits
     const size_t nsplit = (max_positions + 63) / 64;
-    return 4 * nb * (partial_floats(nsplit, n_head, head_dim, 64) + (max_positions + 256) * (size_t)n_head) + 1024;
+    size_t f = partial_floats(nsplit, n_head, head_dim, 64);
+    const size_t n32 = (std::min(max_positions, short_split_max(head_dim)) + 31) / 32;
+    f = std::max(f, partial_floats(n32, n_head, head_dim, 32));
+    return 4 * nb * (f + (max_positions + 256) * (size_t)n_head) + 1024;
 }
 
 int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,

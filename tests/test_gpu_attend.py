@@ -174,14 +174,15 @@ def test_one_split_and_split_merge_agree(ctx, monkeypatch, spec, L):
 
 
 @pytest.mark.parametrize("n_head,n_kv,L,mode", [(4, 1, 3000, SPLIT), (4, 1, 20000, SPLIT), (14, 2, 32768, SPLIT),
-                                                (4, 1, 256, SPLIT), (4, 1, 256, SINGLE), (14, 2, 250, SINGLE),
-                                                (16, 1, 200, SINGLE)])
+                                                (14, 2, 1000, SPLIT), (4, 1, 256, SPLIT), (4, 1, 256, SINGLE),
+                                                (14, 2, 250, SINGLE), (16, 1, 200, SINGLE)])
 def test_attend_skip_across_many_splits(ctx, monkeypatch, n_head, n_kv, L, mode):
     # A few dominant positions; the rest spread across the 1e-8 line, so some
     # splits are left out whole, some kept whole and most straddle it.  Values
     # are large, so a skipped term wrongly kept (or a kept one dropped) shows.
-    # Qwen's geometry at 32768 positions runs the 256-position splits; a
-    # single split drops the same weights itself.
+    # Qwen's geometry at 32768 positions runs the 256-position splits, at
+    # 1000 the two-wave 32-position ones; a single split drops the same
+    # weights itself.
     attn_mode(monkeypatch, mode)
     say("attend skip, many splits", n_head, n_kv, L, mode)
     spec = K.Spec(n_head, n_kv, 64)
