@@ -74,8 +74,8 @@ def test_activation_quantiser_is_bit_exact(ctx, n):
 
 
 SHAPES = {
-    "q8": [(1, 32), (37, 64), (203, 96), (4864, 896), (896, 4864)],
-    "q4": [(1, 32), (37, 64), (203, 96), (4864, 896), (896, 4864)],
+    "q8": [(1, 32), (37, 64), (203, 96), (4864, 896), (896, 4864), (2048, 1408), (1408, 2816)],
+    "q4": [(1, 32), (37, 64), (203, 96), (4864, 896), (896, 4864), (2048, 1408), (1408, 2816)],
     "q4k": [(1, 256), (37, 512), (64, 1024), (4096, 4096)],
     "f32": [(1, 3), (3, 2), (37, 64), (203, 97), (896, 896)],
 }
