@@ -714,9 +714,10 @@ def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256
     res = {"tok_per_s": round(tps, 1), "ms_per_token": round(s / timed * 1e3, 4), "context": [warm, warm + timed],
            # per layer q/k/v, attention, o, gate+up, down; past 256 positions
            # the attention is split and merged (one launch more per layer);
-           # plus the head (each wave keeping its greedy choice) and the argmax,
-           # which also writes the next token's embedding row
-           "launches_per_token": {"positions <= 256": 24 * 5 + 2, "positions > 256": 24 * 6 + 2},
+           # plus the head, whose workgroups keep their greedy choices and
+           # whose last to finish takes the best, advances the step and writes
+           # the next token's embedding row
+           "launches_per_token": {"positions <= 256": 24 * 5 + 1, "positions > 256": 24 * 6 + 1},
            "vs_reference_cpu_q8_112tps": round(tps / 112.0, 2),
            "vs_reference_metal_q8_191tps": round(tps / 191.0, 2), "first_tokens": [int(t) for t in first[:4]]}
     log(f"qwen0.5b q8 decode: {res}")

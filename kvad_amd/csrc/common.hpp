@@ -122,6 +122,7 @@ struct kh_llm {
     float *arg_v = nullptr;                                  // argmax partials
     int *arg_i = nullptr;
     int *arg_n = nullptr;                                    // how many the head GEMV wrote
+    unsigned *arrivals = nullptr;                            // head workgroups done this step (zero between steps)
     int out_cap = 0;
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -216,11 +217,27 @@ struct RouteArgs;
 // its one workgroup computes the token's logits and routes them (r.logits
 // unused); KH_DECLINED where no such kernel is built for the launch's shape.
 int launch_gemv_route(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs, int route_job, const RouteArgs &r);
+// A decode step's end folded into the head GEMV: the last of its workgroups
+// to finish takes the best of their choices against row 0 (the first of
+// equal maxima wins; sampler.rs:217-226), makes it the next token, advances
+// the position, records the step (out[step] while step < out_cap) and
+// writes the token's embedding row to x.
+struct GreedyTail {
+    unsigned *arrivals;  // device: head workgroups done this step (zero between steps)
+    int32_t *token, *pos, *step, *out;
+    int out_cap;
+    int prec;  // the embedding's
+    const void *qs;
+    const float *scales;
+    size_t cols;
+    float *x;
+};
 // One GEMV whose workgroups also keep the greedy choice over their rows
-// r >= 1 (workgroup g: arg_v[g], arg_i[g]; their count to *arg_n);
-// KH_DECLINED for f32 weights or more than `cap` workgroups.
+// r >= 1 (workgroup g: arg_v[g], arg_i[g]; their count to *arg_n), and with
+// `tail` set end the step as GreedyTail says; KH_DECLINED for f32 weights or
+// more than `cap` workgroups.
 int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *arg_v, int *arg_i, int *arg_n,
-                       int cap);
+                       int cap, const GreedyTail *tail = nullptr);
 
 // y[m, rows] = x W^T (+bias) for a few quantised token rows (m small): the
 // weights stream once for all of them.  x holds the rows' codes.

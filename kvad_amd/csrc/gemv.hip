@@ -136,6 +136,62 @@ __global__ __launch_bounds__(256) void norm_qact_kernel(const float *__restrict_
 // lw, lw + nw, ... of its job, loading the next group's weights before it
 // computes the current one.  The first group's loads are issued before the
 // activation is staged, so they fly while the workgroup quantises.  With
+// The step's end (GreedyTail) in the head GEMV's last workgroup.  Each
+// workgroup's choice and row 0's logit are stored at device scope (past the
+// per-XCD L2) and have completed before the workgroup counts its arrival;
+// the last to arrive reads them back at device scope -- no workgroup waits
+// on another and no cache-wide fence is needed.  The best of the choices
+// (the largest, the lowest index on ties) is the same in any reduction
+// order.
+template <int NWV>
+__device__ void greedy_tail(const JobTable &tab, const GemvJob &job, int groups, float *s_av, int *s_ai) {
+    __shared__ int s_last, s_best;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid >> 6;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(tab.tail.arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)groups - 1;
+    __syncthreads();
+    if (!s_last) return;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int t = tid; t < groups; t += WAVE * NWV) {
+        const float v = __hip_atomic_load(tab.arg_v + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int i = __hip_atomic_load(tab.arg_i + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) bv = v, bi = i;
+    }
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        const float v = __shfl_xor(bv, o);
+        const int i = __shfl_xor(bi, o);
+        if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) bv = v, bi = i;
+    }
+    if (lane == 0) s_av[wv] = bv, s_ai[wv] = bi;  // tid 0 read the entries before the last barrier
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < NWV; w++) {
+            const float v = s_av[w];
+            const int i = s_ai[w];
+            if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) bv = v, bi = i;
+        }
+        const GreedyTail &e = tab.tail;
+        // row 0 against the best of rows 1..: the first of equal maxima wins
+        const float first = __hip_atomic_load(job.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int best = job.rows > 1 && first == first && bi >= 0 && bv > first ? bi : 0;
+        s_best = best;
+        *e.token = best;
+        *e.pos = *e.pos + 1;
+        const int k = *e.step;
+        if (e.out && k < e.out_cap) e.out[k] = best;
+        *e.step = k + 1;
+        __hip_atomic_store(e.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const GreedyTail &e = tab.tail;
+    const size_t r = (size_t)s_best;
+    for (size_t k = tid; k < e.cols; k += WAVE * NWV) e.x[k] = dequant_elem(e.prec, e.qs, e.scales, e.cols, r, k);
+}
+
 // ROUTE, the router job (one workgroup, every router row) also keeps its
 // outputs in LDS and its first wave routes them (MoE decode).
 template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB, bool ROUTE = false>
@@ -241,7 +297,8 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
                 if (lane == 0 && r < rows) {
                     float out = job.bias ? v + b : v;
                     if (job.accumulate) out = y0 + out;  // x += proj (llama.rs:273-276)
-                    if (routes && tab.route.arrivals)  // read back by another workgroup: past the L2
+                    // read back by another workgroup: past the L2
+                    if ((routes && tab.route.arrivals) || (argm && r == 0 && tab.tail.arrivals))
                         __hip_atomic_store(job.y + r, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     else
                         job.y[r] = out;
@@ -277,10 +334,16 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
                 if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) bv = v, bi = i;
             }
             const int g = blk - job.wave0;
-            tab.arg_v[g] = bv;
-            tab.arg_i[g] = bi;
+            if (tab.tail.arrivals) {  // read back by the last workgroup: past the L2
+                __hip_atomic_store(tab.arg_v + g, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(tab.arg_i + g, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                tab.arg_v[g] = bv;
+                tab.arg_i[g] = bi;
+            }
             if (g == 0) *tab.arg_n = nw / NWV;
         }
+        if (tab.tail.arrivals) greedy_tail<NWV>(tab, job, nw / NWV, s_av, s_ai);
     }
     if constexpr (ROUTE) {
         if (routes && tab.route.arrivals) {
@@ -929,7 +992,7 @@ int launch_gemv_route(kh_ctx *ctx, int precision, const GemvJob *jobs, int njobs
 }
 
 int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *arg_v, int *arg_i, int *arg_n,
-                       int cap) {
+                       int cap, const GreedyTail *tail) {
     if (precision == KH_F32 || job.dots) return fail(KH_DECLINED, "matvec: the greedy epilogue is built for quantised weights");
     JobTable tab{};
     tab.n = 1;
@@ -939,6 +1002,7 @@ int launch_gemv_argmax(kh_ctx *ctx, int precision, const GemvJob &job, float *ar
     tab.arg_v = arg_v;
     tab.arg_i = arg_i;
     tab.arg_n = arg_n;
+    if (tail) tab.tail = *tail;
     const int maxC = chunks_per_row(precision, job.cols), kind = input_kind(job);
     switch (precision) {
         case KH_Q8: return launch_prec<KH_Q8>(ctx, tab, maxC, job.cols, job.rows, false, kind);

@@ -30,6 +30,7 @@ struct JobTable {
     int arg_job, arg_cap;
     float *arg_v;
     int *arg_i, *arg_n;
+    GreedyTail tail;  // tail.arrivals set: the step ends in this launch
 };
 
 // Chunks of 16 bytes per weight row.

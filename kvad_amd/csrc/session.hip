@@ -99,8 +99,9 @@ struct NextEmbed {
     float *x;
 };
 
-// The partials' count is *pn (the head GEMV's workgroups) or, without pn,
-// ARGMAX_BLOCKS (argmax_partial_kernel).  The chosen token becomes the next
+// The step's end as a launch of its own (f32 heads, KVAD_HEAD_TAIL=0; the
+// head GEMV's greedy_tail otherwise).  The partials' count is *pn (the head
+// GEMV's workgroups) or, without pn, ARGMAX_BLOCKS (argmax_partial_kernel).  The chosen token becomes the next
 // input, the position advances, the step is recorded, and the token's
 // embedding row is written to e.x, so a captured step needs no launch of its
 // own for it.
@@ -301,10 +302,18 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr, bool embed = 
     // the greedy choice (sampler.rs:217-226): each workgroup of the head GEMV
     // keeps its best row, one workgroup then takes the best of them; f32
     // heads, or launches of more workgroups than partials, run a partial pass
+    // and a launch of one workgroup
     bool kept = false;
     if (head->precision != KH_F32) {
-        rc = launch_gemv_argmax(ctx, head->precision, jobs[0].second, m->arg_v, m->arg_i, m->arg_n, ARGMAX_CAP);
+        // the step ends in the head's last workgroup to finish, with no
+        // launch of its own (KVAD_HEAD_TAIL=0: a one-block launch after it)
+        const bool fold = env_int("KVAD_HEAD_TAIL", 1) != 0;
+        const GreedyTail tail{m->arrivals, m->token, m->pos, m->steps, m->out, m->out_cap, m->embed->precision,
+                              m->embed->qs, m->embed->scales, m->embed->cols, m->x};
+        rc = launch_gemv_argmax(ctx, head->precision, jobs[0].second, m->arg_v, m->arg_i, m->arg_n, ARGMAX_CAP,
+                                fold ? &tail : nullptr);
         if (rc != KH_OK && rc != KH_DECLINED) return rc;
+        if (rc == KH_OK && fold) return KH_OK;
         kept = rc == KH_OK;
     }
     if (!kept) {
@@ -649,10 +658,11 @@ int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out) {
         (rc = dev_alloc(&m->hq.qs, hq_n)) || (rc = dev_alloc(&m->hq.scales, hq_n / BLOCK)) ||
         (rc = dev_alloc(&m->hq.sums, hq_n / BLOCK)) || (rc = dev_alloc(&m->state, 3)) ||
         (rc = dev_alloc(&m->arg_v, ARGMAX_CAP)) || (rc = dev_alloc(&m->arg_i, ARGMAX_CAP)) ||
-        (rc = dev_alloc(&m->arg_n, 1)))
+        (rc = dev_alloc(&m->arg_n, 1)) || (rc = dev_alloc(&m->arrivals, 1)))
         return rc;
     m->token = m->state, m->pos = m->state + 1, m->steps = m->state + 2;
     KH_HIP(hipMemset(m->state, 0, 3 * sizeof(int32_t)));
+    KH_HIP(hipMemset(m->arrivals, 0, sizeof(unsigned)));
     m->attn_ws_bytes = attend_ws_bytes((int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, s.n_ctx);
     m->attn_short = std::min(attend_single_max((int)s.head_dim), s.n_ctx);
     m->attn_max = s.n_ctx;
@@ -683,7 +693,7 @@ int kh_llm_free(kh_llm *m) {
         for (void *p : {(void *)m->x, (void *)m->h, (void *)m->qkv, (void *)m->att, (void *)m->g, (void *)m->u,
                         (void *)m->logits, (void *)m->hq.qs, (void *)m->hq.scales, (void *)m->hq.sums,
                         (void *)m->state, (void *)m->final_norm, (void *)m->rope_cos, (void *)m->rope_sin,
-                        m->attn_ws, (void *)m->out, (void *)m->arg_v, (void *)m->arg_i, (void *)m->arg_n})
+                        m->attn_ws, (void *)m->out, (void *)m->arg_v, (void *)m->arg_i, (void *)m->arg_n, (void *)m->arrivals})
             if (p) (void)hipFree(p);
     }
     delete m;
