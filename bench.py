@@ -395,6 +395,37 @@ def mla(torch, K, ctx, stream, dev, gen, args):
     return res
 
 
+def write_q8_cache(path, n_mats, rows, cols, sc, qs):
+    """A cache file of n_mats copies of one q8 matrix, written a array at a
+    time: the container of crates/llm/src/qcache.rs:932-1040 (magic, 56
+    reserved bytes, each array on a 64-byte boundary named by an
+    [offset, count] span, the JSON header after the last array, its offset as
+    a little-endian u64 at the end), with the CPU engine's q8 entries
+    (qcache.rs:986-1005)."""
+    import json
+    import struct
+
+    tensors = {}
+    with open(path, "wb") as f:
+        f.write(b"NANOQ\x00\x00\x01" + bytes(56))
+        at = 64
+
+        def put(a):
+            nonlocal at
+            pad = (64 - at % 64) % 64
+            f.write(bytes(pad))
+            at += pad
+            span = [at, int(a.size)]
+            f.write(a.tobytes())
+            at += a.nbytes
+            return span
+
+        for i in range(n_mats):
+            tensors[f"m{i}"] = {"kind": "q8", "shape": [rows, cols], "scales": put(sc), "qs": put(qs)}
+        header = {"version": 2, "precision": "q8", "repo": "bench/synthetic", "tensors": tensors}
+        f.write(json.dumps(header).encode() + struct.pack("<Q", at))
+
+
 def qcache_upload(K, ctx, n_mats=16, rows=14336, cols=4096):
     """The load path of crates/llm/src/qcache.rs onto the device: a cache file
     of n_mats q8 matrices (Llama-3-8B gate shape, 0.99 GB) written once, then
@@ -403,20 +434,13 @@ def qcache_upload(K, ctx, n_mats=16, rows=14336, cols=4096):
     uploaded from ordinary host memory by kh_weight_q8."""
     import tempfile
 
-    sys.path.insert(0, str(ROOT / "tests"))
-    from nanoq import Writer
-
     rng = np.random.default_rng(0)
     qs = rng.integers(-127, 128, rows * cols, dtype=np.int8)
     sc = rng.random(rows * cols // 32, dtype=np.float32) * 1e-3
     nbytes = n_mats * (qs.nbytes + sc.nbytes)
     with tempfile.TemporaryDirectory() as d:
         path = Path(d) / "bench.nanoq"
-        w = Writer(path)
-        for i in range(n_mats):
-            w.q8(f"m{i}", rows, cols, sc, qs)
-        w.finish()
-        del w
+        write_q8_cache(path, n_mats, rows, cols, sc, qs)
         qc = K.QCache(path)
         for i in range(2):  # warm: page cache and allocator
             qc.weight(ctx, f"m{i}")

@@ -179,9 +179,14 @@ int kh_init(int device, kh_ctx **out) {
     KH_HIP(hipDeviceGetAttribute(&ctx->cu_count, hipDeviceAttributeMultiprocessorCount, device));
     KH_HIP(hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking));
     ctx->stream = ctx->own;
-    int rc = scratch_init(device);  // once per device: the no-allocation entry points' array
-    if (rc) return rc;
-    KH_HIP(hipDeviceSynchronize());
+    // once per device: the no-allocation entry points' array.  Not fatal:
+    // without it only kh_attend_dev_noalloc refuses (KH_EINVAL).
+    (void)scratch_init(device);
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->own);
+        return hip_fail(e, "hipDeviceSynchronize");
+    }
     *out = ctx.release();
     return KH_OK;
 }

@@ -842,7 +842,9 @@ int setup(kh_ctx *ctx, AttnArgs &a, int n_head, int n_kv_head, int head_dim, con
     // short sequences past one split: 32 positions on two waves, twice the
     // workgroups (measured: Qwen geometry L = 1024 9.78 -> 9.52 us per layer,
     // Llama-8B L = 512 11.93 -> 11.54; from 2048 positions they lose)
-    if (forced == 32 || (forced == 0 && nb == 1 && n_positions <= short_split_max(head_dim))) {
+    // (the workspaces size 32-position splits only up to short_split_max, so
+    // the knob is honoured only there)
+    if (n_positions <= short_split_max(head_dim) && (forced == 32 || (forced == 0 && nb == 1))) {
         a.P = 32;
         a.nw = 2;
         a.nsplit = (int)((n_positions + 31) / 32);
@@ -1014,11 +1016,13 @@ int launch_attend_noalloc(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, 
 
 int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
                          const float *v, size_t kstride, size_t vstride, const int32_t *len_dev, int plus_one,
-                         size_t max_positions, float *out, void *ws, const AttnRope *rope) {
+                         size_t max_positions, float *out, void *ws, size_t ws_bytes, const AttnRope *rope) {
     if (max_positions == 0) return fail(KH_EINVAL, "attend: no positions");
     AttnArgs a;
     int rc = setup(ctx, a, n_head, n_kv_head, head_dim, q, k, v, kstride, vstride, max_positions, out);
     if (rc) return rc;
+    if (4 * partial_floats(a.nsplit, n_head, head_dim, a.P) > ws_bytes)
+        return fail(KH_EINVAL, "attend: workspace too small for the launch");
     a.len_dev = len_dev;
     a.plus_one = plus_one;
     if (rope) {  // the caches are written at the new position
@@ -1251,10 +1255,6 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
 }
 
 }  // namespace
-
-size_t mla_ws_bytes(int n_head, size_t max_positions) {
-    return 4 * partial_floats((max_positions + MLA_P - 1) / MLA_P, n_head, MLA_LAT, MLA_P) + 1024;
-}
 
 int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, const float *c, const float *pe,
                size_t cstride, size_t pestride, size_t n_positions, float scale, float *out) {

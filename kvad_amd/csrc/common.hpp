@@ -423,7 +423,8 @@ struct AttnRope {
 // (+1 when plus_one), at most max_positions; partials in `ws` (attend_ws_bytes).
 int launch_attend_devlen(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,
                          const float *v, size_t kv_stride_k, size_t kv_stride_v, const int32_t *len_dev, int plus_one,
-                         size_t max_positions, float *out, void *ws, const AttnRope *rope = nullptr);
+                         size_t max_positions, float *out, void *ws, size_t ws_bytes,
+                         const AttnRope *rope = nullptr);
 size_t attend_ws_bytes(int n_head, int n_kv_head, int head_dim, size_t max_positions);
 // The longest sequence the launches above take as one split (no partials,
 // no merge launch); 0 when none.
@@ -450,6 +451,5 @@ size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size
 // softmax over positions of (q_lat . c_t + q_pe . pe_t) * scale, times c_t.
 int launch_mla(kh_ctx *ctx, int n_head, const float *q_lat, const float *q_pe, const float *c, const float *pe,
                size_t cstride, size_t pestride, size_t n_positions, float scale, float *out);
-size_t mla_ws_bytes(int n_head, size_t max_positions);
 
 }  // namespace kh

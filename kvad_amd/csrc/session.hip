@@ -250,7 +250,7 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr, bool embed = 
         const AttnRope rp{m->qkv + qd, m->qkv + qd + kvd, m->rope_cos, m->rope_sin, L.q_norm, L.k_norm,
                           s.eps, s.rope_interleaved, 0};
         if ((rc = launch_attend_devlen(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, m->qkv, m->kc[l],
-                                       m->vc[l], kvd, kvd, m->pos, 1, m->attn_max, m->att, m->attn_ws, &rp)))
+                                       m->vc[l], kvd, kvd, m->pos, 1, m->attn_max, m->att, m->attn_ws, m->attn_ws_bytes, &rp)))
             return rc;
         jobs.clear();
         jobs.push_back({L.o, gemv_job(L.o, m->att, nullptr, nullptr, m->x, 1)});

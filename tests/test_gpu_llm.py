@@ -31,15 +31,16 @@ LOGIT_RTOL = 2e-3
 
 
 def build(ctx, seed, n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=64, n_ff=256, vocab=512, n_ctx=64,
-          bias=True, qk_norm=False, tied=True, interleaved=False, sd=0.02, prec="q8"):
+          bias=True, qk_norm=False, tied=True, interleaved=False, sd=0.02, prec="q8", head_edit=None):
     spec = dict(n_layer=n_layer, n_embd=n_embd, n_head=n_head, n_kv_head=n_kv_head, head_dim=head_dim, n_ff=n_ff,
                 vocab=vocab, n_ctx=n_ctx, eps=1e-6, rope_interleaved=int(interleaved))
     rng = iter(range(seed, seed + 10000))
     qd, kvd = n_head * head_dim, n_kv_head * head_dim
 
-    def q8(rows, cols, scale=sd, layer=False):
+    def q8(rows, cols, scale=sd, layer=False, edit=None):
         # f32 weights (Precision::F32) when prec == "f32"; Q4_K or q4 layer
-        # weights (the embedding and head stay q8) when prec == "q4k" / "q4"
+        # weights (the embedding and head stay q8) when prec == "q4k" / "q4";
+        # `edit` rewrites a q8 weight's (scales, codes) before upload
         data = O.normal(next(rng), rows * cols, scale)
         if prec == "f32":
             return (data,), K.Weight.from_f32(ctx, data.reshape(rows, cols))
@@ -50,6 +51,8 @@ def build(ctx, seed, n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=64, 
             s4, q4 = O.quantize_q4(data, rows, cols)
             return ("q4", s4, q4), K.Weight.from_q4(ctx, rows, cols, s4, q4)
         s, q = O.quantize_q8(data, rows, cols)
+        if edit is not None:
+            s, q = edit(s.copy(), q.copy())
         return (s, q), K.Weight.from_q8(ctx, rows, cols, s, q)
 
     def vec(n, base=1.0, scale=0.1):
@@ -73,7 +76,7 @@ def build(ctx, seed, n_layer=2, n_embd=128, n_head=4, n_kv_head=2, head_dim=64, 
                     parts.get("k_norm"))
         layers.append(parts)
     embed, emb_h = q8(vocab, n_embd, 0.5)
-    head, head_h = (None, None) if tied else q8(vocab, n_embd, 0.1)
+    head, head_h = (None, None) if tied else q8(vocab, n_embd, 0.1, edit=head_edit)
     final = vec(n_embd)
     m.set_ends(emb_h, final, head_h)
     cos_t, sin_t = O.rope_tables(head_dim, n_ctx, 1e6)
@@ -218,3 +221,23 @@ def test_attention_buckets(ctx, monkeypatch, single, variant):
         _, t = m2.forward(t)
         want.append(t)
     np.testing.assert_array_equal(got, want)
+
+
+def test_forced_short_splits_stay_inside_the_session_workspace(ctx, monkeypatch):
+    # KVAD_ATTN_SPLIT=32 asks for 32-position splits.  The session's
+    # workspace sizes those only up to the 32-position line (1024 positions
+    # at head_dim 64), and past 256 held positions its attention launches run
+    # at the full n_ctx (1536 here): the knob is honoured up to the line and
+    # the launch takes the ordinary split ladder past it, so the results are
+    # the knob-free ones to the bit.
+    say("llm forced 32-position splits past the line")
+    tokens = [(i * 7 + 3) % 512 for i in range(300)]
+    a, _ = build(ctx, 150, n_layer=1, n_ctx=1536)
+    b, _ = build(ctx, 150, n_layer=1, n_ctx=1536)
+    for i, t in enumerate(tokens):
+        monkeypatch.setenv("KVAD_ATTN_SPLIT", "32")
+        la, na = a.forward(t, want_logits=i == len(tokens) - 1)
+        monkeypatch.delenv("KVAD_ATTN_SPLIT")
+        lb, nb = b.forward(t, want_logits=i == len(tokens) - 1)
+        assert na == nb, f"step {i}"
+    np.testing.assert_array_equal(la, lb)
