@@ -367,6 +367,36 @@ typedef struct kh_llm_trace {
     float *x_embed, *qkv, *k_cache, *v_cache, *att, *x_attn, *gate, *up, *x_mlp, *logits;
 } kh_llm_trace;
 int kh_debug_llm_trace(kh_ctx *ctx, kh_llm *m, int32_t token, const kh_llm_trace *tr);
+/* Session::forward(&[u32]) (model/mod.rs:842; CpuSession :1149-1158): n
+ * tokens at the next positions of the held sequence, read in passes cut where
+ * kh_llm_prefill_pass says.  A pass of m > 1 tokens is the reference's
+ * forward_batch (mod.rs:544-549): the embedding rows, run_rows with
+ * Rows::Following (llama.rs:224-289: every row rotated and pushed into the
+ * held cache, row i attending causally over len + i + 1 positions; the
+ * projections on the multi-token GEMV or the int8 GEMM by kh_matmul's rule),
+ * and the head over the last row (llama.rs:404-411); a pass of one token is
+ * kh_llm_forward's step.  logits [vocab] of the last token (host, may be
+ * NULL) and its greedy next token; the cache then holds n more positions.
+ * n = 0 does nothing.  Tokens past the vocabulary, or past n_ctx positions,
+ * are refused (KH_EINVAL) before anything runs. */
+int kh_llm_forward_tokens(kh_ctx *ctx, kh_llm *m, const int32_t *tokens, size_t n, float *logits, int32_t *next);
+/* Session::prefill_pass (model/mod.rs:866; CpuSession :1181-1183): how many
+ * of `left` prompt tokens the next pass reads -- whole chunks from the front,
+ * the rest last.  Feeding kh_llm_forward_tokens a pass at a time, cut here,
+ * gives the logits of one call to the bit. */
+int kh_llm_prefill_pass(const kh_llm *m, size_t left, size_t *pass);
+/* CpuSession::reading (model/mod.rs:1079-1082): `chunk` prompt tokens a pass
+ * (at most 65535); 0 restores the default, KVAD_PREFILL_CHUNK
+ * (mod.rs:1004-1006) or 64. */
+int kh_llm_set_prefill_chunk(kh_llm *m, size_t chunk);
+/* Parity hook (no counterpart in the reference): one pass of n tokens as
+ * kh_llm_forward_tokens runs it, on the rows path even for n = 1, copying each
+ * sub-block's rows out as it ends.  With len = the positions held before the
+ * pass: x_embed [n][n_embd]; qkv [L][n][qd + 2 kvd] (before the head norms and
+ * RoPE); k_cache / v_cache [L][len + n][kvd]; att [L][n][qd]; x_attn [L][n][n_embd];
+ * gate / up [L][n][n_ff] (before swiglu); x_mlp [L][n][n_embd]; logits [vocab]
+ * of the last row.  Any pointer may be NULL. */
+int kh_debug_llm_trace_pass(kh_ctx *ctx, kh_llm *m, const int32_t *tokens, size_t n, const kh_llm_trace *tr);
 /* n greedy steps from `token`, one captured HIP graph replayed per token;
  * tokens[n] receives the tokens generated. */
 int kh_llm_generate(kh_ctx *ctx, kh_llm *m, int32_t token, size_t n, int32_t *tokens);

@@ -121,6 +121,10 @@ _SIGS = {
     "kh_llm_set_rope": (C.c_int, [_p, _p, _p, _sz]),
     "kh_llm_forward": (C.c_int, [_p, _p, C.c_int32, _p, _p]),
     "kh_debug_llm_trace": (C.c_int, [_p, _p, C.c_int32, _p]),
+    "kh_llm_forward_tokens": (C.c_int, [_p, _p, _p, _sz, _p, _p]),
+    "kh_llm_prefill_pass": (C.c_int, [_p, _sz, C.POINTER(_sz)]),
+    "kh_llm_set_prefill_chunk": (C.c_int, [_p, _sz]),
+    "kh_debug_llm_trace_pass": (C.c_int, [_p, _p, _p, _sz, _p]),
     "kh_llm_generate": (C.c_int, [_p, _p, C.c_int32, _sz, _p]),
     "kh_llm_generate_launch": (C.c_int, [_p, _p, _sz]),
     "kh_llm_len": (C.c_int, [_p, C.POINTER(_sz)]),
@@ -715,6 +719,46 @@ class Llm:
         names = ["x_embed", "qkv", "k_cache", "v_cache", "att", "x_attn", "gate", "up", "x_mlp", "logits"]
         ptrs = (_p * len(names))(*[r[k].ctypes.data for k in names])
         _check(lib.kh_debug_llm_trace(self.ctx.h, self.h, token, ptrs))
+        return r
+
+    def forward_tokens(self, tokens, want_logits: bool = True):
+        """Session::forward(&[u32]) (model/mod.rs:842): the tokens at the next
+        positions, read in passes cut where prefill_pass says; (logits of the
+        last token or None, its greedy next token)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.spec.vocab, np.float32) if want_logits else None
+        nxt = C.c_int32()
+        _check(lib.kh_llm_forward_tokens(self.ctx.h, self.h, _ptr(toks), toks.size, _ptr(logits), C.byref(nxt)))
+        return logits, nxt.value
+
+    def prefill_pass(self, left: int) -> int:
+        """Session::prefill_pass (model/mod.rs:866): tokens of `left` the next pass reads."""
+        n = _sz()
+        _check(lib.kh_llm_prefill_pass(self.h, left, C.byref(n)))
+        return n.value
+
+    def reading(self, chunk: int) -> "Llm":
+        """CpuSession::reading (model/mod.rs:1079): `chunk` prompt tokens a pass (0: the default)."""
+        _check(lib.kh_llm_set_prefill_chunk(self.h, chunk))
+        return self
+
+    def trace_pass(self, tokens) -> dict:
+        """One pass of the tokens on the rows path with each sub-block's rows
+        copied out (kh_debug_llm_trace_pass): x_embed [n, e]; per layer qkv
+        [n, qd + 2 kvd], k_cache / v_cache (every position held after the
+        pass), att, x_attn, gate, up, x_mlp; logits of the last row."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        s = self.spec
+        L, n, held = s.n_layer, toks.size, len(self) + toks.size
+        qd, kvd = s.n_head * s.head_dim, s.n_kv_head * s.head_dim
+        r = {"x_embed": np.zeros((n, s.n_embd), np.float32), "qkv": np.zeros((L, n, qd + 2 * kvd), np.float32),
+             "k_cache": np.zeros((L, held, kvd), np.float32), "v_cache": np.zeros((L, held, kvd), np.float32),
+             "att": np.zeros((L, n, qd), np.float32), "x_attn": np.zeros((L, n, s.n_embd), np.float32),
+             "gate": np.zeros((L, n, s.n_ff), np.float32), "up": np.zeros((L, n, s.n_ff), np.float32),
+             "x_mlp": np.zeros((L, n, s.n_embd), np.float32), "logits": np.zeros(s.vocab, np.float32)}
+        names = ["x_embed", "qkv", "k_cache", "v_cache", "att", "x_attn", "gate", "up", "x_mlp", "logits"]
+        ptrs = (_p * len(names))(*[r[k].ctypes.data for k in names])
+        _check(lib.kh_debug_llm_trace_pass(self.ctx.h, self.h, _ptr(toks), n, ptrs))
         return r
 
     def generate(self, token: int, n: int) -> np.ndarray:

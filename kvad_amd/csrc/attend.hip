@@ -167,17 +167,65 @@ __device__ __forceinline__ void rope_load(const AttnArgs &a, RopeIn<HD, NW> &r, 
     }
 }
 
-// Per head: rms_norm with q_norm / k_norm (norm_heads, llama.rs:122-127),
-// then RoPE at position pos (Rope::apply / apply_interleaved,
-// tensor.rs:437-472), into s_rot[head]; when `holds`, the new key (s_rot[G])
-// and value (s_vnew) are also written into the caches at pos.  The caller
-// syncs the workgroup before reading s_rot / s_vnew.
+// One head held by a wave as dims lane + 64 e: rms_norm with `nw`
+// (norm_heads, llama.rs:122-127; none when null), then RoPE at position pos
+// (Rope::apply / apply_interleaved, tensor.rs:437-472), in place.
+template <int HD>
+__device__ __forceinline__ void norm_rope_head(float (&x)[HD / 64], const float *nw, const AttnRope &rp, int lane,
+                                               int pos) {
+    constexpr int HE = HD / 64;
+    const int half = HD / 2;
+    if (nw) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < HE; e++) {
+            const float sq = x[e] * x[e];
+            ss = ss + sq;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + rp.eps);
+#pragma unroll
+        for (int e = 0; e < HE; e++) {
+            const float u = x[e] * inv;
+            x[e] = u * nw[lane + 64 * e];
+        }
+    }
+    float out[HE];
+#pragma unroll
+    for (int e = 0; e < HE; e++) {
+        const int d = lane + 64 * e;
+        // the pair partner: dim d +- half (half split) or d ^ 1 (interleaved)
+        float pv;
+        if (rp.interleaved) {
+            pv = __shfl_xor(x[e], 1);
+        } else {
+            if constexpr (HD == 128) pv = x[e ^ 1];  // d and d + 64 sit in one lane
+            else pv = __shfl_xor(x[e], 32);
+        }
+        const int ip = rp.interleaved ? d >> 1 : d % half;
+        const bool first = rp.interleaved ? (d & 1) == 0 : d < half;
+        const float c = rp.cos_t[(size_t)pos * half + ip], sn = rp.sin_t[(size_t)pos * half + ip];
+        if (first) {  // a = x, b = partner: a c - b s
+            const float ac = x[e] * c, bs = pv * sn;
+            out[e] = ac - bs;
+        } else {      // b = x, a = partner: b c + a s
+            const float bc = x[e] * c, as = pv * sn;
+            out[e] = bc + as;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < HE; e++) x[e] = out[e];
+}
+
+// Per head: norm_rope_head into s_rot[head]; when `holds`, the new key
+// (s_rot[G]) and value (s_vnew) are also written into the caches at pos.
+// The caller syncs the workgroup before reading s_rot / s_vnew.
 template <int HD, int NW>
 __device__ __forceinline__ void rope_apply(const AttnArgs &a, const RopeIn<HD, NW> &r, float (*s_rot)[HD],
                                            float *s_vnew, int wave, int lane, int tid, int G, int kvh, int pos,
                                            bool holds) {
     constexpr int HE = RopeIn<HD, NW>::HE;
-    const int half = HD / 2;
 #pragma unroll
     for (int i = 0; i < RopeIn<HD, NW>::RH; i++) {
         const int h = wave + i * NW;
@@ -185,47 +233,12 @@ __device__ __forceinline__ void rope_apply(const AttnArgs &a, const RopeIn<HD, N
         float x[HE];
 #pragma unroll
         for (int e = 0; e < HE; e++) x[e] = r.x[i][e];
-        const float *nw = h < G ? a.rope.q_norm : a.rope.k_norm;
-        if (nw) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int e = 0; e < HE; e++) {
-                const float sq = x[e] * x[e];
-                ss = ss + sq;
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss = ss + __shfl_xor(ss, o);
-            const float inv = 1.0f / sqrtf(ss / (float)HD + a.rope.eps);
-#pragma unroll
-            for (int e = 0; e < HE; e++) {
-                const float u = x[e] * inv;
-                x[e] = u * nw[lane + 64 * e];
-            }
-        }
+        norm_rope_head<HD>(x, h < G ? a.rope.q_norm : a.rope.k_norm, a.rope, lane, pos);
 #pragma unroll
         for (int e = 0; e < HE; e++) {
             const int d = lane + 64 * e;
-            // the pair partner: dim d +- half (half split) or d ^ 1 (interleaved)
-            float pv;
-            if (a.rope.interleaved) {
-                pv = __shfl_xor(x[e], 1);
-            } else {
-                if constexpr (HD == 128) pv = x[e ^ 1];  // d and d + 64 sit in one lane
-                else pv = __shfl_xor(x[e], 32);
-            }
-            const int ip = a.rope.interleaved ? d >> 1 : d % half;
-            const bool first = a.rope.interleaved ? (d & 1) == 0 : d < half;
-            const float c = a.rope.cos_t[(size_t)pos * half + ip], sn = a.rope.sin_t[(size_t)pos * half + ip];
-            float out;
-            if (first) {  // a = x, b = partner: a c - b s
-                const float ac = x[e] * c, bs = pv * sn;
-                out = ac - bs;
-            } else {      // b = x, a = partner: b c + a s
-                const float bc = x[e] * c, as = pv * sn;
-                out = bc + as;
-            }
-            s_rot[h][d] = out;
-            if (h == G) a.kw[(size_t)pos * a.kstride + (size_t)kvh * HD + d] = out;
+            s_rot[h][d] = x[e];
+            if (h == G) a.kw[(size_t)pos * a.kstride + (size_t)kvh * HD + d] = x[e];
         }
     }
     if (holds) {
@@ -234,6 +247,48 @@ __device__ __forceinline__ void rope_apply(const AttnArgs &a, const RopeIn<HD, N
             s_vnew[d] = v;
             a.vw[(size_t)pos * a.vstride + (size_t)kvh * HD + d] = v;
         }
+    }
+}
+
+// Rows::Following (a prompt read a pass at a time, run_rows with
+// llama.rs:249-257): every row's query and key heads normed and rotated at
+// the row's own position, each row's key and value pushed into the cache
+// row at that position.  The attention launch that follows reads the
+// rotated queries in q and the cache; no row's attention may start before
+// every row of the pass is pushed, which is why this is a launch of its own
+// and not fused into the split kernel as in the one-token step.
+// Grid (n_head + n_kv_head, rows): one wave per head of a row; row i is at
+// position rows[i].L - 1 of cache (rows[i].k, rows[i].v).
+template <int HD>
+__global__ __launch_bounds__(64) void rope_push_rows_kernel(float *q, const float *k, const float *v,
+                                                            const AttnRow *rows, AttnRope rp, int n_head,
+                                                            int n_kv_head, size_t kstride, size_t vstride) {
+    constexpr int HE = HD / 64;
+    const int h = blockIdx.x, i = blockIdx.y, lane = threadIdx.x;
+    const AttnRow r = rows[i];
+    const int pos = r.L - 1;
+    float x[HE];
+    if (h < n_head) {
+        float *src = q + ((size_t)i * n_head + h) * HD;
+#pragma unroll
+        for (int e = 0; e < HE; e++) x[e] = src[lane + 64 * e];
+        norm_rope_head<HD>(x, rp.q_norm, rp, lane, pos);
+#pragma unroll
+        for (int e = 0; e < HE; e++) src[lane + 64 * e] = x[e];
+        return;
+    }
+    const int kvh = h - n_head;
+    const float *ks = k + ((size_t)i * n_kv_head + kvh) * HD;
+    const float *vs = v + ((size_t)i * n_kv_head + kvh) * HD;
+#pragma unroll
+    for (int e = 0; e < HE; e++) x[e] = ks[lane + 64 * e];
+    norm_rope_head<HD>(x, rp.k_norm, rp, lane, pos);
+    float *kd = r.k + (size_t)pos * kstride + (size_t)kvh * HD;
+    float *vd = r.v + (size_t)pos * vstride + (size_t)kvh * HD;
+#pragma unroll
+    for (int e = 0; e < HE; e++) {
+        kd[lane + 64 * e] = x[e];
+        vd[lane + 64 * e] = vs[lane + 64 * e];
     }
 }
 
@@ -933,6 +988,24 @@ int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, con
     if (4 * a.row_floats * nb > ws_bytes) return fail(KH_EINVAL, "attend: workspace too small for the rows");
     carve_partials(a, ws, head_dim);
     return run(ctx, a, head_dim, nb);
+}
+
+int launch_rope_push_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, float *q, const float *k,
+                          const float *v, const AttnRow *rows, int nb, size_t kstride, size_t vstride,
+                          const AttnRope &rope) {
+    if (nb <= 0 || nb > 65535 || n_head <= 0 || n_kv_head <= 0 || n_head + n_kv_head > 65535)
+        return fail(KH_EINVAL, "rope_push_rows: bad row or head count");
+    const dim3 grid((unsigned)(n_head + n_kv_head), (unsigned)nb);
+    if (head_dim == 64)
+        hipLaunchKernelGGL(rope_push_rows_kernel<64>, grid, dim3(64), 0, ctx->stream, q, k, v, rows, rope, n_head,
+                           n_kv_head, kstride, vstride);
+    else if (head_dim == 128)
+        hipLaunchKernelGGL(rope_push_rows_kernel<128>, grid, dim3(64), 0, ctx->stream, q, k, v, rows, rope, n_head,
+                           n_kv_head, kstride, vstride);
+    else
+        return fail(KH_DECLINED, "rope_push_rows: head_dim 64 or 128");
+    KH_HIP(hipGetLastError());
+    return KH_OK;
 }
 
 int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,

@@ -143,6 +143,11 @@ struct kh_llm {
     size_t rows_cap = 0;
     std::vector<char> rows_host;
     std::map<std::pair<size_t, size_t>, hipGraphExec_t> rows_graphs;  // the pass for n rows, per (n, bucket)
+    // a prompt read in passes of up to `chunk` tokens (Session::prefill_pass),
+    // each pass of n > 1 rows captured per (n, attention bucket) in the same
+    // rows buffer
+    size_t chunk = 0;
+    std::map<std::pair<size_t, size_t>, hipGraphExec_t> pass_graphs;
 };
 
 // A conversation's cache set aside (Session::park, model/mod.rs:889-893): per
@@ -395,8 +400,9 @@ int launch_quantize(kh_ctx *ctx, const float *w, size_t rows, size_t cols, int p
 // Small helpers.
 int launch_fill(kh_ctx *ctx, float *p, size_t n, float value);
 int launch_dequant_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out);
-// The same with the row index read from device memory (an embedding lookup).
-int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out);
+// The same with the row indices read from device memory (an embedding
+// lookup): rows r[0..n) into out [n][cols].
+int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out, size_t n = 1);
 // tensor::rms_norm over m rows of n (glue.hip).
 int launch_rms_norm(kh_ctx *ctx, const float *x, const float *w, size_t m, size_t n, float eps, float *out);
 // gate = silu(gate) * up over n floats (glue.hip).
@@ -446,6 +452,12 @@ int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, con
                        int nb, size_t kstride, size_t vstride, size_t max_positions, float *out, void *ws,
                        size_t ws_bytes, const AttnRope *rope = nullptr);
 size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size_t nb);
+// The rows of one sequence's pass (Rows::Following): queries q [nb][n_head][hd]
+// normed and rotated in place, keys k [nb][n_kv][hd] normed, rotated and
+// written with the values v into each row's cache at rows[i].L - 1.
+int launch_rope_push_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, float *q, const float *k,
+                          const float *v, const AttnRow *rows, int nb, size_t kstride, size_t vstride,
+                          const AttnRope &rope);
 
 // Absorbed latent attention (model/deepseek.rs:553-591): out[n_head][512] =
 // softmax over positions of (q_lat . c_t + q_pe . pe_t) * scale, times c_t.

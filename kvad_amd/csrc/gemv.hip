@@ -824,13 +824,14 @@ __global__ void fill_kernel(float *p, size_t n, float value) {
 }
 
 // Weight::row (quant.rs:374-402) and the Q4_K decoder (mpp.rs:304-315).
+// Row r_dev[y] (or r_host) of the weight into out row y, one grid row each.
 __global__ void dequant_row_kernel(int prec, const void *qs, const float *scales, size_t cols, size_t r_host,
                                    const int32_t *r_dev,
                                    float *out) {
-    const size_t r = r_dev ? (size_t)*r_dev : r_host;
+    const size_t r = r_dev ? (size_t)r_dev[blockIdx.y] : r_host;
     size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= cols) return;
-    out[k] = dequant_elem(prec, qs, scales, cols, r, k);
+    out[(size_t)blockIdx.y * cols + k] = dequant_elem(prec, qs, scales, cols, r, k);
 }
 
 }  // namespace
@@ -1104,9 +1105,12 @@ int launch_dequant_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out) {
     return KH_OK;
 }
 
-int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out) {
-    hipLaunchKernelGGL(dequant_row_kernel, dim3((unsigned)((w->cols + 255) / 256)), dim3(256), 0, ctx->stream,
-                       w->precision, (const void *)w->qs, (const float *)w->scales, w->cols, (size_t)0, r, out);
+int launch_dequant_row_dev(kh_ctx *ctx, const kh_weight *w, const int32_t *r, float *out, size_t n) {
+    if (n == 0) return KH_OK;
+    if (n > 65535) return fail(KH_EINVAL, "rows: at most 65535 a launch");
+    hipLaunchKernelGGL(dequant_row_kernel, dim3((unsigned)((w->cols + 255) / 256), (unsigned)n), dim3(256), 0,
+                       ctx->stream, w->precision, (const void *)w->qs, (const float *)w->scales, w->cols, (size_t)0,
+                       r, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }

@@ -222,6 +222,14 @@ int trace_copy(kh_ctx *ctx, float *dst, const float *src, size_t n) {
     return KH_OK;
 }
 
+// n rows of `width` floats (src rows packed) to host rows `pitch` floats apart.
+int trace_rows(kh_ctx *ctx, float *dst, size_t pitch, const float *src, size_t width, size_t n) {
+    KH_HIP(hipMemcpy2DAsync(dst, 4 * pitch, src, 4 * width, 4 * width, n, hipMemcpyDeviceToHost, ctx->stream));
+    return KH_OK;
+}
+
+int head_step(kh_ctx *ctx, kh_llm *m, const float *x, bool record = true);
+
 // One token's launches, all on the context's stream.  With `embed` the
 // step starts from the token's embedding row (llama.rs:384-391); without,
 // from the row the previous step's argmax wrote into x (captured steps).
@@ -292,12 +300,23 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr, bool embed = 
         }
         if (tr && (rc = trace_copy(ctx, tr->x_mlp ? tr->x_mlp + l * s.n_embd : nullptr, m->x, s.n_embd))) return rc;
     }
-    // ---- head (llama.rs:404-411)
+    return head_step(ctx, m, m->x);
+}
+
+// The head over the last residual row x (llama.rs:404-411, Transformer::head
+// with all = false) into m->logits, then the greedy choice (sampler.rs:217-226):
+// the chosen token becomes the next input (its embedding row in m->x), the
+// position advances by one and, with `record`, the step's token is written to
+// the generated tokens (kh_llm_generate's record; a prompt's pass leaves it).
+int head_step(kh_ctx *ctx, kh_llm *m, const float *x, bool record) {
+    int32_t *const out = record ? m->out : nullptr;
+    const kh_llm_spec &s = m->spec;
+    int rc;
     const kh_weight *head = m->head ? m->head : m->embed;
     const bool fh = norm_fusable(head);
-    if (!fh && (rc = launch_rms_norm(ctx, m->x, m->final_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+    if (!fh && (rc = launch_rms_norm(ctx, x, m->final_norm, 1, s.n_embd, s.eps, m->h))) return rc;
     std::vector<std::pair<const kh_weight *, GemvJob>> jobs{
-        {head, normed(gemv_job(head, fh ? m->x : m->h, nullptr, nullptr, m->logits, 0), fh, m->final_norm, s.eps)}};
+        {head, normed(gemv_job(head, fh ? x : m->h, nullptr, nullptr, m->logits, 0), fh, m->final_norm, s.eps)}};
     if (!fh && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) return rc;
     // the greedy choice (sampler.rs:217-226): each workgroup of the head GEMV
     // keeps its best row, one workgroup then takes the best of them; f32
@@ -308,7 +327,7 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr, bool embed = 
         // the step ends in the head's last workgroup to finish, with no
         // launch of its own (KVAD_HEAD_TAIL=0: a one-block launch after it)
         const bool fold = env_int("KVAD_HEAD_TAIL", 1) != 0;
-        const GreedyTail tail{m->arrivals, m->token, m->pos, m->steps, m->out, m->out_cap, m->embed->precision,
+        const GreedyTail tail{m->arrivals, m->token, m->pos, m->steps, out, m->out_cap, m->embed->precision,
                               m->embed->qs, m->embed->scales, m->embed->cols, m->x};
         rc = launch_gemv_argmax(ctx, head->precision, jobs[0].second, m->arg_v, m->arg_i, m->arg_n, ARGMAX_CAP,
                                 fold ? &tail : nullptr);
@@ -324,7 +343,7 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr, bool embed = 
     }
     const NextEmbed ne{m->embed->precision, m->embed->qs, m->embed->scales, m->embed->cols, m->x};
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, ctx->stream, m->logits, (int)s.vocab, m->arg_v,
-                       m->arg_i, kept ? m->arg_n : nullptr, m->token, m->pos, m->steps, m->out, m->out_cap, ne);
+                       m->arg_i, kept ? m->arg_n : nullptr, m->token, m->pos, m->steps, out, m->out_cap, ne);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -396,6 +415,8 @@ RowsBuf rows_layout(const kh_llm_spec &s, size_t cap, char *base) {
 void drop_rows_graphs(kh_llm *m) {
     for (auto &g : m->rows_graphs) (void)hipGraphExecDestroy(g.second);
     m->rows_graphs.clear();
+    for (auto &g : m->pass_graphs) (void)hipGraphExecDestroy(g.second);
+    m->pass_graphs.clear();
 }
 
 int ensure_rows(kh_llm *m, size_t n) {
@@ -461,15 +482,28 @@ int norm_rows(kh_ctx *ctx, const float *x, const float *w, size_t n, size_t e, f
     return launch_norm_qact(ctx, x, w, n, e, eps, need_f32 ? h : nullptr, qa);
 }
 
-// run_rows (llama.rs:224-289) with Rows::Each, then the head over every row
-// (llama.rs:404-416) and each row's greedy token.  The table (tokens, and per
-// layer each row's cache and length) is already on the device.
-int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len) {
+// run_rows (llama.rs:224-289) over n rows whose table (tokens, and per layer
+// each row's cache and length) is already on the device.
+//   Rows::Each (batched decode): every row has a cache of its own; RoPE and
+//   the cache push are fused into the attention's split kernel; then the
+//   head over every row (llama.rs:412-416) and each row's greedy token.
+//   Rows::Following (a prompt's pass, `following`): the rows are one
+//   sequence's next positions in the held cache; every row is rotated and
+//   pushed by a launch of its own before the attention, since row i attends
+//   over the rows before it; then the head over the last row and its greedy
+//   token (Transformer::head with all = false, llama.rs:404-411), which
+//   becomes the session's next input.
+// With a trace (the parity hook kh_debug_llm_trace_pass: a pass of the held
+// sequence, never under capture) each sub-block's rows are copied out as it
+// ends; len0 is the positions held before the pass.
+int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len, bool following = false,
+              const kh_llm_trace *tr = nullptr, size_t len0 = 0) {
     const kh_llm_spec &s = m->spec;
     const size_t e = s.n_embd, qd = s.n_head * s.head_dim, kvd = s.n_kv_head * s.head_dim;
+    const size_t qkvd = qd + 2 * kvd, held = len0 + n;
     int rc;
-    for (size_t i = 0; i < n; i++)  // embed (llama.rs:384-391)
-        if ((rc = launch_dequant_row_dev(ctx, m->embed, b.tok + i, b.x + i * e))) return rc;
+    if ((rc = launch_dequant_row_dev(ctx, m->embed, b.tok, b.x, n))) return rc;  // embed (llama.rs:384-391)
+    if (tr && (rc = trace_copy(ctx, tr->x_embed, b.x, n * e))) return rc;
     for (size_t l = 0; l < s.n_layer; l++) {
         const kh_llm::Layer &L = m->layers[l];
         // ---- attention sub-block (llama.rs:241-275)
@@ -480,12 +514,25 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len
             float *y[3] = {b.q, b.k, b.v};
             if ((rc = project_all(ctx, 3, w, b.h, b.qa, n, bias, y))) return rc;
         }
-        // each row at its own position over its own cache (run_rows,
-        // llama.rs:249-271), RoPE and the cache push fused in
+        if (tr && tr->qkv) {  // [n][q | k | v] per layer, before the rotation
+            float *d = tr->qkv + l * n * qkvd;
+            if ((rc = trace_rows(ctx, d, qkvd, b.q, qd, n)) || (rc = trace_rows(ctx, d + qd, qkvd, b.k, kvd, n)) ||
+                (rc = trace_rows(ctx, d + qd + kvd, qkvd, b.v, kvd, n)))
+                return rc;
+        }
+        // each row at its own position over its cache up to itself (run_rows,
+        // llama.rs:249-271)
         const AttnRow *tab = b.tab + l * n;
         const AttnRope rp{b.k, b.v, m->rope_cos, m->rope_sin, L.q_norm, L.k_norm, s.eps, s.rope_interleaved, kvd};
+        if (following && (rc = launch_rope_push_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q,
+                                                      b.k, b.v, tab, (int)n, kvd, kvd, rp)))
+            return rc;
         if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
-                                     kvd, max_len, b.att, b.ws, b.ws_bytes, &rp)))
+                                     kvd, max_len, b.att, b.ws, b.ws_bytes, following ? nullptr : &rp)))
+            return rc;
+        if (tr && ((rc = trace_copy(ctx, tr->k_cache ? tr->k_cache + l * held * kvd : nullptr, m->kc[l], held * kvd)) ||
+                   (rc = trace_copy(ctx, tr->v_cache ? tr->v_cache + l * held * kvd : nullptr, m->vc[l], held * kvd)) ||
+                   (rc = trace_copy(ctx, tr->att ? tr->att + l * n * qd : nullptr, b.att, n * qd))))
             return rc;
         if (L.o->precision != KH_F32 && n <= (size_t)MULTI_TOKENS && n <= rows_multi_max() &&
             multi_stages_f32(L.o->precision, n, qd)) {
@@ -501,6 +548,7 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len
             if (L.o->precision != KH_F32 && (rc = launch_qact(ctx, b.att, n, qd, b.qa))) return rc;
             if ((rc = project(ctx, L.o, b.att, b.qa, n, nullptr, b.x, 1))) return rc;  // x += o(attn)
         }
+        if (tr && (rc = trace_copy(ctx, tr->x_attn ? tr->x_attn + l * n * e : nullptr, b.x, n * e))) return rc;
         // ---- MLP sub-block (llama.rs:277-285, Ffn::run ffn.rs:370-375)
         if ((rc = norm_rows(ctx, b.x, L.mlp_norm, n, e, s.eps, any_f32({L.gate, L.up}), b.h, b.qa))) return rc;
         {
@@ -509,13 +557,18 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len
             float *y[2] = {b.g, b.u};
             if ((rc = project_all(ctx, 2, w, b.h, b.qa, n, bias, y))) return rc;
         }
+        if (tr && ((rc = trace_copy(ctx, tr->gate ? tr->gate + l * n * s.n_ff : nullptr, b.g, n * s.n_ff)) ||
+                   (rc = trace_copy(ctx, tr->up ? tr->up + l * n * s.n_ff : nullptr, b.u, n * s.n_ff))))
+            return rc;
         if (L.down->precision != KH_F32) {  // QActBatch::new of swiglu(gate, up), then down
             if ((rc = launch_swiglu_qact(ctx, b.g, b.u, n, s.n_ff, b.qa))) return rc;
         } else if ((rc = launch_swiglu(ctx, b.g, b.u, n * s.n_ff))) {
             return rc;
         }
         if ((rc = project(ctx, L.down, b.g, b.qa, n, nullptr, b.x, 1))) return rc;  // x += mlp
+        if (tr && (rc = trace_copy(ctx, tr->x_mlp ? tr->x_mlp + l * n * e : nullptr, b.x, n * e))) return rc;
     }
+    if (following) return head_step(ctx, m, b.x + (n - 1) * e, false);
     // ---- head over every row (llama.rs:412-415), then each row's argmax
     const kh_weight *head = m->head ? m->head : m->embed;
     if ((rc = norm_rows(ctx, b.x, m->final_norm, n, e, s.eps, head->precision == KH_F32, b.h, b.qa))) return rc;
@@ -617,6 +670,110 @@ int replay_steps(kh_ctx *ctx, kh_llm *m, size_t n) {
     if ((rc = launch_dequant_row_dev(ctx, m->embed, m->token, m->x))) return rc;
     for (size_t i = 0; i < n; i++)
         KH_HIP(hipGraphLaunch(m->graphs.at(bucket_max(m, m->len + i + 1)), ctx->stream));
+    return KH_OK;
+}
+
+// ---- a prompt read a pass at a time (Rows::Following) ---------------------
+
+// Session::prefill_pass (model/mod.rs:866; CpuSession :1181-1183): whole
+// chunks from the front, what is left over last.  The chunk is
+// KVAD_PREFILL_CHUNK (the reference's knob, mod.rs:1004-1006) unless the
+// caller set one (CpuSession::reading, :1079-1082).
+size_t pass_len(const kh_llm *m, size_t left) {
+    size_t c = m->chunk;
+    if (!c) {
+        const int v = env_int("KVAD_PREFILL_CHUNK", 0);
+        c = v > 0 ? (size_t)v : 64;
+    }
+    c = std::min<size_t>(c, 65535);
+    return std::min(left, c);
+}
+
+// The attention launch maximum of a pass ending with `held` positions: the
+// next power of two from 64, at most n_ctx (a captured pass serves every
+// pass of its row count up to that length).
+size_t pass_bucket(const kh_llm *m, size_t held) {
+    size_t b = 64;
+    while (b < held) b *= 2;
+    return std::min(b, m->spec.n_ctx);
+}
+
+// The table of a pass of n tokens: tokens, then per layer each row's cache
+// (the held one) and its length after itself (positions len .. len + n - 1).
+void pass_table(kh_llm *m, const int32_t *tokens, size_t n, size_t &tok_bytes, size_t &tab_bytes) {
+    const kh_llm_spec &s = m->spec;
+    tok_bytes = (4 * n + 15) & ~(size_t)15;
+    tab_bytes = sizeof(AttnRow) * n * s.n_layer;
+    m->rows_host.resize(tok_bytes + tab_bytes);
+    std::copy(tokens, tokens + n, reinterpret_cast<int32_t *>(m->rows_host.data()));
+    AttnRow *tab = reinterpret_cast<AttnRow *>(m->rows_host.data() + tok_bytes);
+    for (size_t l = 0; l < s.n_layer; l++)
+        for (size_t i = 0; i < n; i++) tab[l * n + i] = AttnRow{m->kc[l], m->vc[l], (int)(m->len + i + 1)};
+}
+
+// One pass of n >= 1 tokens of the held sequence: n == 1 is the one-token
+// step; more rows run step_rows(following), captured per (n, bucket), or
+// eagerly with a trace.  The state afterwards is the step's: the greedy next
+// token is the input, the position is len + n.  Returns with the stream
+// synchronised (the table's host copy is reused by the next pass).
+int run_pass(kh_ctx *ctx, kh_llm *m, const int32_t *tokens, size_t n, const kh_llm_trace *tr = nullptr) {
+    int rc;
+    if (n == 1 && !tr) {
+        const int32_t st[3] = {tokens[0], (int32_t)m->len, 0};
+        KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
+        m->attn_max = bucket_max(m, m->len + 1);
+        if ((rc = step(ctx, m))) return rc;
+        KH_HIP(hipStreamSynchronize(ctx->stream));
+        m->len += 1;
+        return KH_OK;
+    }
+    if ((rc = ensure_rows(m, n))) return rc;
+    const RowsBuf b = rows_layout(m->spec, m->rows_cap, static_cast<char *>(m->rows_buf));
+    size_t tok_bytes, tab_bytes;
+    pass_table(m, tokens, n, tok_bytes, tab_bytes);
+    const size_t bm = pass_bucket(m, m->len + n);
+    // the head's tail advances the position past the last row
+    const int32_t st[3] = {tokens[n - 1], (int32_t)(m->len + n - 1), 0};
+    KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
+    KH_HIP(hipMemcpyAsync(b.tok, m->rows_host.data(), tok_bytes, hipMemcpyHostToDevice, ctx->stream));
+    KH_HIP(hipMemcpyAsync(b.tab, m->rows_host.data() + tok_bytes, tab_bytes, hipMemcpyHostToDevice, ctx->stream));
+    if (tr) {
+        if ((rc = step_rows(ctx, m, n, b, bm, true, tr, m->len))) return rc;
+    } else {
+        const std::pair<size_t, size_t> key{n, bm};
+        auto it = m->pass_graphs.find(key);
+        if (it == m->pass_graphs.end()) {
+            if ((rc = gemm_split_reserve(ctx))) return rc;
+            KH_HIP(hipStreamSynchronize(ctx->stream));
+            hipGraph_t g = nullptr;
+            KH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+            rc = step_rows(ctx, m, n, b, bm, true);
+            hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+            if (rc) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+            hipGraphExec_t x = nullptr;
+            e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+            it = m->pass_graphs.emplace(key, x).first;
+        }
+        KH_HIP(hipGraphLaunch(it->second, ctx->stream));
+    }
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    m->len += n;
+    return KH_OK;
+}
+
+// Tokens of the held sequence, checked against the vocabulary and the window.
+int check_tokens(const kh_llm *m, const int32_t *tokens, size_t n, const char *what) {
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || (size_t)tokens[i] >= m->spec.vocab)
+            return fail(KH_EINVAL, std::string(what) + ": token out of range");
+    if (m->len + n > m->spec.n_ctx)
+        return fail(KH_EINVAL, std::string(what) + ": the tokens would overrun the context window");
     return KH_OK;
 }
 
@@ -802,6 +959,57 @@ int kh_llm_forward(kh_ctx *ctx, kh_llm *m, int32_t token, float *logits, int32_t
     KH_HIP(hipStreamSynchronize(ctx->stream));
     m->len += 1;
     if (next) *next = nt;
+    return KH_OK;
+}
+
+int kh_llm_forward_tokens(kh_ctx *ctx, kh_llm *m, const int32_t *tokens, size_t n, float *logits, int32_t *next) {
+    if (!ctx || !m || m->ctx != ctx) return fail(KH_EINVAL, "kh_llm_forward_tokens: null argument or foreign context");
+    if (n == 0) return KH_OK;
+    if (!tokens) return fail(KH_EINVAL, "kh_llm_forward_tokens: null tokens");
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = ready(m);
+    if (rc || (rc = check_tokens(m, tokens, n, "kh_llm_forward_tokens"))) return rc;
+    // Session::forward (CpuSession, mod.rs:1149-1158): the tokens in passes
+    // cut where prefill_pass says, the last pass's logits returned
+    for (size_t at = 0; at < n;) {
+        const size_t pass = pass_len(m, n - at);
+        if ((rc = run_pass(ctx, m, tokens + at, pass))) return rc;
+        at += pass;
+    }
+    if (logits) KH_HIP(hipMemcpyAsync(logits, m->logits, 4 * m->spec.vocab, hipMemcpyDeviceToHost, ctx->stream));
+    int32_t nt = 0;
+    KH_HIP(hipMemcpyAsync(&nt, m->token, 4, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    if (next) *next = nt;
+    return KH_OK;
+}
+
+int kh_llm_prefill_pass(const kh_llm *m, size_t left, size_t *pass) {
+    if (!m || !pass) return fail(KH_EINVAL, "kh_llm_prefill_pass: null argument");
+    *pass = pass_len(m, left);
+    return KH_OK;
+}
+
+int kh_llm_set_prefill_chunk(kh_llm *m, size_t chunk) {
+    if (!m) return fail(KH_EINVAL, "kh_llm_set_prefill_chunk: null argument");
+    if (chunk > 65535) return fail(KH_EINVAL, "kh_llm_set_prefill_chunk: at most 65535 tokens a pass");
+    std::lock_guard<std::recursive_mutex> lock(m->ctx->mu);
+    m->chunk = chunk;  // 0: KVAD_PREFILL_CHUNK, else 64
+    return KH_OK;
+}
+
+int kh_debug_llm_trace_pass(kh_ctx *ctx, kh_llm *m, const int32_t *tokens, size_t n, const kh_llm_trace *tr) {
+    if (!ctx || !m || m->ctx != ctx || !tr || !tokens || n == 0)
+        return fail(KH_EINVAL, "kh_debug_llm_trace_pass: null argument or no tokens");
+    if (n > 65535) return fail(KH_EINVAL, "kh_debug_llm_trace_pass: at most 65535 tokens a pass");
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = ready(m);
+    if (rc || (rc = check_tokens(m, tokens, n, "kh_debug_llm_trace_pass"))) return rc;
+    if ((rc = run_pass(ctx, m, tokens, n, tr))) return rc;
+    if (tr->logits) KH_HIP(hipMemcpyAsync(tr->logits, m->logits, 4 * m->spec.vocab, hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
     return KH_OK;
 }
 
