@@ -338,7 +338,7 @@ def measured_traffic():
         return None
 
 
-SECTIONS = ("q8", "prefill", "moe", "decode", "attend", "mla", "qcache")
+SECTIONS = ("q8", "prefill", "moe", "decode", "attend", "mla", "qcache", "session_prefill")
 
 
 def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
@@ -355,6 +355,10 @@ def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
         out["moe_deepseek_v2_lite"] = moe(torch, K, ctx, stream, dev, gen, args)
     if want("decode"):
         out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args)
+    if only == "session_prefill":  # the prompt passes alone (inside "decode" otherwise)
+        m = qwen05b_session(torch, K, ctx, stream, dev, gen)
+        out["qwen05b_q8_prefill"] = prefill_session(m)
+        m.free()
     if want("attend"):
         out["attend_qwen05b"] = attend(torch, K, ctx, stream, dev, gen, args)
     if want("mla"):
@@ -695,13 +699,10 @@ def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8):
     return res
 
 
-def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256):
-    """The second half of BASELINE.json's metric: Qwen2.5-0.5B-shaped q8
-    decode, tokens per second, on the device-resident session (24 layers,
-    n_embd 896, 14/2 heads of 64, ffn 4864, vocab 151936, tied embedding,
-    q/k/v biases; weights ~ N(0, 0.02), norms 1).  Greedy tokens, one HIP
-    graph replay per token; `warm` tokens first, then `timed` tokens timed with
-    HIP events on the session's stream (context warm..warm+timed)."""
+def qwen05b_session(torch, K, ctx, stream, dev, gen, n_ctx=2048):
+    """A device session of Qwen2.5-0.5B's shape, q8 (24 layers, n_embd 896,
+    14/2 heads of 64, ffn 4864, vocab 151936, tied embedding, q/k/v biases;
+    weights ~ N(0, 0.02), norms 1, RoPE theta 1e6)."""
     spec = dict(n_layer=24, n_embd=896, n_head=14, n_kv_head=2, head_dim=64, n_ff=4864, vocab=151936,
                 n_ctx=n_ctx, eps=1e-6, rope_interleaved=0)
     e, qd, kvd, ff = 896, 896, 128, 4864
@@ -725,6 +726,17 @@ def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256
         ang = np.arange(n_ctx, dtype=np.float32)[:, None] * inv[None, :].astype(np.float32)
         m.set_rope(np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32), n_ctx)
     torch.cuda.synchronize()
+    return m
+
+
+def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256):
+    """The second half of BASELINE.json's metric: Qwen2.5-0.5B-shaped q8
+    decode, tokens per second, on the device-resident session
+    (qwen05b_session).  Greedy tokens, one HIP graph replay per token; `warm`
+    tokens first, then `timed` tokens timed with HIP events on the session's
+    stream (context warm..warm+timed)."""
+    m = qwen05b_session(torch, K, ctx, stream, dev, gen, n_ctx)
+    torch.cuda.synchronize()
     first = m.generate(1, warm)  # captures the step's graph
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -745,9 +757,53 @@ def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256
            "vs_reference_cpu_q8_112tps": round(tps / 112.0, 2),
            "vs_reference_metal_q8_191tps": round(tps / 191.0, 2), "first_tokens": [int(t) for t in first[:4]]}
     log(f"qwen0.5b q8 decode: {res}")
+    res["prefill"] = prefill_session(m)
     res["batched"] = decode_batched(torch, m, warm)
     m.free()
     return res
+
+
+def prefill_session(m, n=640, reps=5):
+    """A prompt read on the device (Session::forward(&[u32]), mod.rs:842): n
+    tokens from an empty cache, in passes of prefill_pass tokens (Rows::Following,
+    llama.rs:224-289: the projections on the int8 GEMM, every row's attention
+    causal over the held cache; the default pass, 512, cuts 640 into 512 + 128),
+    host to host: tokens up, last logits and the
+    next token back.  Each pass size is timed as the best of `reps` calls after
+    one untimed call that captures its passes; beside it the same prompt fed
+    one token at a time (kh_llm_forward per token, as the device read prompts
+    before), and the reference's published 640-token prefill at
+    Qwen2.5-0.5B q8 on the M5 Pro CPU: 1.20 s with SMMLA, 6.20 s token at a
+    time (docs/engine.md:587-596)."""
+    prompt = (np.arange(n, dtype=np.int64) * 7919 + 11) % 151936
+    out = {"tokens": n, "reference_m5pro_cpu_s": {"smmla_passes": 1.20, "token_at_a_time": 6.20}}
+    for chunk in (64, 128, 256, 512, 640):  # 512: the default (the reference GPU backend's pass)
+        m.reading(chunk)
+        m.truncate(0)
+        m.forward_tokens(prompt, want_logits=False)
+        best = float("inf")
+        for _ in range(reps):
+            m.truncate(0)
+            t0 = time.perf_counter()
+            m.forward_tokens(prompt, want_logits=True)
+            best = min(best, time.perf_counter() - t0)
+        out[f"chunk_{chunk}"] = {"ms": round(best * 1e3, 3), "tok_per_s": round(n / best, 1),
+                                 "passes": -(-n // chunk)}
+    m.reading(0)
+    m.truncate(0)
+    m.forward(int(prompt[0]), want_logits=False)
+    m.truncate(0)
+    t0 = time.perf_counter()
+    for t in prompt:
+        m.forward(int(t), want_logits=False)
+    s = time.perf_counter() - t0
+    out["token_at_a_time"] = {"ms": round(s * 1e3, 3), "tok_per_s": round(n / s, 1)}
+    out["default_chunk"] = m.prefill_pass(1 << 20)
+    d = out[f"chunk_{out['default_chunk']}"]["ms"] / 1e3
+    out["vs_reference_smmla"] = round(1.20 / d, 1)
+    m.truncate(0)
+    log(f"qwen0.5b q8 prefill: {out}")
+    return out
 
 
 def decode_batched(torch, m, warm, steps=20):

@@ -975,6 +975,15 @@ size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size
     return 4 * nb * (f + (max_positions + 256) * (size_t)n_head) + 1024;
 }
 
+size_t attend_rows_need_bytes(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, size_t max_positions,
+                              size_t nb) {
+    AttnArgs a;
+    if (nb == 0 || nb > 65535 || max_positions == 0 ||
+        setup(ctx, a, n_head, n_kv_head, head_dim, nullptr, nullptr, nullptr, 0, 0, max_positions, nullptr, (int)nb))
+        return 0;
+    return 4 * partial_floats(a.nsplit, n_head, head_dim, a.P) * nb + 1024;
+}
+
 int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,
                        int nb, size_t kstride, size_t vstride, size_t max_positions, float *out, void *ws,
                        size_t ws_bytes, const AttnRope *rope) {

@@ -148,6 +148,9 @@ struct kh_llm {
     // rows buffer
     size_t chunk = 0;
     std::map<std::pair<size_t, size_t>, hipGraphExec_t> pass_graphs;
+    void *pass_buf = nullptr;   // the pass's rows, for pass_cap rows
+    size_t pass_cap = 0;
+    kh::Workspace pass_ws;      // the pass's attention partials
 };
 
 // A conversation's cache set aside (Session::park, model/mod.rs:889-893): per
@@ -452,6 +455,9 @@ int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, con
                        int nb, size_t kstride, size_t vstride, size_t max_positions, float *out, void *ws,
                        size_t ws_bytes, const AttnRope *rope = nullptr);
 size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size_t nb);
+// The partials launch_attend_rows needs for nb rows of at most max_positions
+// on this context (the split it would pick), in bytes; 0 when it would refuse.
+size_t attend_rows_need_bytes(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, size_t max_positions, size_t nb);
 // The rows of one sequence's pass (Rows::Following): queries q [nb][n_head][hd]
 // normed and rotated in place, keys k [nb][n_kv][hd] normed, rotated and
 // written with the values v into each row's cache at rows[i].L - 1.

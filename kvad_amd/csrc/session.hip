@@ -377,7 +377,10 @@ struct RowsBuf {
     size_t ws_bytes, bytes;
 };
 
-RowsBuf rows_layout(const kh_llm_spec &s, size_t cap, char *base) {
+// forward_each's buffers (pass = false), or a prompt pass's (pass = true):
+// no per-row logits or argmax partials (the head reads the last row alone)
+// and no attention workspace, which a pass sizes per launch (pass_ws).
+RowsBuf rows_layout(const kh_llm_spec &s, size_t cap, char *base, bool pass = false) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
         char *p = base ? base + off : nullptr;
@@ -395,16 +398,17 @@ RowsBuf rows_layout(const kh_llm_spec &s, size_t cap, char *base) {
     b.v = reinterpret_cast<float *>(take(4 * cap * kvd));
     b.g = reinterpret_cast<float *>(take(4 * cap * s.n_ff));
     b.u = reinterpret_cast<float *>(take(4 * cap * s.n_ff));
-    b.logits = reinterpret_cast<float *>(take(4 * cap * s.vocab));
-    b.pv = reinterpret_cast<float *>(take(4 * cap * ARGMAX_BLOCKS));
-    b.pi = reinterpret_cast<int *>(take(4 * cap * ARGMAX_BLOCKS));
+    const size_t lr = pass ? 0 : cap;  // rows with logits of their own
+    b.logits = reinterpret_cast<float *>(take(4 * lr * s.vocab));
+    b.pv = reinterpret_cast<float *>(take(4 * lr * ARGMAX_BLOCKS));
+    b.pi = reinterpret_cast<int *>(take(4 * lr * ARGMAX_BLOCKS));
     b.tok = reinterpret_cast<int32_t *>(take(4 * cap));
-    b.next = reinterpret_cast<int32_t *>(take(4 * cap));
+    b.next = reinterpret_cast<int32_t *>(take(4 * lr));
     b.tab = reinterpret_cast<AttnRow *>(take(sizeof(AttnRow) * cap * s.n_layer));
     b.qa.qs = reinterpret_cast<int8_t *>(take(cap * wide));
     b.qa.scales = reinterpret_cast<float *>(take(4 * nb));
     b.qa.sums = reinterpret_cast<int32_t *>(take(4 * nb));
-    b.ws_bytes = attend_rows_ws_bytes((int)s.n_head, (int)s.head_dim, s.n_ctx, cap);
+    b.ws_bytes = pass ? 0 : attend_rows_ws_bytes((int)s.n_head, (int)s.head_dim, s.n_ctx, cap);
     b.ws = take(b.ws_bytes);
     b.bytes = off;
     return b;
@@ -429,6 +433,30 @@ int ensure_rows(kh_llm *m, size_t n) {
     m->rows_cap = 0;
     KH_HIP(hipMalloc(&m->rows_buf, rows_layout(m->spec, cap, nullptr).bytes));
     m->rows_cap = cap;
+    return KH_OK;
+}
+
+// A prompt pass's rows (n of them) and its attention's partials for a launch
+// of at most max_len positions; growing either drops the captured passes,
+// which name the old buffers.
+int ensure_pass(kh_llm *m, size_t n, size_t max_len) {
+    kh_ctx *ctx = m->ctx;
+    if (n > m->pass_cap) {
+        const size_t cap = (n + 7) / 8 * 8;
+        KH_HIP(hipStreamSynchronize(ctx->stream));
+        drop_rows_graphs(m);
+        if (m->pass_buf) (void)hipFree(m->pass_buf);
+        m->pass_buf = nullptr;
+        m->pass_cap = 0;
+        KH_HIP(hipMalloc(&m->pass_buf, rows_layout(m->spec, cap, nullptr, true).bytes));
+        m->pass_cap = cap;
+    }
+    const kh_llm_spec &s = m->spec;
+    const size_t need = attend_rows_need_bytes(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, max_len, n);
+    if (need > m->pass_ws.bytes) {
+        drop_rows_graphs(m);
+        return ensure(ctx, m->pass_ws, need);
+    }
     return KH_OK;
 }
 
@@ -678,12 +706,17 @@ int replay_steps(kh_ctx *ctx, kh_llm *m, size_t n) {
 // Session::prefill_pass (model/mod.rs:866; CpuSession :1181-1183): whole
 // chunks from the front, what is left over last.  The chunk is
 // KVAD_PREFILL_CHUNK (the reference's knob, mod.rs:1004-1006) unless the
-// caller set one (CpuSession::reading, :1079-1082).
+// caller set one (CpuSession::reading, :1079-1082), else DEFAULT_PASS: the
+// reference's GPU backend reads 512 a pass (gpu/src/model.rs:892-897), and
+// here a 640-token Qwen2.5-0.5B prompt takes 27 ms in passes of 64, 10 ms
+// in passes of 256 and 6.4 ms in one pass (each pass is some 340 launches
+// whatever its width, and wider passes give the GEMMs wider tiles).
+constexpr size_t DEFAULT_PASS = 512;
 size_t pass_len(const kh_llm *m, size_t left) {
     size_t c = m->chunk;
     if (!c) {
         const int v = env_int("KVAD_PREFILL_CHUNK", 0);
-        c = v > 0 ? (size_t)v : 64;
+        c = v > 0 ? (size_t)v : DEFAULT_PASS;
     }
     c = std::min<size_t>(c, 65535);
     return std::min(left, c);
@@ -727,11 +760,13 @@ int run_pass(kh_ctx *ctx, kh_llm *m, const int32_t *tokens, size_t n, const kh_l
         m->len += 1;
         return KH_OK;
     }
-    if ((rc = ensure_rows(m, n))) return rc;
-    const RowsBuf b = rows_layout(m->spec, m->rows_cap, static_cast<char *>(m->rows_buf));
+    const size_t bm = pass_bucket(m, m->len + n);
+    if ((rc = ensure_pass(m, n, bm))) return rc;
+    RowsBuf b = rows_layout(m->spec, m->pass_cap, static_cast<char *>(m->pass_buf), true);
+    b.ws = m->pass_ws.ptr;
+    b.ws_bytes = m->pass_ws.bytes;
     size_t tok_bytes, tab_bytes;
     pass_table(m, tokens, n, tok_bytes, tab_bytes);
-    const size_t bm = pass_bucket(m, m->len + n);
     // the head's tail advances the position past the last row
     const int32_t st[3] = {tokens[n - 1], (int32_t)(m->len + n - 1), 0};
     KH_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, ctx->stream));
@@ -844,6 +879,8 @@ int kh_llm_free(kh_llm *m) {
         }
         for (kh_llm_parked *p : m->parked) p->owner = nullptr;  // theirs now, freed with the handle
         if (m->rows_buf) (void)hipFree(m->rows_buf);
+        if (m->pass_buf) (void)hipFree(m->pass_buf);
+        if (m->pass_ws.ptr) (void)hipFree(m->pass_ws.ptr);
         for (auto &L : m->layers)
             for (float *p : {L.attn_norm, L.mlp_norm, L.q_b, L.k_b, L.v_b, L.q_norm, L.k_norm})
                 if (p) (void)hipFree(p);

@@ -90,7 +90,8 @@ def test_a_prompt_read_a_pass_at_a_time_is_the_prompt_read_at_once(ctx, variant)
 def test_prefill_pass_cuts_whole_chunks_from_the_front(ctx, monkeypatch):
     say("prefill_pass")
     m, _ = build(ctx, 301)
-    assert [m.prefill_pass(n) for n in (1, 63, 64, 65, 200)] == [1, 63, 64, 64, 64]  # the default, 64
+    # the default: 512 a pass, the reference's GPU backend's chunk (gpu/src/model.rs:897)
+    assert [m.prefill_pass(n) for n in (1, 63, 512, 513, 2000)] == [1, 63, 512, 512, 512]
     m.reading(5)
     assert [m.prefill_pass(n) for n in (23, 5, 3, 0)] == [5, 5, 3, 0]
     m.reading(0)
@@ -136,11 +137,14 @@ def test_prefill_matches_the_oracle(ctx, monkeypatch, case):
     say("prefill vs oracle worst", case, f"{worst:.2e}")
 
 
-def test_a_prompt_past_the_single_split_line(ctx):
+@pytest.mark.parametrize("chunk", [64, 512])
+def test_a_prompt_past_the_single_split_line(ctx, chunk):
     # 300 positions at head_dim 64: passes of 64 rows whose attention runs as
-    # one split up to 256 positions and split + merged past them
-    say("prefill past the single split")
+    # one split up to 256 positions and split + merged past them, or one pass
+    # of 300 rows
+    say("prefill past the single split", chunk)
     m, mk = build(ctx, 320, n_layer=1, n_ctx=512)
+    m.reading(chunk)
     ref = mk()
     prompt = [(i * 11 + 2) % 512 for i in range(300)]
     logits, nxt = m.forward_tokens(prompt)
