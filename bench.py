@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-column-seconds", type=float, default=0.6,
+                    help="bound on each secondary figure's CPU column (the oracle beside it)")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary (q8, attention) figures")
     ap.add_argument("--only", choices=SECTIONS, default=None,
                     help="run one secondary workload alone (for per-kernel rocprofv3 summaries) and print its figures")
@@ -164,7 +166,8 @@ def main() -> int:
         return 0
 
     if args.only:
-        res = secondary(torch, K, ctx, stream, dev, gen, args, only=args.only)
+        rig = None if args.no_cpu else CpuRig(args.cpu_column_seconds)
+        res = secondary(torch, K, ctx, stream, dev, gen, args, only=args.only, rig=rig)
         print(json.dumps({"section": args.only, "n_gpus": 1, "data": "synthetic", "extra": res}), flush=True)
         ctx.set_stream(None)
         return 0
@@ -287,13 +290,14 @@ def main() -> int:
 
     extra = {"q4k_gemv_per_shape": per_shape, "weight_bytes_resident": weight_bytes,
              "q4k_dequant_step": dequant_step, "q4k_batched_decode_llama3_8b": batched}
+    rig = None if args.no_cpu else CpuRig(args.cpu_column_seconds)
     if not args.no_extra:
-        extra.update(secondary(torch, K, ctx, stream, dev, gen, args))
+        extra.update(secondary(torch, K, ctx, stream, dev, gen, args, rig=rig))
 
     # ---- CPU baseline: the oracle on the host's cores ---------------------
     cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(layers, args.cpu_seconds)
+    if rig is not None:
+        cpu = cpu_baseline(layers, args.cpu_seconds, rig)
 
     result = {
         "metric": "Q4_K GEMV achieved GB/s at Llama-3-8B shapes (single-token decode)",
@@ -341,34 +345,59 @@ def measured_traffic():
 SECTIONS = ("q8", "prefill", "moe", "decode", "attend", "mla", "qcache", "session_prefill")
 
 
-def secondary(torch, K, ctx, stream, dev, gen, args, only=None):
+def secondary(torch, K, ctx, stream, dev, gen, args, only=None, rig=None):
     """The other configs as extra figures: BASELINE configs[0] (Q8 GEMV at
     Qwen2.5-0.5B shapes), [2] (prefill GEMM), [3] (decode attention), [4]
-    (MoE) and the Qwen2.5-0.5B q8 decode session.  `only` picks one."""
+    (MoE) and the Qwen2.5-0.5B q8 decode session.  `only` picks one.  With a
+    CpuRig each figure carries a "cpu" entry: the oracle on the host's cores,
+    timed in the same run."""
     out = {}
     want = lambda name: only is None or only == name
     if want("q8"):
-        out.update(q8_qwen(torch, K, ctx, stream, dev, gen, args))
+        out.update(q8_qwen(torch, K, ctx, stream, dev, gen, args, rig))
     if want("prefill"):
-        out["prefill_gemm"] = prefill(torch, K, ctx, stream, dev, gen, args)
+        out["prefill_gemm"] = prefill(torch, K, ctx, stream, dev, gen, args, rig)
     if want("moe"):
-        out["moe_deepseek_v2_lite"] = moe(torch, K, ctx, stream, dev, gen, args)
+        out["moe_deepseek_v2_lite"] = moe(torch, K, ctx, stream, dev, gen, args, rig=rig)
     if want("decode"):
-        out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args)
+        out["qwen05b_q8_decode"] = decode(torch, K, ctx, stream, dev, gen, args, rig=rig)
     if only == "session_prefill":  # the prompt passes alone (inside "decode" otherwise)
-        m = qwen05b_session(torch, K, ctx, stream, dev, gen)
-        out["qwen05b_q8_prefill"] = prefill_session(m)
+        m, host = qwen05b_session(torch, K, ctx, stream, dev, gen)
+        out["qwen05b_q8_prefill"] = prefill_session(m, rig=rig, host=host)
         m.free()
     if want("attend"):
-        out["attend_qwen05b"] = attend(torch, K, ctx, stream, dev, gen, args)
+        out["attend_qwen05b"] = attend(torch, K, ctx, stream, dev, gen, args, rig)
     if want("mla"):
-        out["mla_deepseek_v2_lite"] = mla(torch, K, ctx, stream, dev, gen, args)
+        out["mla_deepseek_v2_lite"] = mla(torch, K, ctx, stream, dev, gen, args, rig)
     if want("qcache"):
         out["qcache_upload"] = qcache_upload(K, ctx)
     return out
 
 
-def mla(torch, K, ctx, stream, dev, gen, args):
+def mla_cpu(rig, H, L):
+    """The oracle's absorbed latent attention (deepseek.rs:553-591, parallel
+    over heads) on the host, over layers of distinct latent caches."""
+    O = rig.O
+    per = 4 * L * 576
+    nl = rig.layers_past_llc(per, hi=8)
+    rng = np.random.default_rng(L)
+    c = rng.standard_normal((nl, L, 512), dtype=np.float32)
+    pe = rng.standard_normal((nl, L, 64), dtype=np.float32)
+    ql = rng.standard_normal(H * 512, dtype=np.float32)
+    qp = rng.standard_normal(H * 64, dtype=np.float32)
+    b = per + 4 * H * (512 + 64 + 512)
+
+    def make(lib, nt):
+        def run():
+            for l in range(nl):
+                O.mla_attend(H, 512, 64, ql, qp, c[l], pe[l], L, 1.0 / 192 ** 0.5, L=lib)
+        return run, nl, None
+
+    return rig.columns(make, lambda s, n: {"us_per_layer": round(s / n * 1e6, 2), "GBps": round(b * n / s / 1e9, 2),
+                                           "working_set_MB": round(nl * per / 1e6, 1)})
+
+
+def mla(torch, K, ctx, stream, dev, gen, args, rig=None):
     """Absorbed latent attention (model/deepseek.rs:553-591) at DeepSeek-V2-Lite
     geometry: 16 heads, latent 512, rope 64, over nl layers of distinct caches
     ~ N(0, 1); bytes = every cached row (576 floats) read once, plus the
@@ -395,6 +424,8 @@ def mla(torch, K, ctx, stream, dev, gen, args):
                        "TFLOPS": round(2 * H * (576 + 512) * L / s / 1e12, 2), "layers": nl,
                        "memory": "HBM" if nl * 4 * L * 576 > 2 * 256 * 2**20 else "cache-resident (<= 2x 256 MB)"}
         del g, c, pe
+        if rig is not None and L == 32768:
+            res[str(L)]["cpu"] = mla_cpu(rig, H, L)
     log(f"mla: {res}")
     return res
 
@@ -464,7 +495,27 @@ def qcache_upload(K, ctx, n_mats=16, rows=14336, cols=4096):
     return res
 
 
-def q8_qwen(torch, K, ctx, stream, dev, gen, args):
+def q8_ffn_cpu(rig, qlayers, fb):
+    """Weight::matvec_bt's q8 path (QActivation, qrow per row, quant.rs:410-512)
+    on the host over the same 72 FFN matrices (copied back from the device,
+    354.7 MB), one call each, as the device figure beside it."""
+    O = rig.O
+    mats = []
+    for L in qlayers:
+        for name, (rows, cols) in (("gate", (4864, 896)), ("up", (4864, 896)), ("down", (896, 4864))):
+            s8, q8 = L[name].parts()
+            mats.append((s8, q8, rows, cols, L["m" if name == "down" else "h"].cpu().numpy()))
+
+    def make(lib, nt):
+        def run():
+            for s8, q8, rows, cols, x in mats:
+                O.matvec_q8(s8, q8, rows, cols, x, L=lib)
+        return run, len(mats), None
+
+    return rig.columns(make, lambda s, n: {"us_per_gemv": round(s / n * 1e6, 2), "GBps": round(fb / s / 1e9, 2)})
+
+
+def q8_qwen(torch, K, ctx, stream, dev, gen, args, rig=None):
     """Q8 GEMV at Qwen2.5-0.5B decode shapes, 24 layers
     of distinct weights plus the 151936x896 lm_head."""
     out = {}
@@ -483,8 +534,10 @@ def q8_qwen(torch, K, ctx, stream, dev, gen, args):
             qlayers.append(L)
         f = torch.randn(151936, 896, device=dev, generator=gen) * 0.02
         head = K.Weight.quantize_dev(ctx, 151936, 896, f.data_ptr(), K.Q8)
-        f = torch.randn(151936, 896, device=dev, generator=gen) * 0.02
-        head2 = K.Weight.quantize_dev(ctx, 151936, 896, f.data_ptr(), K.Q8)  # with head, past the 256 MB cache
+        heads = [head]
+        for _ in range(3):  # four copies in turn: 615 MB, past twice the 256 MB cache
+            f = torch.randn(151936, 896, device=dev, generator=gen) * 0.02
+            heads.append(K.Weight.quantize_dev(ctx, 151936, 896, f.data_ptr(), K.Q8))
         del f
         xh = torch.randn(896, device=dev, generator=gen)
         yh = torch.empty(151936, device=dev)
@@ -512,14 +565,14 @@ def q8_qwen(torch, K, ctx, stream, dev, gen, args):
     del g
 
     def head_only():
-        for i in range(8):  # two copies in turn: 307 MB, past the 256 MB cache
-            (head, head2)[i & 1].matvec_bt_dev(xh.data_ptr(), yh.data_ptr())
+        for i in range(8):
+            heads[i & 3].matvec_bt_dev(xh.data_ptr(), yh.data_ptr())
 
     g = Graph(torch, ctx, stream, head_only)
     s = g.time(args.steps, args.warmup) / 8
     out["q8_lm_head_151936x896"] = {"GBps": round(q8_bytes(151936, 896) / s / 1e9, 1), "us": round(s * 1e6, 2),
-                                    "rotation": "2 copies, 307.6 MB"}
-    del g
+                                    "rotation": f"4 copies, {4 * q8_bytes(151936, 896) / 1e6:.1f} MB"}
+    del g, heads
 
     def ffn_shapes():
         for L in qlayers:
@@ -532,6 +585,8 @@ def q8_qwen(torch, K, ctx, stream, dev, gen, args):
     out["q8_qwen05b_ffn_single_launches"] = {"GBps": round(fb / s / 1e9, 1), "us_per_gemv": round(s / 72 * 1e6, 2),
                                              "rotation": f"72 matrices, {fb / 1e6:.1f} MB"}
     del g
+    if rig is not None:
+        out["q8_qwen05b_ffn_single_launches"]["cpu"] = q8_ffn_cpu(rig, qlayers, fb)
 
     # the dequantising kernel (Weight::matvec_bt_dequant, quant.rs:522-589)
     # beside the integer path on the same 72 matrices, one launch each
@@ -549,7 +604,30 @@ def q8_qwen(torch, K, ctx, stream, dev, gen, args):
     return out
 
 
-def attend(torch, K, ctx, stream, dev, gen, args):
+def attend_cpu(rig, nh, nkv, hd, L):
+    """model::attend (mod.rs:769-819, parallel over query heads) on the host:
+    per call every layer of `nl` distinct caches (twice the host LLC)."""
+    O = rig.O
+    kvd = nkv * hd
+    per = 2 * 4 * L * kvd
+    nl = rig.layers_past_llc(per)
+    rng = np.random.default_rng(L + nh)
+    ks = rng.standard_normal((nl, L, kvd), dtype=np.float32)
+    vs = rng.standard_normal((nl, L, kvd), dtype=np.float32)
+    q = rng.standard_normal(nh * hd, dtype=np.float32)
+    b = per + 8 * nh * hd
+
+    def make(lib, nt):
+        def run():
+            for l in range(nl):
+                O.attend(nh, nkv, hd, q, ks[l], vs[l], L, L=lib)
+        return run, nl, None
+
+    return rig.columns(make, lambda s, n: {"us_per_layer": round(s / n * 1e6, 2), "GBps": round(b * n / s / 1e9, 2),
+                                           "working_set_MB": round(nl * per / 1e6, 1)})
+
+
+def attend(torch, K, ctx, stream, dev, gen, args, rig=None):
     """GQA decode attention at Qwen2.5-0.5B geometry
     (14 query heads, 2 KV heads, head_dim 64) over 24 layers of distinct f32
     caches ~ N(0, 1); bytes = each K and V row read once, plus q and out."""
@@ -580,12 +658,47 @@ def attend(torch, K, ctx, stream, dev, gen, args):
                            "cache_MB": round(nl * per / 1e6, 1),
                            "memory": "HBM" if nl * per > 2 * 256 * 2**20 else "cache-resident (<= 2x 256 MB)"}
             del g, kv
+            if rig is not None and L >= (8192 if nh == 14 else 2048):  # the lengths the HBM figures are quoted at
+                res[str(L)]["cpu"] = attend_cpu(rig, nh, nkv, hd, L)
         att["qwen05b_14_2_64" if nh == 14 else "llama8b_32_8_128"] = res
     log(f"attend: {att}")
     return att
 
 
-def prefill(torch, K, ctx, stream, dev, gen, args):
+def prefill_cpu(rig, m, k, n, prec):
+    """Weight::matmul_bt on the host (the oracle's x86 path: QActBatch, then
+    row_dot per row and token, quant.rs:751-907; f32: tensor::gemm_bt's 4 x 4
+    register tile, tensor.rs:102-193), with the activation quantisation inside
+    the call as the reference has it.  The large shape runs a sample of its
+    output rows (and, on one thread, of its tokens): the same loop, fewer rows;
+    the (512, 896, 4864) shape runs whole on all threads and at 64 tokens
+    (the reference's own m-sweep size) on one."""
+    O = rig.O
+    rng = np.random.default_rng(m + n)
+    big = m * n * k > 4e9
+    n_all, n_one = (512, 256) if big else (n, n)
+    m_all, m_one = (m, 128) if big else (m, 64)
+    w = (rng.standard_normal((n_all, k), dtype=np.float32) * 0.02).ravel()
+    xs = rng.standard_normal((m_all, k), dtype=np.float32).ravel()
+    wq = O.quantize_q8(w, n_all, k) if prec == "q8" else None
+
+    def make(lib, nt):
+        mm, nn = (m_all, n_all) if nt > 1 else (m_one, n_one)
+        x = xs[:mm * k]
+        if prec == "q8":
+            s8, q8 = wq
+            s8, q8 = s8[:nn * k // 32], q8[:nn * k]
+            run = lambda: O.matmul_q8(s8, q8, nn, k, x, mm, L=lib)
+        else:
+            wf = w[:nn * k]
+            run = lambda: O.matmul_f32(wf, nn, k, x, mm, L=lib)
+        note = None if (mm, nn) == (m, n) else f"{mm} tokens x {nn} of {n} output rows"
+        return run, 2 * mm * nn * k, note
+
+    return rig.columns(make, lambda s, ops: {"GOPS": round(ops / s / 1e9, 2), "ms_per_call": round(s * 1e3, 3)})
+
+
+def prefill(torch, K, ctx, stream, dev, gen, args, rig=None):
     """batched-prefill GEMM, q8 (int8 MFMA) and f32
     (f32 MFMA), at (M, K, N) = (512, 896, 4864) and (2048, 4096, 14336).
     Each call is Weight::matmul_bt on device pointers: the activation
@@ -613,6 +726,8 @@ def prefill(torch, K, ctx, stream, dev, gen, args):
                                           "frac_of_mfma_peak": round(tops / peak, 4),
                                           "peak": f"{peak} T{'OP' if prec == 'q8' else 'FLOP'}/s"}
             del g, w
+            if rig is not None:
+                res[f"{prec}_{m}x{k}x{n}"]["cpu"] = prefill_cpu(rig, m, k, n, prec)
         del f, xs, y
     # the reference's sweep over the batch (docs/engine.md:663-669): mlp.down
     # [896 x 4864], q8, m = 2..128; up to 8 rows take the multi-token GEMV
@@ -643,7 +758,7 @@ def prefill(torch, K, ctx, stream, dev, gen, args):
     return res
 
 
-def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8):
+def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8, rig=None):
     """a DeepSeek-V2-Lite MoE layer at q8 (hidden 2048,
     64 experts of width 1408 + a fused shared expert of width 2816, top-6
     softmax routing).  Decode: one token through n_layers distinct layers
@@ -658,13 +773,19 @@ def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8):
         return K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8)
 
     layers = []
+    first = None  # layer 0's weights, for the host's copy
     with torch.cuda.stream(stream):
         for _ in range(n_layers):
             m = K.Moe(ctx, n_exp, k, hidden, inter)
-            m.set_router(q8(n_exp, hidden, 0.5))
+            ws = {"router": q8(n_exp, hidden, 0.5), "experts": [], "shared": None}
+            m.set_router(ws["router"])
             for x in range(n_exp):
-                m.set_expert(x, q8(inter, hidden), q8(inter, hidden), q8(hidden, inter))
-            m.set_shared(q8(sh, hidden), q8(sh, hidden), q8(hidden, sh))
+                e3 = (q8(inter, hidden), q8(inter, hidden), q8(hidden, inter))
+                m.set_expert(x, *e3)
+                ws["experts"].append(e3)
+            ws["shared"] = (q8(sh, hidden), q8(sh, hidden), q8(hidden, sh))
+            m.set_shared(*ws["shared"])
+            first = first or ws
             layers.append((m, torch.randn(hidden, device=dev, generator=gen), torch.empty(hidden, device=dev)))
     torch.cuda.synchronize()
 
@@ -695,8 +816,48 @@ def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8):
     ops = 2 * M * k * 3 * inter * hidden + 2 * M * 3 * sh * hidden
     res["prefill_512tok"] = {"us": round(s * 1e6, 1), "TOPS": round(ops / s / 1e12, 2), "ops": ops}
     del g
+    if rig is not None:
+        moe_cpu(rig, res, first, m0, hidden, inter, n_exp, k, sh, tok_bytes, ops)
     log(f"moe: {res}")
     return res
+
+
+def moe_cpu(rig, res, ws, dev_layer, hidden, inter, n_exp, top_k, sh, tok_bytes, ops512):
+    """Moe::run (ffn.rs:615-708, the oracle's restatement) on the host with
+    layer 0's weights copied back from the device (0.64 GB): decode over 16
+    tokens in turn (each routes to its own six experts, so the calls stream
+    most of the layer), and the 512-token prefill (64 tokens on one thread).
+    A parity spot check of the device layer against it rides along."""
+    O = rig.O
+    cat = lambda i: tuple(np.concatenate(a) for a in zip(*[e[i].parts() for e in ws["experts"]]))
+    router, gate, up, down = ws["router"].parts(), cat(0), cat(1), cat(2)
+    shared = tuple(w.parts() for w in ws["shared"]) + (sh,)
+    rng = np.random.default_rng(64)
+    toks = rng.standard_normal((512, hidden), dtype=np.float32)
+
+    def layer(x, m, lib):
+        return O.moe_run_q8(x, m, hidden, inter, n_exp, top_k, router, gate, up, down, shared=shared, L=lib)
+
+    want = layer(toks[0], 1, rig.native)
+    got = dev_layer.run(toks[0], 1)
+    res["decode_1tok"]["rel_err_vs_oracle"] = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+
+    def make_dec(lib, nt):
+        def run():
+            for i in range(16):
+                layer(toks[i], 1, lib)
+        return run, 16, None
+
+    res["decode_1tok"]["cpu"] = rig.columns(make_dec, lambda s, n: {"us_per_layer": round(s / n * 1e6, 1),
+                                                                     "GBps": round(tok_bytes * n / s / 1e9, 2)})
+
+    def make_pre(lib, nt):
+        mm = 512 if nt > 1 else 64
+        run = lambda: layer(toks[:mm], mm, lib)
+        return run, ops512 * mm // 512, None if mm == 512 else f"{mm} of the 512 tokens"
+
+    res["prefill_512tok"]["cpu"] = rig.columns(make_pre, lambda s, o: {"GOPS": round(o / s / 1e9, 2),
+                                                                        "ms_per_call": round(s * 1e3, 2)})
 
 
 def qwen05b_session(torch, K, ctx, stream, dev, gen, n_ctx=2048):
@@ -712,30 +873,49 @@ def qwen05b_session(torch, K, ctx, stream, dev, gen, n_ctx=2048):
         return K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8)
 
     ones = np.ones(e, np.float32)
+    layers = []
     with torch.cuda.stream(stream):
         m = K.Llm(ctx, **spec)
         rng = np.random.default_rng(0)
         for l in range(24):
-            m.set_layer(l, q8(qd, e), q8(kvd, e), q8(kvd, e), q8(e, qd), q8(ff, e), q8(ff, e), q8(e, ff), ones, ones,
-                        (rng.standard_normal(qd) * 0.02).astype(np.float32),
-                        (rng.standard_normal(kvd) * 0.02).astype(np.float32),
-                        (rng.standard_normal(kvd) * 0.02).astype(np.float32))
-        m.set_ends(q8(151936, e), ones)
+            L = {n: q8(r, c) for n, (r, c) in dict(q=(qd, e), k=(kvd, e), v=(kvd, e), o=(e, qd), gate=(ff, e),
+                                                    up=(ff, e), down=(e, ff)).items()}
+            L.update(attn_norm=ones, mlp_norm=ones, q_b=(rng.standard_normal(qd) * 0.02).astype(np.float32),
+                     k_b=(rng.standard_normal(kvd) * 0.02).astype(np.float32),
+                     v_b=(rng.standard_normal(kvd) * 0.02).astype(np.float32))
+            m.set_layer(l, *[L[n] for n in ("q", "k", "v", "o", "gate", "up", "down")], ones, ones, L["q_b"],
+                        L["k_b"], L["v_b"])
+            layers.append(L)
+        embed = q8(151936, e)
+        m.set_ends(embed, ones)
         half = 32
         inv = 1.0 / (1e6 ** (np.arange(half, dtype=np.float32) * 2.0 / 64))  # Rope::new, tensor.rs:390-407
         ang = np.arange(n_ctx, dtype=np.float32)[:, None] * inv[None, :].astype(np.float32)
-        m.set_rope(np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32), n_ctx)
+        cos_t, sin_t = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+        m.set_rope(cos_t, sin_t, n_ctx)
     torch.cuda.synchronize()
-    return m
+
+    def host(lib=None):
+        """The same model for the oracle (O.Llm), its weights copied back from
+        the device (0.51 GB), running its matmuls and attention on `lib`."""
+        import oracle as O
+
+        hl = []
+        for L in layers:
+            d = {n: (L[n].parts() if isinstance(L[n], K.Weight) else L[n]) for n in L}
+            hl.append(d)
+        return O.Llm(spec, hl, embed.parts(), ones, None, cos_t.ravel(), sin_t.ravel(), L=lib)
+
+    return m, host
 
 
-def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256):
+def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256, rig=None):
     """The second half of BASELINE.json's metric: Qwen2.5-0.5B-shaped q8
     decode, tokens per second, on the device-resident session
     (qwen05b_session).  Greedy tokens, one HIP graph replay per token; `warm`
     tokens first, then `timed` tokens timed with HIP events on the session's
     stream (context warm..warm+timed)."""
-    m = qwen05b_session(torch, K, ctx, stream, dev, gen, n_ctx)
+    m, host = qwen05b_session(torch, K, ctx, stream, dev, gen, n_ctx)
     torch.cuda.synchronize()
     first = m.generate(1, warm)  # captures the step's graph
     torch.cuda.synchronize()
@@ -757,13 +937,44 @@ def decode(torch, K, ctx, stream, dev, gen, args, n_ctx=2048, warm=32, timed=256
            "vs_reference_cpu_q8_112tps": round(tps / 112.0, 2),
            "vs_reference_metal_q8_191tps": round(tps / 191.0, 2), "first_tokens": [int(t) for t in first[:4]]}
     log(f"qwen0.5b q8 decode: {res}")
-    res["prefill"] = prefill_session(m)
+    ref = None
+    if rig is not None:
+        ref = host(rig.native)
+        m.truncate(0)
+        got, _ = m.forward(1)
+        want = ref.forward(1)
+        res["rel_err_vs_oracle_first_token"] = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+        res["cpu"] = session_cpu(rig, host, ref)
+    res["prefill"] = prefill_session(m, rig=rig, host=host, ref=ref)
     res["batched"] = decode_batched(torch, m, warm)
     m.free()
     return res
 
 
-def prefill_session(m, n=640, reps=5):
+def session_cpu(rig, host, ref):
+    """The oracle's decoder (O.Llm: the forward of llama.rs:224-289 and the
+    head, sequenced in Python over the oracle's C kernels) on the host, one
+    token a call, over the same weights as the device session; the native
+    build's model is `ref`, the portable one is built here."""
+    models = {"native": ref}
+    if len(rig.builds) > 1:
+        models["portable"] = host(rig.builds[0][1])
+    else:
+        models = {"portable": ref}
+
+    def make(lib, nt):
+        mdl = models["native" if lib is rig.native and "native" in models else "portable"]
+
+        def run():
+            if mdl.len >= 1500:
+                mdl.len = 0
+            mdl.forward(7)
+        return run, 1, None
+
+    return rig.columns(make, lambda s, n: {"tok_per_s": round(n / s, 2), "ms_per_token": round(s / n * 1e3, 2)})
+
+
+def prefill_session(m, n=640, reps=5, rig=None, host=None, ref=None):
     """A prompt read on the device (Session::forward(&[u32]), mod.rs:842): n
     tokens from an empty cache, in passes of prefill_pass tokens (Rows::Following,
     llama.rs:224-289: the projections on the int8 GEMM, every row's attention
@@ -802,6 +1013,25 @@ def prefill_session(m, n=640, reps=5):
     d = out[f"chunk_{out['default_chunk']}"]["ms"] / 1e3
     out["vs_reference_smmla"] = round(1.20 / d, 1)
     m.truncate(0)
+    if rig is not None and host is not None:
+        # the oracle's forward_tokens (Rows::Following over the oracle's
+        # matmuls, passes of 64 as the CPU session reads, mod.rs:1004-1006);
+        # all threads: 128 of the 640 tokens, one thread: 64
+        ref = ref if ref is not None else host(rig.native)
+        native_only = [b for b in rig.builds if b[1] is rig.native]
+
+        def make(lib, nt):
+            k = 128 if nt > 1 else 64
+
+            def run():
+                ref.len = 0
+                ref.forward_tokens(prompt[:k], chunk=64)
+            return run, k, f"{k} of the {n} tokens"
+
+        out["cpu"] = rig.columns(make, lambda s, k: {"tok_per_s": round(k / s, 1),
+                                                     "s_for_640_at_this_rate": round(n * s / k, 2)},
+                                 builds=native_only)
+        ref.len = 0
     log(f"qwen0.5b q8 prefill: {out}")
     return out
 
@@ -865,12 +1095,16 @@ def _native_oracle(tmpdir: str):
 
 
 def _calibrated(fn, budget_s: float):
-    """bench_matvec.rs:24-50's protocol: three warm-ups, an iteration count
-    calibrated to about 0.1 s a round (at least one call: a call over these
-    working sets takes longer), best of five rounds; stops early when the
-    column's time budget is spent.  Seconds per call, rounds run."""
+    """bench_matvec.rs:24-50's protocol: three warm-ups (one when a call takes
+    more than 50 ms), an iteration count calibrated to about 0.1 s a round
+    (at least one call: a call over these working sets can take longer), best
+    of five rounds; stops early when the column's time budget is spent.
+    Seconds per call, rounds run."""
     t_end = time.perf_counter() + budget_s
-    for _ in range(3):
+    t = time.perf_counter()
+    fn()
+    if time.perf_counter() - t < 0.05:
+        fn()
         fn()
     t = time.perf_counter()
     fn()
@@ -886,7 +1120,59 @@ def _calibrated(fn, budget_s: float):
     return best, rounds
 
 
-def cpu_baseline(layers, budget_s: float):
+class CpuRig:
+    """The reference's CPU path restated (the oracle's C), timed on this
+    host's cores beside each device figure, in the same run: the portable
+    build (-O3, baseline x86-64, the reference's default target) and
+    -march=native, each on one thread and on all of the process's threads,
+    with bench_matvec.rs:24-50's protocol (_calibrated) under a per-column
+    time budget.  Working sets exceed the host's last-level cache where the
+    shape allows; a workload too long for the budget at one thread runs a
+    stated sample of itself (ops per second are what the columns compare)."""
+
+    def __init__(self, budget_s: float):
+        import tempfile
+
+        import oracle as O
+
+        self.O = O
+        self.tmp = tempfile.TemporaryDirectory()
+        try:
+            native = _native_oracle(self.tmp.name)
+        except Exception as e:  # no compiler on this host: the portable columns only
+            log(f"cpu oracle: no -march=native build ({e})")
+            native = None
+        self.builds = [("portable", O.lib)] + ([("native", native)] if native is not None else [])
+        self.native = native if native is not None else O.lib
+        self.threads = O.threads()
+        self.budget = budget_s
+        self.llc = _host_llc_bytes()
+
+    def columns(self, make, fmt, builds=None):
+        """make(lib, threads) -> (call, units per call, sample note or None);
+        fmt(seconds per call, units) -> the column's figures."""
+        cols = {}
+        for bname, lib in self.builds if builds is None else builds:
+            for nt in (1, self.threads):
+                lib.kvo_set_threads(nt)
+                fn, units, note = make(lib, nt)
+                sec, rounds = _calibrated(fn, self.budget)
+                col = fmt(sec, units)
+                col.update(threads=nt, rounds=rounds)
+                if note:
+                    col["sample"] = note
+                cols[f"{bname}_{nt}t"] = col
+            lib.kvo_set_threads(self.threads)
+        cols["host"] = {"cpu": cpu_model(), "threads": self.threads, "llc_MiB": round(self.llc / 2**20, 1)}
+        return cols
+
+    def layers_past_llc(self, per_layer: int, lo: int = 1, hi: int = 64) -> int:
+        """Distinct copies that make a working set of twice the host LLC."""
+        need = 2 * max(self.llc, 32 << 20)
+        return max(lo, min(hi, -(-need // max(per_layer, 1))))
+
+
+def cpu_baseline(layers, budget_s: float, rig: "CpuRig"):
     """The reference's CPU path restated (the oracle), timed on this host's
     cores: the Q4_K GEMV over the bench's own Llama-3-8B layers (the loop that
     decodes scales once per sub-block, equal to the oracle to the bit), and
@@ -897,8 +1183,6 @@ def cpu_baseline(layers, budget_s: float):
     and eight layers (985 MB) on all threads, so every thread group's share
     exceeds its last-level cache; q8 likewise over 1 and 7 copies of the
     153 MB head."""
-    import tempfile
-
     import numpy as np
 
     import oracle as O
@@ -911,51 +1195,45 @@ def cpu_baseline(layers, budget_s: float):
     threads = O.threads()
     per_col = max(2.0, budget_s / 6)
     cols = {}
-    with tempfile.TemporaryDirectory() as tmp:
-        try:
-            native = _native_oracle(tmp)
-        except Exception as e:  # no compiler on this host: the portable columns only
-            log(f"cpu oracle: no -march=native build ({e})")
-            native = None
-        builds = [("portable", O.lib)] + ([("native", native)] if native is not None else [])
+    builds = rig.builds
 
-        def q4k_pass(lib, nl):
-            def run():
-                for i in range(nl):
-                    for n in names:
-                        rows, cols_ = LLAMA_LAYER[n]
-                        O.matvec_q4k_fast(parts[i][n], rows, cols_, xs[i][n], L=lib)
-            return run
+    def q4k_pass(lib, nl):
+        def run():
+            for i in range(nl):
+                for n in names:
+                    rows, cols_ = LLAMA_LAYER[n]
+                    O.matvec_q4k_fast(parts[i][n], rows, cols_, xs[i][n], L=lib)
+        return run
 
-        layer_bytes = sum(q4k_bytes(*LLAMA_LAYER[n]) for n in names)
-        for bname, lib in builds:
-            for nt, nl in ((1, 1), (threads, nl_all)):
-                lib.kvo_set_threads(nt)
-                sec, rounds = _calibrated(q4k_pass(lib, nl), per_col)
-                cols[f"q4k_{bname}_{nt}t"] = {"GBps": round(nl * layer_bytes / sec / 1e9, 2), "threads": nt,
-                                              "working_set_MB": round(nl * layer_bytes / 1e6, 1), "rounds": rounds}
-            lib.kvo_set_threads(threads)
+    layer_bytes = sum(q4k_bytes(*LLAMA_LAYER[n]) for n in names)
+    for bname, lib in builds:
+        for nt, nl in ((1, 1), (threads, nl_all)):
+            lib.kvo_set_threads(nt)
+            sec, rounds = _calibrated(q4k_pass(lib, nl), per_col)
+            cols[f"q4k_{bname}_{nt}t"] = {"GBps": round(nl * layer_bytes / sec / 1e9, 2), "threads": nt,
+                                          "working_set_MB": round(nl * layer_bytes / 1e6, 1), "rounds": rounds}
+        lib.kvo_set_threads(threads)
 
-        # q8: the lm_head shape, host-side weights ~ N(0, 0.02)
-        hr, hc = 151936, 896
-        s8, q8 = O.quantize_q8(O.normal(900, hr * hc, 0.02), hr, hc)
-        heads = [(s8, q8)] + [(s8.copy(), q8.copy()) for _ in range(6)]  # distinct memory, same values
-        xh = O.normal(950, hc)
-        head_bytes = q8_bytes(hr, hc)
-        for bname, lib in builds:
-            for nt, nh in ((1, 1), (threads, len(heads))):
-                lib.kvo_set_threads(nt)
+    # q8: the lm_head shape, host-side weights ~ N(0, 0.02)
+    hr, hc = 151936, 896
+    s8, q8 = O.quantize_q8(O.normal(900, hr * hc, 0.02), hr, hc)
+    heads = [(s8, q8)] + [(s8.copy(), q8.copy()) for _ in range(6)]  # distinct memory, same values
+    xh = O.normal(950, hc)
+    head_bytes = q8_bytes(hr, hc)
+    for bname, lib in builds:
+        for nt, nh in ((1, 1), (threads, len(heads))):
+            lib.kvo_set_threads(nt)
 
-                def run(lib=lib, nh=nh):
-                    for s8, q8 in heads[:nh]:
-                        O.matvec_q8(s8, q8, hr, hc, xh, L=lib)
-                sec, rounds = _calibrated(run, per_col / 2)
-                cols[f"q8_lm_head_{bname}_{nt}t"] = {"GBps": round(nh * head_bytes / sec / 1e9, 2), "threads": nt,
-                                                     "ms_per_call": round(sec / nh * 1e3, 3),
-                                                     "working_set_MB": round(nh * head_bytes / 1e6, 1),
-                                                     "rounds": rounds}
-            lib.kvo_set_threads(threads)
-        del heads
+            def run(lib=lib, nh=nh):
+                for s8, q8 in heads[:nh]:
+                    O.matvec_q8(s8, q8, hr, hc, xh, L=lib)
+            sec, rounds = _calibrated(run, per_col / 2)
+            cols[f"q8_lm_head_{bname}_{nt}t"] = {"GBps": round(nh * head_bytes / sec / 1e9, 2), "threads": nt,
+                                                 "ms_per_call": round(sec / nh * 1e3, 3),
+                                                 "working_set_MB": round(nh * head_bytes / 1e6, 1),
+                                                 "rounds": rounds}
+        lib.kvo_set_threads(threads)
+    del heads
 
     # parity spot check: the oracle and the device on the same weights and input
     y0 = O.matvec_q4k(parts[0]["o"], 4096, 4096, xs[0]["o"])

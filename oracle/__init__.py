@@ -393,67 +393,97 @@ def moe_run_q8(hs, m: int, hidden: int, inter: int, n_exp: int, top_k: int, rout
 
 
 class Llm:
-    """A Llama-family decoder on the CPU for one token at a time: the forward
-    of crates/llm/src/model/llama.rs:224-289 (run_rows, m = 1) between the
-    embedding and the head (llama.rs:384-415), every operator the oracle's.
+    """A Llama-family decoder on the CPU: the forward of
+    crates/llm/src/model/llama.rs:224-289 between the embedding and the head
+    (llama.rs:384-415), every operator the oracle's -- one token at a time
+    (forward: run_rows with m = 1) or a prompt's pass (forward_rows:
+    Transformer::forward_batch, model/mod.rs:544-549, i.e. run_rows with
+    Rows::Following over m rows and the head over the last one).
     Weights are q8 (scales, qs) pairs, 1-tuples (f32 data,) -- Precision::F32,
     tensor::matvec_bt (tensor.rs:56-79) -- ("q4k", blocks) for Q4_K layer
     weights (matvec_q4k) or ("q4", scales, qs) for q4 ones (matvec_q4); norms
-    and biases f32 arrays."""
+    and biases f32 arrays.  `L` is the oracle build its matmuls and attention
+    run on (the portable one by default)."""
 
-    def __init__(self, spec: dict, layers: list, embed, final_norm, lm_head=None, cos_t=None, sin_t=None):
+    def __init__(self, spec: dict, layers: list, embed, final_norm, lm_head=None, cos_t=None, sin_t=None, L=None):
         self.s, self.layers, self.embed, self.final_norm = spec, layers, embed, final_norm
         self.head = lm_head if lm_head is not None else embed
         self.cos, self.sin = cos_t, sin_t
+        self.L = L
         kvd = spec["n_kv_head"] * spec["head_dim"]
         self.kc = [np.zeros((spec["n_ctx"], kvd), np.float32) for _ in layers]
         self.vc = [np.zeros((spec["n_ctx"], kvd), np.float32) for _ in layers]
         self.len = 0
 
+    def _mm(self, w, rows, cols, xs, m, bias=None):
+        """Weight::matmul_bt (quant.rs:751; m == 1 is matvec_bt, :767-769)."""
+        L = self.L
+        if len(w) == 1:
+            return matmul_f32(w[0], rows, cols, xs, m, bias, L=L)
+        if isinstance(w[0], str) and w[0] == "q4k":
+            return matmul_q4k(w[1], rows, cols, xs, m, bias, L=L)
+        if isinstance(w[0], str) and w[0] == "q4":
+            return matmul_q4(w[1], w[2], rows, cols, xs, m, bias, L=L)
+        return matmul_q8(*w, rows, cols, xs, m, bias, L=L)
+
+    def _row(self, token: int) -> np.ndarray:
+        e = self.s["n_embd"]
+        if len(self.embed) == 1:                                # Weight::row, llama.rs:384-391
+            return np.asarray(self.embed[0], np.float32).reshape(-1, e)[token].copy()
+        return row_q8(*self.embed, e, token)
+
     def forward(self, token: int) -> np.ndarray:
+        """One token at the next position; the logits."""
+        return self.forward_rows([token])
+
+    def forward_rows(self, tokens) -> np.ndarray:
+        """A pass of m tokens at the next positions (Rows::Following): every
+        projection one matmul over the m rows, each row normed, rotated and
+        pushed at its own position, each row attending over the cache up to
+        itself (llama.rs:249-271); the logits of the last row."""
         s = self.s
         e, hd, nh, nkv, eps = s["n_embd"], s["head_dim"], s["n_head"], s["n_kv_head"], s["eps"]
-        qd, kvd, half = nh * hd, nkv * hd, hd // 2
-        pos = self.len
-
-        def mv(w, rows, cols, x, bias=None):
-            if len(w) == 1:
-                return matvec_f32(w[0], rows, cols, x, bias)
-            if isinstance(w[0], str) and w[0] == "q4k":
-                return matvec_q4k(w[1], rows, cols, x, bias)
-            if isinstance(w[0], str) and w[0] == "q4":
-                return matvec_q4(w[1], w[2], rows, cols, x, bias)
-            return matvec_q8(*w, rows, cols, x, bias)
-
-        if len(self.embed) == 1:                                # Weight::row, llama.rs:384-391
-            x = np.asarray(self.embed[0], np.float32).reshape(-1, e)[token].copy()
-        else:
-            x = row_q8(*self.embed, e, token)
+        qd, kvd, half, ff = nh * hd, nkv * hd, hd // 2, s["n_ff"]
+        m, pos0 = len(tokens), self.len
+        assert pos0 + m <= s["n_ctx"], "context window is full"
+        xs = np.stack([self._row(int(t)) for t in tokens]).astype(np.float32)
         rope = rope_apply_interleaved if s.get("rope_interleaved") else rope_apply
-        for l, L in enumerate(self.layers):
-            h = rms_norm(x, L["attn_norm"], eps)
-            q = mv(L["q"], qd, e, h, L.get("q_b"))
-            k = mv(L["k"], kvd, e, h, L.get("k_b"))
-            v = mv(L["v"], kvd, e, h, L.get("v_b"))
-            for head in range(nh):
-                seg = q[head * hd:(head + 1) * hd]
-                if L.get("q_norm") is not None:
-                    seg = rms_norm(seg, L["q_norm"], eps)
-                q[head * hd:(head + 1) * hd] = rope(self.cos, self.sin, half, seg, pos)
-            for head in range(nkv):
-                seg = k[head * hd:(head + 1) * hd]
-                if L.get("k_norm") is not None:
-                    seg = rms_norm(seg, L["k_norm"], eps)
-                k[head * hd:(head + 1) * hd] = rope(self.cos, self.sin, half, seg, pos)
-            self.kc[l][pos], self.vc[l][pos] = k, v             # KvCache::push
-            a = attend(nh, nkv, hd, q, self.kc[l][:pos + 1].ravel(), self.vc[l][:pos + 1].ravel(), pos + 1)
-            x = (x + mv(L["o"], e, qd, a)).astype(np.float32)
-            h = rms_norm(x, L["mlp_norm"], eps)
-            g = mv(L["gate"], s["n_ff"], e, h)
-            u = mv(L["up"], s["n_ff"], e, h)
-            x = (x + mv(L["down"], e, s["n_ff"], swiglu(g, u))).astype(np.float32)
-        self.len += 1
-        return mv(self.head, s["vocab"], e, rms_norm(x, self.final_norm, eps))
+        for l, Lw in enumerate(self.layers):
+            hs = np.stack([rms_norm(xs[i], Lw["attn_norm"], eps) for i in range(m)])
+            q = self._mm(Lw["q"], qd, e, hs, m, Lw.get("q_b")).reshape(m, qd)
+            k = self._mm(Lw["k"], kvd, e, hs, m, Lw.get("k_b")).reshape(m, kvd)
+            v = self._mm(Lw["v"], kvd, e, hs, m, Lw.get("v_b")).reshape(m, kvd)
+            for i in range(m):                                  # llama.rs:251-257
+                pos = pos0 + i
+                for head in range(nh):
+                    seg = q[i, head * hd:(head + 1) * hd]
+                    if Lw.get("q_norm") is not None:
+                        seg = rms_norm(seg, Lw["q_norm"], eps)
+                    q[i, head * hd:(head + 1) * hd] = rope(self.cos, self.sin, half, seg, pos)
+                for head in range(nkv):
+                    seg = k[i, head * hd:(head + 1) * hd]
+                    if Lw.get("k_norm") is not None:
+                        seg = rms_norm(seg, Lw["k_norm"], eps)
+                    k[i, head * hd:(head + 1) * hd] = rope(self.cos, self.sin, half, seg, pos)
+                self.kc[l][pos], self.vc[l][pos] = k[i], v[i]   # KvCache::push
+            att = np.stack([attend(nh, nkv, hd, q[i], self.kc[l][:pos0 + i + 1].ravel(),
+                                   self.vc[l][:pos0 + i + 1].ravel(), pos0 + i + 1, L=self.L) for i in range(m)])
+            xs = (xs + self._mm(Lw["o"], e, qd, att, m).reshape(m, e)).astype(np.float32)
+            hs = np.stack([rms_norm(xs[i], Lw["mlp_norm"], eps) for i in range(m)])
+            g = self._mm(Lw["gate"], ff, e, hs, m).reshape(m, ff)
+            u = self._mm(Lw["up"], ff, e, hs, m).reshape(m, ff)
+            xs = (xs + self._mm(Lw["down"], e, ff, swiglu(g, u), m).reshape(m, e)).astype(np.float32)
+        self.len += m
+        return self._mm(self.head, s["vocab"], e, rms_norm(xs[m - 1], self.final_norm, eps), 1)
+
+    def forward_tokens(self, tokens, chunk: int = 64) -> np.ndarray:
+        """Session::forward (CpuSession, model/mod.rs:1149-1158): passes of
+        `chunk` tokens (KVAD_PREFILL_CHUNK's default, :1004-1006); the last
+        pass's logits."""
+        out = None
+        for at in range(0, len(tokens), chunk):
+            out = self.forward_rows(tokens[at:at + chunk])
+        return out
 
 
 def argmax(v) -> int:

@@ -838,3 +838,72 @@ def test_the_float64_composition_catches_a_wiring_slip(slip):
         L[slip] = np.zeros_like(L[slip])
     errs = _rel_errs(spec, layers, embed, final, cos_t, sin_t, oracle_layers=[layers[0], L])
     assert max(errs) > 1e-2, errs
+
+
+# ---- a prompt's pass (O.Llm.forward_rows, Rows::Following) -----------------
+
+
+def test_a_pass_of_rows_is_its_tokens_one_at_a_time_to_the_bit():
+    # On x86 Weight::matmul_bt runs row_dot, the same two passes as qrow, per
+    # (row, token) (quant.rs:751-907; the SMMLA pair path is aarch64-only,
+    # simd.rs:220-228), and attention, norms and RoPE are per row: a pass of
+    # m rows is its tokens one at a time, bit for bit, cache included.
+    spec, layers, embed, final, cos_t, sin_t = _two_layer_model(False)
+    one = O.Llm(spec, layers, embed, final, None, cos_t, sin_t)
+    rows = O.Llm(spec, layers, embed, final, None, cos_t, sin_t)
+    for t in TOKENS:
+        want = one.forward(t)
+    got = rows.forward_rows(TOKENS)
+    np.testing.assert_array_equal(got, want)
+    for l in range(spec["n_layer"]):
+        np.testing.assert_array_equal(rows.kc[l], one.kc[l])
+        np.testing.assert_array_equal(rows.vc[l], one.vc[l])
+    # and a prompt in passes of three (batched_decode.rs:261-290's shape)
+    passes = O.Llm(spec, layers, embed, final, None, cos_t, sin_t)
+    np.testing.assert_array_equal(passes.forward_tokens(TOKENS, chunk=3), want)
+    assert passes.len == rows.len == one.len == len(TOKENS)
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_a_pass_is_the_float64_composition(interleaved):
+    spec, layers, embed, final, cos_t, sin_t = _two_layer_model(interleaved)
+    want = _f64_llm(spec, layers, embed, final, embed, cos_t, sin_t, TOKENS)[-1]
+    got = O.Llm(spec, layers, embed, final, None, cos_t, sin_t).forward_rows(TOKENS)
+    err = float(np.max(np.abs(got.astype(np.float64) - want))) / float(np.max(np.abs(want)))
+    assert err <= 1e-5, err
+
+
+def test_a_pass_catches_a_row_attending_past_itself():
+    # a pass whose rows all attend over the whole pass (no causal mask) is
+    # caught by the float64 composition: the bar above is not loose enough to
+    # hide a wrong mask
+    spec, layers, embed, final, cos_t, sin_t = _two_layer_model(False)
+    want = _f64_llm(spec, layers, embed, final, embed, cos_t, sin_t, TOKENS)[-2]
+    ref = O.Llm(spec, layers, embed, final, None, cos_t, sin_t)
+    # the second-to-last token's logits with every row seeing the last row's key
+    ref.forward_rows(TOKENS)
+    ref.len = 0
+    m = len(TOKENS) - 1
+    # rerun the first m tokens over the full cache the previous pass left
+    bad = O.Llm(spec, layers, embed, final, None, cos_t, sin_t)
+    bad.kc, bad.vc = [k.copy() for k in ref.kc], [v.copy() for v in ref.vc]
+    orig_attend = O.attend
+
+    def leaky(nh, nkv, hd, q, kc, vc, n, L=None):
+        return orig_attend(nh, nkv, hd, q, bad.kc[leaky.layer][:len(TOKENS)].ravel(),
+                           bad.vc[leaky.layer][:len(TOKENS)].ravel(), len(TOKENS), L=L)
+
+    try:
+        calls = []
+
+        def counting(nh, nkv, hd, q, kc, vc, n, L=None):
+            leaky.layer = (len(calls) // m) % spec["n_layer"]
+            calls.append(n)
+            return leaky(nh, nkv, hd, q, kc, vc, n, L)
+
+        O.attend = counting
+        got = bad.forward_rows(TOKENS[:m])
+    finally:
+        O.attend = orig_attend
+    err = float(np.max(np.abs(got.astype(np.float64) - want))) / float(np.max(np.abs(want)))
+    assert err > 1e-2, err
