@@ -59,18 +59,17 @@ VARIANTS = {
 }
 
 
-@pytest.mark.parametrize("variant", list(VARIANTS))
-def test_each_stage_of_every_layer(ctx, variant):
-    say("llm stages", variant)
-    m, mk = build(ctx, 170, n_layer=3, **VARIANTS[variant])
-    ref = mk()  # for its weights, norms and tables only
+def check_stages(m, ref, tokens):
+    """Every stage of every layer of each token's step, on the device's own
+    inputs to that stage, at the bars above; the worst relative error per
+    stage."""
     s = ref.s
     e, hd, nh, nkv, eps = s["n_embd"], s["head_dim"], s["n_head"], s["n_kv_head"], s["eps"]
     qd, kvd, half, ff = nh * hd, nkv * hd, hd // 2, s["n_ff"]
     rope = O.rope_apply_interleaved if s.get("rope_interleaved") else O.rope_apply
     worst = {}
     note = lambda name, r: worst.__setitem__(name, max(worst.get(name, 0.0), r))
-    for pos, tok in enumerate([3, 17, 500, 42, 7, 7, 99]):
+    for pos, tok in enumerate(tokens):
         tr = m.trace(tok)
         np.testing.assert_array_equal(tr["x_embed"], O.row_q8(*ref.embed, e, tok), err_msg="embedding")
         x = tr["x_embed"]
@@ -109,4 +108,27 @@ def test_each_stage_of_every_layer(ctx, variant):
             x = tr["x_mlp"][l]
         logits = proj(ref.head, s["vocab"], e, O.rms_norm(x, ref.final_norm, eps))
         note("head", close(tr["logits"], logits, f"pos {pos} head"))
+    return worst
+
+
+@pytest.mark.parametrize("variant", list(VARIANTS))
+def test_each_stage_of_every_layer(ctx, variant):
+    say("llm stages", variant)
+    m, mk = build(ctx, 170, n_layer=3, **VARIANTS[variant])
+    worst = check_stages(m, mk(), [3, 17, 500, 42, 7, 7, 99])
     say("llm stages worst", variant, {k: f"{v:.1e}" for k, v in worst.items()})
+
+
+def test_each_stage_at_qwen05b_width_and_depth(ctx):
+    # Qwen2.5-0.5B's widths and depth (24 layers, 896 / 14 / 2 x 64 / 4864,
+    # q/k/v biases; a 4096-token vocabulary): every stage of every layer
+    # holds its bar at the size the benchmark runs, where the logits against
+    # the oracle's own chain drift further than at two layers (each
+    # requantised activation can take the neighbouring code; 24 layers of
+    # them compound): that drift is the chain's, not any stage's.
+    say("llm stages at Qwen2.5-0.5B width")
+    m, mk = build(ctx, 180, n_layer=24, n_embd=896, n_head=14, n_kv_head=2, head_dim=64, n_ff=4864, vocab=4096,
+                  n_ctx=64)
+    ref = mk()
+    worst = check_stages(m, ref, [3, 17, 500])
+    say("llm stages worst (Qwen width)", {k: f"{v:.1e}" for k, v in worst.items()})
