@@ -234,6 +234,38 @@ def main() -> int:
     achieved = step_bytes / sec / 1e9
     log(f"step: {sec * 1e3:.3f} ms, {achieved:.1f} GB/s, {avg_launch * 1e6:.2f} us per GEMV launch")
 
+    # ---- the structure's ceiling: the same 128 launches reading the same
+    # weight bytes with a plain streaming kernel (no activation, no
+    # arithmetic), its launch shape swept; the GEMV's step over it -------------
+    sink = torch.empty(4096, dtype=torch.int32, device=dev)
+    wbytes_step = sum(L[n].bytes for L in layers for n in LLAMA_LAYER)
+
+    def probe_step():
+        for L in layers:
+            K.stream_dev(ctx, [L["q"], L["k"], L["v"]], sink.data_ptr())
+            K.stream_dev(ctx, [L["o"]], sink.data_ptr())
+            K.stream_dev(ctx, [L["gate"], L["up"]], sink.data_ptr())
+            K.stream_dev(ctx, [L["down"]], sink.data_ptr())
+
+    best, sweep = None, {}
+    for wg in (1, 2, 4):
+        for thr in (256, 512):
+            os.environ["KVAD_STREAM_WG_PER_CU"], os.environ["KVAD_STREAM_THREADS"] = str(wg), str(thr)
+            g = Graph(torch, ctx, stream, probe_step)
+            s = g.time(max(5, args.steps // 4), 2)
+            del g
+            sweep[f"{wg}x{thr}"] = round(s * 1e3, 4)
+            if best is None or s < best[0]:
+                best = (s, wg, thr)
+    os.environ.pop("KVAD_STREAM_WG_PER_CU")
+    os.environ.pop("KVAD_STREAM_THREADS")
+    ceiling = {"ms_per_step": round(best[0] * 1e3, 4), "weight_GBps": round(wbytes_step / best[0] / 1e9, 1),
+               "launch": {"workgroups_per_cu": best[1], "threads_per_workgroup": best[2]},
+               "sweep_ms_per_step": sweep,
+               "gemv_step_over_ceiling": round(sec / best[0], 3),
+               "gemv_weight_GBps": round(wbytes_step / sec / 1e9, 1)}
+    log(f"structure ceiling: {ceiling}")
+
     # ---- each config shape as its own launch ------------------------------
     per_shape = {}
     for name in ("o", "up", "down"):
@@ -247,6 +279,18 @@ def main() -> int:
         s = g.time(args.steps, args.warmup) / args.layers
         per_shape[f"{rows}x{cols}"] = {"us": round(s * 1e6, 3), "GBps": round(q4k_bytes(rows, cols) / s / 1e9, 1)}
         del g
+
+        def probe_one():
+            for L in layers:
+                K.stream_dev(ctx, [L[name]], sink.data_ptr())
+
+        os.environ["KVAD_STREAM_WG_PER_CU"], os.environ["KVAD_STREAM_THREADS"] = str(best[1]), str(best[2])
+        g = Graph(torch, ctx, stream, probe_one)
+        sp = g.time(args.steps, args.warmup) / args.layers
+        del g
+        os.environ.pop("KVAD_STREAM_WG_PER_CU")
+        os.environ.pop("KVAD_STREAM_THREADS")
+        per_shape[f"{rows}x{cols}"]["ceiling_us"] = round(sp * 1e6, 3)
     log(f"per shape: {per_shape}")
 
     # the dequantising kernel (quant.rs:522-589) on the same step: one launch
@@ -289,6 +333,7 @@ def main() -> int:
     log(f"batched decode q4k: {batched}")
 
     extra = {"q4k_gemv_per_shape": per_shape, "weight_bytes_resident": weight_bytes,
+             "q4k_step_structure_ceiling": ceiling,
              "q4k_dequant_step": dequant_step, "q4k_batched_decode_llama3_8b": batched}
     rig = None if args.no_cpu else CpuRig(args.cpu_column_seconds)
     if not args.no_extra:

@@ -155,6 +155,13 @@ int kh_matvec_q_dev(kh_ctx *ctx, const kh_weight *w, const int8_t *qs, const flo
 int kh_debug_block_dots(kh_ctx *ctx, const kh_weight *w, const float *x, int32_t *dots);
 /* QActivation::new on the device: qs[n], scales[n/32], sums[n/32]. */
 int kh_debug_qact(kh_ctx *ctx, const float *x, size_t n, int8_t *qs, float *scales, int32_t *sums);
+/* Timing aid (no counterpart in the reference): one launch that reads every
+ * byte of up to four weights once (codes and scales) with 16-byte loads and
+ * no arithmetic, each workgroup writing one word of the device array
+ * sink[4096]; asynchronous on the context's stream.  Set beside the GEMV's
+ * launches over the same weights it gives the HBM ceiling of that launch
+ * structure. */
+int kh_debug_stream_dev(kh_ctx *ctx, size_t n, const kh_weight *const *w, uint32_t *sink);
 
 /* ---- KV cache and attention ------------------------------------------- */
 

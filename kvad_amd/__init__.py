@@ -122,6 +122,7 @@ _SIGS = {
     "kh_llm_forward": (C.c_int, [_p, _p, C.c_int32, _p, _p]),
     "kh_debug_llm_trace": (C.c_int, [_p, _p, C.c_int32, _p]),
     "kh_llm_forward_tokens": (C.c_int, [_p, _p, _p, _sz, _p, _p]),
+    "kh_debug_stream_dev": (C.c_int, [_p, _sz, _p, _p]),
     "kh_llm_prefill_pass": (C.c_int, [_p, _sz, C.POINTER(_sz)]),
     "kh_llm_set_prefill_chunk": (C.c_int, [_p, _sz]),
     "kh_debug_llm_trace_pass": (C.c_int, [_p, _p, _p, _sz, _p]),
@@ -378,6 +379,12 @@ def matvec_many(ctx: Context, jobs) -> list[np.ndarray] | None:
         return None
     _check(rc)
     return ys
+
+
+def stream_dev(ctx: Context, weights, sink_ptr: int) -> None:
+    """kh_debug_stream_dev: one launch reading the weights' bytes once (a timing aid)."""
+    arr = (C.c_void_p * len(weights))(*[w.h.value for w in weights])
+    _check(lib.kh_debug_stream_dev(ctx.h, len(weights), arr, C.c_void_p(sink_ptr)))
 
 
 def qact_dev(ctx: Context, x_ptr: int, m: int, n: int, qs_ptr: int, scales_ptr: int, sums_ptr: int) -> None:

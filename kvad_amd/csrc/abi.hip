@@ -475,6 +475,15 @@ int kh_debug_block_dots(kh_ctx *ctx, const kh_weight *w, const float *x, int32_t
     return matvec_host(ctx, w, x, nullptr, y.data(), dots);
 }
 
+int kh_debug_stream_dev(kh_ctx *ctx, size_t n, const kh_weight *const *w, uint32_t *sink) {
+    if (!ctx || !sink || (n && !w)) return fail(KH_EINVAL, "kh_debug_stream_dev: null argument");
+    if (n > 4) return fail(KH_EINVAL, "kh_debug_stream_dev: at most four weights a launch");
+    for (size_t i = 0; i < n; i++)
+        if (check_weight(w[i])) return KH_EINVAL;
+    Guard g(ctx);
+    return launch_stream(ctx, n, w, sink);
+}
+
 int kh_debug_qact(kh_ctx *ctx, const float *x, size_t n, int8_t *qs, float *scales, int32_t *sums) {
     if (!ctx || !x || !qs || !scales || !sums) return fail(KH_EINVAL, "kh_debug_qact: null argument");
     if (n % BLOCK) return fail(KH_EINVAL, "kh_debug_qact: n must be a multiple of 32");

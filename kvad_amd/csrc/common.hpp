@@ -402,6 +402,10 @@ int launch_quantize(kh_ctx *ctx, const float *w, size_t rows, size_t cols, int p
 
 // Small helpers.
 int launch_fill(kh_ctx *ctx, float *p, size_t n, float value);
+// The weights' bytes read once by a streaming kernel (timing aid); each
+// workgroup writes one word of sink [STREAM_SINK].
+constexpr unsigned STREAM_SINK = 4096;
+int launch_stream(kh_ctx *ctx, size_t n, const kh_weight *const *w, unsigned *sink);
 int launch_dequant_row(kh_ctx *ctx, const kh_weight *w, size_t r, float *out);
 // The same with the row indices read from device memory (an embedding
 // lookup): rows r[0..n) into out [n][cols].

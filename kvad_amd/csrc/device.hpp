@@ -81,6 +81,12 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (a + b) + (c + d);
 }
 
+// Xor over the wave (every lane gets it).
+__device__ __forceinline__ unsigned wave_xor(unsigned v) {
+    for (int o = WAVE / 2; o > 0; o >>= 1) v ^= (unsigned)__shfl_xor((int)v, o);
+    return v;
+}
+
 __device__ __forceinline__ float half_bits_to_float(unsigned h) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffff));
 }

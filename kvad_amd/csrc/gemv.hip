@@ -824,6 +824,52 @@ __global__ void fill_kernel(float *p, size_t n, float value) {
 }
 
 // Weight::row (quant.rs:374-402) and the Q4_K decoder (mpp.rs:304-315).
+// ---- the streaming ceiling of a launch (a timing aid) ----------------------
+// The bytes of up to STREAM_ARRAYS device arrays read once with 16-byte
+// loads and no arithmetic: workgroup b takes the L * blockDim consecutive
+// 16-byte units from b * L * blockDim, each lane issuing all L of its loads
+// (consecutive lanes on consecutive units) before it waits; each lane folds
+// what it read into one word and each workgroup writes one word of `sink`.
+// No activation and no arithmetic: the same launch structure as the GEMV it
+// is set beside, with every byte in flight as early as it can be.
+constexpr int STREAM_ARRAYS = 8;
+struct StreamArgs {
+    const void *p[STREAM_ARRAYS];
+    unsigned end[STREAM_ARRAYS];  // prefix sums of the arrays' 16-byte units
+    int n;
+    unsigned total;
+    unsigned *sink;
+};
+
+template <int L, int AUX>
+__global__ __launch_bounds__(1024) void stream_kernel(StreamArgs a) {
+    const unsigned T = blockDim.x, base = blockIdx.x * T * L + threadIdx.x;
+    int4 v[L];
+#pragma unroll
+    for (int u = 0; u < L; u++) {
+        const unsigned i = base + (unsigned)u * T;
+        int k = 0;
+#pragma unroll
+        for (int j = 0; j < STREAM_ARRAYS - 1; j++) k += (j < a.n - 1 && i >= a.end[j]) ? 1 : 0;
+        const unsigned lo = k ? a.end[k - 1] : 0u;
+        const rsrc_t r = rsrc(a.p[k], (size_t)(a.end[k] - lo) * 16);
+        v[u] = i < a.total ? __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (i - lo) * 16u, 0, AUX))
+                           : make_int4(0, 0, 0, 0);
+    }
+    unsigned fold = 0;
+#pragma unroll
+    for (int u = 0; u < L; u++) fold ^= (unsigned)(v[u].x ^ v[u].y ^ v[u].z ^ v[u].w);
+    fold = wave_xor(fold);
+    __shared__ unsigned s_f[16];
+    if ((threadIdx.x & (WAVE - 1)) == 0) s_f[threadIdx.x >> 6] = fold;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned f = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); w++) f ^= s_f[w];
+        a.sink[blockIdx.x & (STREAM_SINK - 1)] = f;
+    }
+}
+
 // Row r_dev[y] (or r_host) of the weight into out row y, one grid row each.
 __global__ void dequant_row_kernel(int prec, const void *qs, const float *scales, size_t cols, size_t r_host,
                                    const int32_t *r_dev,
@@ -1088,6 +1134,52 @@ size_t fuse_max_cols(int precision) {
     }();
     if (forced) return forced;
     return precision == KH_Q4K ? 16384 : 8192;
+}
+
+int launch_stream(kh_ctx *ctx, size_t n, const kh_weight *const *w, unsigned *sink) {
+    StreamArgs a{};
+    unsigned at = 0;
+    for (size_t i = 0; i < n; i++) {
+        const size_t qb = w[i]->precision == KH_Q8   ? w[i]->rows * w[i]->cols
+                          : w[i]->precision == KH_Q4 ? w[i]->rows * w[i]->cols / 2
+                          : w[i]->precision == KH_Q4K ? w[i]->rows * (w[i]->cols / QK_K) * Q4K_BYTES
+                                                      : 4 * w[i]->rows * w[i]->cols;
+        const size_t sb = w[i]->scales ? 4 * (w[i]->rows * w[i]->cols / BLOCK) : 0;
+        for (int part = 0; part < 2; part++) {
+            const size_t bytes = part ? sb : qb;
+            if (!bytes) continue;
+            if (a.n == STREAM_ARRAYS) return fail(KH_EINVAL, "stream: too many arrays");
+            if (bytes % 16 || (size_t)at + bytes / 16 > 0x7fffffffu) return fail(KH_EINVAL, "stream: array size");
+            at += (unsigned)(bytes / 16);
+            a.p[a.n] = part ? (const void *)w[i]->scales : w[i]->qs;
+            a.end[a.n++] = at;
+        }
+    }
+    if (!a.n) return KH_OK;
+    a.total = at;
+    a.sink = sink;
+    // the launch: `threads` a workgroup, about `wg` workgroups per CU, each
+    // lane L loads (the fewest that keep within that many workgroups)
+    const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int wg = std::max(1, env_int("KVAD_STREAM_WG_PER_CU", 1));      // timing knob
+    const int tk = env_int("KVAD_STREAM_THREADS", 256);                  // timing knob: 256, 512, 1024
+    const int threads = tk == 1024 ? 1024 : tk == 512 ? 512 : 256;
+    const int nt = env_int("KVAD_STREAM_NT", 0);                          // timing knob: non-temporal loads
+    int L = 1;
+    while (L < 16 && (at + (unsigned)(threads * L) - 1) / (unsigned)(threads * L) > (unsigned)(wg * cu)) L *= 2;
+    const unsigned blocks = (at + (unsigned)(threads * L) - 1) / (unsigned)(threads * L);
+#define KH_STREAM(LL)                                                                                      \
+    case LL:                                                                                               \
+        if (nt) hipLaunchKernelGGL((stream_kernel<LL, 2>), dim3(blocks), dim3(threads), 0, ctx->stream, a); \
+        else hipLaunchKernelGGL((stream_kernel<LL, 0>), dim3(blocks), dim3(threads), 0, ctx->stream, a);    \
+        break;
+    switch (L) {
+        KH_STREAM(1) KH_STREAM(2) KH_STREAM(4) KH_STREAM(8)
+        default: KH_STREAM(16)
+    }
+#undef KH_STREAM
+    KH_HIP(hipGetLastError());
+    return KH_OK;
 }
 
 int launch_fill(kh_ctx *ctx, float *p, size_t n, float value) {
