@@ -247,20 +247,25 @@ def main() -> int:
             K.stream_dev(ctx, [L["gate"], L["up"]], sink.data_ptr())
             K.stream_dev(ctx, [L["down"]], sink.data_ptr())
 
+    # 32 waves per CU in three workgroup sizes (fewer measured slower), with
+    # and without the non-temporal cache policy
+    knobs = ("KVAD_STREAM_WG_PER_CU", "KVAD_STREAM_THREADS", "KVAD_STREAM_NT")
     best, sweep = None, {}
-    for wg in (1, 2, 4):
-        for thr in (256, 512):
-            os.environ["KVAD_STREAM_WG_PER_CU"], os.environ["KVAD_STREAM_THREADS"] = str(wg), str(thr)
+    for wg, thr in ((8, 256), (4, 512), (2, 1024)):
+        for nt in (0, 1):
+            for k, v in zip(knobs, (wg, thr, nt)):
+                os.environ[k] = str(v)
             g = Graph(torch, ctx, stream, probe_step)
             s = g.time(max(5, args.steps // 4), 2)
             del g
-            sweep[f"{wg}x{thr}"] = round(s * 1e3, 4)
+            sweep[f"{wg}x{thr}{' nt' if nt else ''}"] = round(s * 1e3, 4)
             if best is None or s < best[0]:
-                best = (s, wg, thr)
-    os.environ.pop("KVAD_STREAM_WG_PER_CU")
-    os.environ.pop("KVAD_STREAM_THREADS")
+                best = (s, wg, thr, nt)
+    for k in knobs:
+        os.environ.pop(k)
     ceiling = {"ms_per_step": round(best[0] * 1e3, 4), "weight_GBps": round(wbytes_step / best[0] / 1e9, 1),
-               "launch": {"workgroups_per_cu": best[1], "threads_per_workgroup": best[2]},
+               "launch": {"workgroups_per_cu": best[1], "threads_per_workgroup": best[2],
+                          "non_temporal": bool(best[3])},
                "sweep_ms_per_step": sweep,
                "gemv_step_over_ceiling": round(sec / best[0], 3),
                "gemv_weight_GBps": round(wbytes_step / sec / 1e9, 1)}
@@ -284,12 +289,13 @@ def main() -> int:
             for L in layers:
                 K.stream_dev(ctx, [L[name]], sink.data_ptr())
 
-        os.environ["KVAD_STREAM_WG_PER_CU"], os.environ["KVAD_STREAM_THREADS"] = str(best[1]), str(best[2])
+        for k, v in zip(knobs, best[1:]):
+            os.environ[k] = str(int(v))
         g = Graph(torch, ctx, stream, probe_one)
         sp = g.time(args.steps, args.warmup) / args.layers
         del g
-        os.environ.pop("KVAD_STREAM_WG_PER_CU")
-        os.environ.pop("KVAD_STREAM_THREADS")
+        for k in knobs:
+            os.environ.pop(k)
         per_shape[f"{rows}x{cols}"]["ceiling_us"] = round(sp * 1e6, 3)
     log(f"per shape: {per_shape}")
 
