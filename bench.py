@@ -73,6 +73,8 @@ def parse():
                     help="only run a MIB-sized copy and two eager steps of the GEMV kernels (for rocprofv3 --pmc)")
     ap.add_argument("--gemm-counters", action="store_true",
                     help="only run three eager q8 prefill GEMMs per shape (for rocprofv3 --pmc)")
+    ap.add_argument("--kernel-counters", choices=("moe_decode", "mla", "attend"), default=None,
+                    help="only run a few eager launches of one secondary workload (for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -162,6 +164,11 @@ def main() -> int:
             torch.cuda.synchronize()
             del w, f, xs, y
         print(json.dumps({"gemm_counters_run": {"shapes_mkn": shapes, "calls_each": 3}}), flush=True)
+        ctx.set_stream(None)
+        return 0
+
+    if args.kernel_counters:
+        counter_workload(torch, K, ctx, stream, dev, gen, args.kernel_counters)
         ctx.set_stream(None)
         return 0
 
@@ -377,6 +384,57 @@ def main() -> int:
     print(json.dumps(result), flush=True)
     ctx.set_stream(None)
     return 0
+
+
+def counter_workload(torch, K, ctx, stream, dev, gen, name, reps=3):
+    """Eager launches of one secondary figure's kernels, for rocprofv3 --pmc
+    passes (graph replays hide per-dispatch counters): the DeepSeek-V2-Lite
+    MoE decode layer (4 distinct layers, one token), latent attention at
+    L = 32768 (4 layers of distinct caches), or GQA attention at Qwen2.5-0.5B
+    geometry and L = 32768 (8 layers)."""
+    with torch.cuda.stream(stream):
+        if name == "moe_decode":
+            hidden, inter, n_exp, k, sh = 2048, 1408, 64, 6, 2816
+
+            def q8(rows, cols, sd=0.02):
+                f = torch.randn(rows, cols, device=dev, generator=gen) * sd
+                return K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8)
+
+            layers = []
+            for _ in range(4):
+                m = K.Moe(ctx, n_exp, k, hidden, inter)
+                m.set_router(q8(n_exp, hidden, 0.5))
+                for x in range(n_exp):
+                    m.set_expert(x, q8(inter, hidden), q8(inter, hidden), q8(hidden, inter))
+                m.set_shared(q8(sh, hidden), q8(sh, hidden), q8(hidden, sh))
+                layers.append((m, torch.randn(hidden, device=dev, generator=gen), torch.empty(hidden, device=dev)))
+            torch.cuda.synchronize()
+            for _ in range(reps):
+                for m, x, y in layers:
+                    m.run_dev(x.data_ptr(), 1, y.data_ptr())
+        elif name == "mla":
+            L, H = 32768, 16
+            c = torch.randn(4, L, 512, device=dev, generator=gen)
+            pe = torch.randn(4, L, 64, device=dev, generator=gen)
+            ql = torch.randn(H * 512, device=dev, generator=gen)
+            qp = torch.randn(H * 64, device=dev, generator=gen)
+            o = torch.empty(H * 512, device=dev)
+            torch.cuda.synchronize()
+            for _ in range(reps):
+                for l in range(4):
+                    K.mla_attend_dev(ctx, H, ql.data_ptr(), qp.data_ptr(), c[l].data_ptr(), pe[l].data_ptr(), L,
+                                     1.0 / 192 ** 0.5, o.data_ptr())
+        else:
+            L, spec = 32768, K.Spec(14, 2, 64)
+            kv = torch.randn(8, 2, L, 128, device=dev, generator=gen)
+            q = torch.randn(14 * 64, device=dev, generator=gen)
+            o = torch.empty(14 * 64, device=dev)
+            torch.cuda.synchronize()
+            for _ in range(reps):
+                for l in range(8):
+                    K.attend_dev(ctx, spec, q.data_ptr(), kv[l, 0].data_ptr(), kv[l, 1].data_ptr(), L, o.data_ptr())
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_counters_run": name, "reps": reps}), flush=True)
 
 
 TRAFFIC = ROOT / "profiles" / "gemv_q4k_llama3_8b_traffic.json"
