@@ -796,6 +796,197 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     merge_head<HD, HD>(a.pm, a.pl, a.pmin, a.pacc, a.psc, ns, a.n_head, h, 0, a.P, L, vrow, a.out);
 }
 
+// A prompt's pass (Rows::Following, run_rows llama.rs:258-271): n rows at
+// consecutive positions of one cache, row i attending over positions
+// 0 .. rows[i].L - 1, the rows already rotated and pushed.  A workgroup
+// takes a tile of 16 columns -- 16 / gc rows x the gc query heads of a head
+// group -- and its NW waves stream the keys and values once for all of
+// them, wave w taking the 16-position tiles w, w + NW, ..., on the matrix
+// cores in the split kernel's layouts (v_mfma_f32_16x16x4f32: S = K Q^T
+// lands as lane (c, j) holding positions 4c .. 4c + 3 of column j; O += P V
+// with V rows 4c + r).  Two passes over the positions: the column's maximum
+// M and sum S = sum e^{s - M} (per wave a running maximum with the sum
+// rescaled when it rises; the waves' (M, S) combined in LDS in wave order),
+// then the reference's weights w = e^{s - M} * (1/S), w < 1e-8 dropped
+// (mod.rs:805-812), times the values, the waves' sums added in LDS in wave
+// order.  Every column's whole sequence is in one workgroup: no partials in
+// memory and no merge launch.  Scores are dot(q, k) * scale (mod.rs:802).
+struct PassArgs {
+    const float *q;        // [n][n_head][HD]
+    const AttnRow *rows;   // [n]: the cache (the same for every row) and each row's length
+    float *out;            // [n][n_head][HD]
+    size_t kstride, vstride;
+    int n, n_head, group, gc;
+    float scale;
+};
+
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_pass_kernel(PassArgs a) {
+    constexpr int NQ4 = HD / 16, VT = HD / 64, NT = HD / 16;
+    constexpr int STEP = 16 * NW;  // positions between one wave's tiles
+    const int tid = threadIdx.x, lane = tid & 63, j16 = lane & 15, c4 = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gc = a.gc, rpt = 16 / gc;
+    const int r0 = blockIdx.x * rpt, h0 = blockIdx.y * gc, kvh = h0 / a.group;
+    const int rlast = min(r0 + rpt, a.n) - 1;
+    const AttnRow first = a.rows[0];
+    const int L = a.rows[rlast].L;  // the longest sequence of the tile
+    const rsrc_t K = rsrc(first.k, (size_t)L * a.kstride * 4), V = rsrc(first.v, (size_t)L * a.vstride * 4);
+    // the lane's column: row r0 + j16 / gc, head h0 + j16 % gc
+    const int cr = r0 + j16 / gc, ch = h0 + j16 % gc;
+    const bool hv = j16 < rpt * gc && cr < a.n;
+    const int last = hv ? a.rows[cr].L - 1 : -1;  // the column attends t <= last
+    f4v qb4[NQ4];
+    {
+        const float *qh = a.q + ((size_t)(hv ? cr : r0) * a.n_head + (hv ? ch : h0)) * HD + 4 * c4;
+#pragma unroll
+        for (int m = 0; m < NQ4; m++) {
+            const float4 f = *reinterpret_cast<const float4 *>(qh + 16 * m);
+            qb4[m] = hv ? f4v{f.x, f.y, f.z, f.w} : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    auto load_k = [&](int t0, f4v (&kq)[NQ4]) {
+        const unsigned off = (unsigned)(((size_t)(t0 + j16) * a.kstride + (size_t)kvh * HD + 4 * c4) * 4);
+#pragma unroll
+        for (int m = 0; m < NQ4; m++)
+            kq[m] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(K, off, 64 * m, 0));
+    };
+    auto load_v = [&](int t0, f4v (&vv)[4][VT]) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const unsigned off =
+                (unsigned)(((size_t)(t0 + 4 * c4 + r) * a.vstride + (size_t)kvh * HD + 4 * j16) * 4);
+#pragma unroll
+            for (int v = 0; v < VT; v++)
+                vv[r][v] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(V, off, 256 * v, 0));
+        }
+    };
+    // scores of positions t0 + 4 c4 + r of the lane's column, -inf where masked
+    auto scores = [&](int t0, const f4v (&kq)[NQ4], float (&s)[4]) {
+        f4v d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < NQ4; m++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(kq[m][c], qb4[m][c], d, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float sc = d[r] * a.scale;
+            s[r] = t0 + 4 * c4 + r <= last ? sc : -INFINITY;
+        }
+    };
+    // Both passes keep the wave's next tile in flight while one is worked
+    // (tiles past L read zeros: the buffers' range ends at L).
+    // pass 1: the maximum M and the sum of e^{s - M}
+    float M = -INFINITY, S = 0.0f;
+    auto stats = [&](int t0, const f4v (&kq)[NQ4]) {
+        float s[4];
+        scores(t0, kq, s);
+        const float mx = rows_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+        const float Mn = fmaxf(M, mx);
+        float e = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) e += s[r] == -INFINITY ? 0.0f : expf(s[r] - Mn);
+        e = rows_sum(e);
+        S = (M == -INFINITY ? 0.0f : S * expf(M - Mn)) + e;
+        M = Mn;
+    };
+    {
+        f4v ka[NQ4], kb[NQ4];
+        load_k(16 * wave, ka);
+        for (int t0 = 16 * wave; t0 < L; t0 += 2 * STEP) {
+            load_k(t0 + STEP, kb);
+            stats(t0, ka);
+            if (t0 + STEP >= L) break;
+            load_k(t0 + 2 * STEP, ka);
+            stats(t0 + STEP, kb);
+        }
+    }
+    if constexpr (NW > 1) {  // the waves' statistics, in wave order
+        __shared__ float s_st[2][NW][16];
+        if (c4 == 0) {
+            s_st[0][wave][j16] = M;
+            s_st[1][wave][j16] = S;
+        }
+        __syncthreads();
+        M = s_st[0][0][j16];
+#pragma unroll
+        for (int w = 1; w < NW; w++) M = fmaxf(M, s_st[0][w][j16]);
+        S = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float mw = s_st[0][w][j16];
+            S = mw == -INFINITY ? S : fmaf(s_st[1][w][j16], expf(mw - M), S);
+        }
+    }
+    const float inv = 1.0f / S;  // inv = 1 / sum, tensor.rs:304
+    // pass 2: the weights times the values
+    f4v acc[NT];
+#pragma unroll
+    for (int q = 0; q < NT; q++) acc[q] = f4v{0.f, 0.f, 0.f, 0.f};
+    auto accumulate = [&](int t0, const f4v (&kq)[NQ4], const f4v (&vv)[4][VT]) {
+        float s[4];
+        scores(t0, kq, s);
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float w = s[r] == -INFINITY ? 0.0f : expf(s[r] - M) * inv;
+            p[r] = w < 1e-8f ? 0.0f : w;  // mod.rs:807
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int q = 0; q < NT; q++)
+                acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], vv[r][q >> 2][q & 3], acc[q], 0, 0, 0);
+    };
+    {
+        f4v ka[NQ4], kb[NQ4], va[4][VT], vb[4][VT];
+        load_k(16 * wave, ka);
+        load_v(16 * wave, va);
+        for (int t0 = 16 * wave; t0 < L; t0 += 2 * STEP) {
+            load_k(t0 + STEP, kb);
+            load_v(t0 + STEP, vb);
+            accumulate(t0, ka, va);
+            if (t0 + STEP >= L) break;
+            load_k(t0 + 2 * STEP, ka);
+            load_v(t0 + 2 * STEP, va);
+            accumulate(t0 + STEP, kb, vb);
+        }
+    }
+    // acc[q][i] is column 4 c4 + i, dim 4 j16 + (q & 3) + 64 (q >> 2)
+    if constexpr (NW == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int col = 4 * c4 + i, row = r0 + col / gc, head = h0 + col % gc;
+            if (col >= rpt * gc || row >= a.n) continue;
+            float *o = a.out + ((size_t)row * a.n_head + head) * HD;
+#pragma unroll
+            for (int v = 0; v < VT; v++)
+                *reinterpret_cast<float4 *>(o + 64 * v + 4 * j16) =
+                    make_float4(acc[4 * v][i], acc[4 * v + 1][i], acc[4 * v + 2][i], acc[4 * v + 3][i]);
+        }
+    } else {  // the waves' sums, added in wave order
+        __shared__ __align__(16) float s_acc[NW][16][HD];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int v = 0; v < VT; v++)
+                *reinterpret_cast<float4 *>(&s_acc[wave][4 * c4 + i][64 * v + 4 * j16]) =
+                    make_float4(acc[4 * v][i], acc[4 * v + 1][i], acc[4 * v + 2][i], acc[4 * v + 3][i]);
+        __syncthreads();
+        for (int i = tid; i < 16 * HD / 4; i += 64 * NW) {
+            const int col = i / (HD / 4), d = 4 * (i % (HD / 4)), row = r0 + col / gc, head = h0 + col % gc;
+            if (col >= rpt * gc || row >= a.n) continue;
+            float4 x = *reinterpret_cast<const float4 *>(&s_acc[0][col][d]);
+#pragma unroll
+            for (int w = 1; w < NW; w++) {
+                const float4 y = *reinterpret_cast<const float4 *>(&s_acc[w][col][d]);
+                x = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+            }
+            *reinterpret_cast<float4 *>(a.out + ((size_t)row * a.n_head + head) * HD + d) = x;
+        }
+    }
+}
+
 // P = 16 R nw positions per workgroup of nw waves: four waves with R in
 // {1, 2, 4} (hd 64) or {1, 2} (hd 128), or eight waves with R in {1, 2} (hd 64)
 // or 1 (hd 128) for P >= 128; the fused-RoPE form when the rope argument is set.
@@ -997,6 +1188,63 @@ int launch_attend_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, con
     if (4 * a.row_floats * nb > ws_bytes) return fail(KH_EINVAL, "attend: workspace too small for the rows");
     carve_partials(a, ws, head_dim);
     return run(ctx, a, head_dim, nb);
+}
+
+// The loads of a pass reach 16 (2 NW + 1) - 1 positions past the longest row.
+constexpr size_t PASS_OVERREACH = 16 * (2 * 8 + 1);
+
+bool attend_pass_fits(int head_dim, size_t kstride, size_t vstride, size_t max_positions) {
+    if (env_int("KVAD_PASS_ATTN", 1) == 0) return false;
+    return (head_dim == 64 || head_dim == 128) && (max_positions + PASS_OVERREACH) * kstride * 4 < 0xffffffffull &&
+           (max_positions + PASS_OVERREACH) * vstride * 4 < 0xffffffffull;
+}
+
+// Waves per workgroup of a pass: doubled from one while the grid holds
+// fewer than two waves per SIMD (2048) and each wave keeps at least four
+// 16-position tiles of the longest row; KVAD_PASS_WAVES (1, 2, 4, 8) fixes it.
+int pass_waves(int workgroups, size_t max_positions) {
+    const int forced = env_int("KVAD_PASS_WAVES", 0);
+    if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
+    int nw = 1;
+    while (nw < 8 && (size_t)workgroups * nw < 2048 && (size_t)nw * 2 * 64 <= max_positions) nw *= 2;
+    return nw;
+}
+
+template <int HD>
+void launch_pass(kh_ctx *ctx, int nw, dim3 grid, const PassArgs &a) {
+    switch (nw) {
+        case 1: hipLaunchKernelGGL((attn_pass_kernel<HD, 1>), grid, dim3(64), 0, ctx->stream, a); break;
+        case 2: hipLaunchKernelGGL((attn_pass_kernel<HD, 2>), grid, dim3(128), 0, ctx->stream, a); break;
+        case 4: hipLaunchKernelGGL((attn_pass_kernel<HD, 4>), grid, dim3(256), 0, ctx->stream, a); break;
+        default: hipLaunchKernelGGL((attn_pass_kernel<HD, 8>), grid, dim3(512), 0, ctx->stream, a); break;
+    }
+}
+
+int launch_attend_pass(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,
+                       int n, size_t kstride, size_t vstride, size_t max_positions, float *out) {
+    if (n <= 0 || n_kv_head <= 0 || n_head <= 0 || n_head % n_kv_head != 0)
+        return fail(KH_EINVAL, "attend_pass: bad row or head count");
+    if (!attend_pass_fits(head_dim, kstride, vstride, max_positions))
+        return fail(KH_DECLINED, "attend_pass: head_dim 64 or 128 and caches under 4 GiB per layer");
+    PassArgs a{};
+    a.q = q;
+    a.rows = rows;
+    a.out = out;
+    a.kstride = kstride;
+    a.vstride = vstride;
+    a.n = n;
+    a.n_head = n_head;
+    a.group = n_head / n_kv_head;
+    a.gc = heads_per_wg(a.group);
+    a.scale = 1.0f / sqrtf((float)head_dim);  // mod.rs:777
+    const int rpt = 16 / a.gc;
+    const dim3 grid((unsigned)((n + rpt - 1) / rpt), (unsigned)(n_head / a.gc));
+    if (grid.y > 65535) return fail(KH_EINVAL, "attend_pass: too many head groups");
+    const int nw = pass_waves((int)(grid.x * grid.y), max_positions);
+    if (head_dim == 64) launch_pass<64>(ctx, nw, grid, a);
+    else launch_pass<128>(ctx, nw, grid, a);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
 }
 
 int launch_rope_push_rows(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, float *q, const float *k,

@@ -462,6 +462,15 @@ size_t attend_rows_ws_bytes(int n_head, int head_dim, size_t max_positions, size
 // The partials launch_attend_rows needs for nb rows of at most max_positions
 // on this context (the split it would pick), in bytes; 0 when it would refuse.
 size_t attend_rows_need_bytes(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, size_t max_positions, size_t nb);
+// Attention of one sequence's pass (Rows::Following): n rows of q (rotated)
+// over one cache (rows[0]'s), row i over positions 0 .. rows[i].L - 1, every
+// row's whole sequence in one wave (no partials), at most max_positions.
+// attend_pass_fits says whether the launch takes the shape (head_dim 64 or
+// 128, the cache addressed in 32 bits) and is not switched off
+// (KVAD_PASS_ATTN=0 keeps a pass on launch_attend_rows).
+bool attend_pass_fits(int head_dim, size_t kstride, size_t vstride, size_t max_positions);
+int launch_attend_pass(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const AttnRow *rows,
+                       int n, size_t kstride, size_t vstride, size_t max_positions, float *out);
 // The rows of one sequence's pass (Rows::Following): queries q [nb][n_head][hd]
 // normed and rotated in place, keys k [nb][n_kv][hd] normed, rotated and
 // written with the values v into each row's cache at rows[i].L - 1.

@@ -555,9 +555,13 @@ int step_rows(kh_ctx *ctx, kh_llm *m, size_t n, const RowsBuf &b, size_t max_len
         if (following && (rc = launch_rope_push_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q,
                                                       b.k, b.v, tab, (int)n, kvd, kvd, rp)))
             return rc;
-        if ((rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd,
-                                     kvd, max_len, b.att, b.ws, b.ws_bytes, following ? nullptr : &rp)))
-            return rc;
+        if (following && attend_pass_fits((int)s.head_dim, kvd, kvd, max_len))
+            rc = launch_attend_pass(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd, kvd,
+                                    max_len, b.att);
+        else
+            rc = launch_attend_rows(ctx, (int)s.n_head, (int)s.n_kv_head, (int)s.head_dim, b.q, tab, (int)n, kvd, kvd,
+                                    max_len, b.att, b.ws, b.ws_bytes, following ? nullptr : &rp);
+        if (rc) return rc;
         if (tr && ((rc = trace_copy(ctx, tr->k_cache ? tr->k_cache + l * held * kvd : nullptr, m->kc[l], held * kvd)) ||
                    (rc = trace_copy(ctx, tr->v_cache ? tr->v_cache + l * held * kvd : nullptr, m->vc[l], held * kvd)) ||
                    (rc = trace_copy(ctx, tr->att ? tr->att + l * n * qd : nullptr, b.att, n * qd))))

@@ -15,8 +15,11 @@ bit, the same cache length, and the same next-token logits.  Beyond it:
     steps are the same arithmetic there), at the session bar 2e-3 x max, with
     the next token the argmax of those logits exactly; passes on the
     multi-token GEMV (<= 32 rows) and on the int8 / f32 GEMM (> 32 rows);
-    every row's attention as one split and split + merged; a prompt past the
-    single-split line (300 positions);
+    the attention on the pass kernel (every row's whole sequence in one
+    workgroup, the default; its positions dealt over 1, 2, 4 or 8 waves,
+    KVAD_PASS_WAVES) and, with KVAD_PASS_ATTN=0, on the rows launch as
+    one split and as split + merged; a prompt past the single-split line
+    (300 positions) both ways;
   * every stage of every layer of a pass on the device's own inputs, through
     kh_debug_llm_trace_pass, at the stage bars of test_gpu_llm_stages
     (projections 1e-5, the pushed keys 1e-6 and values exact, attention of
@@ -102,22 +105,38 @@ def test_prefill_pass_cuts_whole_chunks_from_the_front(ctx, monkeypatch):
 
 
 CASES = {
-    # (variant, prompt length, chunk, attention split)
-    "gemv_rows": ("qwen2_q8", 23, 64, "single"),     # one pass of 23 rows: multi-token GEMVs
+    # (variant, prompt length, chunk, attention: the pass kernel, or the
+    # rows launch as one split or split + merged)
+    "gemv_rows": ("qwen2_q8", 23, 64, "pass"),       # one pass of 23 rows: multi-token GEMVs
+    "gemv_rows_single": ("qwen2_q8", 23, 64, "single"),
     "gemm_rows": ("qwen2_q8", 40, 40, "single"),     # one pass of 40 rows: the int8 GEMM
+    "gemm_pass": ("qwen3_q8", 40, 40, "pass"),
     "gemm_split": ("qwen3_q8", 40, 40, "split"),     # every row split and merged
-    "f32_gemm": ("llama_f32", 40, 40, "single"),     # the f32 GEMM
-    "q4k_gemm": ("llama_q4k", 37, 64, "single"),
-    "q4_passes": ("qwen2_q4", 23, 7, "single"),
-    "hd128_passes": ("llama_hd128_q8", 30, 8, "split"),
+    "f32_gemm": ("llama_f32", 40, 40, "pass"),       # the f32 GEMM
+    "q4k_gemm": ("llama_q4k", 37, 64, "pass"),
+    "q4_passes": ("qwen2_q4", 23, 7, "pass"),
+    "hd128_passes": ("llama_hd128_q8", 30, 8, "pass"),
+    "hd128_passes_w8": ("llama_hd128_q8", 30, 8, "pass:8"),
+    "hd128_split": ("llama_hd128_q8", 30, 8, "split"),
+    "gemm_pass_w4": ("qwen2_q8", 40, 40, "pass:4"),
 }
+
+
+def attention_path(monkeypatch, attn):
+    # "pass" (waves per workgroup by the launch's rule), "pass:W" (W waves),
+    # "single" / "split": the rows launch
+    if attn.startswith("pass:"):
+        monkeypatch.setenv("KVAD_PASS_WAVES", attn[5:])
+    elif attn != "pass":
+        monkeypatch.setenv("KVAD_PASS_ATTN", "0")
+    if attn == "split":
+        monkeypatch.setenv("KVAD_ATTN_SINGLE", "0")
 
 
 @pytest.mark.parametrize("case", list(CASES))
 def test_prefill_matches_the_oracle(ctx, monkeypatch, case):
     variant, n, chunk, attn = CASES[case]
-    if attn == "split":
-        monkeypatch.setenv("KVAD_ATTN_SINGLE", "0")
+    attention_path(monkeypatch, attn)
     say("prefill vs oracle", case)
     m, mk = build(ctx, 310, **VARIANTS[variant])
     m.reading(chunk)
@@ -137,12 +156,14 @@ def test_prefill_matches_the_oracle(ctx, monkeypatch, case):
     say("prefill vs oracle worst", case, f"{worst:.2e}")
 
 
+@pytest.mark.parametrize("attn", ["pass", "pass:8", "single"])
 @pytest.mark.parametrize("chunk", [64, 512])
-def test_a_prompt_past_the_single_split_line(ctx, chunk):
-    # 300 positions at head_dim 64: passes of 64 rows whose attention runs as
-    # one split up to 256 positions and split + merged past them, or one pass
-    # of 300 rows
-    say("prefill past the single split", chunk)
+def test_a_prompt_past_the_single_split_line(ctx, monkeypatch, chunk, attn):
+    # 300 positions at head_dim 64: passes of 64 rows, or one pass of 300
+    # rows, on the pass kernel or on the rows launch (one split up to 256
+    # positions, split + merged past them)
+    attention_path(monkeypatch, attn)
+    say("prefill past the single split", chunk, attn)
     m, mk = build(ctx, 320, n_layer=1, n_ctx=512)
     m.reading(chunk)
     ref = mk()
@@ -188,17 +209,26 @@ def test_refusals_leave_the_session_as_it_was(ctx):
 
 
 STAGE_VARIANTS = {
-    "qwen2_gemv": ("qwen2_q8", 3, 6),           # 3 positions held, a pass of 6 rows
-    "qwen3_gemm": ("qwen3_q8", 2, 40),          # a pass of 40 rows on the int8 GEMM
-    "llama_hd128": ("llama_hd128_q8", 4, 12),
+    # (variant, positions held, rows in the pass, attention)
+    "qwen2_gemv": ("qwen2_q8", 3, 6, "pass"),          # 3 positions held, a pass of 6 rows
+    "qwen3_gemm": ("qwen3_q8", 2, 40, "pass"),         # a pass of 40 rows on the int8 GEMM
+    "qwen3_gemm_rows": ("qwen3_q8", 2, 40, "single"),
+    "llama_hd128": ("llama_hd128_q8", 4, 12, "pass"),
+    "llama_hd128_split": ("llama_hd128_q8", 4, 12, "split"),
+    "qwen2_long": ("qwen2_q8", 70, 37, "pass"),        # rows over 71 .. 107 positions
+    "qwen2_long_w2": ("qwen2_q8", 70, 37, "pass:2"),   # the positions dealt over 2, 4, 8 waves
+    "qwen2_long_w4": ("qwen2_q8", 70, 37, "pass:4"),
+    "qwen2_long_w8": ("qwen2_q8", 70, 37, "pass:8"),
+    "hd128_long_w4": ("llama_hd128_q8", 50, 21, "pass:4"),
 }
 
 
 @pytest.mark.parametrize("case", list(STAGE_VARIANTS))
-def test_each_stage_of_a_pass(ctx, case):
-    variant, held, n = STAGE_VARIANTS[case]
+def test_each_stage_of_a_pass(ctx, monkeypatch, case):
+    variant, held, n, attn = STAGE_VARIANTS[case]
+    attention_path(monkeypatch, attn)
     say("prefill stages", case)
-    m, mk = build(ctx, 350, n_layer=3, **VARIANTS[variant])
+    m, mk = build(ctx, 350, n_layer=3, n_ctx=max(64, held + n), **VARIANTS[variant])
     ref = mk()  # for its weights, norms and tables only
     s = ref.s
     e, hd, nh, nkv, eps = s["n_embd"], s["head_dim"], s["n_head"], s["n_kv_head"], s["eps"]
