@@ -43,11 +43,14 @@ def test_version_and_error_slot_work_without_a_device():
     assert kvad_amd.lib.kh_last_error() is not None
 
 
+GUIDE = ROOT / "INTEGRATION.md"  # the integration guide shipped beside the library
+
+
 def _build_rs() -> str:
-    """The build.rs step INTEGRATION.md hands a kvad maintainer."""
-    text = (ROOT / "INTEGRATION.md").read_text()
+    """The build.rs step the integration guide hands a kvad maintainer."""
+    text = GUIDE.read_text()
     m = re.search(r"```rust\n// crates/llm/build\.rs.*?```", text, flags=re.S)
-    assert m, "INTEGRATION.md has no build.rs step"
+    assert m, "the integration guide has no build.rs step"
     return m.group(0)
 
 
