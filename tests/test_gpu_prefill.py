@@ -51,6 +51,12 @@ VARIANTS = {
     "llama_q4k": dict(bias=False, interleaved=True, n_head=4, n_kv_head=2, head_dim=64, n_embd=256, n_ff=512,
                       prec="q4k"),
     "qwen2_q4": dict(bias=True, prec="q4"),
+    # head layouts the pass kernel tiles differently (16 columns = rows x
+    # the group's query heads): MHA (16 rows a tile), Qwen2.5-0.5B's group
+    # of 7 (2 rows, 14 columns), MQA with 16 heads (1 row)
+    "mha_q8": dict(bias=False, n_head=4, n_kv_head=4),
+    "gqa7_q8": dict(bias=True, n_head=14, n_kv_head=2, n_embd=256),
+    "mqa16_q8": dict(bias=False, n_head=16, n_kv_head=1, n_embd=256),
 }
 
 PROMPT = [(i * 7 + 3) % 512 for i in range(23)]  # batched_decode.rs:263 (VOCAB = 512 here)
@@ -220,6 +226,9 @@ STAGE_VARIANTS = {
     "qwen2_long_w4": ("qwen2_q8", 70, 37, "pass:4"),
     "qwen2_long_w8": ("qwen2_q8", 70, 37, "pass:8"),
     "hd128_long_w4": ("llama_hd128_q8", 50, 21, "pass:4"),
+    "mha": ("mha_q8", 5, 37, "pass"),
+    "gqa7": ("gqa7_q8", 5, 37, "pass:4"),
+    "mqa16": ("mqa16_q8", 5, 37, "pass:2"),
 }
 
 
