@@ -115,6 +115,7 @@ struct kh_llm {
     std::vector<float *> kc, vc;                             // per layer [n_ctx, kv_dim]
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *u = nullptr,
           *logits = nullptr;
+    float *hsw = nullptr;                                    // swiglu(gate, up) of the step's SwiGLU pair
     kh::QAct hq{};
     int32_t *state = nullptr;                                // token, pos, step
     int32_t *token = nullptr, *pos = nullptr, *steps = nullptr;
@@ -205,7 +206,18 @@ struct GemvJob {
     int cols;
     int wave0;              // set by the launcher: first workgroup of the job
     int nwaves;             // set by the launcher: waves working on the job
+    // SwiGLU pairs (the decode step's gate and up, ffn.rs:370-386): when w2
+    // is set, the job's rows are gate row i (w, ws) and up row i (w2, ws2)
+    // interleaved, rows = 2 * n_ff; gate row i goes to y[i], up row i to
+    // y2[i] and swiglu(gate, up) (tensor.rs:344-350) to h[i].  No bias, no
+    // accumulate; the job is its launch's only one.
+    const void *w2;
+    const float *ws2;
+    float *y2, *h;
 };
+// Whether a SwiGLU-pair job takes `precision` weights `cols` wide (the
+// launch needs an even number of rows a step).
+bool gemv_pairs_fit(int precision, size_t cols);
 
 // Weight::matvec_bt_dequant (quant.rs:522-589, dequant.hip): y = x W^T
 // (+ bias) with the weights unpacked to f32 and x used as it is, for q8, q4

@@ -194,8 +194,10 @@ __device__ void greedy_tail(const JobTable &tab, const GemvJob &job, int groups,
 
 // ROUTE, the router job (one workgroup, every router row) also keeps its
 // outputs in LDS and its first wave routes them (MoE decode).
-template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB, bool ROUTE = false>
+template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB, bool ROUTE = false,
+          bool PAIR = false>
 __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
+    static_assert(!PAIR || R % 2 == 0, "SwiGLU pairs take an even number of rows a step");
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float s_lg[ROUTE ? MAX_EXPERTS : 1];  // the router's logits
     const int tid = threadIdx.x;
@@ -218,9 +220,10 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     const int nw = job.nwaves;                              // waves on this job
     const int lw = (blk - job.wave0) * NWV + wv;            // this wave among them
 
-    size_t wbytes = PREC == KH_Q8 ? (size_t)rows * cols
-                    : PREC == KH_Q4 ? (size_t)rows * cols / 2
-                                    : (size_t)rows * (cols / QK_K) * Q4K_BYTES;
+    const int wrows = PAIR ? rows / 2 : rows;  // rows of each weight
+    size_t wbytes = PREC == KH_Q8 ? (size_t)wrows * cols
+                    : PREC == KH_Q4 ? (size_t)wrows * cols / 2
+                                    : (size_t)wrows * (cols / QK_K) * Q4K_BYTES;
     const void *wp = job.w;
     const float *wsp = job.ws;
     if (job.wtab) {  // an expert chosen on the device (MoE decode)
@@ -230,7 +233,9 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
         wsp = uniform_ptr(job.wstab[x]);
     }
     const rsrc_t W = rsrc(wp, wbytes);
-    const rsrc_t WS = rsrc(wsp, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
+    const rsrc_t WS = rsrc(wsp, PREC == KH_Q4K ? 0 : (size_t)wrows * nb * 4);
+    const rsrc_t W2 = PAIR ? rsrc(job.w2, wbytes) : W;
+    const rsrc_t WS2 = PAIR ? rsrc(job.ws2, PREC == KH_Q4K ? 0 : (size_t)wrows * nb * 4) : WS;
 
     // the wave's work: its row groups, each cut into nseg segments, walked in
     // order; step s is group lw + (s / nseg) * nw, segment s % nseg.  Two
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     const int steps = my_groups * nseg;
     auto load_step = [&](Chunks<PREC, CPL, R> &c, int s) {
         __builtin_amdgcn_sched_barrier(0);
-        load_chunks<PREC, CPL, R>(c, W, WS, (lw + (s / nseg) * nw) * R, cols, nb, s % nseg, lane);
+        load_chunks<PREC, CPL, R, PAIR>(c, W, WS, (lw + (s / nseg) * nw) * R, cols, nb, s % nseg, lane, W2, WS2);
         __builtin_amdgcn_sched_barrier(0);
     };
     Stage<KIND, stage_batch(CPL, WIDE)> st;
@@ -281,7 +286,21 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
         const int k = step / nseg, seg = step % nseg;
         const int r0 = (lw + k * nw) * R;
         compute_chunks<PREC, CPL, R, DOTS>(c, acc, sq, ssc, ssum, seg, lane, r0, rows, nb, C, job.dots);
-        if (seg == nseg - 1) {
+        if (PAIR && seg == nseg - 1) {
+            // gate row (r0 + i) / 2 and its up row: both, and swiglu of the pair
+#pragma unroll
+            for (int i = 0; i < R; i += 2) {
+                const float g = wave_sum(acc[i]), u = wave_sum(acc[i + 1]);
+                const int r = (r0 + i) >> 1;
+                if (lane == 0 && r < wrows) {
+                    job.y[r] = g;
+                    job.y2[r] = u;
+                    job.h[r] = swiglu1(g, u);
+                }
+                acc[i] = 0.0f;
+                acc[i + 1] = 0.0f;
+            }
+        } else if (seg == nseg - 1) {
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const float v = wave_sum(acc[i]);
@@ -608,7 +627,7 @@ __global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
     const rsrc_t WS = rsrc(job.ws, PREC == KH_Q4K ? 0 : (size_t)rows * nb * 4);
     auto load_step = [&](Chunks<PREC, CPL, 1> &c, int s) {
         __builtin_amdgcn_sched_barrier(0);
-        load_chunks<PREC, CPL, 1>(c, W, WS, lw + (s / nseg) * nw, cols, nb, s % nseg, lane);
+        load_chunks<PREC, CPL, 1>(c, W, WS, lw + (s / nseg) * nw, cols, nb, s % nseg, lane, W, WS);
         __builtin_amdgcn_sched_barrier(0);
     };
     Chunks<PREC, CPL, 1> ca, cb;
@@ -707,11 +726,31 @@ void launch_kind(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int k
     else launch_one<PREC, CPL, R, IN_CODES, WIDE, NWV>(ctx, tab, blocks, lds);
 }
 
+template <int PREC, int CPL, int R>
+void launch_pair(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int kind) {
+    if (kind == IN_NORM)
+        hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_NORM, false, false, WPB, false, true>), dim3(blocks),
+                           dim3(WAVE * WPB), lds, ctx->stream, tab);
+    else
+        hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_F32, false, false, WPB, false, true>), dim3(blocks),
+                           dim3(WAVE * WPB), lds, ctx->stream, tab);
+}
+
 template <int PREC>
 int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_total, bool dots, int kind) {
     const int cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
     Plan p = plan_for(PREC, maxC, maxCols, rows_total, cu);
     if (dots) p = {8, 1, 2, WPB};  // block dots (a debugging aid): one kernel shape serves every width
+    // a SwiGLU pair takes its rows two at a time: an even number a step
+    const bool pair = tab.j[0].w2 != nullptr;
+    if (pair) {
+        if (tab.n != 1 || dots || tab.route_job || tab.arg_job || tab.j[0].bias || tab.j[0].accumulate ||
+            tab.j[0].rows % 2 || (kind != IN_NORM && kind != IN_F32))
+            return fail(KH_EINVAL, "matvec: a SwiGLU pair is its launch's only job, without bias or residual");
+        if (p.cpl > 4) return fail(KH_DECLINED, "matvec: no SwiGLU-pair kernel for rows this wide");
+        if (p.r % 2) p.r = 2;
+        p.nwv = WPB;
+    }
     for (int i = 0; i < tab.n; i++) {
         size_t wb = (size_t)tab.j[i].rows * tab.j[i].cols;
         if (wb >= 0xfff00000ull) return fail(KH_DECLINED, "matvec: weights of 4 GiB or more are not addressed here");
@@ -744,6 +783,18 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     const bool wide = !stage_fits(kind, pb, stage_batch(p.cpl, false), p.nwv);
     if (wide && !(p.cpl >= 4 || (p.r == 1 && stage_fits(kind, pb, stage_batch(p.cpl, true), p.nwv))))
         return fail(KH_DECLINED, "matvec: an f32 activation this wide is quantised in a launch of its own");
+    if (pair) {
+        if (wide) return fail(KH_DECLINED, "matvec: no SwiGLU-pair kernel for an input this wide");
+#define KH_PAIR(CPL, R)                                                       \
+    if (p.cpl == CPL && p.r == R) {                                           \
+        launch_pair<PREC, CPL, R>(ctx, tab, blocks, lds, kind);               \
+        KH_HIP(hipGetLastError());                                            \
+        return KH_OK;                                                         \
+    }
+        KH_PAIR(1, 4) KH_PAIR(1, 2) KH_PAIR(2, 4) KH_PAIR(2, 2) KH_PAIR(3, 2) KH_PAIR(4, 2)
+#undef KH_PAIR
+        return fail(KH_DECLINED, "matvec: no SwiGLU-pair kernel for this plan");
+    }
     if (dots) {
         dim3 grid(blocks), block(WAVE * WPB);
         if (kind == IN_CODES)
@@ -1125,6 +1176,12 @@ bool matmul_takes_multi(size_t m, size_t rows, size_t cols) {
     // 12.4; 896x896 7.9 / 12.1; 896x4864 18.1 / 12.0; 151936x896 (a
     // vocabulary head) 95.9 / 72.7, at 8 rows 49.7 / 72.0.
     return m <= (size_t)MULTI_TOKENS || (m <= 16 && cols <= 2048 && rows <= 16384);
+}
+
+bool gemv_pairs_fit(int precision, size_t cols) {
+    if (precision == KH_F32 || env_int("KVAD_GEMV_PAIR", 1) == 0) return false;
+    if (precision == KH_Q4K) return true;  // one or two chunks a lane
+    return (chunks_per_row(precision, (int)cols) + WAVE - 1) / WAVE <= 4;
 }
 
 size_t fuse_max_cols(int precision) {

@@ -107,16 +107,21 @@ struct Chunks {
     float s[R][CPL];     // q8/q4 block scales
 };
 
-template <int PREC, int CPL, int R>
-__device__ __forceinline__ void load_chunks(Chunks<PREC, CPL, R> &c, const rsrc_t &W, const rsrc_t &WS, int r0,
-                                            int cols, int nb, int seg, int lane) {
+// PAIR: rows r0 + i alternate between two weights (W, WS for even i, W2,
+// WS2 for odd), row (r0 + i) / 2 of each (r0 is even).
+template <int PREC, int CPL, int R, bool PAIR = false>
+__device__ __forceinline__ void load_chunks(Chunks<PREC, CPL, R> &c, const rsrc_t &W1, const rsrc_t &WS1, int r0,
+                                            int cols, int nb, int seg, int lane, const rsrc_t &W2,
+                                            const rsrc_t &WS2) {
     // Offsets are a row's part, the same in every lane (made scalar with
     // readfirstlane, so the compiler cannot fold it into a per-lane multiply),
     // plus the lane's part, the same at every step.  The whole offset stays
     // in the vector operand, which the buffer's range check covers.
 #pragma unroll
     for (int i = 0; i < R; i++) {
-        const unsigned r = (unsigned)(r0 + i);
+        const unsigned r = PAIR ? (unsigned)((r0 + i) >> 1) : (unsigned)(r0 + i);
+        const rsrc_t &W = PAIR && (i & 1) ? W2 : W1;
+        const rsrc_t &WS = PAIR && (i & 1) ? WS2 : WS1;
         if constexpr (PREC == KH_Q8) {
             // chunk gl = seg * 64 * CPL + lane: weights 16 gl.., block gl / 2
             const unsigned uw = __builtin_amdgcn_readfirstlane(r * (unsigned)cols + (unsigned)(seg * CPL) * 1024u);

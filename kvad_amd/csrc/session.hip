@@ -276,12 +276,30 @@ int step(kh_ctx *ctx, kh_llm *m, const kh_llm_trace *tr = nullptr, bool embed = 
         const bool fm = norm_fusable(L.gate) && norm_fusable(L.up);
         const float *min_ = fm ? m->x : m->h;
         if (!fm && (rc = launch_rms_norm(ctx, m->x, L.mlp_norm, 1, s.n_embd, s.eps, m->h))) return rc;
+        // gate and up as one SwiGLU-pair job where the rows fit: each pair's
+        // swiglu is written once (hsw) and down stages it as it is, in place
+        // of every down workgroup recomputing swiglu(gate, up); the same
+        // values, so the same codes
+        bool paired = false;
+        if (fm && L.gate->precision == L.up->precision && L.gate->rows == L.up->rows && L.gate->cols == L.up->cols &&
+            gemv_pairs_fit(L.gate->precision, L.gate->cols) && L.down->precision != KH_F32 && fusable(L.down)) {
+            GemvJob j = normed(gemv_job(L.gate, min_, nullptr, nullptr, m->g, 0), true, L.mlp_norm, s.eps);
+            j.w2 = L.up->qs, j.ws2 = L.up->scales, j.y2 = m->u, j.h = m->hsw;
+            j.rows = 2 * (int)L.gate->rows;
+            rc = launch_gemv(ctx, L.gate->precision, &j, 1);
+            if (rc && rc != KH_DECLINED) return rc;
+            paired = rc == KH_OK;
+        }
         jobs.clear();
-        jobs.push_back({L.gate, normed(gemv_job(L.gate, min_, nullptr, nullptr, m->g, 0), fm, L.mlp_norm, s.eps)});
-        jobs.push_back({L.up, normed(gemv_job(L.up, min_, nullptr, nullptr, m->u, 0), fm, L.mlp_norm, s.eps)});
-        if ((!fm && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) || (rc = run_jobs(ctx, jobs))) return rc;
-        jobs.clear();
-        if (L.down->precision == KH_F32) {  // swiglu_inplace (ffn.rs:386), then the f32 GEMV
+        if (!paired) {
+            jobs.push_back({L.gate, normed(gemv_job(L.gate, min_, nullptr, nullptr, m->g, 0), fm, L.mlp_norm, s.eps)});
+            jobs.push_back({L.up, normed(gemv_job(L.up, min_, nullptr, nullptr, m->u, 0), fm, L.mlp_norm, s.eps)});
+            if ((!fm && (rc = wide_input(ctx, m, jobs, m->h, s.n_embd))) || (rc = run_jobs(ctx, jobs))) return rc;
+            jobs.clear();
+        }
+        if (paired) {  // down over swiglu(gate, up) as staged f32
+            jobs.push_back({L.down, gemv_job(L.down, m->hsw, nullptr, nullptr, m->x, 1)});
+        } else if (L.down->precision == KH_F32) {  // swiglu_inplace (ffn.rs:386), then the f32 GEMV
             if ((rc = launch_swiglu(ctx, m->g, m->u, s.n_ff))) return rc;
             jobs.push_back({L.down, gemv_job(L.down, m->g, nullptr, nullptr, m->x, 1)});
         } else if (fusable(L.down)) {
@@ -850,7 +868,7 @@ int kh_llm_new(kh_ctx *ctx, const kh_llm_spec *spec, kh_llm **out) {
     const size_t hq_n = std::max(s.n_ff, std::max(qd, s.n_embd));
     if ((rc = dev_alloc(&m->x, s.n_embd)) || (rc = dev_alloc(&m->h, s.n_embd)) ||
         (rc = dev_alloc(&m->qkv, qd + 2 * kvd)) || (rc = dev_alloc(&m->att, qd)) || (rc = dev_alloc(&m->g, s.n_ff)) ||
-        (rc = dev_alloc(&m->u, s.n_ff)) || (rc = dev_alloc(&m->logits, s.vocab)) ||
+        (rc = dev_alloc(&m->u, s.n_ff)) || (rc = dev_alloc(&m->hsw, s.n_ff)) || (rc = dev_alloc(&m->logits, s.vocab)) ||
         (rc = dev_alloc(&m->hq.qs, hq_n)) || (rc = dev_alloc(&m->hq.scales, hq_n / BLOCK)) ||
         (rc = dev_alloc(&m->hq.sums, hq_n / BLOCK)) || (rc = dev_alloc(&m->state, 3)) ||
         (rc = dev_alloc(&m->arg_v, ARGMAX_CAP)) || (rc = dev_alloc(&m->arg_i, ARGMAX_CAP)) ||
@@ -889,6 +907,7 @@ int kh_llm_free(kh_llm *m) {
             for (float *p : {L.attn_norm, L.mlp_norm, L.q_b, L.k_b, L.v_b, L.q_norm, L.k_norm})
                 if (p) (void)hipFree(p);
         for (void *p : {(void *)m->x, (void *)m->h, (void *)m->qkv, (void *)m->att, (void *)m->g, (void *)m->u,
+                        (void *)m->hsw,
                         (void *)m->logits, (void *)m->hq.qs, (void *)m->hq.scales, (void *)m->hq.sums,
                         (void *)m->state, (void *)m->final_norm, (void *)m->rope_cos, (void *)m->rope_sin,
                         m->attn_ws, (void *)m->out, (void *)m->arg_v, (void *)m->arg_i, (void *)m->arg_n, (void *)m->arrivals})

@@ -223,6 +223,36 @@ def test_attention_buckets(ctx, monkeypatch, single, variant):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("variant,kw", [("q8", dict(bias=True)), ("q4", dict(bias=True, prec="q4")),
+                                        ("q4k", FORWARD_VARIANTS["llama_q4k"])])
+def test_swiglu_pairs_equal_two_jobs(ctx, monkeypatch, variant, kw):
+    # The step's gate and up as one SwiGLU-pair GEMV (gate row i and up row i
+    # side by side, swiglu of the pair written once, down staging it as an
+    # f32 input) against two jobs with down staging swiglu(gate, up) in
+    # every workgroup (KVAD_GEMV_PAIR=0): the same values, the same codes,
+    # so the same logits to the bit, captured steps and per-token calls alike.
+    say("llm swiglu pairs", variant)
+    tokens = [3, 17, 500, 42, 7, 7, 99, 1, 256, 12]
+    a, _ = build(ctx, 190, **kw)
+    b, _ = build(ctx, 190, **kw)
+    for i, t in enumerate(tokens):
+        monkeypatch.delenv("KVAD_GEMV_PAIR", raising=False)
+        la, na = a.forward(t)
+        monkeypatch.setenv("KVAD_GEMV_PAIR", "0")
+        lb, nb = b.forward(t)
+        np.testing.assert_array_equal(la, lb, err_msg=f"step {i}")
+        assert na == nb
+    monkeypatch.delenv("KVAD_GEMV_PAIR", raising=False)
+    c1, _ = build(ctx, 191, **kw)
+    c2, _ = build(ctx, 191, **kw)
+    got = c1.generate(5, 8)
+    t, want = 5, []
+    for _ in range(8):
+        _, t = c2.forward(t)
+        want.append(t)
+    np.testing.assert_array_equal(got, want)
+
+
 def test_forced_short_splits_stay_inside_the_session_workspace(ctx, monkeypatch):
     # KVAD_ATTN_SPLIT=32 asks for 32-position splits.  The session's
     # workspace sizes those only up to the 32-position line (1024 positions
