@@ -155,6 +155,13 @@ int kh_matvec_q_dev(kh_ctx *ctx, const kh_weight *w, const int8_t *qs, const flo
 int kh_debug_block_dots(kh_ctx *ctx, const kh_weight *w, const float *x, int32_t *dots);
 /* QActivation::new on the device: qs[n], scales[n/32], sums[n/32]. */
 int kh_debug_qact(kh_ctx *ctx, const float *x, size_t n, int8_t *qs, float *scales, int32_t *sums);
+/* Self-check (no counterpart in the reference): the device arithmetic of
+ * QActivation::new (quant.rs:1051-1059) over every float.  counts[0] and
+ * counts[1]: scales and inverses, for each finite amax >= 0, that differ from
+ * the IEEE quotients amax / 127 and 1 / scale; counts[2]: codes, for each of
+ * the 2^32 patterns t, that differ from t.round().clamp(-127.0, 127.0) as i8.
+ * All three are 0 on a correct build.  Synchronous. */
+int kh_debug_quant_check(kh_ctx *ctx, uint64_t *counts);
 /* Timing aid (no counterpart in the reference): one launch that reads every
  * byte of up to four weights once (codes and scales) with 16-byte loads and
  * no arithmetic, each workgroup writing one word of the device array

@@ -95,6 +95,7 @@ _SIGS = {
     "kh_matvec_q_dev": (C.c_int, [_p, _p, _p, _p, _p, _p, _p]),
     "kh_debug_block_dots": (C.c_int, [_p, _p, _p, _p]),
     "kh_debug_qact": (C.c_int, [_p, _p, _sz, _p, _p, _p]),
+    "kh_debug_quant_check": (C.c_int, [_p, _p]),
     "kh_kv_new": (C.c_int, [_p, _sz, _sz, _sz, _sz, C.POINTER(_p)]),
     "kh_kv_free": (C.c_int, [_p]),
     "kh_kv_push": (C.c_int, [_p, _sz, _p, _p, _sz]),
@@ -401,6 +402,15 @@ def qact(ctx: Context, x):
     su = np.empty(n // 32, np.int32)
     _check(lib.kh_debug_qact(ctx.h, _ptr(x), n, _ptr(qs), _ptr(sc), _ptr(su)))
     return qs, sc, su
+
+
+def quant_check(ctx: Context):
+    """The activation quantiser's arithmetic over every float (a self-check):
+    (scales, inverses, codes) that differ from IEEE division and Rust's
+    rounding; all zero on a correct build."""
+    counts = np.zeros(3, np.uint64)
+    _check(lib.kh_debug_quant_check(ctx.h, _ptr(counts)))
+    return tuple(int(c) for c in counts)
 
 
 class QCache:

@@ -503,6 +503,19 @@ int kh_debug_qact(kh_ctx *ctx, const float *x, size_t n, int8_t *qs, float *scal
     return KH_OK;
 }
 
+int kh_debug_quant_check(kh_ctx *ctx, uint64_t *counts) {
+    if (!ctx || !counts) return fail(KH_EINVAL, "kh_debug_quant_check: null argument");
+    Guard g(ctx);
+    int rc = ensure(ctx, ctx->io, 256);
+    if (rc) return rc;
+    unsigned long long *d = static_cast<unsigned long long *>(ctx->io.ptr);
+    KH_HIP(hipMemsetAsync(d, 0, 3 * sizeof(unsigned long long), ctx->stream));
+    if ((rc = launch_quant_check(ctx, d))) return rc;
+    KH_HIP(hipMemcpyAsync(counts, d, 3 * sizeof(unsigned long long), hipMemcpyDeviceToHost, ctx->stream));
+    KH_HIP(hipStreamSynchronize(ctx->stream));
+    return KH_OK;
+}
+
 int kh_qact_dev(kh_ctx *ctx, const float *x, size_t m, size_t n, int8_t *qs, float *scales, int32_t *sums) {
     if (!ctx || !x || !qs || !scales || !sums) return fail(KH_EINVAL, "kh_qact_dev: null argument");
     if (n % BLOCK) return fail(KH_EINVAL, "kh_qact_dev: n must be a multiple of 32");

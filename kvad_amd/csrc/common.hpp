@@ -180,6 +180,7 @@ int ensure(kh_ctx *ctx, Workspace &w, size_t bytes);
 // ---- launchers (each defined in the .hip file that holds its kernels) ----
 // Activation quantiser: m rows of k floats -> QAct.  k % 32 == 0.
 int launch_qact(kh_ctx *ctx, const float *x, size_t m, size_t k, const QAct &out);
+int launch_quant_check(kh_ctx *ctx, unsigned long long *counts);  // counts[3], device, zeroed
 
 // One GEMV job: y[rows] = x W^T (+bias) for a quantised or f32 weight.
 struct GemvJob {

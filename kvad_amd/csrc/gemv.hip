@@ -56,6 +56,36 @@ __global__ __launch_bounds__(256) void qact_kernel(const float *__restrict__ x, 
     }
 }
 
+// The activation quantiser's arithmetic against its definition for every
+// float: counts[0] scales and counts[1] inverses (qscale of each finite
+// amax >= 0) that differ from the IEEE quotients amax / 127 and 1 / scale,
+// counts[2] codes (qround of each of the 2^32 patterns) that differ from
+// Rust's t.round().clamp(-127.0, 127.0) as i8 (NaN to 0).
+__global__ __launch_bounds__(256) void quant_check_kernel(unsigned long long *counts) {
+    unsigned long long ns = 0, ni = 0, nr = 0;
+    const unsigned long long stride = (unsigned long long)gridDim.x * blockDim.x;
+    for (unsigned long long u = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; u < (1ull << 32);
+         u += stride) {
+        const unsigned b = (unsigned)u;
+        if (b <= 0x7f7fffffu) {
+            const float a = __builtin_bit_cast(float, b);
+            const float sref = a / 127.0f;
+            const float iref = sref > 0.0f ? 1.0f / sref : 0.0f;
+            float sc, inv;
+            qscale(a, sc, inv);
+            ns += __builtin_bit_cast(unsigned, sc) != __builtin_bit_cast(unsigned, sref);
+            ni += __builtin_bit_cast(unsigned, inv) != __builtin_bit_cast(unsigned, iref);
+        }
+        const float t = __builtin_bit_cast(float, b);
+        int ref = 0;
+        if (t == t) ref = (int)fminf(fmaxf(roundf(t), -127.0f), 127.0f);
+        nr += qround(t) != ref;
+    }
+    if (ns) atomicAdd(counts + 0, ns);
+    if (ni) atomicAdd(counts + 1, ni);
+    if (nr) atomicAdd(counts + 2, nr);
+}
+
 // QActBatch::new of h = swiglu(g, u) (tensor.rs:344-350, quant.rs:693-714).
 __global__ __launch_bounds__(256) void swiglu_qact_kernel(const float *__restrict__ g, const float *__restrict__ u,
                                                          size_t nblocks, int8_t *__restrict__ qs,
@@ -941,6 +971,12 @@ int launch_qact(kh_ctx *ctx, const float *x, size_t m, size_t k, const QAct &out
     size_t threads = nblocks * 8;
     dim3 grid((unsigned)((threads + 255) / 256)), block(256);
     hipLaunchKernelGGL(qact_kernel, grid, block, 0, ctx->stream, x, nblocks, out.qs, out.scales, out.sums);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
+int launch_quant_check(kh_ctx *ctx, unsigned long long *counts) {
+    hipLaunchKernelGGL(quant_check_kernel, dim3(8192), dim3(256), 0, ctx->stream, counts);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }

@@ -56,26 +56,62 @@ __device__ __forceinline__ float swiglu1(float g, float u) {
 // activation quantisation: 8 lanes per 32-block, 4 values each
 // ---------------------------------------------------------------------------
 
+// The block's scale amax / 127 and its inverse (quant.rs:1052-1053), each
+// rounded once as IEEE division rounds them, in a third of the instructions
+// of two divides:
+//  - amax / 127: the product with RN(1/127) corrected once by its exact
+//    residual amax - 127 q (Markstein's division step, P. Markstein, IBM J.
+//    Res. Dev. 34(1), 1990);
+//  - 1 / scale: v_rcp_f32 (within an ulp) and one Markstein step.
+// Both equal the IEEE results for every finite amax >= 0 whose scale is zero
+// or normal (kh_debug_quant_check scans all 2^32 floats); an infinite amax,
+// or a scale that underflows to a subnormal, takes the divides.
+__device__ __forceinline__ void qscale(float amax, float &scale, float &inv) {
+    constexpr float r = 0x1.020408p-7f;  // RN(1/127)
+    const float q = amax * r;
+    const float rem = __builtin_fmaf(-q, 127.0f, amax);
+    scale = __builtin_fmaf(rem, r, q);
+    // +0 or +normal (v_cmp_class: bit 6 = +0, bit 8 = +normal)
+    if (__builtin_expect(__builtin_amdgcn_classf(scale, (1 << 6) | (1 << 8)), 1)) {
+        const float y = __builtin_amdgcn_rcpf(scale);
+        const float e = __builtin_fmaf(-scale, y, 1.0f);
+        inv = scale > 0.0f ? __builtin_fmaf(e, y, y) : 0.0f;
+    } else {
+        scale = amax / 127.0f;
+        inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    }
+}
+
+// (t.round().clamp(-127.0, 127.0) as i8) of quant.rs:1059: half away from
+// zero as trunc(t + copysign(0.5 - 2^-25, t)) (the sum rounds up to the next
+// integer exactly when t's fraction is at least a half), the clamp on the
+// integer; NaN gives 0 and +-inf +-127, as Rust's saturating cast does.
+// Equal to the definition for all 2^32 floats (kh_debug_quant_check).
+__device__ __forceinline__ int qround(float t) {
+    const int q = (int)(t + __builtin_copysignf(0x1.fffffep-2f, t));
+    return min(max(q, -127), 127);
+}
+
 // One lane's share of QActivation::new (quant.rs:1051-1064): returns the four
 // codes packed; *scale and *sum are the block's (same in all 8 lanes).
 __device__ __forceinline__ int quantize4(float4 v, float *scale_out, int *sum_out) {
-    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    a = fmaxf(a, dppf<DPP_XOR1>(a));
-    a = fmaxf(a, dppf<DPP_XOR2>(a));
-    a = fmaxf(a, dppf<DPP_HALF_MIRROR>(a));
-    float scale = a / 127.0f;
-    float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-    float e[4] = {v.x, v.y, v.z, v.w};
-    int packed = 0, s = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        float t = e[k] * inv;
-        t = roundf(t);
-        t = fminf(fmaxf(t, -127.0f), 127.0f);
-        int q = (int)t;
-        s += q;
-        packed |= (q & 0xff) << (8 * k);
-    }
+    // the block's amax over its 8 lanes; NaN is passed over, as f32::max does
+    // (fmax with 0 also maps a lane of four NaN to 0), and the non-negative
+    // values compare as their bit patterns do, so the lanes meet with
+    // integer maxima
+    const float a4 = fmaxf(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))), 0.0f);
+    int ab = __builtin_bit_cast(int, a4);
+    ab = max(ab, dpp<DPP_XOR1>(ab));
+    ab = max(ab, dpp<DPP_XOR2>(ab));
+    ab = max(ab, dpp<DPP_HALF_MIRROR>(ab));
+    float scale, inv;
+    qscale(__builtin_bit_cast(float, ab), scale, inv);
+    const int q0 = qround(v.x * inv), q1 = qround(v.y * inv), q2 = qround(v.z * inv), q3 = qround(v.w * inv);
+    // bytes q0 q1 q2 q3, low to high
+    const unsigned p01 = __builtin_amdgcn_perm((unsigned)q1, (unsigned)q0, 0x0c0c0400u);
+    const unsigned p23 = __builtin_amdgcn_perm((unsigned)q3, (unsigned)q2, 0x0c0c0400u);
+    const int packed = (int)(p01 | (p23 << 16));
+    int s = (q0 + q1) + (q2 + q3);
     s += dpp<DPP_XOR1>(s);
     s += dpp<DPP_XOR2>(s);
     s += dpp<DPP_HALF_MIRROR>(s);

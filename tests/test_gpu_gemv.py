@@ -66,11 +66,23 @@ def test_activation_quantiser_is_bit_exact(ctx, n):
     x = O.normal(7, n)
     x[:32] *= 1000.0  # an outlier block
     x[32:64] = 0.0    # an all-zero block
+    x[64:96] *= 1e-38  # scales below the normal range: the divides' branch
+    x[96:128] *= 1e-41  # subnormal inputs
+    x[128:160] = np.float32(3e38) * np.sign(x[128:160])  # near the largest float
     qs, sc, su = K.qact(ctx, x)
     q2, s2, u2 = O.qact(x)
     np.testing.assert_array_equal(qs, q2)
     np.testing.assert_array_equal(sc.view(np.uint32), s2.view(np.uint32))
     np.testing.assert_array_equal(su, u2)
+
+
+def test_quantiser_arithmetic_over_every_float(ctx):
+    # the scale amax / 127, its inverse and the rounding of quant.rs:1052-1059
+    # as the device computes them (a Markstein-corrected product and
+    # reciprocal, an add-and-truncate rounding), against IEEE division and
+    # round-half-away-from-zero for all 2^32 floats
+    say("quantiser arithmetic, every float")
+    assert K.quant_check(ctx) == (0, 0, 0)
 
 
 SHAPES = {
