@@ -578,11 +578,11 @@ __device__ __forceinline__ void compute_multi(const Chunks<PREC, CPL, 1> &c, flo
                 lo += dpp<DPP_XOR1>(lo);
                 hi += dpp<DPP_XOR1>(hi);
                 const int d = half ? hi : lo;
-                float t1 = dl * (float)d;
-                float t2 = ml * (float)asum;
-                float sc = t1 - t2;
-                sc = as * sc;
-                acc[k] += sc;
+                // the single-token kernel's roundings (compute_chunks): ml * asum,
+                // dl * d less that, then into the row, each rounded once
+                const float t2 = __builtin_fmaf(ml, (float)asum, -0.0f);
+                const float sc = __builtin_fmaf(dl, (float)d, -t2);
+                acc[k] = __builtin_fmaf(as, sc, acc[k]);
             }
         }
     }

@@ -297,16 +297,16 @@ __device__ __forceinline__ void compute_chunks(const Chunks<PREC, CPL, R> &c, fl
                 const int4 h = c.h[i][t];
                 unsigned sc, mn;
                 q4k_scale_min_bfe(h, L, sc, mn);
-                // (d * sc) * dot rounded once, as f32(d) * sc is exact; sc * dot
-                // (|dot| < 2^16, sc < 64) and mn * asum are exact 24-bit products,
-                // so d * (sc * dot) is the same single rounding
+                // sc * dot (|dot| < 2^16, sc < 64) and mn * asum are exact 24-bit
+                // products, and f32(d) * sc is exact, so d * (sc * dot) is the
+                // block's d * sc * dot: dmin * mn * asum rounded once, d * sc *
+                // dot less that rounded once (one fma, which takes the f16
+                // header halves as they are), then one fma into the row
                 const int isc = mul24((int)sc, d);
                 const int imn = mul24((int)mn, asum);
-                float t1 = half_bits_to_float((unsigned)h.x) * (float)isc;
-                float t2 = half_bits_to_float((unsigned)h.x >> 16) * (float)imn;
-                float s = t1 - t2;
-                s = as * s;
-                acc[i] += s;
+                const float t2 = __builtin_fmaf(half_bits_to_float((unsigned)h.x >> 16), (float)imn, -0.0f);
+                const float s = __builtin_fmaf(half_bits_to_float((unsigned)h.x), (float)isc, -t2);
+                acc[i] = __builtin_fmaf(as, s, acc[i]);
                 if (DOTS && g < C && r0 + i < rows) dots[(size_t)(r0 + i) * nb + (g >> 3) * 8 + j] = d;
             }
         }
