@@ -277,10 +277,14 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     // activation.
     const int my_groups = lw < ngroups ? (ngroups - lw + nw - 1) / nw : 0;
     const int steps = my_groups * nseg;
-    auto load_step = [&](Chunks<PREC, CPL, R> &c, int s) {
+    // loads are issued, and steps computed, in step order: each keeps a
+    // cursor (its row group lw + k * nw and segment) instead of dividing
+    int lk = 0, lseg = 0;
+    auto load_step = [&](Chunks<PREC, CPL, R> &c) {
         __builtin_amdgcn_sched_barrier(0);
-        load_chunks<PREC, CPL, R, PAIR>(c, W, WS, (lw + (s / nseg) * nw) * R, cols, nb, s % nseg, lane, W2, WS2);
+        load_chunks<PREC, CPL, R, PAIR>(c, W, WS, (lw + lk * nw) * R, cols, nb, lseg, lane, W2, WS2);
         __builtin_amdgcn_sched_barrier(0);
+        if (++lseg == nseg) lseg = 0, lk++;
     };
     Stage<KIND, stage_batch(CPL, WIDE)> st;
     stage_load<KIND, stage_batch(CPL, WIDE), NWV>(job, st, nb, tid);
@@ -298,7 +302,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
     Chunks<PREC, CPL, R> ca, cb;
-    load_step(ca, 0);
+    load_step(ca);  // step 0
 
     // ---- stage the activation in LDS (zero blocks pad the tail) ---------
     int8_t *sq = reinterpret_cast<int8_t *>(lds);
@@ -312,8 +316,8 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     for (int i = 0; i < R; i++) acc[i] = 0.0f;
     // one step: the dot products of `c`, then (at a row group's last
     // segment) the rows' sums written out
-    auto run_step = [&](const Chunks<PREC, CPL, R> &c, int step) {
-        const int k = step / nseg, seg = step % nseg;
+    int k = 0, seg = 0;
+    auto run_step = [&](const Chunks<PREC, CPL, R> &c) {
         const int r0 = (lw + k * nw) * R;
         compute_chunks<PREC, CPL, R, DOTS>(c, acc, sq, ssc, ssum, seg, lane, r0, rows, nb, C, job.dots);
         if (PAIR && seg == nseg - 1) {
@@ -358,16 +362,17 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
                 acc[i] = 0.0f;
             }
         }
+        if (++seg == nseg) seg = 0, k++;
     };
     // Every way back to the top of the loop has issued the same loads in the
     // same order (the steps' loads in flight are always even, then odd), so
     // each step waits only for its own loads; the last steps leave the loop
     // by paths of their own and issue nothing past the wave's work.
     for (int step = 0; step < steps; step += 2) {
-        load_step(cb, step + 1);
-        run_step(ca, step);
-        load_step(ca, step + 2);
-        if (step + 1 < steps) run_step(cb, step + 1);
+        load_step(cb);  // step + 1
+        run_step(ca);   // step
+        load_step(ca);  // step + 2
+        if (step + 1 < steps) run_step(cb);
     }
     if (argm) {  // the workgroup's choice: its waves' in wave order, the lowest index on ties
         __shared__ float s_av[NWV];
