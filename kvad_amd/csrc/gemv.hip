@@ -234,10 +234,17 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     const int lane = tid & (WAVE - 1);
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int blk = blockIdx.x;
-    int ji = 0;
-    for (int i = 1; i < tab.n; i++)
-        if (blk >= tab.j[i].wave0) ji = i;
+    const int ji = job_of(tab, blk);
     const GemvJob &job = tab.j[ji];
+    // The job's fields that come before the first vector loads, held in
+    // scalar registers at one point: one batch of scalar loads and one wait
+    // (loaded where first used, each would cost a round trip of its own).
+    __asm__ volatile("" ::"s"(job.rows), "s"(job.cols), "s"(job.nwaves), "s"(job.wave0), "s"(job.w), "s"(job.ws),
+                     "s"(job.wtab), "s"(job.xf), "s"(job.bias), "s"(job.accumulate), "s"(job.y));
+    if constexpr (KIND == IN_SWIGLU) __asm__ volatile("" ::"s"(job.xf2));
+    if constexpr (KIND == IN_NORM) __asm__ volatile("" ::"s"(job.norm_w), "s"(job.norm_eps));
+    if constexpr (KIND == IN_CODES) __asm__ volatile("" ::"s"(job.xq), "s"(job.xs), "s"(job.xsum));
+    if constexpr (PAIR) __asm__ volatile("" ::"s"(job.w2), "s"(job.ws2), "s"(job.y2), "s"(job.h));
     const bool routes = ROUTE && ji == tab.route_job - 1;  // uniform per workgroup
     const bool argm = ji == tab.arg_job - 1;              // uniform per workgroup
     float arg_bv = -INFINITY;                             // the wave's greedy choice (lane 0)
@@ -434,10 +441,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
 __global__ __launch_bounds__(256) void gemv_f32_kernel(JobTable tab) {
     const int lane = threadIdx.x & (WAVE - 1);
     const int blk = blockIdx.x;
-    int ji = 0;
-    for (int i = 1; i < tab.n; i++)
-        if (blk >= tab.j[i].wave0) ji = i;
-    const GemvJob &job = tab.j[ji];
+    const GemvJob &job = tab.j[job_of(tab, blk)];
     const int rows = job.rows, cols = job.cols;
     const int lw = (blk - job.wave0) * WAVES_PER_BLOCK + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const float *W = static_cast<const float *>(job.w);
@@ -810,6 +814,7 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
         tab.j[i].nwaves = nwg * p.nwv;
         blocks += nwg;
     }
+    set_first(tab);
     if (blocks == 0) return KH_OK;
     if (tab.arg_job && tab.j[tab.arg_job - 1].nwaves / p.nwv > tab.arg_cap)
         return fail(KH_DECLINED, "matvec: more workgroups than greedy partials");
@@ -896,6 +901,7 @@ int launch_f32(kh_ctx *ctx, JobTable &tab) {
         tab.j[i].nwaves = nw;
         blocks += (nw + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
     }
+    set_first(tab);
     if (blocks == 0) return KH_OK;
     hipLaunchKernelGGL(gemv_f32_kernel, dim3(blocks), dim3(256), 0, ctx->stream, tab);
     KH_HIP(hipGetLastError());

@@ -17,8 +17,12 @@ constexpr int WAVES_PER_BLOCK = 4;
 constexpr int MAX_JOBS = 24;
 
 struct JobTable {
-    GemvJob j[MAX_JOBS];
+    // the launch's n jobs; first[i] is job i's first workgroup, ascending,
+    // INT_MAX past the n jobs, so a workgroup finds its job from one batch
+    // of scalar loads
     int n;
+    int first[MAX_JOBS];
+    GemvJob j[MAX_JOBS];
     // ROUTE kernels: 1 + the job whose one workgroup, having computed a
     // token's router logits, also routes them (route.hpp); 0: none
     int route_job;
@@ -32,6 +36,28 @@ struct JobTable {
     int *arg_i, *arg_n;
     GreedyTail tail;  // tail.arrivals set: the step ends in this launch
 };
+
+// The job of workgroup `blk`: the last job whose first workgroup is at or
+// before it (jobs without workgroups start where the next one does).
+__device__ __forceinline__ int job_of(const JobTable &tab, int blk) {
+    // (first[i] - blk - 1) is negative exactly when first[i] <= blk: its
+    // sign bit counts, in scalar registers, for jobs 1..16 (one 64-byte
+    // load); jobs 17.. are looked at only past job 16
+    auto at_or_before = [&](int i) { return (int)((unsigned)(tab.first[i] - blk - 1) >> 31); };
+    int ji = 0;
+#pragma unroll
+    for (int i = 1; i <= 16; i++) ji += at_or_before(i);
+    if (ji == 16) {
+#pragma unroll
+        for (int i = 17; i < MAX_JOBS; i++) ji += at_or_before(i);
+    }
+    return ji;
+}
+
+// The job table's workgroup index, once every job's wave0 is set.
+inline void set_first(JobTable &tab) {
+    for (int i = 0; i < MAX_JOBS; i++) tab.first[i] = i < tab.n ? tab.j[i].wave0 : 0x7fffffff;
+}
 
 // Chunks of 16 bytes per weight row.
 __host__ __device__ inline int chunks_per_row(int prec, int cols) {
