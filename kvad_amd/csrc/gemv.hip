@@ -226,7 +226,8 @@ __device__ void greedy_tail(const JobTable &tab, const GemvJob &job, int groups,
 // outputs in LDS and its first wave routes them (MoE decode).
 template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB, bool ROUTE = false,
           bool PAIR = false>
-__global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
+__global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned f1, unsigned f2, unsigned f3,
+                                                          JobTable tab) {
     static_assert(!PAIR || R % 2 == 0, "SwiGLU pairs take an even number of rows a step");
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float s_lg[ROUTE ? MAX_EXPERTS : 1];  // the router's logits
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(JobTable tab) {
     const int lane = tid & (WAVE - 1);
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int blk = blockIdx.x;
-    const int ji = job_of(tab, blk);
+    const int ji = job_of(tab, Firsts{{f0, f1, f2, f3}}, blk);
     const GemvJob &job = tab.j[ji];
     // The job's fields that come before the first vector loads, held in
     // scalar registers at one point: one batch of scalar loads and one wait
@@ -753,8 +754,9 @@ Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
 
 template <int PREC, int CPL, int R, int KIND, bool WIDE, int NWV>
 void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds) {
+    const Firsts fp = packed_first(tab);
     hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, KIND, false, WIDE, NWV>), dim3(blocks), dim3(WAVE * NWV), lds,
-                       ctx->stream, tab);
+                       ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], tab);
 }
 
 template <int PREC, int CPL, int R, bool WIDE, int NWV = WPB>
@@ -767,12 +769,13 @@ void launch_kind(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int k
 
 template <int PREC, int CPL, int R>
 void launch_pair(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int kind) {
+    const Firsts fp = packed_first(tab);
     if (kind == IN_NORM)
         hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_NORM, false, false, WPB, false, true>), dim3(blocks),
-                           dim3(WAVE * WPB), lds, ctx->stream, tab);
+                           dim3(WAVE * WPB), lds, ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], tab);
     else
         hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_F32, false, false, WPB, false, true>), dim3(blocks),
-                           dim3(WAVE * WPB), lds, ctx->stream, tab);
+                           dim3(WAVE * WPB), lds, ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], tab);
 }
 
 template <int PREC>
@@ -816,6 +819,7 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     }
     set_first(tab);
     if (blocks == 0) return KH_OK;
+    if (blocks >= 0xffff) return fail(KH_DECLINED, "matvec: 65535 workgroups or more in one launch");
     if (tab.arg_job && tab.j[tab.arg_job - 1].nwaves / p.nwv > tab.arg_cap)
         return fail(KH_DECLINED, "matvec: more workgroups than greedy partials");
     const int pb = padded_blocks(PREC, maxC, p.cpl);
@@ -839,10 +843,13 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     }
     if (dots) {
         dim3 grid(blocks), block(WAVE * WPB);
+        const Firsts fp = packed_first(tab);
         if (kind == IN_CODES)
-            hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_CODES, true>), grid, block, lds, ctx->stream, tab);
+            hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_CODES, true>), grid, block, lds, ctx->stream, fp.f[0],
+                               fp.f[1], fp.f[2], fp.f[3], tab);
         else if (kind == IN_F32)
-            hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_F32, true>), grid, block, lds, ctx->stream, tab);
+            hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_F32, true>), grid, block, lds, ctx->stream, fp.f[0],
+                               fp.f[1], fp.f[2], fp.f[3], tab);
         else
             return fail(KH_EINVAL, "matvec: block dots are offered for plain and pre-quantised inputs only");
         KH_HIP(hipGetLastError());
@@ -861,10 +868,11 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
         return KH_OK;                                                         \
     }
     if (tab.route_job) {  // the MoE decode step's router with its routing
+        const Firsts fpr = packed_first(tab);
 #define KH_ROUTE(CPL, R)                                                                                       \
     if (p.cpl == CPL && p.r == R) {                                                                            \
         hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_F32, false, false, WPB, true>), dim3(blocks),         \
-                           dim3(WAVE * WPB), lds, ctx->stream, tab);                                           \
+                           dim3(WAVE * WPB), lds, ctx->stream, fpr.f[0], fpr.f[1], fpr.f[2], fpr.f[3], tab);   \
         KH_HIP(hipGetLastError());                                                                             \
         return KH_OK;                                                                                          \
     }

@@ -38,25 +38,51 @@ struct JobTable {
 };
 
 // The job of workgroup `blk`: the last job whose first workgroup is at or
-// before it (jobs without workgroups start where the next one does).
-__device__ __forceinline__ int job_of(const JobTable &tab, int blk) {
-    // (first[i] - blk - 1) is negative exactly when first[i] <= blk: its
-    // sign bit counts, in scalar registers, for jobs 1..16 (one 64-byte
-    // load); jobs 17.. are looked at only past job 16
-    auto at_or_before = [&](int i) { return (int)((unsigned)(tab.first[i] - blk - 1) >> 31); };
+// before it (jobs without workgroups start where the next one does).  v - blk
+// - 1 has its sign bit set exactly when v <= blk (v, blk < 2^31), a count in
+// scalar registers.  Jobs 1..8 come packed as 16-bit words in the kernel's
+// first four arguments, which are preloaded into scalar registers; jobs 9..
+// are looked up in the table by workgroups past job 8 only.
+struct Firsts {
+    unsigned f[4];
+};
+__device__ __forceinline__ int at_or_before(unsigned v, int blk) { return (int)((v - (unsigned)blk - 1u) >> 31); }
+__device__ __forceinline__ int job_of(const JobTable &tab, const Firsts &fp, int blk) {
     int ji = 0;
 #pragma unroll
-    for (int i = 1; i <= 16; i++) ji += at_or_before(i);
+    for (int k = 0; k < 4; k++) ji += at_or_before(fp.f[k] & 0xffffu, blk) + at_or_before(fp.f[k] >> 16, blk);
+    if (ji == 8) {
+#pragma unroll
+        for (int i = 9; i < MAX_JOBS; i++) ji += at_or_before((unsigned)tab.first[i], blk);
+    }
+    return ji;
+}
+// The same from the table alone (one batch of scalar loads for jobs 1..16).
+__device__ __forceinline__ int job_of(const JobTable &tab, int blk) {
+    int ji = 0;
+#pragma unroll
+    for (int i = 1; i <= 16; i++) ji += at_or_before((unsigned)tab.first[i], blk);
     if (ji == 16) {
 #pragma unroll
-        for (int i = 17; i < MAX_JOBS; i++) ji += at_or_before(i);
+        for (int i = 17; i < MAX_JOBS; i++) ji += at_or_before((unsigned)tab.first[i], blk);
     }
     return ji;
 }
 
-// The job table's workgroup index, once every job's wave0 is set.
+// The job table's workgroup index, once every job's wave0 is set; and jobs
+// 1..8 of it packed for the kernel's arguments (launches have fewer than
+// 0xffff workgroups).
 inline void set_first(JobTable &tab) {
     for (int i = 0; i < MAX_JOBS; i++) tab.first[i] = i < tab.n ? tab.j[i].wave0 : 0x7fffffff;
+}
+inline Firsts packed_first(const JobTable &tab) {
+    Firsts fp;
+    for (int k = 0; k < 4; k++) {
+        const unsigned lo = (unsigned)(tab.first[2 * k + 1] < 0xffff ? tab.first[2 * k + 1] : 0xffff);
+        const unsigned hi = (unsigned)(tab.first[2 * k + 2] < 0xffff ? tab.first[2 * k + 2] : 0xffff);
+        fp.f[k] = lo | hi << 16;
+    }
+    return fp;
 }
 
 // Chunks of 16 bytes per weight row.
