@@ -16,12 +16,13 @@ Flags that matter for parity:
                                      the scaling epilogues read them (the
                                      default parks them in AGPRs and copies
                                      every value out: one more VALU op each)
-  -mllvm -amdgpu-kernarg-preload-count=4
-                                     a kernel's first four argument words
-                                     arrive in scalar registers (the GEMV's
-                                     job index), no load round trip; code
-                                     objects keep a preamble that loads them
-                                     where the firmware does not preload
+  -mllvm -amdgpu-kernarg-preload-count=14
+                                     a kernel's first fourteen argument
+                                     words arrive in scalar registers (the
+                                     GEMV's job index and its first job's
+                                     pointers and sizes), no load round trip;
+                                     code objects keep a preamble that loads
+                                     them where the firmware does not preload
 """
 from __future__ import annotations
 
@@ -47,7 +48,7 @@ FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
-    "-mllvm", "-amdgpu-kernarg-preload-count=4",
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-Wall",
     "-Wno-unused-function",
 ]

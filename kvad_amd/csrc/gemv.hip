@@ -227,6 +227,8 @@ __device__ void greedy_tail(const JobTable &tab, const GemvJob &job, int groups,
 template <int PREC, int CPL, int R, int KIND, bool DOTS, bool WIDE = false, int NWV = WPB, bool ROUTE = false,
           bool PAIR = false>
 __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned f1, unsigned f2, unsigned f3,
+                                                          const void *w_0, const float *ws_0, const float *xf_0,
+                                                          const float *x2_0, int rows_0, unsigned colsnw_0,
                                                           JobTable tab) {
     static_assert(!PAIR || R % 2 == 0, "SwiGLU pairs take an even number of rows a step");
     extern __shared__ __align__(16) unsigned char lds[];
@@ -237,34 +239,43 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
     const int blk = blockIdx.x;
     const int ji = job_of(tab, Firsts{{f0, f1, f2, f3}}, blk);
     const GemvJob &job = tab.j[ji];
-    // The job's fields that come before the first vector loads, held in
-    // scalar registers at one point: one batch of scalar loads and one wait
-    // (loaded where first used, each would cost a round trip of its own).
-    __asm__ volatile("" ::"s"(job.rows), "s"(job.cols), "s"(job.nwaves), "s"(job.wave0), "s"(job.w), "s"(job.ws),
-                     "s"(job.wtab), "s"(job.xf), "s"(job.bias), "s"(job.accumulate), "s"(job.y));
-    if constexpr (KIND == IN_SWIGLU) __asm__ volatile("" ::"s"(job.xf2));
-    if constexpr (KIND == IN_NORM) __asm__ volatile("" ::"s"(job.norm_w), "s"(job.norm_eps));
-    if constexpr (KIND == IN_CODES) __asm__ volatile("" ::"s"(job.xq), "s"(job.xs), "s"(job.xsum));
-    if constexpr (PAIR) __asm__ volatile("" ::"s"(job.w2), "s"(job.ws2), "s"(job.y2), "s"(job.h));
+    // What the first vector loads need: job 0's from the kernel's arguments
+    // (preloaded into scalar registers, so a one-job launch issues its first
+    // loads with no scalar load at all), other jobs' from the table in one
+    // batch of scalar loads and one wait.  Top bit of colsnw_0: job 0 reads
+    // its weights through an expert table, or is too large for the packing.
+    const void *jw;
+    const float *jws, *jxf, *jx2;
+    int rows, cols, nw, wave0;
+    const bool fast = ji == 0 && !(colsnw_0 >> 31);
+    if (fast) {
+        jw = w_0, jws = ws_0, jxf = xf_0, jx2 = x2_0;
+        rows = rows_0, cols = (int)(colsnw_0 & 0xffffu), nw = (int)(colsnw_0 >> 16), wave0 = 0;
+    } else {
+        jw = job.w, jws = job.ws, jxf = job.xf;
+        jx2 = KIND == IN_SWIGLU ? job.xf2 : KIND == IN_NORM ? job.norm_w : nullptr;
+        rows = job.rows, cols = job.cols, nw = job.nwaves, wave0 = job.wave0;
+        __asm__ volatile("" ::"s"(rows), "s"(cols), "s"(nw), "s"(wave0), "s"(jw), "s"(jws), "s"(jxf), "s"(jx2),
+                         "s"(job.wtab));
+    }
     const bool routes = ROUTE && ji == tab.route_job - 1;  // uniform per workgroup
     const bool argm = ji == tab.arg_job - 1;              // uniform per workgroup
     float arg_bv = -INFINITY;                             // the wave's greedy choice (lane 0)
     int arg_bi = -1;
-    const int rows = job.rows, cols = job.cols, nb = cols / BLOCK;
+    const int nb = cols / BLOCK;
     const int C = chunks_per_row(PREC, cols);
     const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
     const int PB = padded_blocks(PREC, C, CPL);
     const int ngroups = (rows + R - 1) / R;
-    const int nw = job.nwaves;                              // waves on this job
-    const int lw = (blk - job.wave0) * NWV + wv;            // this wave among them
+    const int lw = (blk - wave0) * NWV + wv;  // this wave among the job's nw
 
     const int wrows = PAIR ? rows / 2 : rows;  // rows of each weight
     size_t wbytes = PREC == KH_Q8 ? (size_t)wrows * cols
                     : PREC == KH_Q4 ? (size_t)wrows * cols / 2
                                     : (size_t)wrows * (cols / QK_K) * Q4K_BYTES;
-    const void *wp = job.w;
-    const float *wsp = job.ws;
-    if (job.wtab) {  // an expert chosen on the device (MoE decode)
+    const void *wp = jw;
+    const float *wsp = jws;
+    if (!fast && job.wtab) {  // an expert chosen on the device (MoE decode)
         // one address for the wave: the buffer descriptors stay in scalar registers
         const int x = __builtin_amdgcn_readfirstlane(*job.sel);
         wp = uniform_ptr(job.wtab[x]);
@@ -295,10 +306,14 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
         if (++lseg == nseg) lseg = 0, lk++;
     };
     Stage<KIND, stage_batch(CPL, WIDE)> st;
-    stage_load<KIND, stage_batch(CPL, WIDE), NWV>(job, st, nb, tid);
+    stage_load<KIND, stage_batch(CPL, WIDE), NWV>(job, jxf, jx2, st, nb, tid);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    Chunks<PREC, CPL, R> ca, cb;
+    load_step(ca);  // step 0
     // The bias and residual values of the wave's rows, lane k * R + i holding
-    // those of row (lw + k * nw) * R + i, also ahead of the weights (a load in
-    // the epilogue would wait for every weight load in flight).
+    // those of row (lw + k * nw) * R + i: ahead of every later step's weights
+    // (a load in the epilogue would wait for every weight load in flight),
+    // behind step 0's, whose issue does not wait for these fields.
     const int my_rows = my_groups * R;
     const bool pre = my_rows <= WAVE;
     float pbias = 0.0f, pres = 0.0f;
@@ -308,9 +323,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
         if (job.bias) pbias = bldf(rsrc(job.bias, (size_t)rows * 4), off);
         if (job.accumulate) pres = bldf(rsrc(job.y, (size_t)rows * 4), off);
     }
-    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
-    Chunks<PREC, CPL, R> ca, cb;
-    load_step(ca);  // step 0
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- stage the activation in LDS (zero blocks pad the tail) ---------
     int8_t *sq = reinterpret_cast<int8_t *>(lds);
@@ -395,7 +408,7 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
                 const int i = s_ai[w];
                 if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) bv = v, bi = i;
             }
-            const int g = blk - job.wave0;
+            const int g = blk - wave0;
             if (tab.tail.arrivals) {  // read back by the last workgroup: past the L2
                 __hip_atomic_store(tab.arg_v + g, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(tab.arg_i + g, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -755,8 +768,9 @@ Plan plan_for(int prec, int maxC, int maxCols, int rows_total, int cu_count) {
 template <int PREC, int CPL, int R, int KIND, bool WIDE, int NWV>
 void launch_one(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds) {
     const Firsts fp = packed_first(tab);
+    const Lead ld = lead_job(tab);
     hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, KIND, false, WIDE, NWV>), dim3(blocks), dim3(WAVE * NWV), lds,
-                       ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], tab);
+                       ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], ld.w, ld.ws, ld.xf, ld.x2, ld.rows, ld.colsnw, tab);
 }
 
 template <int PREC, int CPL, int R, bool WIDE, int NWV = WPB>
@@ -770,12 +784,13 @@ void launch_kind(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int k
 template <int PREC, int CPL, int R>
 void launch_pair(kh_ctx *ctx, const JobTable &tab, int blocks, size_t lds, int kind) {
     const Firsts fp = packed_first(tab);
+    const Lead ld = lead_job(tab);
     if (kind == IN_NORM)
         hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_NORM, false, false, WPB, false, true>), dim3(blocks),
-                           dim3(WAVE * WPB), lds, ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], tab);
+                           dim3(WAVE * WPB), lds, ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], ld.w, ld.ws, ld.xf, ld.x2, ld.rows, ld.colsnw, tab);
     else
         hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_F32, false, false, WPB, false, true>), dim3(blocks),
-                           dim3(WAVE * WPB), lds, ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], tab);
+                           dim3(WAVE * WPB), lds, ctx->stream, fp.f[0], fp.f[1], fp.f[2], fp.f[3], ld.w, ld.ws, ld.xf, ld.x2, ld.rows, ld.colsnw, tab);
 }
 
 template <int PREC>
@@ -844,12 +859,13 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     if (dots) {
         dim3 grid(blocks), block(WAVE * WPB);
         const Firsts fp = packed_first(tab);
+    const Lead ld = lead_job(tab);
         if (kind == IN_CODES)
             hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_CODES, true>), grid, block, lds, ctx->stream, fp.f[0],
-                               fp.f[1], fp.f[2], fp.f[3], tab);
+                               fp.f[1], fp.f[2], fp.f[3], ld.w, ld.ws, ld.xf, ld.x2, ld.rows, ld.colsnw, tab);
         else if (kind == IN_F32)
             hipLaunchKernelGGL((gemv_kernel<PREC, 8, 1, IN_F32, true>), grid, block, lds, ctx->stream, fp.f[0],
-                               fp.f[1], fp.f[2], fp.f[3], tab);
+                               fp.f[1], fp.f[2], fp.f[3], ld.w, ld.ws, ld.xf, ld.x2, ld.rows, ld.colsnw, tab);
         else
             return fail(KH_EINVAL, "matvec: block dots are offered for plain and pre-quantised inputs only");
         KH_HIP(hipGetLastError());
@@ -869,10 +885,11 @@ int launch_prec(kh_ctx *ctx, JobTable &tab, int maxC, int maxCols, int rows_tota
     }
     if (tab.route_job) {  // the MoE decode step's router with its routing
         const Firsts fpr = packed_first(tab);
+        const Lead ld = lead_job(tab);
 #define KH_ROUTE(CPL, R)                                                                                       \
     if (p.cpl == CPL && p.r == R) {                                                                            \
         hipLaunchKernelGGL((gemv_kernel<PREC, CPL, R, IN_F32, false, false, WPB, true>), dim3(blocks),         \
-                           dim3(WAVE * WPB), lds, ctx->stream, fpr.f[0], fpr.f[1], fpr.f[2], fpr.f[3], tab);   \
+                           dim3(WAVE * WPB), lds, ctx->stream, fpr.f[0], fpr.f[1], fpr.f[2], fpr.f[3], ld.w, ld.ws, ld.xf, ld.x2, ld.rows, ld.colsnw, tab);   \
         KH_HIP(hipGetLastError());                                                                             \
         return KH_OK;                                                                                          \
     }

@@ -75,6 +75,19 @@ __device__ __forceinline__ int job_of(const JobTable &tab, int blk) {
 inline void set_first(JobTable &tab) {
     for (int i = 0; i < MAX_JOBS; i++) tab.first[i] = i < tab.n ? tab.j[i].wave0 : 0x7fffffff;
 }
+// Job 0's fields for the kernel's preloaded arguments (see gemv_kernel).
+struct Lead {
+    const void *w;
+    const float *ws, *xf, *x2;
+    int rows;
+    unsigned colsnw;  // cols | nwaves << 16; top bit: read job 0 from the table
+};
+inline Lead lead_job(const JobTable &tab) {
+    const GemvJob &j = tab.j[0];
+    const bool slow = j.wtab || j.cols > 0xffff || j.nwaves > 0x7fff;
+    return {j.w, j.ws, j.xf, j.xf2 ? j.xf2 : j.norm_w, j.rows,
+            slow ? 1u << 31 : (unsigned)j.cols | (unsigned)j.nwaves << 16};
+}
 inline Firsts packed_first(const JobTable &tab) {
     Firsts fp;
     for (int k = 0; k < 4; k++) {
@@ -388,7 +401,8 @@ __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.
 // or int4 c of the codes and scale and sum c.  One such batch covers the
 // whole activation (the launcher checks it: stage_fits).
 template <int KIND, int SB, int NWV>
-__device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &st, int nb, int tid) {
+__device__ __forceinline__ void stage_load(const GemvJob &job, const float *xf, const float *x2, Stage<KIND, SB> &st,
+                                           int nb, int tid) {
     constexpr int T = WAVE * NWV;
     // buffer loads: past the input's end they return zeros, with no branch
     if constexpr (KIND == IN_CODES) {
@@ -401,9 +415,9 @@ __device__ __forceinline__ void stage_load(const GemvJob &job, Stage<KIND, SB> &
             st.u[k] = make_float4(bldf(S, c * 4), __builtin_bit_cast(float, bldi(M, c * 4)), 0.f, 0.f);
         }
     } else {
-        const rsrc_t X = rsrc(job.xf, (size_t)nb * BLOCK * 4);
-        const void *x2 = KIND == IN_SWIGLU ? (const void *)job.xf2 : KIND == IN_NORM ? (const void *)job.norm_w : job.xf;
-        const rsrc_t X2 = rsrc(x2, (size_t)nb * BLOCK * 4);
+        // x2: swiglu's second input or the norm's weights
+        const rsrc_t X = rsrc(xf, (size_t)nb * BLOCK * 4);
+        const rsrc_t X2 = rsrc(KIND == IN_F32 ? xf : x2, (size_t)nb * BLOCK * 4);
 #pragma unroll
         for (int k = 0; k < SB; k++) {
             const unsigned c = (unsigned)(k * T + tid);
