@@ -960,20 +960,33 @@ struct StreamArgs {
     unsigned *sink;
 };
 
+// The first three arrays, their ends, the count, the total and the sink come
+// as the kernel's first arguments, preloaded into scalar registers as the
+// GEMV's first job is, so the probe pays no more scalar loads than the GEMV
+// before its first load; arrays 3.. are read from `a`.
 template <int L, int AUX>
-__global__ __launch_bounds__(1024) void stream_kernel(StreamArgs a) {
+__global__ __launch_bounds__(1024) void stream_kernel(const void *p0, const void *p1, const void *p2, unsigned e0,
+                                                      unsigned e1, unsigned e2, int n, unsigned total,
+                                                      unsigned *sink, StreamArgs a) {
     const unsigned T = blockDim.x, base = blockIdx.x * T * L + threadIdx.x;
     int4 v[L];
 #pragma unroll
     for (int u = 0; u < L; u++) {
         const unsigned i = base + (unsigned)u * T;
-        int k = 0;
+        int k = (n > 1 && i >= e0 ? 1 : 0) + (n > 2 && i >= e1 ? 1 : 0);
+        const void *p = k == 0 ? p0 : k == 1 ? p1 : p2;
+        unsigned lo = k == 0 ? 0u : k == 1 ? e0 : e1, hi = k == 0 ? e0 : k == 1 ? e1 : e2;
+        if (n > 3 && i >= e2) {  // array 3 or later
+            k = 3;
 #pragma unroll
-        for (int j = 0; j < STREAM_ARRAYS - 1; j++) k += (j < a.n - 1 && i >= a.end[j]) ? 1 : 0;
-        const unsigned lo = k ? a.end[k - 1] : 0u;
-        const rsrc_t r = rsrc(a.p[k], (size_t)(a.end[k] - lo) * 16);
-        v[u] = i < a.total ? __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (i - lo) * 16u, 0, AUX))
-                           : make_int4(0, 0, 0, 0);
+            for (int j = 3; j < STREAM_ARRAYS - 1; j++) k += (j < n - 1 && i >= a.end[j]) ? 1 : 0;
+            p = a.p[k];
+            lo = a.end[k - 1];
+            hi = a.end[k];
+        }
+        const rsrc_t r = rsrc(p, (size_t)(hi - lo) * 16);
+        v[u] = i < total ? __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, (i - lo) * 16u, 0, AUX))
+                         : make_int4(0, 0, 0, 0);
     }
     unsigned fold = 0;
 #pragma unroll
@@ -985,7 +998,7 @@ __global__ __launch_bounds__(1024) void stream_kernel(StreamArgs a) {
     if (threadIdx.x == 0) {
         unsigned f = 0;
         for (int w = 0; w < (int)(blockDim.x >> 6); w++) f ^= s_f[w];
-        a.sink[blockIdx.x & (STREAM_SINK - 1)] = f;
+        sink[blockIdx.x & (STREAM_SINK - 1)] = f;
     }
 }
 
@@ -1301,8 +1314,10 @@ int launch_stream(kh_ctx *ctx, size_t n, const kh_weight *const *w, unsigned *si
     const unsigned blocks = (at + (unsigned)(threads * L) - 1) / (unsigned)(threads * L);
 #define KH_STREAM(LL)                                                                                      \
     case LL:                                                                                               \
-        if (nt) hipLaunchKernelGGL((stream_kernel<LL, 2>), dim3(blocks), dim3(threads), 0, ctx->stream, a); \
-        else hipLaunchKernelGGL((stream_kernel<LL, 0>), dim3(blocks), dim3(threads), 0, ctx->stream, a);    \
+        if (nt) hipLaunchKernelGGL((stream_kernel<LL, 2>), dim3(blocks), dim3(threads), 0, ctx->stream, a.p[0], \
+                                   a.p[1], a.p[2], a.end[0], a.end[1], a.end[2], a.n, a.total, a.sink, a);    \
+        else hipLaunchKernelGGL((stream_kernel<LL, 0>), dim3(blocks), dim3(threads), 0, ctx->stream, a.p[0],  \
+                                a.p[1], a.p[2], a.end[0], a.end[1], a.end[2], a.n, a.total, a.sink, a);       \
         break;
     switch (L) {
         KH_STREAM(1) KH_STREAM(2) KH_STREAM(4) KH_STREAM(8)
