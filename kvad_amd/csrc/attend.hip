@@ -293,7 +293,10 @@ __global__ __launch_bounds__(64) void rope_push_rows_kernel(float *q, const floa
 }
 
 template <int HD, int R, int NW, bool ROPE>
-__global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
+// `len_dev` (a.len_dev) leads the arguments, which are preloaded into scalar
+// registers: the length's load is issued with the arguments' own, not after.
+__global__ __launch_bounds__(64 * NW) void attn_split_kernel(const int32_t *len_dev, AttnArgs a) {
+    const int len_raw = len_dev ? *len_dev : 0;  // ahead of at_row's branch on the arguments
     at_row(a, HD);
     constexpr int NQ4 = HD / 16;  // float4s per lane of a key row: products of 16 dims
     constexpr int VT = HD / 64;  // float4s per lane of a value row
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j16 = lane & 15, c4 = lane >> 4;
-    const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
+    const int L = len_dev ? min(len_raw + a.plus_one, a.L) : a.L;
     const int nsplit = (L + P - 1) / P;
     if (split >= nsplit) return;
     const int t0 = split * P;
@@ -781,10 +784,11 @@ __device__ __forceinline__ void merge_head(const float *pm, const float *pl, con
 }
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(const int32_t *len_dev, AttnArgs a) {
+    const int len_raw = len_dev ? *len_dev : 0;  // ahead of at_row's branch on the arguments
     at_row(a, HD);
     const int h = blockIdx.x;
-    const int L = a.len_dev ? min(*a.len_dev + a.plus_one, a.L) : a.L;
+    const int L = len_dev ? min(len_raw + a.plus_one, a.L) : a.L;
     const int ns = (L + a.P - 1) / a.P;
     if (ns <= 1) return;  // the split kernel finished a single split itself
     const rsrc_t V = rsrc(a.v, (size_t)L * a.vstride * 4);
@@ -995,16 +999,16 @@ void launch_split_r(const AttnArgs &a, dim3 grid, hipStream_t stream) {
     const int r = a.P / (16 * a.nw);
     const dim3 block(64 * a.nw);
     if (a.nw == 2) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 2, ROPE>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 2, ROPE>), grid, block, 0, stream, a.len_dev, a);
     } else if (a.nw == 8) {
-        if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1, 8, ROPE>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((attn_split_kernel<64, 2, 8, ROPE>), grid, block, 0, stream, a);
+        if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1, 8, ROPE>), grid, block, 0, stream, a.len_dev, a);
+        else hipLaunchKernelGGL((attn_split_kernel<64, 2, 8, ROPE>), grid, block, 0, stream, a.len_dev, a);
     } else if (r == 1) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 4, ROPE>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 4, ROPE>), grid, block, 0, stream, a.len_dev, a);
     } else if (HD == 128 || r == 2) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 2, 4, ROPE>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn_split_kernel<HD, 2, 4, ROPE>), grid, block, 0, stream, a.len_dev, a);
     } else {
-        hipLaunchKernelGGL((attn_split_kernel<64, 4, 4, ROPE>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn_split_kernel<64, 4, 4, ROPE>), grid, block, 0, stream, a.len_dev, a);
     }
 }
 
@@ -1134,9 +1138,9 @@ int run(kh_ctx *ctx, const AttnArgs &a, int head_dim, int nb = 1) {
     KH_HIP(hipGetLastError());
     if (a.nsplit > 1) {
         if (head_dim == 64)
-            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a);
+            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a.len_dev, a);
         else
-            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a);
+            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a.len_dev, a);
         KH_HIP(hipGetLastError());
     }
     return KH_OK;
