@@ -292,12 +292,24 @@ __global__ __launch_bounds__(64) void rope_push_rows_kernel(float *q, const floa
     }
 }
 
-template <int HD, int R, int NW, bool ROPE>
-// `len_dev` (a.len_dev) leads the arguments, which are preloaded into scalar
-// registers: the length's load is issued with the arguments' own, not after.
-__global__ __launch_bounds__(64 * NW) void attn_split_kernel(const int32_t *len_dev, AttnArgs a) {
-    const int len_raw = len_dev ? *len_dev : 0;  // ahead of at_row's branch on the arguments
-    at_row(a, HD);
+
+// The fields the first loads need lead the arguments, which are preloaded
+// into scalar registers (the build's kernarg preload): the device length's
+// load is issued at once, and the key, value and query loads wait on no
+// scalar load.  ROWS (batched rows, or fields too wide for the words) takes
+// them from the argument struct and the row table instead.  gg: group | gc
+// << 15 | plus_one << 31.
+template <int HD, int R, int NW, bool ROPE, bool ROWS>
+__global__ __launch_bounds__(64 * NW) void attn_split_kernel(const int32_t *len_dev, const float *k0, const float *v0,
+                                                             const float *q0, unsigned kst0, unsigned vst0, int L0,
+                                                             unsigned gg, AttnArgs a) {
+    const int len_raw = len_dev ? *len_dev : 0;
+    if constexpr (ROWS) {
+        at_row(a, HD);
+    } else {
+        a.k = k0, a.v = v0, a.q = q0, a.kstride = kst0, a.vstride = vst0, a.L = L0;
+        a.group = (int)(gg & 0x7fffu), a.gc = (int)((gg >> 15) & 0x7fffu), a.plus_one = (int)(gg >> 31);
+    }
     constexpr int NQ4 = HD / 16;  // float4s per lane of a key row: products of 16 dims
     constexpr int VT = HD / 64;  // float4s per lane of a value row
     constexpr int NT = HD / 16;  // 16-column tiles of the output
@@ -374,6 +386,10 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const int32_t *len_
             for (int v = 0; v < VT; v++)
                 vv[u][r][v] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(V, off, 256 * v, 0));
         }
+    // every key and value load is issued before any score is computed: left
+    // to itself the scheduler interleaves them with the products and drains
+    // the queue between batches, a round trip each
+    __builtin_amdgcn_sched_barrier(0);
 
     if (rope) {
         __shared__ __align__(16) float s_rot[17][HD];
@@ -994,28 +1010,41 @@ __global__ __launch_bounds__(64 * NW) void attn_pass_kernel(PassArgs a) {
 // P = 16 R nw positions per workgroup of nw waves: four waves with R in
 // {1, 2, 4} (hd 64) or {1, 2} (hd 128), or eight waves with R in {1, 2} (hd 64)
 // or 1 (hd 128) for P >= 128; the fused-RoPE form when the rope argument is set.
-template <int HD, bool ROPE>
+template <int HD, bool ROPE, bool ROWS>
 void launch_split_r(const AttnArgs &a, dim3 grid, hipStream_t stream) {
     const int r = a.P / (16 * a.nw);
     const dim3 block(64 * a.nw);
+    const unsigned gg = (unsigned)a.group | (unsigned)a.gc << 15 | (a.plus_one ? 1u << 31 : 0u);
+#define KH_SPLIT(HH, RR, NN)                                                                                  \
+    hipLaunchKernelGGL((attn_split_kernel<HH, RR, NN, ROPE, ROWS>), grid, block, 0, stream, a.len_dev, a.k, a.v, \
+                       a.q, (unsigned)a.kstride, (unsigned)a.vstride, a.L, gg, a)
     if (a.nw == 2) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 2, ROPE>), grid, block, 0, stream, a.len_dev, a);
+        KH_SPLIT(HD, 1, 2);
     } else if (a.nw == 8) {
-        if (r == 1) hipLaunchKernelGGL((attn_split_kernel<HD, 1, 8, ROPE>), grid, block, 0, stream, a.len_dev, a);
-        else hipLaunchKernelGGL((attn_split_kernel<64, 2, 8, ROPE>), grid, block, 0, stream, a.len_dev, a);
+        if (r == 1) KH_SPLIT(HD, 1, 8);
+        else KH_SPLIT(64, 2, 8);
     } else if (r == 1) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 1, 4, ROPE>), grid, block, 0, stream, a.len_dev, a);
+        KH_SPLIT(HD, 1, 4);
     } else if (HD == 128 || r == 2) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, 2, 4, ROPE>), grid, block, 0, stream, a.len_dev, a);
+        KH_SPLIT(HD, 2, 4);
     } else {
-        hipLaunchKernelGGL((attn_split_kernel<64, 4, 4, ROPE>), grid, block, 0, stream, a.len_dev, a);
+        KH_SPLIT(64, 4, 4);
     }
+#undef KH_SPLIT
 }
 
 template <int HD>
 void launch_split(const AttnArgs &a, dim3 grid, hipStream_t stream) {
-    if (a.rope.kraw) launch_split_r<HD, true>(a, grid, stream);
-    else launch_split_r<HD, false>(a, grid, stream);
+    // the row table, or fields too wide for the preloaded words: from the struct
+    const bool rows = a.rows || a.kstride > 0x7fffffffu || a.vstride > 0x7fffffffu || a.group > 0x7fff ||
+                      a.gc > 0x7fff;
+    if (a.rope.kraw) {
+        if (rows) launch_split_r<HD, true, true>(a, grid, stream);
+        else launch_split_r<HD, true, false>(a, grid, stream);
+    } else {
+        if (rows) launch_split_r<HD, false, true>(a, grid, stream);
+        else launch_split_r<HD, false, false>(a, grid, stream);
+    }
 }
 
 }  // namespace
