@@ -641,6 +641,23 @@ __device__ __forceinline__ void merge_head(const float *pm, const float *pl, con
     __shared__ float s_kw[CAP];
 
     const int sg = tid / NQ, dq = tid % NQ;
+    // each thread a run of splits, its statistics held in registers: loaded
+    // first (the reductions below wait on them, and loads complete in issue
+    // order), as buffer loads that read zero past the last split, under a
+    // bound uniform over the workgroup, so no load waits on a branch
+    const int per = (ns + 255) / 256, i0 = tid * per, n = min(ns - i0, per);
+    const size_t sbytes = (size_t)ns * n_head * 4;
+    const rsrc_t PM = rsrc(pm, sbytes), PL = rsrc(pl, sbytes), PN = rsrc(pmin, sbytes);
+    float m[PER], l[PER], mn[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        if (u < per) {
+            const unsigned o = (unsigned)(((size_t)(i0 + u) * n_head + h) * 4);
+            m[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(PM, o, 0, 0));
+            l[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(PL, o, 0, 0));
+            mn[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(PN, o, 0, 0));
+        }
+    }
     const rsrc_t PA = rsrc(pacc, (size_t)ns * n_head * HD * 4);
     auto pa_load = [&](int i) {  // zeros past the last split (buffer range)
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -650,18 +667,10 @@ __device__ __forceinline__ void merge_head(const float *pm, const float *pl, con
 #pragma unroll
     for (int u = 0; u < NB; u++) v[u] = pa_load(sg + u * NSG);
 
-    // each thread a run of splits, held in registers
-    const int per = (ns + 255) / 256, i0 = tid * per, n = min(ns - i0, per);
-    float m[PER], l[PER], mn[PER];
     float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < PER; u++) {
-        if (u < n) {
-            const size_t o = (size_t)(i0 + u) * n_head + h;
-            m[u] = pm[o], l[u] = pl[o], mn[u] = pmin[o];
-            mx = fmaxf(mx, m[u]);
-        }
-    }
+    for (int u = 0; u < PER; u++)
+        if (u < n) mx = fmaxf(mx, m[u]);
     const float M = block_reduce(mx, s_w[0], [](float x, float y) { return fmaxf(x, y); });
     float s = 0.0f;
     float c[PER];
@@ -799,10 +808,21 @@ __device__ __forceinline__ void merge_head(const float *pm, const float *pl, con
     }
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const int32_t *len_dev, AttnArgs a) {
-    const int len_raw = len_dev ? *len_dev : 0;  // ahead of at_row's branch on the arguments
-    at_row(a, HD);
+// The partials' pointers, the length and the split size lead the arguments
+// (preloaded, as the split kernel's): ROWS (batched rows, or head counts
+// past 16 bits) takes them from the struct and the row table.  pn: P |
+// plus_one << 31; hg: n_head | group << 16.
+template <int HD, bool ROWS>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const int32_t *len_dev, float *pm0, float *pl0, float *pmin0,
+                                                         float *pacc0, int L0, unsigned pn, unsigned hg,
+                                                         AttnArgs a) {
+    const int len_raw = len_dev ? *len_dev : 0;
+    if constexpr (ROWS) {
+        at_row(a, HD);
+    } else {
+        a.n_head = (int)(hg & 0xffffu), a.group = (int)(hg >> 16);
+        a.pm = pm0, a.pl = pl0, a.pmin = pmin0, a.pacc = pacc0, a.L = L0, a.P = (int)(pn & 0x7fffffffu), a.plus_one = (int)(pn >> 31);
+    }
     const int h = blockIdx.x;
     const int L = len_dev ? min(len_raw + a.plus_one, a.L) : a.L;
     const int ns = (L + a.P - 1) / a.P;
@@ -1166,10 +1186,21 @@ int run(kh_ctx *ctx, const AttnArgs &a, int head_dim, int nb = 1) {
     else launch_split<128>(a, grid, ctx->stream);
     KH_HIP(hipGetLastError());
     if (a.nsplit > 1) {
-        if (head_dim == 64)
-            hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a.len_dev, a);
-        else
-            hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(a.n_head, 1, nb), dim3(256), 0, ctx->stream, a.len_dev, a);
+        const dim3 mg(a.n_head, 1, nb);
+        const unsigned pn = (unsigned)a.P | (a.plus_one ? 1u << 31 : 0u);
+        const unsigned hg = (unsigned)a.n_head | (unsigned)a.group << 16;
+        const bool rows = a.rows || a.n_head > 0xffff || a.group > 0xffff;
+#define KH_MERGE(HH, RW)                                                                                           \
+    hipLaunchKernelGGL((attn_merge_kernel<HH, RW>), mg, dim3(256), 0, ctx->stream, a.len_dev, a.pm, a.pl, a.pmin, \
+                       a.pacc, a.L, pn, hg, a)
+        if (head_dim == 64) {
+            if (rows) KH_MERGE(64, true);
+            else KH_MERGE(64, false);
+        } else {
+            if (rows) KH_MERGE(128, true);
+            else KH_MERGE(128, false);
+        }
+#undef KH_MERGE
         KH_HIP(hipGetLastError());
     }
     return KH_OK;
