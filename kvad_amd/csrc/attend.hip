@@ -140,42 +140,35 @@ __device__ __forceinline__ float rows_min(float x) {
 // w = exp(s - M) * (1/S) with w < 1e-8 dropped (mod.rs:805-812).
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// Fused RoPE (the session's step).  Wave w takes heads w, w + NW, ...: the
-// G query heads, then (in the workgroup holding the new position) the KV
-// head's new key as head G; lane l holds dims l (+ 64) of the head, loaded
-// ahead of the K and V loads and rotated while they fly.
-template <int HD, int NW>
-struct RopeIn {
-    static constexpr int RH = (16 + NW) / NW;  // heads per wave (at most G + 1 <= 17 heads)
-    static constexpr int HE = HD / 64;         // dims per lane
-    float x[RH][HE];
-};
-
-template <int HD, int NW>
-__device__ __forceinline__ void rope_load(const AttnArgs &a, RopeIn<HD, NW> &r, int wave, int lane, int G, int h0,
-                                          int kvh, bool holds) {
-#pragma unroll
-    for (int i = 0; i < RopeIn<HD, NW>::RH; i++) {
-        const int h = wave + i * NW;
-#pragma unroll
-        for (int e = 0; e < RopeIn<HD, NW>::HE; e++) r.x[i][e] = 0.0f;
-        if (h < G || (h == G && holds)) {  // uniform per wave
-            const float *src = h < G ? a.q + (size_t)(h0 + h) * HD : a.rope.kraw + (size_t)kvh * HD;
-#pragma unroll
-            for (int e = 0; e < RopeIn<HD, NW>::HE; e++) r.x[i][e] = src[lane + 64 * e];
-        }
-    }
-}
-
 // One head held by a wave as dims lane + 64 e: rms_norm with `nw`
 // (norm_heads, llama.rs:122-127; none when null), then RoPE at position pos
 // (Rope::apply / apply_interleaved, tensor.rs:437-472), in place.
 template <int HD>
-__device__ __forceinline__ void norm_rope_head(float (&x)[HD / 64], const float *nw, const AttnRope &rp, int lane,
-                                               int pos) {
+struct RopeVals {
+    static constexpr int HE = HD / 64;
+    float w[HE], c[HE], sn[HE];  // norm weights (1 when none), cos and sin of the lane's dims
+};
+// The values norm_rope_head multiplies by: loaded apart from the arithmetic,
+// so a kernel can issue these loads ahead of others it waits on first.
+template <int HD>
+__device__ __forceinline__ void rope_vals_load(RopeVals<HD> &v, const float *nw, const AttnRope &rp, int lane, int pos) {
     constexpr int HE = HD / 64;
     const int half = HD / 2;
-    if (nw) {
+#pragma unroll
+    for (int e = 0; e < HE; e++) {
+        const int d = lane + 64 * e;
+        const int ip = rp.interleaved ? d >> 1 : d % half;
+        v.w[e] = nw ? nw[d] : 1.0f;
+        v.c[e] = rp.cos_t[(size_t)pos * half + ip];
+        v.sn[e] = rp.sin_t[(size_t)pos * half + ip];
+    }
+}
+template <int HD>
+__device__ __forceinline__ void norm_rope_vals(float (&x)[HD / 64], const RopeVals<HD> &v, bool normed,
+                                               const AttnRope &rp, int lane) {
+    constexpr int HE = HD / 64;
+    const int half = HD / 2;
+    if (normed) {
         float ss = 0.0f;
 #pragma unroll
         for (int e = 0; e < HE; e++) {
@@ -188,7 +181,7 @@ __device__ __forceinline__ void norm_rope_head(float (&x)[HD / 64], const float 
 #pragma unroll
         for (int e = 0; e < HE; e++) {
             const float u = x[e] * inv;
-            x[e] = u * nw[lane + 64 * e];
+            x[e] = u * v.w[e];
         }
     }
     float out[HE];
@@ -203,9 +196,8 @@ __device__ __forceinline__ void norm_rope_head(float (&x)[HD / 64], const float 
             if constexpr (HD == 128) pv = x[e ^ 1];  // d and d + 64 sit in one lane
             else pv = __shfl_xor(x[e], 32);
         }
-        const int ip = rp.interleaved ? d >> 1 : d % half;
         const bool first = rp.interleaved ? (d & 1) == 0 : d < half;
-        const float c = rp.cos_t[(size_t)pos * half + ip], sn = rp.sin_t[(size_t)pos * half + ip];
+        const float c = v.c[e], sn = v.sn[e];
         if (first) {  // a = x, b = partner: a c - b s
             const float ac = x[e] * c, bs = pv * sn;
             out[e] = ac - bs;
@@ -216,6 +208,45 @@ __device__ __forceinline__ void norm_rope_head(float (&x)[HD / 64], const float 
     }
 #pragma unroll
     for (int e = 0; e < HE; e++) x[e] = out[e];
+}
+template <int HD>
+__device__ __forceinline__ void norm_rope_head(float (&x)[HD / 64], const float *nw, const AttnRope &rp, int lane,
+                                               int pos) {
+    RopeVals<HD> v;
+    rope_vals_load<HD>(v, nw, rp, lane, pos);
+    norm_rope_vals<HD>(x, v, nw != nullptr, rp, lane);
+}
+
+// Fused RoPE (the session's step).  Wave w takes heads w, w + NW, ...: the
+// G query heads, then (in the workgroup holding the new position) the KV
+// head's new key as head G; lane l holds dims l (+ 64) of the head, loaded
+// with its norm weights, cos and sin (and the new value) ahead of the K and
+// V loads, and rotated while they fly.
+template <int HD, int NW>
+struct RopeIn {
+    static constexpr int RH = (16 + NW) / NW;  // heads per wave (at most G + 1 <= 17 heads)
+    static constexpr int HE = HD / 64;         // dims per lane
+    float x[RH][HE];
+    RopeVals<HD> v[RH];                        // their norm weights, cos and sin
+    float vnew;                                // the new value's dim tid (tid < HD, holding split)
+};
+
+template <int HD, int NW>
+__device__ __forceinline__ void rope_load(const AttnArgs &a, RopeIn<HD, NW> &r, int wave, int lane, int G, int h0,
+                                          int kvh, bool holds, int pos, int tid) {
+#pragma unroll
+    for (int i = 0; i < RopeIn<HD, NW>::RH; i++) {
+        const int h = wave + i * NW;
+#pragma unroll
+        for (int e = 0; e < RopeIn<HD, NW>::HE; e++) r.x[i][e] = 0.0f;
+        if (h < G || (h == G && holds)) {  // uniform per wave
+            const float *src = h < G ? a.q + (size_t)(h0 + h) * HD : a.rope.kraw + (size_t)kvh * HD;
+#pragma unroll
+            for (int e = 0; e < RopeIn<HD, NW>::HE; e++) r.x[i][e] = src[lane + 64 * e];
+            rope_vals_load<HD>(r.v[i], h < G ? a.rope.q_norm : a.rope.k_norm, a.rope, lane, pos);
+        }
+    }
+    r.vnew = holds && tid < HD ? a.rope.vraw[(size_t)kvh * HD + tid] : 0.0f;
 }
 
 // Per head: norm_rope_head into s_rot[head]; when `holds`, the new key
@@ -233,7 +264,7 @@ __device__ __forceinline__ void rope_apply(const AttnArgs &a, const RopeIn<HD, N
         float x[HE];
 #pragma unroll
         for (int e = 0; e < HE; e++) x[e] = r.x[i][e];
-        norm_rope_head<HD>(x, h < G ? a.rope.q_norm : a.rope.k_norm, a.rope, lane, pos);
+        norm_rope_vals<HD>(x, r.v[i], (h < G ? a.rope.q_norm : a.rope.k_norm) != nullptr, a.rope, lane);
 #pragma unroll
         for (int e = 0; e < HE; e++) {
             const int d = lane + 64 * e;
@@ -241,12 +272,9 @@ __device__ __forceinline__ void rope_apply(const AttnArgs &a, const RopeIn<HD, N
             if (h == G) a.kw[(size_t)pos * a.kstride + (size_t)kvh * HD + d] = x[e];
         }
     }
-    if (holds) {
-        for (int d = tid; d < HD; d += 64 * NW) {
-            const float v = a.rope.vraw[(size_t)kvh * HD + d];
-            s_vnew[d] = v;
-            a.vw[(size_t)pos * a.vstride + (size_t)kvh * HD + d] = v;
-        }
+    if (holds && tid < HD) {  // NW >= 2 waves: one dim a thread
+        s_vnew[tid] = r.vnew;
+        a.vw[(size_t)pos * a.vstride + (size_t)kvh * HD + tid] = r.vnew;
     }
 }
 
@@ -357,7 +385,7 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const int32_t *len_
     const bool holds = rope && pos >= t0 && pos < t0 + P;
     RopeIn<HD, NW> xr;
     if (rope) {
-        rope_load<HD, NW>(a, xr, wave, lane, G, h0, kvh, holds);
+        rope_load<HD, NW>(a, xr, wave, lane, G, h0, kvh, holds, pos, tid);
     } else {
         const float *qh = a.q + (size_t)(h0 + (hv ? j16 : 0)) * HD + 4 * c4;
 #pragma unroll
