@@ -273,6 +273,15 @@ int launch_gemv_multi(kh_ctx *ctx, const kh_weight *w, const QAct &x, size_t m, 
 // With xf set, the rows are f32 ([m][cols]) and every workgroup quantises
 // them as it stages them (the same codes as launch_qact); x is then unused.
 constexpr int MULTI_JOBS = 3;
+// The second and third jobs' first workgroups of a multi-token launch as one
+// 16-bit-pair word (0xffff: no such job), passed as a leading kernel
+// argument, which the build preloads into a scalar register: a workgroup
+// finds its job without a load.
+inline unsigned multi_firsts(int njobs, int g1, int g2) {
+    const unsigned a = njobs > 1 && g1 < 0xffff ? (unsigned)g1 : 0xffffu;
+    const unsigned b = njobs > 2 && g2 < 0xffff ? (unsigned)g2 : 0xffffu;
+    return a | b << 16;
+}
 // Whether the multi-token GEMV should stage m f32 rows of `cols` itself
 // (quantising them in every workgroup) rather than read codes quantised once
 // by a launch of their own: only while the stage is small.

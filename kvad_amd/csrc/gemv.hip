@@ -617,14 +617,16 @@ __device__ __forceinline__ void compute_multi(const Chunks<PREC, CPL, 1> &c, flo
 // of its first step are requested right after, so they fly while the
 // workgroup waits on the stage).
 template <int PREC, int CPL, int T>
-__global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(MultiArgs a) {
+__global__ __launch_bounds__(WAVE * WPB) void gemv_multi_kernel(unsigned g12, MultiArgs a) {
+    static_assert(MULTI_JOBS == 3, "g12 holds jobs 1 and 2");
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    int ji = 0;
-    for (int i = 1; i < a.njobs; i++)
-        if ((int)blockIdx.x >= a.j[i].wg0) ji = i;
+    const int ji = ((int)blockIdx.x >= (int)(g12 & 0xffffu) ? 1 : 0) + ((int)blockIdx.x >= (int)(g12 >> 16) ? 1 : 0);
     const MultiJob &job = a.j[ji];
+    // the fields the first loads need, in one batch of scalar loads
+    __asm__ volatile("" ::"s"(job.w), "s"(job.ws), "s"(job.rows), "s"(job.wg0), "s"(job.nwaves), "s"(a.cols),
+                     "s"(a.m), "s"(a.xq), "s"(a.xs), "s"(a.xsum), "s"(a.xf));
     const int rows = job.rows, cols = a.cols, nb = cols / BLOCK;
     const int C = chunks_per_row(PREC, cols);
     const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
@@ -1052,11 +1054,14 @@ int launch_swiglu_qact(kh_ctx *ctx, const float *g, const float *u, size_t m, si
 
 template <int PREC, int T>
 int launch_multi_t(kh_ctx *ctx, const MultiArgs &a, int cpl, int blocks, size_t lds) {
+    if (blocks >= 0xffff) return fail(KH_DECLINED, "matmul: 65535 workgroups or more in one launch");
     dim3 grid(blocks), block(WAVE * WPB);
     if (cpl == 1)
-        hipLaunchKernelGGL((gemv_multi_kernel<PREC, 1, T>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((gemv_multi_kernel<PREC, 1, T>), grid, block, lds, ctx->stream,
+                           multi_firsts(a.njobs, a.j[1].wg0, a.j[2].wg0), a);
     else
-        hipLaunchKernelGGL((gemv_multi_kernel<PREC, 2, T>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((gemv_multi_kernel<PREC, 2, T>), grid, block, lds, ctx->stream,
+                           multi_firsts(a.njobs, a.j[1].wg0, a.j[2].wg0), a);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }

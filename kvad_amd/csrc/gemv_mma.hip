@@ -308,15 +308,17 @@ __device__ __forceinline__ void compute_unit(const Unit<PREC, PAIR> &u, v4f &acc
 }
 
 template <int PREC, bool PAIR, int NW, int R>
-__global__ __launch_bounds__(WAVE * NW) void gemv_mma_kernel(MmaArgs a) {
+__global__ __launch_bounds__(WAVE * NW) void gemv_mma_kernel(unsigned g12, MmaArgs a) {
+    static_assert(MULTI_JOBS == 3, "g12 holds jobs 1 and 2");
     __shared__ __align__(16) float s_ex[NW][256];
     __shared__ __align__(16) float s_red[NW][WAVE * 4];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    int ji = 0;
-    for (int i = 1; i < a.njobs; i++)
-        if ((int)blockIdx.x >= a.j[i].g0) ji = i;
+    const int ji = ((int)blockIdx.x >= (int)(g12 & 0xffffu) ? 1 : 0) + ((int)blockIdx.x >= (int)(g12 >> 16) ? 1 : 0);
     const MmaJob &job = a.j[ji];
+    // the fields the first loads need, in one batch of scalar loads
+    __asm__ volatile("" ::"s"(job.w), "s"(job.ws), "s"(job.rows), "s"(job.g0), "s"(a.cols), "s"(a.m), "s"(a.units),
+                     "s"(a.xq), "s"(a.xs), "s"(a.xsum));
     const int rg = (int)blockIdx.x - job.g0, rows = job.rows, nb = a.cols / BLOCK;
 
     Lane L;
@@ -383,12 +385,14 @@ __global__ __launch_bounds__(WAVE * NW) void gemv_mma_kernel(MmaArgs a) {
 
 template <int PREC, bool PAIR, int R>
 int launch_nw(kh_ctx *ctx, const MmaArgs &a, int nwg, int nw) {
+    if (nwg >= 0xffff) return fail(KH_DECLINED, "matmul: 65535 workgroups or more in one launch");
+    const unsigned g12 = multi_firsts(a.njobs, a.j[1].g0, a.j[2].g0);
     if (nw == 16)
-        hipLaunchKernelGGL((gemv_mma_kernel<PREC, PAIR, 16, R>), dim3(nwg), dim3(WAVE * 16), 0, ctx->stream, a);
+        hipLaunchKernelGGL((gemv_mma_kernel<PREC, PAIR, 16, R>), dim3(nwg), dim3(WAVE * 16), 0, ctx->stream, g12, a);
     else if (nw == 8)
-        hipLaunchKernelGGL((gemv_mma_kernel<PREC, PAIR, 8, R>), dim3(nwg), dim3(WAVE * 8), 0, ctx->stream, a);
+        hipLaunchKernelGGL((gemv_mma_kernel<PREC, PAIR, 8, R>), dim3(nwg), dim3(WAVE * 8), 0, ctx->stream, g12, a);
     else
-        hipLaunchKernelGGL((gemv_mma_kernel<PREC, PAIR, 4, R>), dim3(nwg), dim3(WAVE * 4), 0, ctx->stream, a);
+        hipLaunchKernelGGL((gemv_mma_kernel<PREC, PAIR, 4, R>), dim3(nwg), dim3(WAVE * 4), 0, ctx->stream, g12, a);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
