@@ -1556,6 +1556,23 @@ __global__ __launch_bounds__(64 * NW) void mla_split_kernel(MlaArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; e++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(kq[k][i][e], q4[e], d, 0, 0, 0);
         }
+    // The value rows (the latent c again, in the P V operand layout), every
+    // load issued now, before the softmax's reductions and barriers: left to
+    // itself the scheduler streams them after the barriers, two at a time
+    // with a wait between.
+    const int D0 = DW * wave;
+    f4v vv[NW][4][VG];
+#pragma unroll
+    for (int u = 0; u < NW; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const size_t p = (size_t)(t0 + 16 * u + 4 * c4 + r);
+            const unsigned off = (unsigned)((p * a.cstride + D0 + 4 * j16) * 4);
+#pragma unroll
+            for (int v = 0; v < VG; v++)
+                vv[u][r][v] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 256 * v, 0));
+        }
+    __builtin_amdgcn_sched_barrier(0);
     float s[4], mx = -INFINITY, mn = INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -1609,19 +1626,8 @@ __global__ __launch_bounds__(64 * NW) void mla_split_kernel(MlaArgs a) {
     for (int r = 0; r < 4; r++) sP[j16][16 * wave + 4 * c4 + r] = e[r];
     __syncthreads();
 
-    // values: wave w forms dims DW w .. DW w + DW - 1 for every position of the split
-    const int D0 = DW * wave;
-    f4v vv[NW][4][VG];
-#pragma unroll
-    for (int u = 0; u < NW; u++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const size_t p = (size_t)(t0 + 16 * u + 4 * c4 + r);
-            const unsigned off = (unsigned)((p * a.cstride + D0 + 4 * j16) * 4);
-#pragma unroll
-            for (int v = 0; v < VG; v++)
-                vv[u][r][v] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(C, off, 256 * v, 0));
-        }
+    // values: wave w forms dims DW w .. DW w + DW - 1 for every position of
+    // the split (their loads were issued after the scores)
     f4v acc[4 * VG];
 #pragma unroll
     for (int q = 0; q < 4 * VG; q++) acc[q] = f4v{0.f, 0.f, 0.f, 0.f};
