@@ -242,27 +242,39 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
     // What the first vector loads need: job 0's from the kernel's arguments
     // (preloaded into scalar registers, so a one-job launch issues its first
     // loads with no scalar load at all), other jobs' from the table in one
-    // batch of scalar loads and one wait.  Top bit of colsnw_0: job 0 reads
-    // its weights through an expert table, or is too large for the packing.
-    const void *jw;
-    const float *jws, *jxf, *jx2;
-    int rows, cols, nw, wave0;
-    const bool fast = ji == 0 && !(colsnw_0 >> 31);
-    if (fast) {
-        jw = w_0, jws = ws_0, jxf = xf_0, jx2 = x2_0;
-        rows = rows_0, cols = (int)(colsnw_0 & 0xffffu), nw = (int)(colsnw_0 >> 16), wave0 = 0;
+    // batch of scalar loads and one wait.  colsnw_0 = cols | nwaves << 16,
+    // bit 30: every job stages job 0's input (the same activation and
+    // columns), so any job's activation loads issue at once and its weight
+    // fields' load overlaps them; bit 31: job 0 reads its weights through an
+    // expert table, or is too large for the packing.
+    const bool lead = !(colsnw_0 >> 31);
+    const bool fast = ji == 0 && lead;
+    const bool shared = lead && ((colsnw_0 >> 30) & 1u);
+    const float *jxf, *jx2;
+    int cols;
+    if (fast || shared) {
+        jxf = xf_0, jx2 = x2_0, cols = (int)(colsnw_0 & 0xffffu);
     } else {
-        jw = job.w, jws = job.ws, jxf = job.xf;
-        jx2 = KIND == IN_SWIGLU ? job.xf2 : KIND == IN_NORM ? job.norm_w : nullptr;
-        rows = job.rows, cols = job.cols, nw = job.nwaves, wave0 = job.wave0;
-        __asm__ volatile("" ::"s"(rows), "s"(cols), "s"(nw), "s"(wave0), "s"(jw), "s"(jws), "s"(jxf), "s"(jx2),
-                         "s"(job.wtab));
+        jxf = job.xf, jx2 = KIND == IN_SWIGLU ? job.xf2 : KIND == IN_NORM ? job.norm_w : nullptr, cols = job.cols;
+        __asm__ volatile("" ::"s"(jxf), "s"(jx2), "s"(cols));
+    }
+    const int nb = cols / BLOCK;
+    Stage<KIND, stage_batch(CPL, WIDE)> st;
+    stage_load<KIND, stage_batch(CPL, WIDE), NWV>(job, jxf, jx2, st, nb, tid);
+    __builtin_amdgcn_sched_barrier(0);  // the activation loads ahead of everything after
+    const void *jw;
+    const float *jws;
+    int rows, nw, wave0;
+    if (fast) {
+        jw = w_0, jws = ws_0, rows = rows_0, nw = (int)((colsnw_0 >> 16) & 0x3fffu), wave0 = 0;
+    } else {
+        jw = job.w, jws = job.ws, rows = job.rows, nw = job.nwaves, wave0 = job.wave0;
+        __asm__ volatile("" ::"s"(rows), "s"(nw), "s"(wave0), "s"(jw), "s"(jws), "s"(job.wtab));
     }
     const bool routes = ROUTE && ji == tab.route_job - 1;  // uniform per workgroup
     const bool argm = ji == tab.arg_job - 1;              // uniform per workgroup
     float arg_bv = -INFINITY;                             // the wave's greedy choice (lane 0)
     int arg_bi = -1;
-    const int nb = cols / BLOCK;
     const int C = chunks_per_row(PREC, cols);
     const int nseg = (C + WAVE * CPL - 1) / (WAVE * CPL);
     const int PB = padded_blocks(PREC, C, CPL);
@@ -305,9 +317,6 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
         __builtin_amdgcn_sched_barrier(0);
         if (++lseg == nseg) lseg = 0, lk++;
     };
-    Stage<KIND, stage_batch(CPL, WIDE)> st;
-    stage_load<KIND, stage_batch(CPL, WIDE), NWV>(job, jxf, jx2, st, nb, tid);
-    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
     Chunks<PREC, CPL, R> ca, cb;
     load_step(ca);  // step 0
     // The bias and residual values of the wave's rows, lane k * R + i holding

@@ -80,13 +80,18 @@ struct Lead {
     const void *w;
     const float *ws, *xf, *x2;
     int rows;
-    unsigned colsnw;  // cols | nwaves << 16; top bit: read job 0 from the table
+    unsigned colsnw;  // cols | nwaves << 16; bit 30: every job stages job 0's input; bit 31: job 0 from the table
 };
 inline Lead lead_job(const JobTable &tab) {
     const GemvJob &j = tab.j[0];
-    const bool slow = j.wtab || j.cols > 0xffff || j.nwaves > 0x7fff;
+    const bool slow = j.wtab || j.cols > 0xffff || j.nwaves > 0x3fff;
+    bool shared = j.xf != nullptr;  // an f32 input (codes made elsewhere come from the table)
+    for (int i = 1; i < tab.n && shared; i++) {
+        const GemvJob &o = tab.j[i];
+        shared = o.xf == j.xf && o.xf2 == j.xf2 && o.norm_w == j.norm_w && o.cols == j.cols;
+    }
     return {j.w, j.ws, j.xf, j.xf2 ? j.xf2 : j.norm_w, j.rows,
-            slow ? 1u << 31 : (unsigned)j.cols | (unsigned)j.nwaves << 16};
+            slow ? 1u << 31 : (unsigned)j.cols | (unsigned)j.nwaves << 16 | (shared ? 1u << 30 : 0u)};
 }
 inline Firsts packed_first(const JobTable &tab) {
     Firsts fp;
