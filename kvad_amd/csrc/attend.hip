@@ -840,6 +840,93 @@ __device__ __forceinline__ void merge_head(const float *pm, const float *pl, con
 // (preloaded, as the split kernel's): ROWS (batched rows, or head counts
 // past 16 bits) takes them from the struct and the row table.  pn: P |
 // plus_one << 31; hg: n_head | group << 16.
+// The merge of one head without barriers, for up to 16 * 256 / (HD / 4)
+// splits (256 at head_dim 64, 128 at 128): every load is issued at once
+// (each wave reads every split's max, sum and minimum, four splits a lane,
+// and its quarter of the dims of every split's partial values, HD / 16
+// float4s a lane-row of 64 / (HD / 16) splits), the maximum and the sum are
+// wave butterflies (each wave computes the same ones, in the same order),
+// the weights e^{m_j - M} pass through the wave's own LDS row, and the
+// split groups' sums meet by butterfly.  Returns false, having written
+// nothing, when a split straddles the 1e-8 line (some but not all of its
+// weights skipped): the caller then runs merge_head, which handles those.
+template <int HD>
+__device__ __forceinline__ bool merge_head_fast(const float *pm, const float *pl, const float *pmin, const float *pacc,
+                                                int ns, int n_head, int h, float *out) {
+    constexpr int NQ = HD / 16;     // float4s of a wave's dims
+    constexpr int SG = 64 / NQ;     // split groups a wave-row holds
+    constexpr int PJ = 16;          // partial values a lane holds at most
+    constexpr int PS = 4;           // splits of statistics a lane holds
+    static_assert(SG * PJ <= PS * 64, "statistics cover every split the partials do");
+    __shared__ float s_c[4][PS * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int dq = lane % NQ, sg = lane / NQ;
+    const size_t sb = (size_t)ns * n_head * 4;
+    const rsrc_t PM = rsrc(pm, sb), PL = rsrc(pl, sb), PN = rsrc(pmin, sb);
+    const rsrc_t PA = rsrc(pacc, sb * HD);
+    float m[PS], l[PS], mn[PS];
+#pragma unroll
+    for (int u = 0; u < PS; u++) {  // past the last split: out of range, zero
+        const unsigned o = (unsigned)((((size_t)(lane + 64 * u)) * n_head + h) * 4);
+        m[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(PM, o, 0, 0));
+        l[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(PL, o, 0, 0));
+        mn[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(PN, o, 0, 0));
+    }
+    float4 v[PJ];
+    const int d = (HD / 4) * wave + 4 * dq;
+#pragma unroll
+    for (int k = 0; k < PJ; k++) {  // split sg + SG k
+        const unsigned o = (unsigned)((((size_t)(sg + SG * k) * n_head + h) * HD + d) * 4);
+        v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(PA, o, 0, 0));
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < PS; u++)
+        if (lane + 64 * u < ns) mx = fmaxf(mx, m[u]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float c[PS], sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PS; u++) {
+        c[u] = lane + 64 * u < ns ? expf(m[u] - mx) : 0.0f;
+        sum = fmaf(l[u], c[u], sum);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o);
+    const float inv = 1.0f / sum;  // inv = 1 / sum, tensor.rs:304
+    bool straddle = false;
+#pragma unroll
+    for (int u = 0; u < PS; u++) {
+        if (lane + 64 * u < ns) {
+            const bool out_whole = c[u] * inv < 1e-8f;  // every weight of the split is skipped
+            if (!out_whole && expf(mn[u] - mx) * inv < 1e-8f) straddle = true;
+            s_c[wave][lane + 64 * u] = out_whole ? 0.0f : c[u];
+        }
+    }
+    if (__builtin_amdgcn_ballot_w64(straddle)) return false;  // the same in every wave
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");    // the wave's own LDS row
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < PJ; k++) {
+        const int j = sg + SG * k;
+        const float cj = j < ns ? s_c[wave][j] : 0.0f;
+        x.x = fmaf(cj, v[k].x, x.x);
+        x.y = fmaf(cj, v[k].y, x.y);
+        x.z = fmaf(cj, v[k].z, x.z);
+        x.w = fmaf(cj, v[k].w, x.w);
+    }
+#pragma unroll
+    for (int o = NQ; o < 64; o <<= 1) {  // the split groups, lane bits above dq
+        x.x = x.x + __shfl_xor(x.x, o);
+        x.y = x.y + __shfl_xor(x.y, o);
+        x.z = x.z + __shfl_xor(x.z, o);
+        x.w = x.w + __shfl_xor(x.w, o);
+    }
+    if (sg == 0)
+        *reinterpret_cast<float4 *>(out + (size_t)h * HD + d) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
+    return true;
+}
+
 template <int HD, bool ROWS>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const int32_t *len_dev, float *pm0, float *pl0, float *pmin0,
                                                          float *pacc0, int L0, unsigned pn, unsigned hg,
@@ -861,6 +948,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const int32_t *len_dev,
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               V, (unsigned)(((size_t)t * a.vstride + voff + 4 * d4) * 4), 0, 0));
     };
+    if (ns <= 16 * 64 / (HD / 16) && merge_head_fast<HD>(a.pm, a.pl, a.pmin, a.pacc, ns, a.n_head, h, a.out)) return;
     merge_head<HD, HD>(a.pm, a.pl, a.pmin, a.pacc, a.psc, ns, a.n_head, h, 0, a.P, L, vrow, a.out);
 }
 
