@@ -840,24 +840,30 @@ __device__ __forceinline__ void merge_head(const float *pm, const float *pl, con
 // (preloaded, as the split kernel's): ROWS (batched rows, or head counts
 // past 16 bits) takes them from the struct and the row table.  pn: P |
 // plus_one << 31; hg: n_head | group << 16.
-// The merge of one head without barriers, for up to 16 * 256 / (HD / 4)
-// splits (256 at head_dim 64, 128 at 128): every load is issued at once
-// (each wave reads every split's max, sum and minimum, four splits a lane,
-// and its quarter of the dims of every split's partial values, HD / 16
-// float4s a lane-row of 64 / (HD / 16) splits), the maximum and the sum are
+// The merge of dims d0 .. d0 + D of one head (rows of HD) without barriers,
+// for up to merge_fast_max(D) splits (128 for 64 or 128 dims): every
+// load is issued at once (each wave reads every split's max, sum and
+// minimum, four splits a lane, and its quarter of the dims of every split's
+// partial values, D / 16 float4s a lane-row of 64 / (D / 16) splits), the maximum and the sum are
 // wave butterflies (each wave computes the same ones, in the same order),
 // the weights e^{m_j - M} pass through the wave's own LDS row, and the
 // split groups' sums meet by butterfly.  Returns false, having written
 // nothing, when a split straddles the 1e-8 line (some but not all of its
 // weights skipped): the caller then runs merge_head, which handles those.
-template <int HD>
+// The most splits merge_head_fast takes for D dims: its partial values'
+// split groups and its statistics' four splits a lane both cover them, and
+// no more than 128: the more splits, the likelier one straddles the 1e-8
+// line, and a straddle costs the fast path's loads on top of merge_head's
+// (latent attention at L = 32768, 256 splits of random data: 40.8 -> 43.2 us
+// per layer when taken).
+constexpr int merge_fast_max(int d) { return 16 * 64 / (d / 16) < 128 ? 16 * 64 / (d / 16) : 128; }
+template <int HD, int D>
 __device__ __forceinline__ bool merge_head_fast(const float *pm, const float *pl, const float *pmin, const float *pacc,
-                                                int ns, int n_head, int h, float *out) {
-    constexpr int NQ = HD / 16;     // float4s of a wave's dims
+                                                int ns, int n_head, int h, int d0, float *out) {
+    constexpr int NQ = D / 16;      // float4s of a wave's dims
     constexpr int SG = 64 / NQ;     // split groups a wave-row holds
     constexpr int PJ = 16;          // partial values a lane holds at most
     constexpr int PS = 4;           // splits of statistics a lane holds
-    static_assert(SG * PJ <= PS * 64, "statistics cover every split the partials do");
     __shared__ float s_c[4][PS * 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int dq = lane % NQ, sg = lane / NQ;
@@ -873,7 +879,7 @@ __device__ __forceinline__ bool merge_head_fast(const float *pm, const float *pl
         mn[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(PN, o, 0, 0));
     }
     float4 v[PJ];
-    const int d = (HD / 4) * wave + 4 * dq;
+    const int d = d0 + (D / 4) * wave + 4 * dq;
 #pragma unroll
     for (int k = 0; k < PJ; k++) {  // split sg + SG k
         const unsigned o = (unsigned)((((size_t)(sg + SG * k) * n_head + h) * HD + d) * 4);
@@ -948,7 +954,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const int32_t *len_dev,
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               V, (unsigned)(((size_t)t * a.vstride + voff + 4 * d4) * 4), 0, 0));
     };
-    if (ns <= 16 * 64 / (HD / 16) && merge_head_fast<HD>(a.pm, a.pl, a.pmin, a.pacc, ns, a.n_head, h, a.out)) return;
+    if (ns <= merge_fast_max(HD) && merge_head_fast<HD, HD>(a.pm, a.pl, a.pmin, a.pacc, ns, a.n_head, h, 0, a.out))
+        return;
     merge_head<HD, HD>(a.pm, a.pl, a.pmin, a.pacc, a.psc, ns, a.n_head, h, 0, a.P, L, vrow, a.out);
 }
 
@@ -1766,6 +1773,9 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               C, (unsigned)(((size_t)t * a.cstride + 4 * d4) * 4), 0, 0));
     };
+    if (a.nsplit <= merge_fast_max(D) &&
+        merge_head_fast<MLA_LAT, D>(a.pm, a.pl, a.pmin, a.pacc, a.nsplit, a.n_head, h, D * blockIdx.y, a.out))
+        return;
     merge_head<MLA_LAT, D>(a.pm, a.pl, a.pmin, a.pacc, a.psc, a.nsplit, a.n_head, h, D * blockIdx.y, a.P, a.L,
                            vrow, a.out);
 }
