@@ -347,6 +347,17 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
     // one step: the dot products of `c`, then (at a row group's last
     // segment) the rows' sums written out
     int k = 0, seg = 0;
+    // The epilogue's fields, read once into scalar registers: read in the loop,
+    // under the epilogue's conditions, each was a scalar load and a wait
+    // every row group.
+    float *const yo = job.y;
+    const float *const bo = job.bias;
+    const int accum = job.accumulate;
+    const int y_atomic = routes && tab.route.arrivals ? 1 : 0;  // read back by another workgroup
+    const int y0_atomic = argm && tab.tail.arrivals ? 1 : 0;     // row 0 likewise
+    float *const y2o = PAIR ? job.y2 : nullptr;
+    float *const ho = PAIR ? job.h : nullptr;
+    __asm__ volatile("" ::"s"(yo), "s"(bo), "s"(accum), "s"(y_atomic), "s"(y0_atomic), "s"(y2o), "s"(ho));
     auto run_step = [&](const Chunks<PREC, CPL, R> &c) {
         const int r0 = (lw + k * nw) * R;
         compute_chunks<PREC, CPL, R, DOTS>(c, acc, sq, ssc, ssum, seg, lane, r0, rows, nb, C, job.dots);
@@ -357,9 +368,9 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
                 const float g = wave_sum(acc[i]), u = wave_sum(acc[i + 1]);
                 const int r = (r0 + i) >> 1;
                 if (lane == 0 && r < wrows) {
-                    job.y[r] = g;
-                    job.y2[r] = u;
-                    job.h[r] = swiglu1(g, u);
+                    yo[r] = g;
+                    y2o[r] = u;
+                    ho[r] = swiglu1(g, u);
                 }
                 acc[i] = 0.0f;
                 acc[i + 1] = 0.0f;
@@ -374,17 +385,17 @@ __global__ __launch_bounds__(WAVE * NWV) void gemv_kernel(unsigned f0, unsigned 
                     b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pbias), k * R + i));
                     y0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pres), k * R + i));
                 } else if (r < rows) {  // scalar loads: they wait on no weight load
-                    if (job.bias) b = ((const_f32 *)job.bias)[r];
-                    if (job.accumulate) y0 = ((const_f32 *)job.y)[r];
+                    if (bo) b = ((const_f32 *)bo)[r];
+                    if (accum) y0 = ((const_f32 *)yo)[r];
                 }
                 if (lane == 0 && r < rows) {
-                    float out = job.bias ? v + b : v;
-                    if (job.accumulate) out = y0 + out;  // x += proj (llama.rs:273-276)
+                    float out = bo ? v + b : v;
+                    if (accum) out = y0 + out;  // x += proj (llama.rs:273-276)
                     // read back by another workgroup: past the L2
-                    if ((routes && tab.route.arrivals) || (argm && r == 0 && tab.tail.arrivals))
-                        __hip_atomic_store(job.y + r, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (y_atomic || (y0_atomic && r == 0))
+                        __hip_atomic_store(yo + r, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     else
-                        job.y[r] = out;
+                        yo[r] = out;
                     if (routes) s_lg[r] = out;
                     // rows in increasing order: a later equal value never wins
                     if (argm && r >= 1 && out == out && (arg_bi < 0 || out > arg_bv)) arg_bv = out, arg_bi = r;
