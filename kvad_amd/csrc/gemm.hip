@@ -80,10 +80,55 @@ constexpr int BK = 128;              // k per stage (bytes of int8)
 constexpr int NBS = BK / BLOCK;      // 32-blocks per stage
 constexpr int ASTR = BK + 16;        // LDS row stride, bytes
 
+// A wave's RT x TT tiles when all of them lie inside the output (and the
+// output and bias are 16-byte aligned with rows a multiple of 4 wide): one
+// float4 per four rows, no per-element bounds and no branches.  dst is the
+// output (bias and accumulate as store_tiles) or a split's partial plane
+// (neither).  Returns false, having written nothing, otherwise.
+template <int RT, int TT>
+__device__ __forceinline__ bool store_tiles_full(const GemmArgs &a, float *dst, bool partial, const v16f (&acc)[RT][TT],
+                                                 int r_base, int t_base, int t_end, int lane) {
+    const float *bias = partial ? nullptr : a.bias;
+    const bool accumulate = !partial && a.accumulate;
+    if ((a.N & 3) || r_base + RT * 32 > a.N || t_base + TT * 32 > t_end ||
+        (((uintptr_t)dst | (uintptr_t)bias) & 15))
+        return false;
+    const rsrc_t Y = rsrc(dst + (size_t)t_base * a.N + r_base, ((size_t)(TT * 32 - 1) * a.N + RT * 32) * 4);
+    float4 bv[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            bv[rt][g] = bias ? *reinterpret_cast<const float4 *>(bias + r_base + rt * 32 + 8 * g + 4 * (lane >> 5))
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const unsigned off = ((unsigned)(tt * 32 + (lane & 31)) * (unsigned)a.N +
+                                      (unsigned)(rt * 32 + 8 * g + 4 * (lane >> 5))) * 4u;
+                float4 v = make_float4(acc[rt][tt][4 * g], acc[rt][tt][4 * g + 1], acc[rt][tt][4 * g + 2],
+                                       acc[rt][tt][4 * g + 3]);
+                if (!partial) {  // + bias (0 without one), finish, quant.rs:849-858
+                    const float4 b = bv[rt][g];
+                    v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+                }
+                if (accumulate) {  // x += proj (llama.rs:273-276)
+                    const float4 o = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(Y, off, 0, 0));
+                    v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, v), Y, off, 0, 0);
+            }
+    return true;
+}
+
 // Writes a 32x32 accumulator tile (lane: token l&31, rows 8g + 4(l>>5) + e).
 template <int RT, int TT>
 __device__ __forceinline__ void store_tiles(const GemmArgs &a, const v16f (&acc)[RT][TT], int r_base, int t_base,
                                             int t_end, int lane) {
+    if (store_tiles_full<RT, TT>(a, a.y, false, acc, r_base, t_base, t_end, lane)) return;
     const bool vec = (a.N & 3) == 0;
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
@@ -123,6 +168,7 @@ __device__ __forceinline__ void store_partials(const GemmArgs &a, const v16f (&a
                                                int t_end, int lane) {
     const size_t plane = (size_t)a.M * a.N;
     float *part = a.part + blockIdx.z * plane;
+    if (store_tiles_full<RT, TT>(a, part, true, acc, r_base, t_base, t_end, lane)) return;
     const bool vec = (a.N & 3) == 0;
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
