@@ -923,7 +923,12 @@ def moe(torch, K, ctx, stream, dev, gen, args, n_layers=8, rig=None):
     g = Graph(torch, ctx, stream, pre)
     s = g.time(max(5, args.steps // 5), 2, settle=1.0)
     ops = 2 * M * k * 3 * inter * hidden + 2 * M * 3 * sh * hidden
-    res["prefill_512tok"] = {"us": round(s * 1e6, 1), "TOPS": round(ops / s / 1e12, 2), "ops": ops}
+    # 512 tokens x k picks over n_exp experts pick every expert (about 48
+    # rows each), so the layer reads every expert's weights once: HBM-bound
+    # (651 MB at 8 TB/s = 81 us against 71 G int8 ops at 5 POP/s = 14 us)
+    pre_bytes = q8b(n_exp, hidden) + 3 * q8b(sh, hidden) + n_exp * 3 * q8b(inter, hidden) + 8 * M * hidden
+    res["prefill_512tok"] = {"us": round(s * 1e6, 1), "TOPS": round(ops / s / 1e12, 2), "ops": ops,
+                             "GBps": round(pre_bytes / s / 1e9, 1), "bytes": pre_bytes, "bound": "hbm"}
     del g
     if rig is not None:
         moe_cpu(rig, res, first, m0, hidden, inter, n_exp, k, sh, tok_bytes, ops)
