@@ -73,7 +73,7 @@ def parse():
                     help="only run a MIB-sized copy and two eager steps of the GEMV kernels (for rocprofv3 --pmc)")
     ap.add_argument("--gemm-counters", action="store_true",
                     help="only run three eager q8 prefill GEMMs per shape (for rocprofv3 --pmc)")
-    ap.add_argument("--kernel-counters", choices=("moe_decode", "mla", "attend"), default=None,
+    ap.add_argument("--kernel-counters", choices=("moe_decode", "moe_prefill", "mla", "attend"), default=None,
                     help="only run a few eager launches of one secondary workload (for rocprofv3 --pmc)")
     return ap.parse_args()
 
@@ -389,29 +389,32 @@ def main() -> int:
 def counter_workload(torch, K, ctx, stream, dev, gen, name, reps=3):
     """Eager launches of one secondary figure's kernels, for rocprofv3 --pmc
     passes (graph replays hide per-dispatch counters): the DeepSeek-V2-Lite
-    MoE decode layer (4 distinct layers, one token), latent attention at
+    MoE decode layer (4 distinct layers, one token) or prefill (one layer,
+    512 tokens), latent attention at
     L = 32768 (4 layers of distinct caches), or GQA attention at Qwen2.5-0.5B
     geometry and L = 32768 (8 layers)."""
     with torch.cuda.stream(stream):
-        if name == "moe_decode":
+        if name in ("moe_decode", "moe_prefill"):
             hidden, inter, n_exp, k, sh = 2048, 1408, 64, 6, 2816
+            n_layers, M = (4, 1) if name == "moe_decode" else (1, 512)
 
             def q8(rows, cols, sd=0.02):
                 f = torch.randn(rows, cols, device=dev, generator=gen) * sd
                 return K.Weight.quantize_dev(ctx, rows, cols, f.data_ptr(), K.Q8)
 
             layers = []
-            for _ in range(4):
+            for _ in range(n_layers):
                 m = K.Moe(ctx, n_exp, k, hidden, inter)
                 m.set_router(q8(n_exp, hidden, 0.5))
                 for x in range(n_exp):
                     m.set_expert(x, q8(inter, hidden), q8(inter, hidden), q8(hidden, inter))
                 m.set_shared(q8(sh, hidden), q8(sh, hidden), q8(hidden, sh))
-                layers.append((m, torch.randn(hidden, device=dev, generator=gen), torch.empty(hidden, device=dev)))
+                layers.append((m, torch.randn(M, hidden, device=dev, generator=gen),
+                               torch.empty(M, hidden, device=dev)))
             torch.cuda.synchronize()
             for _ in range(reps):
                 for m, x, y in layers:
-                    m.run_dev(x.data_ptr(), 1, y.data_ptr())
+                    m.run_dev(x.data_ptr(), M, y.data_ptr())
         elif name == "mla":
             L, H = 32768, 16
             c = torch.randn(4, L, 512, device=dev, generator=gen)
