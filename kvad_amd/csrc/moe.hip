@@ -35,6 +35,97 @@ __global__ __launch_bounds__(64) void route_kernel(RouteArgs r) {
     route_one(r, blockIdx.x, r.logits + (size_t)blockIdx.x * r.n);
 }
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes > 0xffffffffu ? 0xffffffffu : bytes), 0x00020000);
+}
+
+// A batch's routes with each token's logits made in its own workgroup (q8
+// routers), in place of the router GEMM, its split-K reduce and route_kernel:
+// token blockIdx.x's quantised row (the QActBatch::new codes and scales every
+// expert reads) against every router row -- per 32-block the exact i32 dot
+// scaled by ws * xs (qrow pass 2, quant.rs:443-451), the row's blocks summed
+// in each lane (blocks lane, lane + 64, ...) and then over the wave by a
+// fixed butterfly -- into LDS and `logits`, then route_one over them.  Each
+// wave takes rows wave * ER + i of every group of 4 * ER rows, all their
+// loads in flight together.  Rows and blocks past the ends read zeros.
+template <int NB>
+__global__ __launch_bounds__(256) void route_rows_kernel(RouteArgs r, float *logits, const int8_t *xq, const float *xs,
+                                                         const int8_t *wq, const float *wsc, int cols) {
+    constexpr int ER = 16 / NB;  // rows a wave has in flight
+    __shared__ float s_lg[MAX_EXPERTS];
+    const int tok = blockIdx.x, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = cols / BLOCK, n = r.n;
+    const rsrc_t X = rsrc(xq + (size_t)tok * cols, (size_t)cols);
+    const rsrc_t XS = rsrc(xs + (size_t)tok * nb, (size_t)nb * 4);
+    const rsrc_t W = rsrc(wq, (size_t)n * cols);
+    const rsrc_t WS = rsrc(wsc, (size_t)n * nb * 4);
+    auto ld16 = [](const rsrc_t &q, unsigned off) {
+        return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(q, off, 0, 0));
+    };
+    auto ldf = [](const rsrc_t &q, unsigned off) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(q, off, 0, 0));
+    };
+    constexpr unsigned OOB = 0xffffffffu;
+    int4 a[NB][2];
+    float as[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const int b = lane + 64 * j;
+        const unsigned o = b < nb ? (unsigned)b * BLOCK : OOB;
+        a[j][0] = ld16(X, o), a[j][1] = ld16(X, o == OOB ? OOB : o + 16);
+        as[j] = ldf(XS, b < nb ? (unsigned)b * 4 : OOB);
+    }
+    for (int e0 = wave * ER; e0 < n; e0 += 4 * ER) {
+        int4 w[ER][NB][2];
+        float s[ER][NB];
+#pragma unroll
+        for (int i = 0; i < ER; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const int e = e0 + i, b = lane + 64 * j;
+                const bool ok = e < n && b < nb;
+                const unsigned o = ok ? (unsigned)e * (unsigned)cols + (unsigned)b * BLOCK : OOB;
+                w[i][j][0] = ld16(W, o), w[i][j][1] = ld16(W, ok ? o + 16 : OOB);
+                s[i][j] = ldf(WS, ok ? ((unsigned)e * (unsigned)nb + (unsigned)b) * 4 : OOB);
+            }
+        __builtin_amdgcn_sched_barrier(0);  // every row's loads in flight before the first dot
+        float acc[ER];
+#pragma unroll
+        for (int i = 0; i < ER; i++) {
+            acc[i] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                int d = __builtin_amdgcn_sdot4(w[i][j][0].x, a[j][0].x, 0, false);
+                d = __builtin_amdgcn_sdot4(w[i][j][0].y, a[j][0].y, d, false);
+                d = __builtin_amdgcn_sdot4(w[i][j][0].z, a[j][0].z, d, false);
+                d = __builtin_amdgcn_sdot4(w[i][j][0].w, a[j][0].w, d, false);
+                d = __builtin_amdgcn_sdot4(w[i][j][1].x, a[j][1].x, d, false);
+                d = __builtin_amdgcn_sdot4(w[i][j][1].y, a[j][1].y, d, false);
+                d = __builtin_amdgcn_sdot4(w[i][j][1].z, a[j][1].z, d, false);
+                d = __builtin_amdgcn_sdot4(w[i][j][1].w, a[j][1].w, d, false);
+                const float sc = s[i][j] * as[j];
+                acc[i] += sc * (float)d;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+            for (int i = 0; i < ER; i++) acc[i] += __shfl_xor(acc[i], o);
+        if (lane < ER && e0 + lane < n) {
+            float v = acc[0];
+#pragma unroll
+            for (int i = 1; i < ER; i++) v = lane == i ? acc[i] : v;
+            s_lg[e0 + lane] = v;
+            logits[(size_t)tok * n + e0 + lane] = v;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) route_one(r, tok, s_lg);
+}
+
 // by_expert (ffn.rs:627-640): the picks' rows grouped by expert, experts in
 // order.  Within an expert the rows are placed by LDS atomics, in no fixed
 // order: no output depends on it (each row's products and its mix are its
@@ -414,6 +505,29 @@ PrefillBufs prefill_bufs(kh_ctx *ctx, const kh_moe *moe, size_t m) {
     return b;
 }
 
+// route_rows_kernel for m tokens quantised in q against a q8 router; KH_DECLINED
+// where it is not built for the router (other precisions, rows past 256
+// blocks, limits route_one does not take, KVAD_DEQUANT).
+int launch_route_rows(kh_ctx *ctx, const RouteArgs &r, float *logits, const QAct &q, const kh_weight *router, size_t m) {
+    const size_t cols = router->cols, nb = cols / BLOCK;
+    if (router->precision != KH_Q8 || cols % BLOCK || nb > 256 || dequant_selected() || r.n > MAX_EXPERTS ||
+        r.top_k > MAX_TOPK || r.n_group > MAX_GROUPS || m > 0x7fffffff)
+        return KH_DECLINED;
+    const dim3 grid((unsigned)m);
+    const int8_t *wq = static_cast<const int8_t *>(router->qs);
+    if (nb <= 64)
+        hipLaunchKernelGGL(route_rows_kernel<1>, grid, dim3(256), 0, ctx->stream, r, logits, q.qs, q.scales, wq,
+                           router->scales, (int)cols);
+    else if (nb <= 128)
+        hipLaunchKernelGGL(route_rows_kernel<2>, grid, dim3(256), 0, ctx->stream, r, logits, q.qs, q.scales, wq,
+                           router->scales, (int)cols);
+    else
+        hipLaunchKernelGGL(route_rows_kernel<4>, grid, dim3(256), 0, ctx->stream, r, logits, q.qs, q.scales, wq,
+                           router->scales, (int)cols);
+    KH_HIP(hipGetLastError());
+    return KH_OK;
+}
+
 int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out) {
     const size_t n = moe->n_experts, k = moe->top_k, hid = moe->hidden, inter = moe->inter;
     const size_t sh = moe->sgate ? moe->sgate->rows : 0;
@@ -434,12 +548,18 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     // shared one (QActBatch::new, quant.rs:693-714)
     if ((rc = launch_qact(ctx, hs, m, hid, hq))) return rc;
     // router logits (any precision; quantised weights read the codes above,
-    // the ones matmul_bt would make), then the routes
-    if (moe->router->precision != KH_F32 && moe->router->cols == hid)
-        rc = launch_matmul_q(ctx, moe->router, hq, m, nullptr, logits, 0);
-    else
-        rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits);
-    if (rc || (rc = launch_route(ctx, route_args(moe, logits, pe, pw, cnt), (int)m))) return rc;
+    // the ones matmul_bt would make), then the routes: for q8 routers one
+    // launch, a workgroup per token
+    const RouteArgs ra = route_args(moe, logits, pe, pw, cnt);
+    rc = launch_route_rows(ctx, ra, logits, hq, moe->router, m);
+    if (rc == KH_DECLINED) {
+        if (moe->router->precision != KH_F32 && moe->router->cols == hid)
+            rc = launch_matmul_q(ctx, moe->router, hq, m, nullptr, logits, 0);
+        else
+            rc = matmul_device(ctx, moe->router, hs, m, nullptr, logits);
+        if (!rc) rc = launch_route(ctx, ra, (int)m);
+    }
+    if (rc) return rc;
     // by_expert, and the tiles of the grouped GEMMs
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(GROUP_THREADS), 0, ctx->stream, pe, pw, cnt, (int)m, (int)k,
                        (int)n, tile_m, row_token, row_weight, pos, wpos, tiles);

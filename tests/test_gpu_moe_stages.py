@@ -136,6 +136,19 @@ def test_each_stage_of_a_small_layer(ctx, m):
     say("moe stages small worst", m, {k: f"{v:.1e}" for k, v in worst.items()}, f"flips {flips}/{codes}")
 
 
+@pytest.mark.parametrize("hidden", [4096, 8192])
+def test_each_stage_with_wide_router_rows(ctx, hidden):
+    # a batch's router logits come from one workgroup per token, one 32-block
+    # of the row per lane: rows of 4096 and 8192 values take two and four
+    # blocks a lane (and fewer rows in flight a wave)
+    say("moe stages wide router rows", hidden)
+    L = Layer(ctx, hidden=hidden, inter=64, n_exp=24, top_k=3, seed=930 + hidden // 1024)
+    m = 7
+    hs = O.normal(931, m * hidden)
+    worst, flips, codes = check_stages(L, hs, m, range(m))
+    say("moe stages wide worst", hidden, {k: f"{v:.1e}" for k, v in worst.items()}, f"flips {flips}/{codes}")
+
+
 @pytest.fixture(scope="module")
 def deepseek(ctx):
     # hidden 2048, 64 routed experts of width 1408, top-6,
