@@ -144,44 +144,43 @@ __device__ __forceinline__ void route_one(const RouteArgs &r, int tok, const flo
         }
     }
     wave_lds_sync();
-    const int got = s_best;
+    const int got = __builtin_amdgcn_readfirstlane(s_best);  // the same in every lane
 
-    if (lane == 0) {
-        const bool normalised = r.norm_topk && r.top_k > 1;
-        if (normalised) {  // ffn.rs:296-302
-            float total = 0.0f;
-            for (int i = 0; i < got; i++) total += s_pick_w[i];
-            total += 1e-20f;
-            for (int i = 0; i < got; i++) s_pick_w[i] /= total;
-        }
-        if (r.always_scale || !normalised)
-            for (int i = 0; i < got; i++) s_pick_w[i] *= r.scale;
-        int32_t *e = r.experts + (size_t)tok * r.top_k;
-        float *w = r.weights + (size_t)tok * r.top_k;
-        for (int i = 0; i < r.top_k; i++) {
-            e[i] = i < got ? s_pick_e[i] : -1;
-            w[i] = i < got ? s_pick_w[i] : 0.0f;
-        }
-        r.count[tok] = got;
-        if (r.sorted_experts) {
-            // the picks in expert order; unused slots name expert 0 with
-            // weight 0, so a kernel that reads every slot stays in bounds
-            int se[MAX_TOPK];
-            float sw[MAX_TOPK];
-            for (int i = 0; i < got; i++) {
-                int j = i;
-                while (j > 0 && se[j - 1] > s_pick_e[i]) {
-                    se[j] = se[j - 1];
-                    sw[j] = sw[j - 1];
-                    j--;
-                }
-                se[j] = s_pick_e[i];
-                sw[j] = s_pick_w[i];
-            }
-            for (int i = 0; i < r.top_k; i++) {
-                r.sorted_experts[(size_t)tok * r.top_k + i] = i < got ? se[i] : 0;
-                r.sorted_weights[(size_t)tok * r.top_k + i] = i < got ? sw[i] : 0.0f;
-            }
+    // Lane i holds pick i.  The normalising total is summed in pick order
+    // (one lane's values read across, as the reference adds them), each
+    // pick's divide and scale are its own lane's, and every lane writes its
+    // own slots.
+    const bool mine = lane < got;
+    const int pe = mine ? s_pick_e[lane] : 0;
+    float pw = mine ? s_pick_w[lane] : 0.0f;
+    const bool normalised = r.norm_topk && r.top_k > 1;
+    if (normalised) {  // ffn.rs:296-302
+        float total = 0.0f;
+        for (int i = 0; i < got; i++)
+            total += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pw), i));
+        total += 1e-20f;
+        pw = pw / total;
+    }
+    if (r.always_scale || !normalised) pw *= r.scale;
+    if (lane < r.top_k) {
+        r.experts[(size_t)tok * r.top_k + lane] = mine ? pe : -1;
+        r.weights[(size_t)tok * r.top_k + lane] = mine ? pw : 0.0f;
+    }
+    if (lane == 0) r.count[tok] = got;
+    if (r.sorted_experts) {
+        // the picks in expert order (each pick's place is the number of
+        // picks naming a smaller expert; the experts are distinct); unused
+        // slots name expert 0 with weight 0, so a kernel that reads every
+        // slot stays in bounds
+        int at = 0;
+        for (int i = 0; i < got; i++) at += __builtin_amdgcn_readlane(pe, i) < pe;
+        const size_t o = (size_t)tok * r.top_k;
+        if (mine) {
+            r.sorted_experts[o + at] = pe;
+            r.sorted_weights[o + at] = pw;
+        } else if (lane < r.top_k) {
+            r.sorted_experts[o + lane] = 0;
+            r.sorted_weights[o + lane] = 0.0f;
         }
     }
 }
