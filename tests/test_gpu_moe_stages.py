@@ -149,6 +149,17 @@ def test_each_stage_with_wide_router_rows(ctx, hidden):
     say("moe stages wide worst", hidden, {k: f"{v:.1e}" for k, v in worst.items()}, f"flips {flips}/{codes}")
 
 
+def test_each_stage_with_many_experts(ctx):
+    # 160 experts (DeepSeek-V2's count): each wave of the per-token router
+    # takes rows wave * 16 .. + 15 of every 64, three rounds, the last partial
+    say("moe stages 160 experts")
+    L = Layer(ctx, hidden=512, inter=32, n_exp=160, top_k=6, seed=940)
+    m = 9
+    hs = O.normal(941, m * 512)
+    worst, flips, codes = check_stages(L, hs, m, range(m))
+    say("moe stages 160 worst", {k: f"{v:.1e}" for k, v in worst.items()}, f"flips {flips}/{codes}")
+
+
 @pytest.fixture(scope="module")
 def deepseek(ctx):
     # hidden 2048, 64 routed experts of width 1408, top-6,
