@@ -510,7 +510,8 @@ PrefillBufs prefill_bufs(kh_ctx *ctx, const kh_moe *moe, size_t m) {
 // blocks, limits route_one does not take, KVAD_DEQUANT).
 int launch_route_rows(kh_ctx *ctx, const RouteArgs &r, float *logits, const QAct &q, const kh_weight *router, size_t m) {
     const size_t cols = router->cols, nb = cols / BLOCK;
-    if (router->precision != KH_Q8 || cols % BLOCK || nb > 256 || dequant_selected() || r.n > MAX_EXPERTS ||
+    if (router->precision != KH_Q8 || cols % BLOCK || nb > 256 || router->rows != (size_t)r.n ||
+        dequant_selected() || r.n > MAX_EXPERTS ||
         r.top_k > MAX_TOPK || r.n_group > MAX_GROUPS || m > 0x7fffffff)
         return KH_DECLINED;
     const dim3 grid((unsigned)m);
