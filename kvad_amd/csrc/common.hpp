@@ -404,16 +404,6 @@ struct RouteArgs {
     int groups;
 };
 int launch_route(kh_ctx *ctx, const RouteArgs &r, int m);
-// Groups m tokens' picks by expert (expert order, then token order): rows
-// [m*top_k] of (token, weight), each token's k-th pick's row in pos, and the
-// grouped-GEMM tile table for tiles of tile_m rows.
-int launch_moe_group(kh_ctx *ctx, const int32_t *experts, const float *weights, const int32_t *count, int m,
-                     int top_k, int n_exp, int tile_m, int32_t *row_token, float *row_weight, int32_t *pos,
-                     int32_t *tiles);
-// out[i] = base[i] (or 0) + sum over token i's picks in expert order of w * y[pos].
-int launch_moe_combine(kh_ctx *ctx, const float *base, const float *y, const int32_t *experts,
-                       const float *weights, const int32_t *count, const int32_t *pos, int m, int top_k,
-                       int hidden, float *out);
 
 // Split decode attention over one layer's cache, device pointers.
 int launch_attend(kh_ctx *ctx, int n_head, int n_kv_head, int head_dim, const float *q, const float *k,

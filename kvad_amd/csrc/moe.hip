@@ -222,25 +222,28 @@ __global__ __launch_bounds__(GROUP_THREADS) void group_kernel(const int32_t *exp
 // order (the mix order, ffn.rs:775-805): pick k's row is pos[t * top_k + k]
 // (in expert order, as group_kernel writes it) or, `pos` null, t * top_k + k
 // (the picks already in expert order); weights in the same order.  Grid:
-// (hidden / 256, tokens); every load of a thread is independent, so they fly
-// together.
+// (hidden / 256, tokens).  Every slot's row and weight are loaded together
+// with the pick count, not after it (a slot past the count holds a stale
+// row, clamped into the `rows` rows of y, whose product is left out of the
+// sum), so the value loads wait on one round trip, not two.
 __global__ __launch_bounds__(256) void combine_kernel(const float *base, const float *y, const float *weights,
                                                      const int32_t *count, const int32_t *pos, int top_k, int hidden,
-                                                     float *out) {
+                                                     int rows, float *out) {
     const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
-    const int n = count[t];
     int pr[MAX_TOPK];
     float pw[MAX_TOPK];
 #pragma unroll
     for (int k = 0; k < MAX_TOPK; k++) {
-        const bool ok = k < n;
-        pr[k] = ok ? (pos ? pos[(size_t)t * top_k + k] : t * top_k + k) : 0;
+        const bool ok = k < top_k;
+        const int r = ok ? (pos ? pos[(size_t)t * top_k + k] : t * top_k + k) : 0;
+        pr[k] = min(max(r, 0), rows - 1);
         pw[k] = ok ? weights[(size_t)t * top_k + k] : 0.0f;
     }
+    const int n = count[t];
     if (i >= hidden) return;
     float yv[MAX_TOPK];
 #pragma unroll
-    for (int k = 0; k < MAX_TOPK; k++) yv[k] = k < n ? y[(size_t)pr[k] * hidden + i] : 0.0f;
+    for (int k = 0; k < MAX_TOPK; k++) yv[k] = k < top_k ? y[(size_t)pr[k] * hidden + i] : 0.0f;
     float v = base ? base[(size_t)t * hidden + i] : 0.0f;
 #pragma unroll
     for (int k = 0; k < MAX_TOPK; k++) {
@@ -427,7 +430,7 @@ int moe_decode(kh_ctx *ctx, kh_moe *moe, const float *x, float *out) {
     }
     // (5) out = shared, then + w * y in expert order
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((hid + 255) / 256), 1), dim3(256), 0, ctx->stream,
-                       sh ? ys : nullptr, y, sw, cnt, nullptr, (int)k, (int)hid, out);
+                       sh ? ys : nullptr, y, sw, cnt, nullptr, (int)k, (int)hid, (int)k, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
@@ -592,7 +595,7 @@ int moe_prefill(kh_ctx *ctx, kh_moe *moe, const float *hs, size_t m, float *out)
     if ((rc = launch_gemm_q(ctx, moe->precision, d, (int)max_tiles, tile_m))) return rc;
     // out = shared, then + w * y per token in expert order
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((hid + 255) / 256), (unsigned)m), dim3(256), 0, ctx->stream,
-                       base, y, wpos, cnt, pos, (int)k, (int)hid, out);
+                       base, y, wpos, cnt, pos, (int)k, (int)hid, (int)total, out);
     KH_HIP(hipGetLastError());
     return KH_OK;
 }
