@@ -24,9 +24,10 @@ __device__ __forceinline__ int total_key(float f) {
 }
 
 // Router::route for one token, run by one wave (ffn.rs:256-309), over the
-// token's logits `lg` (global memory or LDS).  The softmax's sum and the
-// normalisation run in one lane in index order, as the reference sums them;
-// the top-k picks the largest choice, the lowest index on ties.  Only the
+// token's logits `lg` (global memory or LDS).  The softmax's sum runs in one
+// lane in index order and the picks' normalising total in pick order, as the
+// reference sums them; the top-k picks the largest choice, the lowest index
+// on ties.  Only the
 // calling wave takes part: it syncs with itself (wave_lds_sync), never with
 // the rest of its workgroup.
 __device__ __forceinline__ void route_one(const RouteArgs &r, int tok, const float *lg) {
