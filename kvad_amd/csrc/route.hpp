@@ -27,9 +27,8 @@ __device__ __forceinline__ int total_key(float f) {
 // token's logits `lg` (global memory or LDS).  The softmax's sum runs in one
 // lane in index order and the picks' normalising total in pick order, as the
 // reference sums them; the top-k picks the largest choice, the lowest index
-// on ties.  Only the
-// calling wave takes part: it syncs with itself (wave_lds_sync), never with
-// the rest of its workgroup.
+// on ties.  Only the calling wave takes part: it syncs with itself
+// (wave_lds_sync), never with the rest of its workgroup.
 __device__ __forceinline__ void route_one(const RouteArgs &r, int tok, const float *lg) {
     const int lane = threadIdx.x & 63, n = r.n;
     __shared__ __align__(16) float s_score[MAX_EXPERTS], s_choice[MAX_EXPERTS];  // padded to n16
